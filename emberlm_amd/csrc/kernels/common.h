@@ -1,0 +1,74 @@
+// Shared helpers for the gfx950 kernels behind include/ember_hip.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "ember_hip.h"
+
+namespace ember {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kWave = 64;
+
+inline int status_of(hipError_t e) { return e == hipSuccess ? EMBER_OK : static_cast<int>(e); }
+
+// Status of the most recent launch on this thread.
+inline int launch_status() { return status_of(hipGetLastError()); }
+
+inline hipStream_t as_stream(ember_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline unsigned grid_1d(int64_t n, int threads, int64_t cap = 1 << 20) {
+  int64_t g = (n + threads - 1) / threads;
+  if (g > cap) g = cap;
+  if (g < 1) g = 1;
+  return static_cast<unsigned>(g);
+}
+
+// Full-wave (64-lane) reductions through DPP-free shuffles.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Block-wide sum for blockDim.x = 64 * nwaves; result valid in every lane.
+// `smem` holds at least nwaves floats.  Fixed reduction order (deterministic).
+__device__ __forceinline__ float block_sum(float v, float* smem) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) smem[wid] = v;
+  __syncthreads();
+  float t = 0.0f;
+  for (int i = 0; i < nw; ++i) t += smem[i];
+  return t;
+}
+
+__device__ __forceinline__ float block_max(float v, float* smem) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  v = wave_max(v);
+  __syncthreads();
+  if (lane == 0) smem[wid] = v;
+  __syncthreads();
+  float t = -INFINITY;
+  for (int i = 0; i < nw; ++i) t = fmaxf(t, smem[i]);
+  return t;
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace ember

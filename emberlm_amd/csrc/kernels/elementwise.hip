@@ -1,0 +1,159 @@
+// Elementwise kernels: residual add, autograd fan-in accumulate, scale, SiLU
+// and the fused SwiGLU forward/backward.
+//
+// Reference: src/ops/elementwise.cu:15-69 (one thread per element, silu with
+// __expf forward and expf backward), mul_scalar (repeat_kv.cu:45-51) and
+// addinto (autograd.cu:88-93).  Here every kernel streams float4 with a
+// grid-stride loop, and MLP::forward's silu -> mul pair (mlp.h:16-21) is one
+// pass that never writes silu(g).
+#include "common.h"
+
+using namespace ember;
+
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float sigmoidf_acc(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+enum class Op { kAdd, kSub, kMul, kScale, kAccum, kSilu, kSiluBwd, kSwigluFwd };
+
+template <Op OP>
+__device__ __forceinline__ float apply(float a, float b, float alpha) {
+  switch (OP) {
+    case Op::kAdd: return a + b;
+    case Op::kSub: return a - b;
+    case Op::kMul: return a * b;
+    case Op::kScale: return a * alpha;
+    case Op::kAccum: return a + b;
+    case Op::kSilu: return a * sigmoidf_acc(a);
+    case Op::kSiluBwd: {
+      const float s = sigmoidf_acc(a);
+      return b * (s + a * s * (1.0f - s));
+    }
+    case Op::kSwigluFwd: return a * sigmoidf_acc(a) * b;
+  }
+  return 0.f;
+}
+
+// y[i] = op(a[i], b[i]); b may be null for unary ops.  Pointers may alias
+// (y == a for accumulate); each element is read before it is written by the
+// same thread.
+template <Op OP, bool VEC>
+__global__ __launch_bounds__(kThreads) void binary_kernel(const float* a, const float* b, float* y,
+                                                          int64_t n, float alpha) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (VEC) {
+    const int64_t n4 = n / 4;
+    for (int64_t i = tid; i < n4; i += stride) {
+      const f32x4 va = reinterpret_cast<const f32x4*>(a)[i];
+      const f32x4 vb = b ? reinterpret_cast<const f32x4*>(b)[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+      f32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = apply<OP>(va[e], vb[e], alpha);
+      reinterpret_cast<f32x4*>(y)[i] = o;
+    }
+    for (int64_t i = n4 * 4 + tid; i < n; i += stride) y[i] = apply<OP>(a[i], b ? b[i] : 0.f, alpha);
+  } else {
+    for (int64_t i = tid; i < n; i += stride) y[i] = apply<OP>(a[i], b ? b[i] : 0.f, alpha);
+  }
+}
+
+template <Op OP>
+int run(const float* a, const float* b, float* y, int64_t n, float alpha, ember_stream_t s) {
+  if (n < 0) return EMBER_EINVAL;
+  if (n == 0) return EMBER_OK;
+  if (!a || !y) return EMBER_EINVAL;
+  const bool vec = aligned16(a) && aligned16(y) && (!b || aligned16(b));
+  const unsigned g = grid_1d(vec ? (n + 3) / 4 : n, kThreads, 8192);
+  if (vec)
+    binary_kernel<OP, true><<<g, kThreads, 0, as_stream(s)>>>(a, b, y, n, alpha);
+  else
+    binary_kernel<OP, false><<<g, kThreads, 0, as_stream(s)>>>(a, b, y, n, alpha);
+  return launch_status();
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void swiglu_bwd_kernel(const float* __restrict__ g,
+                                                              const float* __restrict__ u,
+                                                              const float* dh, float* dg,
+                                                              float* du, int64_t n) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  auto one = [](float gv, float uv, float d, float& og, float& ou) {
+    const float s = sigmoidf_acc(gv);
+    const float si = gv * s;
+    og = d * uv * (s + gv * s * (1.0f - s));
+    ou = d * si;
+  };
+  if (VEC) {
+    const int64_t n4 = n / 4;
+    for (int64_t i = tid; i < n4; i += stride) {
+      const f32x4 vg = reinterpret_cast<const f32x4*>(g)[i];
+      const f32x4 vu = reinterpret_cast<const f32x4*>(u)[i];
+      const f32x4 vd = reinterpret_cast<const f32x4*>(dh)[i];
+      f32x4 og, ou;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float a, b;
+        one(vg[e], vu[e], vd[e], a, b);
+        og[e] = a;
+        ou[e] = b;
+      }
+      reinterpret_cast<f32x4*>(dg)[i] = og;
+      reinterpret_cast<f32x4*>(du)[i] = ou;
+    }
+    for (int64_t i = n4 * 4 + tid; i < n; i += stride) one(g[i], u[i], dh[i], dg[i], du[i]);
+  } else {
+    for (int64_t i = tid; i < n; i += stride) one(g[i], u[i], dh[i], dg[i], du[i]);
+  }
+}
+
+}  // namespace
+
+extern "C" int ember_add(const float* a, const float* b, float* y, int64_t n, ember_stream_t s) {
+  if (n > 0 && !b) return EMBER_EINVAL;
+  return run<Op::kAdd>(a, b, y, n, 0.f, s);
+}
+extern "C" int ember_sub(const float* a, const float* b, float* y, int64_t n, ember_stream_t s) {
+  if (n > 0 && !b) return EMBER_EINVAL;
+  return run<Op::kSub>(a, b, y, n, 0.f, s);
+}
+extern "C" int ember_mul(const float* a, const float* b, float* y, int64_t n, ember_stream_t s) {
+  if (n > 0 && !b) return EMBER_EINVAL;
+  return run<Op::kMul>(a, b, y, n, 0.f, s);
+}
+extern "C" int ember_scale(const float* x, float alpha, float* y, int64_t n, ember_stream_t s) {
+  return run<Op::kScale>(x, nullptr, y, n, alpha, s);
+}
+extern "C" int ember_accumulate(float* y, const float* x, int64_t n, ember_stream_t s) {
+  if (n > 0 && !x) return EMBER_EINVAL;
+  return run<Op::kAccum>(y, x, y, n, 0.f, s);
+}
+extern "C" int ember_silu(const float* x, float* y, int64_t n, ember_stream_t s) {
+  return run<Op::kSilu>(x, nullptr, y, n, 0.f, s);
+}
+extern "C" int ember_silu_bwd(const float* x, const float* g, float* dx, int64_t n,
+                              ember_stream_t s) {
+  if (n > 0 && !g) return EMBER_EINVAL;
+  return run<Op::kSiluBwd>(x, g, dx, n, 0.f, s);
+}
+extern "C" int ember_swiglu_fwd(const float* g, const float* u, float* h, int64_t n,
+                                ember_stream_t s) {
+  if (n > 0 && !u) return EMBER_EINVAL;
+  return run<Op::kSwigluFwd>(g, u, h, n, 0.f, s);
+}
+extern "C" int ember_swiglu_bwd(const float* g, const float* u, const float* dh, float* dg,
+                                float* du, int64_t n, ember_stream_t s) {
+  if (n < 0) return EMBER_EINVAL;
+  if (n == 0) return EMBER_OK;
+  if (!g || !u || !dh || !dg || !du) return EMBER_EINVAL;
+  const bool vec = aligned16(g) && aligned16(u) && aligned16(dh) && aligned16(dg) && aligned16(du);
+  const unsigned grid = grid_1d(vec ? (n + 3) / 4 : n, kThreads, 8192);
+  if (vec)
+    swiglu_bwd_kernel<true><<<grid, kThreads, 0, as_stream(s)>>>(g, u, dh, dg, du, n);
+  else
+    swiglu_bwd_kernel<false><<<grid, kThreads, 0, as_stream(s)>>>(g, u, dh, dg, du, n);
+  return launch_status();
+}

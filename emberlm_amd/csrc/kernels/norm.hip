@@ -1,0 +1,298 @@
+// RMSNorm forward/backward (block norms and per-head QK-Norm).
+//
+// Reference: rms_norm_kernel_f32 / rms_norm_backward_kernel_f32
+// (src/ops/norm.cu:17-106).  The reference gives every row a 256-thread block
+// (half idle at H = 128) and sums dw with atomicAdd.  Here a row is owned by a
+// group of LPR lanes (LPR = 64 for H >= 256, fewer for the 64/128-wide
+// QK-Norm rows, so one wave covers several rows), rows are read as float4,
+// and dw is reduced deterministically: each block sums its rows in a fixed
+// order into a workspace row, then one pass sums the workspace rows in order.
+#include "common.h"
+
+using namespace ember;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxBwdBlocks = 1024;
+
+__device__ __forceinline__ float group_sum(float v, int lpr) {
+  for (int o = lpr >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// Lanes per row for a row of H floats read as float4 (H % 4 == 0).
+inline int lanes_per_row(int64_t H) {
+  int64_t c = H / 4;
+  int lpr = 1;
+  while (lpr < 64 && lpr < c) lpr <<= 1;
+  return lpr;
+}
+
+template <int LPR>
+__global__ __launch_bounds__(kThreads) void rmsnorm_fwd_vec(const float* __restrict__ x,
+                                                            const float* __restrict__ w,
+                                                            float* __restrict__ y,
+                                                            float* __restrict__ rstd,
+                                                            int64_t rows, int64_t H, float eps) {
+  constexpr int RPB = kThreads / LPR;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
+  const int sub = threadIdx.x % LPR;
+  const int64_t nc = H / 4;
+  const bool live = row < rows;
+  const f32x4* xr = reinterpret_cast<const f32x4*>(x + (live ? row : 0) * H);
+  float ss = 0.f;
+  if (live)
+    for (int64_t c = sub; c < nc; c += LPR) {
+      const f32x4 v = xr[c];
+      ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+    }
+  ss = group_sum(ss, LPR);
+  if (!live) return;
+  const float s = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
+  if (rstd && sub == 0) rstd[row] = s;
+  f32x4* yr = reinterpret_cast<f32x4*>(y + row * H);
+  const f32x4* wv = reinterpret_cast<const f32x4*>(w);
+  for (int64_t c = sub; c < nc; c += LPR) {
+    const f32x4 v = xr[c], ww = wv[c];
+    f32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = v[e] * s * ww[e];
+    yr[c] = o;
+  }
+}
+
+// Any H: one block per row, scalar accesses.
+__global__ __launch_bounds__(kThreads) void rmsnorm_fwd_scalar(const float* __restrict__ x,
+                                                               const float* __restrict__ w,
+                                                               float* __restrict__ y,
+                                                               float* __restrict__ rstd,
+                                                               int64_t rows, int64_t H, float eps) {
+  __shared__ float red[kThreads / kWave];
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * H;
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < H; i += kThreads) ss += xr[i] * xr[i];
+  ss = block_sum(ss, red);
+  const float s = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
+  if (rstd && threadIdx.x == 0) rstd[row] = s;
+  for (int64_t i = threadIdx.x; i < H; i += kThreads) y[row * H + i] = xr[i] * s * w[i];
+}
+
+// Backward, float4 path.  Block b handles rows b*RPB + slot + k*grid*RPB.
+// MAXC = float4 chunks per lane (H/4/LPR rounded up) kept as dw partials.
+template <int LPR, int MAXC>
+__global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
+    const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ w,
+    const float* __restrict__ rstd, float* __restrict__ dx, float* __restrict__ dw_part,
+    int64_t rows, int64_t H, float eps) {
+  constexpr int RPB = kThreads / LPR;
+  extern __shared__ __attribute__((aligned(16))) float red[];  // [RPB][H]
+  const int slot = threadIdx.x / LPR;
+  const int sub = threadIdx.x % LPR;
+  const int64_t nc = H / 4;
+  const float invH = 1.0f / static_cast<float>(H);
+  const f32x4* wv = reinterpret_cast<const f32x4*>(w);
+  f32x4 acc[MAXC];
+#pragma unroll
+  for (int j = 0; j < MAXC; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int64_t step = static_cast<int64_t>(gridDim.x) * RPB;
+  for (int64_t row0 = static_cast<int64_t>(blockIdx.x) * RPB; row0 < rows; row0 += step) {
+    const int64_t row = row0 + slot;
+    const bool live = row < rows;
+    const f32x4* xr = reinterpret_cast<const f32x4*>(x + (live ? row : 0) * H);
+    const f32x4* gr = reinterpret_cast<const f32x4*>(dy + (live ? row : 0) * H);
+    float ss = 0.f, c = 0.f;
+    if (live)
+#pragma unroll
+      for (int j = 0; j < MAXC; ++j) {
+        const int64_t ci = sub + static_cast<int64_t>(j) * LPR;
+        if (ci < nc) {
+          const f32x4 v = xr[ci], g = gr[ci], ww = wv[ci];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            ss += v[e] * v[e];
+            c += g[e] * ww[e] * v[e];
+          }
+        }
+      }
+    ss = group_sum(ss, LPR);
+    c = group_sum(c, LPR);
+    if (!live) continue;
+    const float s = rstd ? rstd[row] : 1.0f / sqrtf(ss * invH + eps);
+    const float k = s * s * c * invH;
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j) {
+      const int64_t ci = sub + static_cast<int64_t>(j) * LPR;
+      if (ci < nc) {
+        const f32x4 v = xr[ci], g = gr[ci], ww = wv[ci];
+        f32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o[e] = s * (g[e] * ww[e] - v[e] * k);
+          acc[j][e] += g[e] * v[e] * s;
+        }
+        if (dx) reinterpret_cast<f32x4*>(dx + row * H)[ci] = o;
+      }
+    }
+  }
+  if (!dw_part) return;
+  // Combine the RPB row slots of this block in slot order.
+#pragma unroll
+  for (int j = 0; j < MAXC; ++j) {
+    const int64_t ci = sub + static_cast<int64_t>(j) * LPR;
+    if (ci < nc) reinterpret_cast<f32x4*>(red + slot * H)[ci] = acc[j];
+  }
+  __syncthreads();
+  for (int64_t col = threadIdx.x; col < H; col += kThreads) {
+    float t = 0.f;
+    for (int sl = 0; sl < RPB; ++sl) t += red[sl * H + col];
+    dw_part[static_cast<int64_t>(blockIdx.x) * H + col] = t;
+  }
+}
+
+// Any H (slow path): block per row for dx; dw partial per block of rows.
+__global__ __launch_bounds__(kThreads) void rmsnorm_bwd_scalar(
+    const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ w,
+    const float* __restrict__ rstd, float* __restrict__ dx, float* __restrict__ dw_part,
+    int64_t rows, int64_t H, float eps) {
+  __shared__ float red[kThreads / kWave];
+  const float invH = 1.0f / static_cast<float>(H);
+  for (int64_t col0 = 0; col0 < H; col0 += kThreads) {
+    if (dw_part && col0 + threadIdx.x < H) dw_part[blockIdx.x * H + col0 + threadIdx.x] = 0.f;
+  }
+  __syncthreads();
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const float* xr = x + row * H;
+    const float* gr = dy + row * H;
+    float ss = 0.f, c = 0.f;
+    for (int64_t i = threadIdx.x; i < H; i += kThreads) {
+      ss += xr[i] * xr[i];
+      c += gr[i] * w[i] * xr[i];
+    }
+    ss = block_sum(ss, red);
+    c = block_sum(c, red);
+    const float s = rstd ? rstd[row] : 1.0f / sqrtf(ss * invH + eps);
+    for (int64_t i = threadIdx.x; i < H; i += kThreads) {
+      if (dx) dx[row * H + i] = s * (gr[i] * w[i] - xr[i] * s * s * c * invH);
+      if (dw_part) dw_part[blockIdx.x * H + i] += gr[i] * xr[i] * s;
+    }
+  }
+}
+
+__global__ void column_sum(const float* __restrict__ part, float* __restrict__ out, int64_t nrows,
+                           int64_t H) {
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (col >= H) return;
+  float t = 0.f;
+  for (int64_t r = 0; r < nrows; ++r) t += part[r * H + col];
+  out[col] = t;
+}
+
+bool vec_ok(int64_t H, const void* a, const void* b) {
+  return H % 4 == 0 && aligned16(a) && aligned16(b);
+}
+
+int64_t bwd_blocks(int64_t rows, int64_t H, bool vec) {
+  const int64_t rpb = vec ? kThreads / lanes_per_row(H) : 1;
+  int64_t nb = (rows + rpb - 1) / rpb;
+  if (nb > kMaxBwdBlocks) nb = kMaxBwdBlocks;
+  if (nb < 1) nb = 1;
+  return nb;
+}
+
+template <int LPR>
+int launch_bwd_lpr(int64_t nb, const float* dy, const float* x, const float* w, const float* rstd,
+                   float* dx, float* part, int64_t rows, int64_t H, float eps, hipStream_t st) {
+  const int64_t chunks = (H / 4 + LPR - 1) / LPR;
+  const size_t lds = static_cast<size_t>(kThreads / LPR) * H * sizeof(float);
+  if (lds > 64 * 1024) return EMBER_EINVAL;
+#define EMBER_BWD_CASE(MC)                                                                     \
+  if (chunks <= MC) {                                                                          \
+    rmsnorm_bwd_vec<LPR, MC><<<static_cast<unsigned>(nb), kThreads, part ? lds : 0, st>>>(     \
+        dy, x, w, rstd, dx, part, rows, H, eps);                                               \
+    return launch_status();                                                                    \
+  }
+  EMBER_BWD_CASE(1)
+  EMBER_BWD_CASE(2)
+  EMBER_BWD_CASE(4)
+  EMBER_BWD_CASE(8)
+  EMBER_BWD_CASE(16)
+#undef EMBER_BWD_CASE
+  return EMBER_EINVAL;
+}
+
+}  // namespace
+
+extern "C" int ember_rmsnorm_fwd(const float* x, const float* w, float* y, float* rstd,
+                                 int64_t rows, int64_t H, float eps, ember_stream_t s) {
+  if (rows < 0 || H <= 0 || (rows > 0 && (!x || !w || !y))) return EMBER_EINVAL;
+  if (rows == 0) return EMBER_OK;
+  hipStream_t st = as_stream(s);
+  if (vec_ok(H, x, y) && aligned16(w)) {
+    const int lpr = lanes_per_row(H);
+    const unsigned nb = static_cast<unsigned>((rows + kThreads / lpr - 1) / (kThreads / lpr));
+    switch (lpr) {
+      case 1: rmsnorm_fwd_vec<1><<<nb, kThreads, 0, st>>>(x, w, y, rstd, rows, H, eps); break;
+      case 2: rmsnorm_fwd_vec<2><<<nb, kThreads, 0, st>>>(x, w, y, rstd, rows, H, eps); break;
+      case 4: rmsnorm_fwd_vec<4><<<nb, kThreads, 0, st>>>(x, w, y, rstd, rows, H, eps); break;
+      case 8: rmsnorm_fwd_vec<8><<<nb, kThreads, 0, st>>>(x, w, y, rstd, rows, H, eps); break;
+      case 16: rmsnorm_fwd_vec<16><<<nb, kThreads, 0, st>>>(x, w, y, rstd, rows, H, eps); break;
+      case 32: rmsnorm_fwd_vec<32><<<nb, kThreads, 0, st>>>(x, w, y, rstd, rows, H, eps); break;
+      default: rmsnorm_fwd_vec<64><<<nb, kThreads, 0, st>>>(x, w, y, rstd, rows, H, eps); break;
+    }
+  } else {
+    if (rows > 0x7fffffff) return EMBER_EINVAL;
+    rmsnorm_fwd_scalar<<<static_cast<unsigned>(rows), kThreads, 0, st>>>(x, w, y, rstd, rows, H,
+                                                                         eps);
+  }
+  return launch_status();
+}
+
+extern "C" size_t ember_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t H) {
+  if (rows <= 0 || H <= 0) return 0;
+  const bool vec = H % 4 == 0 && H / 4 <= 16 * 64;
+  return static_cast<size_t>(bwd_blocks(rows, H, vec)) * H * sizeof(float);
+}
+
+extern "C" int ember_rmsnorm_bwd(const float* dy, const float* x, const float* w,
+                                 const float* rstd, float* dx, float* dw, int64_t rows, int64_t H,
+                                 float eps, void* workspace, size_t workspace_bytes,
+                                 ember_stream_t s) {
+  if (rows < 0 || H <= 0 || !w) return EMBER_EINVAL;
+  if (rows > 0 && (!dy || !x)) return EMBER_EINVAL;
+  hipStream_t st = as_stream(s);
+  if (rows == 0) {
+    if (dw) return ember_fill(dw, H, 0.f, s);
+    return EMBER_OK;
+  }
+  const bool vec = H % 4 == 0 && H / 4 <= 16 * 64 && aligned16(dy) && aligned16(x) &&
+                   aligned16(w) && (!dx || aligned16(dx));
+  float* part = nullptr;
+  const int64_t nb = bwd_blocks(rows, H, H % 4 == 0 && H / 4 <= 16 * 64);
+  if (dw) {
+    const size_t need = static_cast<size_t>(nb) * H * sizeof(float);
+    if (!workspace || workspace_bytes < need) return EMBER_EWORKSPACE;
+    part = static_cast<float*>(workspace);
+  }
+  int rc;
+  if (vec) {
+    switch (lanes_per_row(H)) {
+      case 1: rc = launch_bwd_lpr<1>(nb, dy, x, w, rstd, dx, part, rows, H, eps, st); break;
+      case 2: rc = launch_bwd_lpr<2>(nb, dy, x, w, rstd, dx, part, rows, H, eps, st); break;
+      case 4: rc = launch_bwd_lpr<4>(nb, dy, x, w, rstd, dx, part, rows, H, eps, st); break;
+      case 8: rc = launch_bwd_lpr<8>(nb, dy, x, w, rstd, dx, part, rows, H, eps, st); break;
+      case 16: rc = launch_bwd_lpr<16>(nb, dy, x, w, rstd, dx, part, rows, H, eps, st); break;
+      case 32: rc = launch_bwd_lpr<32>(nb, dy, x, w, rstd, dx, part, rows, H, eps, st); break;
+      default: rc = launch_bwd_lpr<64>(nb, dy, x, w, rstd, dx, part, rows, H, eps, st); break;
+    }
+  } else {
+    rmsnorm_bwd_scalar<<<static_cast<unsigned>(nb), kThreads, 0, st>>>(dy, x, w, rstd, dx, part,
+                                                                       rows, H, eps);
+    rc = launch_status();
+  }
+  if (rc || !dw) return rc;
+  column_sum<<<static_cast<unsigned>((H + 255) / 256), 256, 0, st>>>(part, dw, nb, H);
+  return launch_status();
+}

@@ -1,0 +1,230 @@
+/*
+ * ember_hip.h -- C ABI of the MI355X (gfx950) kernels for emberlm's training hot path.
+ *
+ * This is the drop-in boundary: the C++ Tensor/autograd/Module layer
+ * (include/ctd/...) calls only these functions, and a foreign binding needs
+ * nothing else.  Conventions:
+ *   - every function returns an int status: EMBER_OK (0), a negative EMBER_E*
+ *     code for a rejected argument, or a positive hipError_t value;
+ *   - nothing throws and no kernel entry point allocates device memory;
+ *     functions that need scratch take an explicit workspace and export a
+ *     *_workspace_bytes() size query;
+ *   - pointers are device pointers unless the name says host; all tensors are
+ *     fp32 row-major contiguous unless stated (token ids are int64);
+ *   - work is enqueued on the given stream (NULL = the default stream) and is
+ *     asynchronous to the host;
+ *   - 64-bit sizes and offsets throughout (the reference's int32 row*V
+ *     indexing, src/ops/loss.cu:112-113 and 263-264, overflows at N*V > 2^31).
+ * Each declaration cites the reference function it replaces.
+ */
+#ifndef EMBER_HIP_H
+#define EMBER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* ember_stream_t; /* hipStream_t */
+typedef void* ember_event_t;  /* hipEvent_t */
+
+enum {
+  EMBER_OK = 0,
+  EMBER_EINVAL = -1,     /* bad size, shape, null pointer or flag */
+  EMBER_EWORKSPACE = -2, /* workspace missing or too small */
+  EMBER_EALIGN = -3,     /* pointer alignment the kernel requires is not met */
+  EMBER_EMASKSUM = -4    /* sum(loss_mask) == 0 in cross-entropy backward */
+};
+
+/* Human-readable text for a status code (static storage). */
+const char* ember_status_string(int status);
+
+/* ------------------------------------------------------------------ runtime
+ * Replace cudaMalloc/cudaFree/cudaMallocHost and cudaMemcpy of
+ * src/core/allocator.cpp:14-57 and src/core/tensor.cpp:84-108. */
+int ember_get_device_count(int* count);
+int ember_set_device(int device);
+int ember_get_device(int* device);
+int ember_device_malloc(void** ptr, size_t bytes);
+int ember_device_free(void* ptr);
+/* Page-locked host memory (hipHostMalloc); the reference's offload path used
+ * pageable memory instead (src/core/optim.cu:114-117). */
+int ember_host_malloc_pinned(void** ptr, size_t bytes);
+int ember_host_free_pinned(void* ptr);
+/* kind: 0 host->device, 1 device->host, 2 device->device, 3 host->host */
+int ember_memcpy_async(void* dst, const void* src, size_t bytes, int kind, ember_stream_t s);
+int ember_memcpy(void* dst, const void* src, size_t bytes, int kind);
+int ember_mem_get_info(size_t* free_bytes, size_t* total_bytes);
+int ember_device_synchronize(void);
+/* Streams are created at the default priority. */
+int ember_stream_create(ember_stream_t* s);
+int ember_stream_destroy(ember_stream_t s);
+int ember_stream_synchronize(ember_stream_t s);
+int ember_event_create(ember_event_t* e);
+int ember_event_destroy(ember_event_t e);
+int ember_event_record(ember_event_t e, ember_stream_t s);
+int ember_event_synchronize(ember_event_t e);
+int ember_stream_wait_event(ember_stream_t s, ember_event_t e);
+int ember_event_elapsed_ms(float* ms, ember_event_t start, ember_event_t stop);
+/* Device name / CU count / HBM bytes of the current device. */
+int ember_device_info(char* name, size_t name_cap, int* cu_count, size_t* hbm_bytes);
+
+/* ---------------------------------------------------------------- fills
+ * Counter-based generator (SplitMix64 + Box-Muller): element i of a stream
+ * depends only on (seed, offset + i), so host and device agree and any slice
+ * can be regenerated.  Used for seeded synthetic weights and activations. */
+int ember_fill_normal(float* p, int64_t n, uint64_t seed, uint64_t offset, float mean,
+                      float stddev, ember_stream_t s);
+int ember_fill(float* p, int64_t n, float value, ember_stream_t s);
+
+/* ----------------------------------------------------------------- GEMM
+ * C[b] = alpha * op(A[b]) op(B[b]) + beta * C[b], fp32 operands, fp32 MFMA.
+ * op(A) is MxK: A is stored [M,K] (lda >= K) or, when transa, [K,M] (lda >= M);
+ * op(B) is KxN: B is stored [K,N] (ldb >= N) or, when transb, [N,K] (ldb >= K).
+ * C is [M,N] with ldc >= N.  batch >= 1 with element strides sA/sB/sC.
+ * Replaces cublasSgemm / cublasSgemmStridedBatched in ops::matmul_impl and
+ * ops::bmm_impl (src/ops/matmul.cpp:13-49, 51-93; row-major trick 38-47). */
+int ember_gemm_f32(int transa, int transb, int64_t M, int64_t N, int64_t K, float alpha,
+                   const float* A, int64_t lda, int64_t sA, const float* B, int64_t ldb,
+                   int64_t sB, float beta, float* C, int64_t ldc, int64_t sC, int64_t batch,
+                   ember_stream_t s);
+
+/* -------------------------------------------------------------- RMSNorm
+ * y = x * rsqrt(mean(x^2) + eps) * w over rows of length H; rstd[rows] (may be
+ * NULL) receives rsqrt(mean(x^2)+eps).  Replaces rms_norm_kernel_f32
+ * (src/ops/norm.cu:17-49) for block norms and per-head QK-Norm. */
+int ember_rmsnorm_fwd(const float* x, const float* w, float* y, float* rstd, int64_t rows,
+                      int64_t H, float eps, ember_stream_t s);
+/* dx and dw from dy (src/ops/norm.cu:51-106).  dw is written (not accumulated)
+ * through a deterministic two-stage reduction in `workspace`; either dx or dw
+ * may be NULL.  rstd may be NULL (recomputed). */
+size_t ember_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t H);
+int ember_rmsnorm_bwd(const float* dy, const float* x, const float* w, const float* rstd,
+                      float* dx, float* dw, int64_t rows, int64_t H, float eps, void* workspace,
+                      size_t workspace_bytes, ember_stream_t s);
+
+/* ----------------------------------------------------------------- RoPE
+ * Frequencies of the D/2 rotation pairs in float, following src/ops/rope.cu:37-46
+ * (llama3 band scaling when factor > 1).  Host-only helper. */
+int ember_rope_freqs_host(float* freqs_out, int D, float theta, float factor,
+                          float low_freq_factor, float high_freq_factor,
+                          int original_max_pos);
+/* y = R(sign * angle) x for x [B,T,H,D], pairs (i, i+D/2), angle = float(pos0+t)*freq[i]
+ * rounded to fp32 (rope.cu:49); sign = -1 is RopeBackward's transpose
+ * (rope.cu:106-118).  freqs_host: D/2 values from ember_rope_freqs_host (passed
+ * by value to the kernel).  y may equal x (in place, apply_rope_inplace).
+ * D even and <= 256.  Replaces rope_kernel_f32 (src/ops/rope.cu:17-56). */
+int ember_rope(const float* x, float* y, int64_t B, int64_t T, int64_t H, int64_t D,
+               int64_t pos0, const float* freqs_host, float sign, ember_stream_t s);
+
+/* --------------------------------------------------------- elementwise
+ * Replace src/ops/elementwise.cu:15-69, repeat_kv.cu:45-51 and
+ * autograd.cu:88-93 (addinto). */
+int ember_add(const float* a, const float* b, float* y, int64_t n, ember_stream_t s);
+int ember_sub(const float* a, const float* b, float* y, int64_t n, ember_stream_t s);
+int ember_mul(const float* a, const float* b, float* y, int64_t n, ember_stream_t s);
+int ember_scale(const float* x, float alpha, float* y, int64_t n, ember_stream_t s);
+/* y += x (autograd fan-in, autograd.cu:86-118). */
+int ember_accumulate(float* y, const float* x, int64_t n, ember_stream_t s);
+int ember_silu(const float* x, float* y, int64_t n, ember_stream_t s);
+int ember_silu_bwd(const float* x, const float* g, float* dx, int64_t n, ember_stream_t s);
+/* Fused SwiGLU: h = silu(g) * u (MLP::forward, include/ctd/nn/mlp.h:16-21). */
+int ember_swiglu_fwd(const float* g, const float* u, float* h, int64_t n, ember_stream_t s);
+/* dg = dh * u * silu'(g), du = dh * silu(g) (MulBackward + SiluBackward,
+ * elementwise.cu:57-69, 186-238). */
+int ember_swiglu_bwd(const float* g, const float* u, const float* dh, float* dg, float* du,
+                     int64_t n, ember_stream_t s);
+
+/* ------------------------------------------------ unfused attention ops
+ * The reference's attention chain, kept for the ops:: API and parity tests. */
+/* Row softmax over the last dim N (src/ops/softmax.cu:17-52). */
+int ember_softmax_fwd(const float* x, float* y, int64_t rows, int64_t N, ember_stream_t s);
+/* dx = y * (g - sum(g*y)) (softmax.cu:54-80). */
+int ember_softmax_bwd(const float* y, const float* g, float* dx, int64_t rows, int64_t N,
+                      ember_stream_t s);
+/* out = (k > q0 + q) ? fill : in, rows of [*, Tq, Tk] (src/ops/mask.cu:15-52);
+ * backward uses fill = 0 on the upstream grad.  out may equal in. */
+int ember_causal_mask(const float* in, float* out, int64_t rows, int64_t Tq, int64_t Tk,
+                      int64_t q0, float fill, ember_stream_t s);
+/* [BT,Hk,D] -> [BT,Hk*group,D] and its group-sum (src/ops/repeat_kv.cu:16-43). */
+int ember_repeat_kv(const float* x, float* y, int64_t BT, int64_t Hk, int64_t group,
+                    int64_t D, ember_stream_t s);
+int ember_repeat_kv_sum(const float* y, float* x, int64_t BT, int64_t Hk, int64_t group,
+                        int64_t D, ember_stream_t s);
+/* Generic rank<=6 permutation y.shape[i] = shape[perm[i]] (src/ops/permute.cu:20-127);
+ * shape/perm are host arrays, passed by value (no device allocation or sync). */
+int ember_permute(const float* x, float* y, int ndim, const int64_t* shape_host,
+                  const int* perm_host, ember_stream_t s);
+
+/* ------------------------------------------------ fused causal attention
+ * Causal GQA attention over q [B,T,H,D], k/v [B,T,Hk,D] -> o [B,T,H,D] with
+ * lse [B,H,T] (natural-log log-sum-exp of the scaled, masked scores).  Equals
+ * the reference chain bmm -> mul_scalar -> apply_causal_mask -> softmax -> bmm
+ * with repeat_kv_heads/permute (include/ctd/nn/attention.h:100-143) without
+ * materialising [B*H,T,T]; head h reads KV head h / (H/Hk).  D in {64, 128}. */
+int ember_attn_fwd(const float* q, const float* k, const float* v, float* o, float* lse,
+                   int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D, float scale,
+                   ember_stream_t s);
+/* Backward of ember_attn_fwd: dq [B,T,H,D], dk/dv [B,T,Hk,D] (written, summed
+ * over each KV head's query group in a fixed order: deterministic).
+ * workspace >= ember_attn_bwd_workspace_bytes(). Replaces BmmBackward,
+ * SoftmaxBackward, CausalMaskBackward, MulScalarBackward, RepeatKvBackward and
+ * PermuteBackward of the chain (matmul.cpp:137-152, softmax.cu:54-80,
+ * mask.cu:41-52, repeat_kv.cu:29-43, permute.cu). */
+size_t ember_attn_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H);
+int ember_attn_bwd(const float* q, const float* k, const float* v, const float* o,
+                   const float* lse, const float* dout, float* dq, float* dk, float* dv,
+                   int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D, float scale,
+                   void* workspace, size_t workspace_bytes, ember_stream_t s);
+
+/* ---------------------------------------------------- masked cross-entropy
+ * Per row r: lse[r] = log sum_v exp(logits[r,v]); loss[0] = sum_r mask[r]*(lse[r]
+ * - logits[r,tgt[r]]) / sum_r mask[r] (0 when the mask sums to 0); mask_sum[0].
+ * Deterministic (fixed-order reduction in workspace, no atomics).  Replaces
+ * ce_masked_fwd/mean kernels (src/ops/loss.cu:253-310); no [N,V] probabilities
+ * are written. */
+size_t ember_ce_masked_fwd_workspace_bytes(int64_t N);
+int ember_ce_masked_fwd(const float* logits, const int64_t* tgt, const float* mask, int64_t N,
+                        int64_t V, float* lse, float* loss, float* mask_sum, void* workspace,
+                        size_t workspace_bytes, ember_stream_t s);
+/* dlogits = (dloss[0] / mask_sum[0]) * mask * (exp(logits - lse) - onehot(tgt))
+ * (src/ops/loss.cu:312-329, 382-408), with dloss and mask_sum read on the device.
+ * dlogits may equal logits (in place).  Targets outside [0,V) are rejected by
+ * the forward's caller; the kernel skips them. */
+int ember_ce_masked_bwd(const float* logits, const int64_t* tgt, const float* mask,
+                        const float* lse, const float* dloss, const float* mask_sum, int64_t N,
+                        int64_t V, float* dlogits, ember_stream_t s);
+
+/* -------------------------------------------------------------- embedding
+ * out[i,:] = w[ids[i],:] (src/ops/embedding.cu:15-24). */
+int ember_embedding_fwd(const int64_t* ids, const float* w, float* out, int64_t n, int64_t H,
+                        int64_t V, ember_stream_t s);
+/* dw[v,:] (+)= sum over i with ids[i]==v of dy[i,:], summed in increasing i
+ * (deterministic, no atomics); accumulate=0 zero-fills dw first.  Replaces the
+ * atomicAdd scatter of src/ops/embedding.cu:28-39, 71-87. */
+size_t ember_embedding_bwd_workspace_bytes(int64_t n, int64_t V);
+int ember_embedding_bwd(const int64_t* ids, const float* dy, float* dw, int64_t n, int64_t H,
+                        int64_t V, int accumulate, void* workspace, size_t workspace_bytes,
+                        ember_stream_t s);
+
+/* ------------------------------------------------------------------ AdamW
+ * m = b1 m + (1-b1) g; v = b2 v + (1-b2) g^2;
+ * p -= lr * ((m/bc1) / (sqrt(v/bc2) + eps) + wd * p)
+ * (adamw_step_kernel_f32, src/core/optim.cu:54-73). */
+int ember_adamw(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1,
+                float beta2, float eps, float wd, float bc1, float bc2, ember_stream_t s);
+
+/* ------------------------------------------------------- grad-norm clip
+ * out[0] = sum over tensors of sum(g^2), fixed-order two-stage reduction.
+ * ptrs/sizes are host arrays of `count` device pointers and lengths.
+ * Replaces sum_sq_kernel_f32 + atomicAdd (src/core/optim.cu:221-239). */
+size_t ember_sumsq_workspace_bytes(int count);
+int ember_sumsq_multi(const float* const* ptrs_host, const int64_t* sizes_host, int count,
+                      float* out, void* workspace, size_t workspace_bytes, ember_stream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* EMBER_HIP_H */

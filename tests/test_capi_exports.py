@@ -1,0 +1,61 @@
+"""CPU checks of the C-ABI library: it loads, exports every symbol declared in
+include/ember_hip.h, and its host-only helpers agree with the oracle.
+No GPU compute is launched here."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle as O
+from emberlm_amd import capi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    text = open(os.path.join(ROOT, "include", "ember_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ember_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = capi.lib()
+    names = declared_functions()
+    assert len(names) > 40
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    unbound = [n for n in names if n not in capi.SIGNATURES]
+    assert not unbound, unbound
+
+
+def test_status_strings():
+    lib = capi.lib()
+    assert lib.ember_status_string(0) == b"ok"
+    assert b"invalid" in lib.ember_status_string(-1)
+    assert b"loss_mask" in lib.ember_status_string(-4)
+
+
+@pytest.mark.parametrize("D,theta,factor", [(64, 1e5, 0.0), (128, 1e6, 0.0), (64, 5e5, 32.0),
+                                            (8, 1e4, 0.0)])
+def test_rope_freqs_match_oracle_bitwise(D, theta, factor):
+    out = (C.c_float * (D // 2))()
+    capi.check(capi.lib().ember_rope_freqs_host(out, D, theta, factor, 1.0, 4.0, 8192))
+    ref = [O.rope_freq(i, D, theta, factor, 1.0, 4.0, 8192) for i in range(D // 2)]
+    assert np.array_equal(np.array(out[:], dtype=np.float32), np.array(ref, dtype=np.float32))
+
+
+def test_argument_validation_without_gpu():
+    lib = capi.lib()
+    # invalid shapes are rejected before any device call
+    assert lib.ember_gemm_f32(0, 0, -1, 2, 2, 1.0, None, 2, 0, None, 2, 0, 0.0, None, 2, 0, 1,
+                              None) == -1
+    assert lib.ember_attn_fwd(None, None, None, None, None, 1, 4, 3, 2, 64, 1.0, None) == -1
+    assert lib.ember_attn_fwd(None, None, None, None, None, 1, 4, 2, 2, 96, 1.0, None) == -1
+    assert lib.ember_rope(None, None, 1, 1, 1, 7, 0, None, 1.0, None) == -1
+    # zero-size work is a no-op
+    assert lib.ember_add(None, None, None, 0, None) == 0
+    assert lib.ember_rmsnorm_bwd_workspace_bytes(32768, 2048) > 0
+    assert lib.ember_attn_bwd_workspace_bytes(8, 4096, 16) == 8 * 4096 * 16 * 4
+    assert lib.ember_ce_masked_fwd_workspace_bytes(32768) == 32768 * 4

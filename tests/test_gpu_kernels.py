@@ -1,0 +1,414 @@
+"""GPU parity of every kernel behind include/ember_hip.h against the CPU oracle.
+
+Called through the C ABI (ctypes); torch only provides device buffers.  Sizes
+are the configs' real per-op shapes where the oracle finishes in seconds, plus
+ragged/odd shapes that take the scalar paths; bitwise run-to-run determinism
+is checked for every kernel that the checkpointed recompute relies on.
+Tolerance: |a-b| <= 1e-4|b| + 1e-4 max|b| and relative L2 <= 1e-4 (fp32 vs the
+fp64 oracle); AdamW 1e-5.
+"""
+import ctypes as C
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+from emberlm_amd import capi
+from tests.helpers import assert_close, call, dev, empty, host, p
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+I64 = C.c_int64
+
+
+def rng(s=0):
+    return np.random.default_rng(s)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    torch.cuda.init()
+
+
+# ------------------------------------------------------------------ GEMM
+def gemm(a, b, ta, tb, alpha=1.0, beta=0.0, c=None):
+    A, B = dev(a), dev(b)
+    M = a.shape[1] if ta else a.shape[0]
+    K = a.shape[0] if ta else a.shape[1]
+    N = b.shape[0] if tb else b.shape[1]
+    Cm = dev(c) if c is not None else empty((M, N))
+    call("ember_gemm_f32", int(ta), int(tb), M, N, K, alpha, p(A), a.shape[1], 0, p(B),
+         b.shape[1], 0, beta, p(Cm), N, 0, 1, None)
+    return host(Cm)
+
+
+@pytest.mark.parametrize("M,N,K,ta,tb", [
+    (256, 576, 576, 0, 1),    # c1 q/o projection (Linear, NT)
+    (256, 192, 576, 0, 1),    # c1 k/v projection
+    (256, 1536, 576, 0, 1),   # c1 gate/up
+    (256, 576, 1536, 0, 0),   # c1 down dX (NN)
+    (1536, 576, 256, 1, 0),   # c1 dW (TN, K = tokens)
+    (37, 53, 29, 0, 0), (37, 53, 29, 0, 1), (37, 53, 29, 1, 0), (37, 53, 29, 1, 1),
+    (130, 129, 18, 1, 1), (1, 1, 1, 0, 0),
+])
+def test_gemm_vs_oracle(M, N, K, ta, tb):
+    r = rng(M + N + K)
+    a = r.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    b = r.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    assert_close(gemm(a, b, ta, tb), O.matmul(a, b, ta, tb), name="gemm")
+
+
+def test_gemm_alpha_beta_and_kat():
+    # tests/test_matmul.cpp:48-67 known answer
+    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    b = np.arange(1, 13, dtype=np.float32).reshape(3, 4)
+    assert np.array_equal(gemm(a, b, 0, 0), [[38, 44, 50, 56], [83, 98, 113, 128]])
+    r = rng(3)
+    a = r.standard_normal((70, 40)).astype(np.float32)
+    b = r.standard_normal((40, 90)).astype(np.float32)
+    c = r.standard_normal((70, 90)).astype(np.float32)
+    got = gemm(a, b, 0, 0, alpha=0.5, beta=1.0, c=c)
+    assert_close(got, 0.5 * O.matmul(a, b) + c, name="alpha/beta")
+
+
+def test_gemm_batched():
+    r = rng(4)
+    a = r.standard_normal((3, 64, 40)).astype(np.float32)
+    b = r.standard_normal((3, 72, 40)).astype(np.float32)
+    A, B = dev(a), dev(b)
+    Cm = empty((3, 64, 72))
+    call("ember_gemm_f32", 0, 1, 64, 72, 40, 1.0, p(A), 40, 64 * 40, p(B), 40, 72 * 40, 0.0, p(Cm),
+         72, 64 * 72, 3, None)
+    assert_close(host(Cm), O.bmm(a, b, False, True), name="bmm")
+
+
+def test_gemm_full_size_vs_torch_and_deterministic():
+    # c5 gate projection shape, checked against torch's fp32 GEMM on the GPU.
+    M, N, K = 32768, 6144, 2048
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(M, K, device="cuda", generator=g)
+    w = torch.randn(N, K, device="cuda", generator=g) * 0.02
+    out = empty((M, N))
+    call("ember_gemm_f32", 0, 1, M, N, K, 1.0, p(x), K, 0, p(w), K, 0, 0.0, p(out), N, 0, 1, None)
+    ref = x @ w.t()
+    torch.cuda.synchronize()
+    rel = ((out - ref).norm() / ref.norm()).item()
+    assert rel < 1e-5, rel
+    out2 = empty((M, N))
+    call("ember_gemm_f32", 0, 1, M, N, K, 1.0, p(x), K, 0, p(w), K, 0, 0.0, p(out2), N, 0, 1, None)
+    assert torch.equal(out, out2)
+
+
+# -------------------------------------------------------------- RMSNorm
+@pytest.mark.parametrize("rows,H,eps", [(256, 576, 1e-5), (4096, 128, 1e-6), (999, 64, 1e-5),
+                                        (33, 2048, 1e-6), (7, 30, 1e-5), (3, 4, 1e-5)])
+def test_rmsnorm_fwd_bwd_vs_oracle(rows, H, eps):
+    r = rng(rows + H)
+    x = r.standard_normal((rows, H)).astype(np.float32)
+    w = (1 + 0.1 * r.standard_normal(H)).astype(np.float32)
+    dy = r.standard_normal((rows, H)).astype(np.float32)
+    X, W, DY = dev(x), dev(w), dev(dy)
+    Y, RS = empty((rows, H)), empty((rows,))
+    call("ember_rmsnorm_fwd", p(X), p(W), p(Y), p(RS), rows, H, eps, None)
+    assert_close(host(Y), O.rmsnorm_fwd(x, w, eps), name="rms fwd")
+    ws_n = int(capi.lib().ember_rmsnorm_bwd_workspace_bytes(rows, H))
+    WS = empty((max(ws_n // 4, 1),))
+    DX, DW = empty((rows, H)), empty((H,))
+    call("ember_rmsnorm_bwd", p(DY), p(X), p(W), p(RS), p(DX), p(DW), rows, H, eps, p(WS), ws_n, None)
+    dx_ref, dw_ref = O.rmsnorm_bwd(dy, x, w, eps)
+    assert_close(host(DX), dx_ref, name="rms dx")
+    assert_close(host(DW), dw_ref, name="rms dw")
+    # recompute rstd path and bitwise determinism
+    DX2, DW2 = empty((rows, H)), empty((H,))
+    call("ember_rmsnorm_bwd", p(DY), p(X), p(W), None, p(DX2), p(DW2), rows, H, eps, p(WS), ws_n, None)
+    assert torch.equal(DW, DW2)
+    Y2 = empty((rows, H))
+    call("ember_rmsnorm_fwd", p(X), p(W), p(Y2), None, rows, H, eps, None)
+    assert torch.equal(Y, Y2)
+
+
+def test_rmsnorm_full_size_c5():
+    rows, H = 32768, 2048
+    x = torch.randn(rows, H, device="cuda")
+    w = torch.rand(H, device="cuda") + 0.5
+    y = empty((rows, H))
+    call("ember_rmsnorm_fwd", p(x), p(w), p(y), None, rows, H, 1e-6, None)
+    ref = x * torch.rsqrt((x.double() ** 2).mean(-1, keepdim=True) + 1e-6).float() * w
+    torch.cuda.synchronize()
+    assert ((y - ref).abs().max() / ref.abs().max()).item() < 1e-5
+
+
+# ----------------------------------------------------------------- RoPE
+def freqs(D, theta, factor=0.0):
+    out = (C.c_float * (D // 2))()
+    capi.check(capi.lib().ember_rope_freqs_host(out, D, theta, factor, 1.0, 4.0, 8192))
+    return out
+
+
+@pytest.mark.parametrize("B,T,H,D,theta,factor,pos0,sign", [
+    (1, 256, 9, 64, 1e5, 0.0, 0, 1.0),       # c1 Q
+    (2, 300, 2, 128, 1e6, 0.0, 0, -1.0),     # c3/c5 head_dim, transpose (backward)
+    (1, 2048, 2, 64, 5e5, 32.0, 0, 1.0),     # c4 llama3 scaling, full T
+    (1, 4096, 1, 128, 1e6, 0.0, 0, 1.0),     # c5 full T (large angles)
+    (1, 5, 3, 8, 1e4, 0.0, 7, 1.0),          # position offset (test_rope.cpp:57-72)
+])
+def test_rope_vs_oracle(B, T, H, D, theta, factor, pos0, sign):
+    r = rng(T + D)
+    x = r.standard_normal((B, T, H, D)).astype(np.float32)
+    X, Y = dev(x), empty((B, T, H, D))
+    call("ember_rope", p(X), p(Y), B, T, H, D, pos0, freqs(D, theta, factor), sign, None)
+    ref = O.rope(x, theta, pos0=pos0, sign=sign, factor=factor)
+    assert_close(host(Y), ref, name="rope")
+    # in place (apply_rope_inplace) gives the same bits
+    call("ember_rope", p(X), p(X), B, T, H, D, pos0, freqs(D, theta, factor), sign, None)
+    assert torch.equal(X, Y)
+
+
+def test_rope_roundtrip_identity():
+    x = torch.randn(2, 64, 4, 128, device="cuda")
+    y, z = torch.empty_like(x), torch.empty_like(x)
+    fr = freqs(128, 1e6)
+    call("ember_rope", p(x), p(y), 2, 64, 4, 128, 0, fr, 1.0, None)
+    call("ember_rope", p(y), p(z), 2, 64, 4, 128, 0, fr, -1.0, None)
+    torch.cuda.synchronize()
+    assert (z - x).abs().max().item() < 1e-5
+
+
+# ----------------------------------------------------------- elementwise
+def test_elementwise_vs_oracle():
+    r = rng(5)
+    n = 1536 * 256 + 3  # odd tail
+    a = (r.standard_normal(n) * 3).astype(np.float32)
+    b = r.standard_normal(n).astype(np.float32)
+    g = r.standard_normal(n).astype(np.float32)
+    A, Bt, G = dev(a), dev(b), dev(g)
+    Y = empty((n,))
+    call("ember_add", p(A), p(Bt), p(Y), n, None)
+    assert np.array_equal(host(Y), a + b)
+    call("ember_mul", p(A), p(Bt), p(Y), n, None)
+    assert np.array_equal(host(Y), a * b)
+    call("ember_sub", p(A), p(Bt), p(Y), n, None)
+    assert np.array_equal(host(Y), a - b)
+    call("ember_scale", p(A), 0.125, p(Y), n, None)
+    assert np.array_equal(host(Y), a * np.float32(0.125))
+    call("ember_silu", p(A), p(Y), n, None)
+    assert_close(host(Y), O.silu(a), name="silu")
+    call("ember_silu_bwd", p(A), p(G), p(Y), n, None)
+    assert_close(host(Y), O.silu_bwd(a, g), name="silu bwd")
+    call("ember_swiglu_fwd", p(A), p(Bt), p(Y), n, None)
+    assert_close(host(Y), O.silu(a) * b, name="swiglu fwd")
+    DG, DU = empty((n,)), empty((n,))
+    call("ember_swiglu_bwd", p(A), p(Bt), p(G), p(DG), p(DU), n, None)
+    assert_close(host(DG), O.silu_bwd(a, g * b), name="swiglu dg")
+    assert_close(host(DU), g * O.silu(a), name="swiglu du")
+    Z = dev(b)
+    call("ember_accumulate", p(Z), p(A), n, None)
+    assert np.array_equal(host(Z), b + a)
+    # misaligned (scalar) path
+    call("ember_add", C.c_void_p(A.data_ptr() + 4), C.c_void_p(Bt.data_ptr() + 4), p(Y), n - 1, None)
+    assert np.array_equal(host(Y)[: n - 1], a[1:] + b[1:])
+
+
+# ------------------------------------------------------- cross-entropy
+@pytest.mark.parametrize("N,V", [(64, 49152), (8, 151936), (33, 1001), (5, 7)])
+def test_ce_masked_vs_oracle(N, V):
+    r = rng(N + V)
+    logits = (r.standard_normal((N, V)) * 2).astype(np.float32)
+    tgt = r.integers(0, V, N).astype(np.int64)
+    mask = (r.random(N) > 0.4).astype(np.float32)
+    mask[0] = 1.0
+    L, T_, M = dev(logits), dev(tgt), dev(mask)
+    lse, loss, ms = empty((N,)), empty((1,)), empty((1,))
+    ws = empty((N,))
+    call("ember_ce_masked_fwd", p(L), p(T_), p(M), N, V, p(lse), p(loss), p(ms), p(ws), N * 4, None)
+    ref_loss, ref_lse, ref_ms = O.ce_masked_fwd(logits, tgt, mask)
+    assert abs(host(loss)[0] - ref_loss) <= 1e-5 * abs(ref_loss)
+    assert host(ms)[0] == ref_ms
+    live = mask > 0
+    assert_close(host(lse)[live], ref_lse[live], name="lse")
+    dl = dev(np.array([0.7], np.float32))
+    D_ = empty((N, V))
+    call("ember_ce_masked_bwd", p(L), p(T_), p(M), p(lse), p(dl), p(ms), N, V, p(D_), None)
+    ref_d = O.ce_masked_bwd(logits, tgt, mask, dy=0.7)
+    assert_close(host(D_), ref_d, name="dlogits")
+    assert (host(D_)[~live] == 0).all()
+    # in place over the logits gives the same bits
+    call("ember_ce_masked_bwd", p(L), p(T_), p(M), p(lse), p(dl), p(ms), N, V, p(L), None)
+    assert torch.equal(L, D_)
+
+
+def test_ce_zero_mask_loss_is_zero():
+    N, V = 4, 16
+    L = torch.randn(N, V, device="cuda")
+    T_ = torch.zeros(N, dtype=torch.int64, device="cuda")
+    M = torch.zeros(N, device="cuda")
+    lse, loss, ms, ws = empty((N,)), empty((1,)), empty((1,)), empty((N,))
+    call("ember_ce_masked_fwd", p(L), p(T_), p(M), N, V, p(lse), p(loss), p(ms), p(ws), N * 4, None)
+    assert host(loss)[0] == 0.0 and host(ms)[0] == 0.0
+
+
+# ------------------------------------------------------------ embedding
+def test_embedding_kat_and_bwd():
+    V, H = 7, 5
+    w = np.array([[v * 10 + h for h in range(H)] for v in range(V)], np.float32)
+    ids = np.array([3, 0, 6, 3], np.int64)
+    W, I = dev(w), dev(ids)
+    out = empty((4, H))
+    call("ember_embedding_fwd", p(I), p(W), p(out), 4, H, V, None)
+    assert np.array_equal(host(out), w[ids])
+    r = rng(6)
+    n, V, H = 4096, 49152, 576
+    ids = r.integers(0, 300, n).astype(np.int64)  # many repeats
+    dy = r.standard_normal((n, H)).astype(np.float32)
+    I, DY = dev(ids), dev(dy)
+    DW = empty((V, H))
+    call("ember_embedding_bwd", p(I), p(DY), p(DW), n, H, V, 0, None, 0, None)
+    got = host(DW)
+    assert_close(got[:300], O.embedding_bwd(ids, dy, V)[:300], name="emb dw")
+    assert (got[300:] == 0).all()
+    DW2 = empty((V, H))
+    call("ember_embedding_bwd", p(I), p(DY), p(DW2), n, H, V, 0, None, 0, None)
+    assert torch.equal(DW, DW2)
+    call("ember_embedding_bwd", p(I), p(DY), p(DW2), n, H, V, 1, None, 0, None)  # accumulate
+    assert_close(host(DW2)[:300], 2 * O.embedding_bwd(ids, dy, V)[:300], name="emb accumulate")
+
+
+# ---------------------------------------------------------------- AdamW
+def test_adamw_vs_oracle():
+    r = rng(7)
+    n = 100003
+    pp, g = r.standard_normal(n).astype(np.float32), r.standard_normal(n).astype(np.float32)
+    m, v = (0.1 * r.standard_normal(n)).astype(np.float32), r.random(n).astype(np.float32) * 0.01
+    P, G, Mt, Vt = dev(pp), dev(g), dev(m), dev(v)
+    lr, b1, b2, eps, wd = 1e-4, 0.9, 0.95, 1e-8, 0.1
+    bc1, bc2 = np.float32(1 - 0.9 ** 3), np.float32(1 - 0.95 ** 3)
+    call("ember_adamw", p(P), p(G), p(Mt), p(Vt), n, lr, b1, b2, eps, wd, float(bc1), float(bc2), None)
+    rp, rm, rv = O.adamw(pp, g, m, v, np.float32(lr), np.float32(b1), np.float32(b2), np.float32(eps),
+                         np.float32(wd), bc1, bc2)
+    for got, ref, name in [(P, rp, "p"), (Mt, rm, "m"), (Vt, rv, "v")]:
+        err = np.abs(host(got) - ref)
+        assert (err <= 1e-5 * np.abs(ref) + 1e-12).all(), name
+
+
+def test_sumsq_multi():
+    r = rng(8)
+    arrs = [r.standard_normal(s).astype(np.float32) for s in (4, 9, 16, 1000003, 1)]
+    ts = [dev(a) for a in arrs]
+    ptrs = (C.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
+    sizes = (C.c_int64 * len(ts))(*[a.size for a in arrs])
+    lib = capi.lib()
+    wsb = lib.ember_sumsq_workspace_bytes(len(ts))
+    ws, out = empty((wsb // 4,)), empty((1,))
+    call("ember_sumsq_multi", ptrs, sizes, len(ts), p(out), p(ws), wsb, None)
+    ref = sum(float((a.astype(np.float64) ** 2).sum()) for a in arrs)
+    assert abs(host(out)[0] - ref) <= 1e-5 * ref
+    # ClipGradNorm KAT: three all-ones grads of 4, 9, 16 elements -> sqrt(29)
+    ones = [dev(np.ones(s, np.float32)) for s in (4, 9, 16)]
+    ptrs = (C.c_void_p * 3)(*[t.data_ptr() for t in ones])
+    sizes = (C.c_int64 * 3)(4, 9, 16)
+    call("ember_sumsq_multi", ptrs, sizes, 3, p(out), p(ws), wsb, None)
+    assert abs(math.sqrt(host(out)[0]) - math.sqrt(29)) < 1e-5
+
+
+# ------------------------------------------------------------ attention
+@pytest.mark.parametrize("B,T,H,Hk,D", [
+    (1, 256, 9, 3, 64),     # c1 block attention (SmolLM2 shape)
+    (1, 200, 4, 2, 128),    # ragged T, Qwen3 head_dim
+    (2, 130, 2, 2, 64),     # MHA, two batches, ragged
+    (1, 1, 2, 1, 128),      # single token
+])
+def test_attention_fwd_bwd_vs_oracle(B, T, H, Hk, D):
+    r = rng(B * T + H + D)
+    q = r.standard_normal((B, T, H, D)).astype(np.float32)
+    k = r.standard_normal((B, T, Hk, D)).astype(np.float32)
+    v = r.standard_normal((B, T, Hk, D)).astype(np.float32)
+    do = r.standard_normal((B, T, H, D)).astype(np.float32)
+    scale = 1.0 / math.sqrt(D)
+    Q, K, Vv, DO = dev(q), dev(k), dev(v), dev(do)
+    Ot, L = empty((B, T, H, D)), empty((B, H, T))
+    call("ember_attn_fwd", p(Q), p(K), p(Vv), p(Ot), p(L), B, T, H, Hk, D, scale, None)
+    o_ref, lse_ref = O.attention_fwd(q, k, v, scale)
+    assert_close(host(Ot), o_ref, name="attn o")
+    assert_close(host(L), lse_ref, name="attn lse")
+    lib = capi.lib()
+    wsb = lib.ember_attn_bwd_workspace_bytes(B, T, H)
+    WS = empty((wsb // 4,))
+    DQ, DK, DV = empty((B, T, H, D)), empty((B, T, Hk, D)), empty((B, T, Hk, D))
+    call("ember_attn_bwd", p(Q), p(K), p(Vv), p(Ot), p(L), p(DO), p(DQ), p(DK), p(DV), B, T, H, Hk,
+         D, scale, p(WS), wsb, None)
+    dq_ref, dk_ref, dv_ref = O.attention_bwd(q, k, v, do, scale)
+    assert_close(host(DQ), dq_ref, name="dq")
+    assert_close(host(DK), dk_ref, name="dk")
+    assert_close(host(DV), dv_ref, name="dv")
+    # bitwise run-to-run determinism (forward and backward)
+    O2, L2 = empty((B, T, H, D)), empty((B, H, T))
+    call("ember_attn_fwd", p(Q), p(K), p(Vv), p(O2), p(L2), B, T, H, Hk, D, scale, None)
+    DQ2, DK2, DV2 = empty((B, T, H, D)), empty((B, T, Hk, D)), empty((B, T, Hk, D))
+    call("ember_attn_bwd", p(Q), p(K), p(Vv), p(Ot), p(L), p(DO), p(DQ2), p(DK2), p(DV2), B, T, H,
+         Hk, D, scale, p(WS), wsb, None)
+    assert torch.equal(Ot, O2) and torch.equal(L, L2)
+    assert torch.equal(DQ, DQ2) and torch.equal(DK, DK2) and torch.equal(DV, DV2)
+
+
+def test_attention_full_T_c5_vs_torch_sdpa():
+    # c5 per-head shape at full T=4096: one batch row, one KV group (2 query heads).
+    B, T, H, Hk, D = 1, 4096, 2, 1, 128
+    g = torch.Generator(device="cuda").manual_seed(1)
+    q = torch.randn(B, T, H, D, device="cuda", generator=g)
+    k = torch.randn(B, T, Hk, D, device="cuda", generator=g)
+    v = torch.randn(B, T, Hk, D, device="cuda", generator=g)
+    o, lse = empty((B, T, H, D)), empty((B, H, T))
+    call("ember_attn_fwd", p(q), p(k), p(v), p(o), p(lse), B, T, H, Hk, D, 1 / math.sqrt(D), None)
+    # fp32 math reference on the GPU, one head at a time ([T,T] fp32 = 64 MB)
+    for h in range(H):
+        s = (q[0, :, h] @ k[0, :, 0].t().contiguous()) / math.sqrt(D)
+        s = s.masked_fill(torch.triu(torch.ones(T, T, dtype=torch.bool, device="cuda"), 1), -math.inf)
+        ref = torch.softmax(s, -1) @ v[0, :, 0]
+        torch.cuda.synchronize()
+        rel = ((o[0, :, h] - ref).norm() / ref.norm()).item()
+        assert rel < 1e-5, rel
+        assert ((lse[0, h] - torch.logsumexp(s, -1)).abs().max()).item() < 1e-4
+
+
+# ----------------------------------------------------- unfused chain ops
+def test_reference_chain_ops_vs_oracle():
+    r = rng(9)
+    rows, N = 64, 300
+    x = (r.standard_normal((rows, N)) * 4).astype(np.float32)
+    g = r.standard_normal((rows, N)).astype(np.float32)
+    X, G, Y, DX = dev(x), dev(g), empty((rows, N)), empty((rows, N))
+    call("ember_softmax_fwd", p(X), p(Y), rows, N, None)
+    y = host(Y)
+    assert_close(y, O.softmax_fwd(x), name="softmax")
+    call("ember_softmax_bwd", p(Y), p(G), p(DX), rows, N, None)
+    assert_close(host(DX), O.softmax_bwd(y, g), name="softmax bwd")
+    s = np.ones((2, 4, 4), np.float32)
+    S = dev(s)
+    call("ember_causal_mask", p(S), p(S), 8, 4, 4, 0, -3.4028234663852886e38, None)
+    assert np.array_equal(host(S), O.causal_mask(s).astype(np.float32))
+    kv = r.standard_normal((2, 5, 3, 16)).astype(np.float32)
+    KV, Y = dev(kv), empty((2, 5, 6, 16))
+    call("ember_repeat_kv", p(KV), p(Y), 10, 3, 2, 16, None)
+    assert np.array_equal(host(Y), O.repeat_kv(kv, 2))
+    Z = empty((2, 5, 3, 16))
+    call("ember_repeat_kv_sum", p(Y), p(Z), 10, 3, 2, 16, None)
+    assert np.array_equal(host(Z), 2 * kv)
+    t = np.arange(2 * 3 * 4 * 2, dtype=np.float32).reshape(2, 3, 4, 2)
+    Tt, Y = dev(t), empty((2, 4, 3, 2))
+    shape = (C.c_int64 * 4)(2, 3, 4, 2)
+    perm = (C.c_int * 4)(0, 2, 1, 3)
+    call("ember_permute", p(Tt), p(Y), 4, shape, perm, None)
+    assert np.array_equal(host(Y), t.transpose(0, 2, 1, 3))
+
+
+def test_fill_normal_statistics_and_reproducible():
+    n = 1 << 22
+    a, b = empty((n,)), empty((n,))
+    call("ember_fill_normal", p(a), n, 0, 0, 0.0, 0.02, None)
+    call("ember_fill_normal", p(b), n, 0, 0, 0.0, 0.02, None)
+    assert torch.equal(a, b)
+    assert abs(a.mean().item()) < 1e-4 and abs(a.std().item() - 0.02) < 1e-4
