@@ -1,0 +1,219 @@
+// Model presets, forward paths, HF-named weight loading and parameter grouping.
+// Reference: include/ctd/nn/model.h:19-217 and src/nn/model.cpp:24-100.
+#include "ctd/nn/model.h"
+
+#include <stdexcept>
+#include <string>
+
+#include "ctd/ops/loss.h"
+
+namespace ctd::nn {
+
+LlamaConfig smollm2_135m_config() {
+  LlamaConfig c{};
+  c.vocab_size = 49152;
+  c.hidden_size = 576;
+  c.intermediate_size = 1536;
+  c.num_hidden_layers = 30;
+  c.num_attention_heads = 9;
+  c.num_key_value_heads = 3;
+  c.head_dim = 64;
+  c.max_position_embeddings = 8192;
+  c.rms_norm_eps = 1e-5f;
+  c.rope_theta = 100000.0f;
+  c.tie_word_embeddings = true;
+  return c;
+}
+
+LlamaConfig smollm2_360m_config() {
+  LlamaConfig c = smollm2_135m_config();
+  c.hidden_size = 960;
+  c.intermediate_size = 2560;
+  c.num_hidden_layers = 32;
+  c.num_attention_heads = 15;
+  c.num_key_value_heads = 5;
+  return c;
+}
+
+LlamaConfig qwen3_0_6b_config() {
+  LlamaConfig c{};
+  c.vocab_size = 151936;
+  c.hidden_size = 1024;
+  c.intermediate_size = 3072;
+  c.num_hidden_layers = 28;
+  c.num_attention_heads = 16;
+  c.num_key_value_heads = 8;
+  c.head_dim = 128;
+  c.max_position_embeddings = 40960;
+  c.rms_norm_eps = 1e-6f;
+  c.rope_theta = 1000000.0f;
+  c.tie_word_embeddings = true;
+  c.qk_norm = true;
+  return c;
+}
+
+LlamaConfig qwen3_1_7b_config() {
+  LlamaConfig c = qwen3_0_6b_config();
+  c.hidden_size = 2048;
+  c.intermediate_size = 6144;
+  return c;
+}
+
+LlamaConfig llama3_2_1b_config() {
+  LlamaConfig c{};
+  c.vocab_size = 128256;
+  c.hidden_size = 2048;
+  c.intermediate_size = 8192;
+  c.num_hidden_layers = 16;
+  c.num_attention_heads = 32;
+  c.num_key_value_heads = 8;
+  c.head_dim = 64;
+  c.max_position_embeddings = 131072;
+  c.rms_norm_eps = 1e-5f;
+  c.rope_theta = 500000.0f;
+  c.tie_word_embeddings = true;
+  c.qk_norm = false;
+  c.rope_scaling_factor = 32.0f;
+  c.rope_scaling_low_freq_factor = 1.0f;
+  c.rope_scaling_high_freq_factor = 4.0f;
+  c.rope_scaling_original_max_pos = 8192;
+  return c;
+}
+
+LlamaConfig autodetect_config(const TensorDict& w) {
+  auto it = w.find("model.embed_tokens.weight");
+  if (it == w.end()) throw std::runtime_error("autodetect_config: missing model.embed_tokens.weight");
+  const int64_t vocab = it->second.shape().at(0);
+  const int64_t hidden = it->second.shape().at(1);
+  if (hidden == 576) return smollm2_135m_config();
+  if (hidden == 960) return smollm2_360m_config();
+  if (hidden == 1024 && vocab == 151936) return qwen3_0_6b_config();
+  if (hidden == 2048 && vocab == 151936) return qwen3_1_7b_config();
+  if (hidden == 2048 && vocab == 128256) return llama3_2_1b_config();
+  throw std::runtime_error("autodetect_config: unsupported hidden_size=" + std::to_string(hidden) +
+                           " vocab_size=" + std::to_string(vocab));
+}
+
+Tensor Model::forward(const Tensor& input_ids) const {
+  autograd::NoGradGuard ng;
+  return forward_train_logits(input_ids);
+}
+
+Tensor Model::forward_train_logits(const Tensor& input_ids) const {
+  Tensor h = embed_tokens.forward(input_ids);
+  for (const auto& layer : layers) {
+    if (gradient_checkpointing) {
+      h = autograd::checkpoint([&layer](const Tensor& x) { return layer.forward_train(x); }, h);
+    } else {
+      h = layer.forward_train(h);
+    }
+  }
+  h = norm.forward(h);
+  Linear lm_head{embed_tokens.weight};  // tied head
+  return lm_head.forward(h);
+}
+
+Tensor Model::forward_train(const Tensor& input_ids, const Tensor& targets) const {
+  const int64_t total = input_ids.numel();
+  Tensor logits = forward_train_logits(input_ids);
+  const int64_t V = logits.shape().back();
+  return ops::cross_entropy(logits.reshape({total, V}), targets.reshape({total}));
+}
+
+Tensor Model::forward_train_masked(const Tensor& input_ids, const Tensor& targets,
+                                   const Tensor& loss_mask) const {
+  const int64_t total = input_ids.numel();
+  Tensor logits = forward_train_logits(input_ids);
+  const int64_t V = logits.shape().back();
+  return ops::cross_entropy_masked(logits.reshape({total, V}), targets.reshape({total}),
+                                   loss_mask.reshape({total}));
+}
+
+namespace {
+const Tensor& must(const TensorDict& w, const std::string& key) {
+  auto it = w.find(key);
+  if (it == w.end()) throw std::runtime_error("build_model: missing weight '" + key + "'");
+  return it->second;
+}
+Tensor maybe(const TensorDict& w, const std::string& key) {
+  auto it = w.find(key);
+  return it != w.end() ? it->second : Tensor{};
+}
+}  // namespace
+
+Model build_model(const TensorDict& w, const LlamaConfig& cfg) {
+  Model m;
+  m.config = cfg;
+  m.embed_tokens = Embedding{must(w, "model.embed_tokens.weight")};
+  m.norm = RMSNorm{must(w, "model.norm.weight"), cfg.rms_norm_eps};
+  m.layers.reserve(static_cast<size_t>(cfg.num_hidden_layers));
+  for (int i = 0; i < cfg.num_hidden_layers; ++i) {
+    const std::string p = "model.layers." + std::to_string(i) + ".";
+    TransformerBlock blk{
+        .input_layernorm = {must(w, p + "input_layernorm.weight"), cfg.rms_norm_eps},
+        .post_attention_layernorm = {must(w, p + "post_attention_layernorm.weight"),
+                                     cfg.rms_norm_eps},
+        .self_attn =
+            {
+                .q_proj = {must(w, p + "self_attn.q_proj.weight")},
+                .k_proj = {must(w, p + "self_attn.k_proj.weight")},
+                .v_proj = {must(w, p + "self_attn.v_proj.weight")},
+                .o_proj = {must(w, p + "self_attn.o_proj.weight")},
+                .num_heads = cfg.num_attention_heads,
+                .num_kv_heads = cfg.num_key_value_heads,
+                .head_dim = cfg.head_dim,
+                .rope_theta = cfg.rope_theta,
+                .rope_scaling = {cfg.rope_scaling_factor, cfg.rope_scaling_low_freq_factor,
+                                 cfg.rope_scaling_high_freq_factor,
+                                 cfg.rope_scaling_original_max_pos},
+                .q_norm = {maybe(w, p + "self_attn.q_norm.weight"), cfg.rms_norm_eps},
+                .k_norm = {maybe(w, p + "self_attn.k_norm.weight"), cfg.rms_norm_eps},
+            },
+        .mlp =
+            {
+                .gate_proj = {must(w, p + "mlp.gate_proj.weight")},
+                .up_proj = {must(w, p + "mlp.up_proj.weight")},
+                .down_proj = {must(w, p + "mlp.down_proj.weight")},
+            },
+    };
+    m.layers.push_back(std::move(blk));
+  }
+  return m;
+}
+
+Model::NamedParameters Model::collect_parameters() {
+  NamedParameters out;
+  auto add = [&](const std::string& name, Tensor& t, bool decay) {
+    t.requires_grad_(true);
+    out.all.emplace_back(name, t);
+    if (decay) {
+      out.decay.push_back(t);
+      out.decay_names.push_back(name);
+    } else {
+      out.no_decay.push_back(t);
+      out.no_decay_names.push_back(name);
+    }
+  };
+  add("model.embed_tokens.weight", embed_tokens.weight, true);  // tied with the LM head
+  for (size_t i = 0; i < layers.size(); ++i) {
+    const std::string p = "model.layers." + std::to_string(i) + ".";
+    auto& L = layers[i];
+    add(p + "input_layernorm.weight", L.input_layernorm.weight, false);
+    add(p + "self_attn.q_proj.weight", L.self_attn.q_proj.weight, true);
+    add(p + "self_attn.k_proj.weight", L.self_attn.k_proj.weight, true);
+    add(p + "self_attn.v_proj.weight", L.self_attn.v_proj.weight, true);
+    add(p + "self_attn.o_proj.weight", L.self_attn.o_proj.weight, true);
+    if (L.self_attn.has_qk_norm()) {
+      add(p + "self_attn.q_norm.weight", L.self_attn.q_norm.weight, false);
+      add(p + "self_attn.k_norm.weight", L.self_attn.k_norm.weight, false);
+    }
+    add(p + "post_attention_layernorm.weight", L.post_attention_layernorm.weight, false);
+    add(p + "mlp.gate_proj.weight", L.mlp.gate_proj.weight, true);
+    add(p + "mlp.up_proj.weight", L.mlp.up_proj.weight, true);
+    add(p + "mlp.down_proj.weight", L.mlp.down_proj.weight, true);
+  }
+  add("model.norm.weight", norm.weight, false);
+  return out;
+}
+
+}  // namespace ctd::nn

@@ -1,0 +1,515 @@
+// Ops on the training block's path: matmul/bmm, RMSNorm, RoPE, elementwise,
+// fused SwiGLU and fused causal attention.  Each public op launches through
+// the C ABI and, when an input requires grad, records a backward node with
+// the reference's gradient formulas (src/ops/*.cu, src/ops/matmul.cpp).
+#include <cmath>
+#include <utility>
+
+#include "ctd/ops/attention.h"
+#include "ctd/ops/elementwise.h"
+#include "ctd/ops/matmul.h"
+#include "ctd/ops/norm.h"
+#include "ctd/ops/rope.h"
+#include "op_util.h"
+
+namespace ctd::ops {
+
+using namespace detail;
+
+// ================================================================== matmul
+namespace {
+
+struct MM {
+  int64_t M, N, K, lda, ldb;
+};
+
+MM mm_dims(const Tensor& a, const Tensor& b, bool ta, bool tb, const char* op) {
+  check_f32(a, op, "a");
+  check_f32(b, op, "b");
+  require(a.dim() == 2 && b.dim() == 2, std::string(op) + ": expected 2-D operands");
+  MM d;
+  d.M = ta ? a.shape()[1] : a.shape()[0];
+  d.K = ta ? a.shape()[0] : a.shape()[1];
+  const int64_t kb = tb ? b.shape()[1] : b.shape()[0];
+  d.N = tb ? b.shape()[0] : b.shape()[1];
+  require(d.K == kb, std::string(op) + ": inner dimension mismatch (" + std::to_string(d.K) +
+                         " vs " + std::to_string(kb) + ")");
+  d.lda = a.shape()[1];
+  d.ldb = b.shape()[1];
+  return d;
+}
+
+// Forward y = op(a) op(b); backward table of src/ops/matmul.cpp:99-118.
+template <typename F>
+std::pair<Tensor, Tensor> matmul_like_backward(const Tensor& dy, const Tensor& a,
+                                               const Tensor& b, bool ta, bool tb, bool need_a,
+                                               bool need_b, F mm) {
+  Tensor dA, dB;
+  if (!ta && !tb) {
+    if (need_a) dA = mm(dy, b, false, true);
+    if (need_b) dB = mm(a, dy, true, false);
+  } else if (ta && !tb) {
+    if (need_a) dA = mm(b, dy, false, true);
+    if (need_b) dB = mm(a, dy, false, false);
+  } else if (!ta && tb) {
+    if (need_a) dA = mm(dy, b, false, false);
+    if (need_b) dB = mm(dy, a, true, false);
+  } else {
+    if (need_a) dA = mm(b, dy, true, true);
+    if (need_b) dB = mm(dy, a, true, true);
+  }
+  return {dA, dB};
+}
+
+struct MatmulBackward : autograd::Node {
+  Tensor a, b;
+  bool ta = false, tb = false;
+  const char* name() const override { return "MatmulBackward"; }
+  std::vector<Tensor> backward(const std::vector<Tensor>& go) override {
+    autograd::NoGradGuard ng;
+    const bool na = next_edges.at(0).node != nullptr, nb = next_edges.at(1).node != nullptr;
+    auto [dA, dB] = matmul_like_backward(go.at(0), a, b, ta, tb, na, nb, matmul_impl);
+    a = Tensor{};
+    b = Tensor{};
+    return {dA, dB};
+  }
+};
+
+struct BmmBackward : autograd::Node {
+  Tensor a, b;
+  bool ta = false, tb = false;
+  const char* name() const override { return "BmmBackward"; }
+  std::vector<Tensor> backward(const std::vector<Tensor>& go) override {
+    autograd::NoGradGuard ng;
+    const bool na = next_edges.at(0).node != nullptr, nb = next_edges.at(1).node != nullptr;
+    auto [dA, dB] = matmul_like_backward(go.at(0), a, b, ta, tb, na, nb, bmm_impl);
+    a = Tensor{};
+    b = Tensor{};
+    return {dA, dB};
+  }
+};
+
+}  // namespace
+
+Tensor matmul_impl(const Tensor& a, const Tensor& b, bool transa, bool transb) {
+  const MM d = mm_dims(a, b, transa, transb, "matmul");
+  Tensor c = Tensor::empty({d.M, d.N}, DType::kFloat32, a.device());
+  void* ev = runtime::gemm_profile_begin();
+  CTD_CHECK(ember_gemm_f32(transa, transb, d.M, d.N, d.K, 1.0f, cfp(a), d.lda, 0, cfp(b), d.ldb,
+                           0, 0.0f, fp(c), d.N, 0, 1, S()));
+  runtime::gemm_profile_end(ev, 2.0 * d.M * d.N * d.K);
+  return c;
+}
+
+Tensor matmul(const Tensor& a, const Tensor& b, bool transa, bool transb) {
+  Tensor y = matmul_impl(a, b, transa, transb);
+  if (autograd::any_requires_grad({a, b})) {
+    auto node = std::make_shared<MatmulBackward>();
+    node->a = a.detach();
+    node->b = b.detach();
+    node->ta = transa;
+    node->tb = transb;
+    node->next_edges = autograd::collect_next_edges({a, b});
+    autograd::set_history(y, std::move(node));
+  }
+  return y;
+}
+
+Tensor bmm_impl(const Tensor& a, const Tensor& b, bool transa, bool transb) {
+  check_f32(a, "bmm", "a");
+  check_f32(b, "bmm", "b");
+  require(a.dim() == 3 && b.dim() == 3 && a.shape()[0] == b.shape()[0],
+          "bmm: expected [B,*,*] operands with equal batch");
+  const int64_t Bt = a.shape()[0];
+  const int64_t M = transa ? a.shape()[2] : a.shape()[1];
+  const int64_t K = transa ? a.shape()[1] : a.shape()[2];
+  const int64_t kb = transb ? b.shape()[2] : b.shape()[1];
+  const int64_t N = transb ? b.shape()[1] : b.shape()[2];
+  require(K == kb, "bmm: inner dimension mismatch");
+  Tensor c = Tensor::empty({Bt, M, N}, DType::kFloat32, a.device());
+  void* ev = runtime::gemm_profile_begin();
+  CTD_CHECK(ember_gemm_f32(transa, transb, M, N, K, 1.0f, cfp(a), a.shape()[2],
+                           a.shape()[1] * a.shape()[2], cfp(b), b.shape()[2],
+                           b.shape()[1] * b.shape()[2], 0.0f, fp(c), N, M * N, Bt, S()));
+  runtime::gemm_profile_end(ev, 2.0 * Bt * M * N * K);
+  return c;
+}
+
+Tensor bmm(const Tensor& a, const Tensor& b, bool transa, bool transb) {
+  Tensor y = bmm_impl(a, b, transa, transb);
+  if (autograd::any_requires_grad({a, b})) {
+    auto node = std::make_shared<BmmBackward>();
+    node->a = a.detach();
+    node->b = b.detach();
+    node->ta = transa;
+    node->tb = transb;
+    node->next_edges = autograd::collect_next_edges({a, b});
+    autograd::set_history(y, std::move(node));
+  }
+  return y;
+}
+
+// ================================================================= RMSNorm
+namespace {
+
+void check_norm(const Tensor& x, const Tensor& w) {
+  check_f32(x, "rms_norm", "x");
+  check_f32(w, "rms_norm", "weight");
+  require(x.dim() >= 1, "rms_norm: x must have >= 1 dim");
+  require(w.dim() == 1 && w.shape()[0] == x.shape().back(), "rms_norm: weight shape mismatch");
+}
+
+std::pair<Tensor, Tensor> rms_bwd(const Tensor& dy, const Tensor& x, const Tensor& w,
+                                  const Tensor* rstd, float eps, bool need_dx, bool need_dw) {
+  const int64_t H = x.shape().back();
+  const int64_t rows = x.numel() / H;
+  Tensor dx = need_dx ? empty_like(x) : Tensor{};
+  Tensor dw = need_dw ? empty_like(w) : Tensor{};
+  const size_t wsb = need_dw ? ember_rmsnorm_bwd_workspace_bytes(rows, H) : 0;
+  Tensor ws = wsb ? workspace(wsb) : Tensor{};
+  CTD_CHECK(ember_rmsnorm_bwd(cfp(dy), cfp(x), cfp(w), rstd ? cfp(*rstd) : nullptr,
+                              need_dx ? fp(dx) : nullptr, need_dw ? fp(dw) : nullptr, rows, H, eps,
+                              wsb ? ws.data_ptr() : nullptr, wsb, S()));
+  return {dx, dw};
+}
+
+struct RmsNormBackward : autograd::Node {
+  Tensor x, w, rstd;
+  float eps = 1e-5f;
+  const char* name() const override { return "RmsNormBackward"; }
+  std::vector<Tensor> backward(const std::vector<Tensor>& go) override {
+    autograd::NoGradGuard ng;
+    check_f32(go.at(0), "rms_norm backward", "grad");
+    auto r = rms_bwd(go[0], x, w, &rstd, eps, next_edges.at(0).node != nullptr,
+                     next_edges.at(1).node != nullptr);
+    x = w = rstd = Tensor{};
+    return {r.first, r.second};
+  }
+};
+
+}  // namespace
+
+Tensor rms_norm_impl(const Tensor& x, const Tensor& weight, float eps) {
+  check_norm(x, weight);
+  const int64_t H = x.shape().back();
+  Tensor y = empty_like(x);
+  CTD_CHECK(ember_rmsnorm_fwd(cfp(x), cfp(weight), fp(y), nullptr, x.numel() / H, H, eps, S()));
+  return y;
+}
+
+std::pair<Tensor, Tensor> rms_norm_backward_impl(const Tensor& dy, const Tensor& x,
+                                                 const Tensor& w, float eps) {
+  check_norm(x, w);
+  check_f32(dy, "rms_norm backward", "dy");
+  require(dy.shape() == x.shape(), "rms_norm backward: dy shape mismatch");
+  return rms_bwd(dy, x, w, nullptr, eps, true, true);
+}
+
+Tensor rms_norm(const Tensor& x, const Tensor& weight, float eps) {
+  check_norm(x, weight);
+  if (!autograd::any_requires_grad({x, weight})) return rms_norm_impl(x, weight, eps);
+  const int64_t H = x.shape().back();
+  const int64_t rows = x.numel() / H;
+  Tensor y = empty_like(x);
+  Tensor rstd = Tensor::empty({rows}, DType::kFloat32, x.device());
+  CTD_CHECK(ember_rmsnorm_fwd(cfp(x), cfp(weight), fp(y), fp(rstd), rows, H, eps, S()));
+  auto node = std::make_shared<RmsNormBackward>();
+  node->x = x.detach();
+  node->w = weight.detach();
+  node->rstd = rstd;
+  node->eps = eps;
+  node->next_edges = autograd::collect_next_edges({x, weight});
+  autograd::set_history(y, std::move(node));
+  return y;
+}
+
+// ==================================================================== RoPE
+namespace {
+
+struct RopeArgs {
+  int64_t B, T, H, D;
+  float freqs[128];
+};
+
+RopeArgs rope_args(const Tensor& x, float theta, const RopeScaling& sc) {
+  check_f32(x, "rope");
+  require(x.dim() == 4, "rope: expected [B, T, H, D]");
+  RopeArgs a{x.shape()[0], x.shape()[1], x.shape()[2], x.shape()[3], {}};
+  require(a.D % 2 == 0, "rope: head_dim must be even");
+  require(a.D <= 256, "rope: head_dim must be <= 256");
+  CTD_CHECK(ember_rope_freqs_host(a.freqs, static_cast<int>(a.D), theta, sc.factor,
+                                  sc.low_freq_factor, sc.high_freq_factor, sc.original_max_pos));
+  return a;
+}
+
+void launch_rope(const Tensor& x, Tensor& y, int pos0, float theta, const RopeScaling& sc,
+                 float sign) {
+  RopeArgs a = rope_args(x, theta, sc);
+  CTD_CHECK(ember_rope(cfp(x), fp(y), a.B, a.T, a.H, a.D, pos0, a.freqs, sign, S()));
+}
+
+struct RopeBackward : autograd::Node {
+  int position_start = 0;
+  float theta = 10000.0f;
+  RopeScaling scaling;
+  const char* name() const override { return "RopeBackward"; }
+  std::vector<Tensor> backward(const std::vector<Tensor>& go) override {
+    autograd::NoGradGuard ng;
+    return {rope_transpose_impl(go.at(0), position_start, theta, scaling)};
+  }
+};
+
+}  // namespace
+
+void apply_rope_inplace(Tensor& x, int position_start, float theta, const RopeScaling& scaling) {
+  launch_rope(x, x, position_start, theta, scaling, 1.0f);
+}
+
+Tensor rope_impl(const Tensor& x, int position_start, float theta, const RopeScaling& scaling) {
+  Tensor y = Tensor::empty(x.shape(), x.dtype(), x.device());
+  launch_rope(x, y, position_start, theta, scaling, 1.0f);
+  return y;
+}
+
+Tensor rope_transpose_impl(const Tensor& x, int position_start, float theta,
+                           const RopeScaling& scaling) {
+  Tensor y = Tensor::empty(x.shape(), x.dtype(), x.device());
+  launch_rope(x, y, position_start, theta, scaling, -1.0f);
+  return y;
+}
+
+Tensor rope(const Tensor& x, int position_start, float theta, const RopeScaling& scaling) {
+  Tensor y = rope_impl(x, position_start, theta, scaling);
+  if (autograd::any_requires_grad({x})) {
+    auto node = std::make_shared<RopeBackward>();
+    node->position_start = position_start;
+    node->theta = theta;
+    node->scaling = scaling;
+    node->next_edges = autograd::collect_next_edges({x});
+    autograd::set_history(y, std::move(node));
+  }
+  return y;
+}
+
+// ============================================================= elementwise
+namespace {
+
+void check_binary(const Tensor& a, const Tensor& b, const char* op) {
+  check_f32(a, op, "a");
+  check_f32(b, op, "b");
+  require(a.shape() == b.shape(), std::string(op) + ": shape mismatch");
+}
+
+struct AddBackward : autograd::Node {
+  const char* name() const override { return "AddBackward"; }
+  std::vector<Tensor> backward(const std::vector<Tensor>& go) override {
+    // Both inputs receive dy; the engine copies on write if a slot is later
+    // accumulated into (src/ops/elementwise.cu:177-184 made two copies up front).
+    return {go.at(0), go.at(0)};
+  }
+};
+
+struct MulBackward : autograd::Node {
+  Tensor a, b;
+  const char* name() const override { return "MulBackward"; }
+  std::vector<Tensor> backward(const std::vector<Tensor>& go) override {
+    autograd::NoGradGuard ng;
+    Tensor da, db;
+    if (next_edges.at(0).node) da = mul_impl(go.at(0), b);
+    if (next_edges.at(1).node) db = mul_impl(go.at(0), a);
+    a = b = Tensor{};
+    return {da, db};
+  }
+};
+
+struct SiluBackward : autograd::Node {
+  Tensor x;
+  const char* name() const override { return "SiluBackward"; }
+  std::vector<Tensor> backward(const std::vector<Tensor>& go) override {
+    autograd::NoGradGuard ng;
+    Tensor dx = silu_backward_impl(x, go.at(0));
+    x = Tensor{};
+    return {dx};
+  }
+};
+
+struct SwigluBackward : autograd::Node {
+  Tensor g, u;
+  const char* name() const override { return "SwigluBackward"; }
+  std::vector<Tensor> backward(const std::vector<Tensor>& go) override {
+    autograd::NoGradGuard ng;
+    check_f32(go.at(0), "swiglu backward", "grad");
+    Tensor dg = empty_like(g), du = empty_like(u);
+    CTD_CHECK(ember_swiglu_bwd(cfp(g), cfp(u), cfp(go[0]), fp(dg), fp(du), g.numel(), S()));
+    g = u = Tensor{};
+    return {dg, du};
+  }
+};
+
+}  // namespace
+
+Tensor add_impl(const Tensor& a, const Tensor& b) {
+  check_binary(a, b, "add");
+  Tensor y = empty_like(a);
+  CTD_CHECK(ember_add(cfp(a), cfp(b), fp(y), a.numel(), S()));
+  return y;
+}
+
+Tensor add(const Tensor& a, const Tensor& b) {
+  Tensor y = add_impl(a, b);
+  if (autograd::any_requires_grad({a, b})) {
+    auto node = std::make_shared<AddBackward>();
+    node->next_edges = autograd::collect_next_edges({a, b});
+    autograd::set_history(y, std::move(node));
+  }
+  return y;
+}
+
+Tensor mul_impl(const Tensor& a, const Tensor& b) {
+  check_binary(a, b, "mul");
+  Tensor y = empty_like(a);
+  CTD_CHECK(ember_mul(cfp(a), cfp(b), fp(y), a.numel(), S()));
+  return y;
+}
+
+Tensor mul(const Tensor& a, const Tensor& b) {
+  Tensor y = mul_impl(a, b);
+  if (autograd::any_requires_grad({a, b})) {
+    auto node = std::make_shared<MulBackward>();
+    node->a = a.detach();
+    node->b = b.detach();
+    node->next_edges = autograd::collect_next_edges({a, b});
+    autograd::set_history(y, std::move(node));
+  }
+  return y;
+}
+
+Tensor silu_impl(const Tensor& x) {
+  check_f32(x, "silu");
+  Tensor y = empty_like(x);
+  CTD_CHECK(ember_silu(cfp(x), fp(y), x.numel(), S()));
+  return y;
+}
+
+Tensor silu(const Tensor& x) {
+  Tensor y = silu_impl(x);
+  if (autograd::any_requires_grad({x})) {
+    auto node = std::make_shared<SiluBackward>();
+    node->x = x.detach();
+    node->next_edges = autograd::collect_next_edges({x});
+    autograd::set_history(y, std::move(node));
+  }
+  return y;
+}
+
+Tensor sub_impl(const Tensor& a, const Tensor& b) {
+  check_binary(a, b, "sub");
+  Tensor y = empty_like(a);
+  CTD_CHECK(ember_sub(cfp(a), cfp(b), fp(y), a.numel(), S()));
+  return y;
+}
+
+Tensor scale_impl(const Tensor& x, float alpha) {
+  check_f32(x, "scale");
+  Tensor y = empty_like(x);
+  CTD_CHECK(ember_scale(cfp(x), alpha, fp(y), x.numel(), S()));
+  return y;
+}
+
+Tensor silu_backward_impl(const Tensor& x, const Tensor& g) {
+  check_binary(x, g, "silu_backward");
+  Tensor y = empty_like(x);
+  CTD_CHECK(ember_silu_bwd(cfp(x), cfp(g), fp(y), x.numel(), S()));
+  return y;
+}
+
+Tensor swiglu_impl(const Tensor& g, const Tensor& u) {
+  check_binary(g, u, "swiglu");
+  Tensor h = empty_like(g);
+  CTD_CHECK(ember_swiglu_fwd(cfp(g), cfp(u), fp(h), g.numel(), S()));
+  return h;
+}
+
+Tensor swiglu(const Tensor& g, const Tensor& u) {
+  Tensor h = swiglu_impl(g, u);
+  if (autograd::any_requires_grad({g, u})) {
+    auto node = std::make_shared<SwigluBackward>();
+    node->g = g.detach();
+    node->u = u.detach();
+    node->next_edges = autograd::collect_next_edges({g, u});
+    autograd::set_history(h, std::move(node));
+  }
+  return h;
+}
+
+// =============================================================== attention
+namespace {
+
+struct AttnDims {
+  int64_t B, T, H, Hk, D;
+};
+
+AttnDims attn_dims(const Tensor& q, const Tensor& k, const Tensor& v) {
+  check_f32(q, "causal_attention", "q");
+  check_f32(k, "causal_attention", "k");
+  check_f32(v, "causal_attention", "v");
+  require(q.dim() == 4 && k.dim() == 4 && v.dim() == 4, "causal_attention: expected [B,T,H,D]");
+  AttnDims d{q.shape()[0], q.shape()[1], q.shape()[2], k.shape()[2], q.shape()[3]};
+  require(k.shape() == v.shape(), "causal_attention: k and v shapes differ");
+  require(k.shape()[0] == d.B && k.shape()[1] == d.T && k.shape()[3] == d.D,
+          "causal_attention: q/k shape mismatch");
+  require(d.Hk > 0 && d.H % d.Hk == 0, "causal_attention: num_heads % num_kv_heads != 0");
+  require(d.D == 64 || d.D == 128, "causal_attention: head_dim must be 64 or 128");
+  return d;
+}
+
+struct CausalAttentionBackward : autograd::Node {
+  Tensor q, k, v, o, lse;
+  float scale = 1.0f;
+  const char* name() const override { return "CausalAttentionBackward"; }
+  std::vector<Tensor> backward(const std::vector<Tensor>& go) override {
+    autograd::NoGradGuard ng;
+    const Tensor& dout = go.at(0);
+    check_f32(dout, "causal_attention backward", "grad");
+    const AttnDims d = attn_dims(q, k, v);
+    Tensor dq = empty_like(q), dk = empty_like(k), dv = empty_like(v);
+    const size_t wsb = ember_attn_bwd_workspace_bytes(d.B, d.T, d.H);
+    Tensor ws = workspace(wsb);
+    CTD_CHECK(ember_attn_bwd(cfp(q), cfp(k), cfp(v), cfp(o), cfp(lse), cfp(dout), fp(dq), fp(dk),
+                             fp(dv), d.B, d.T, d.H, d.Hk, d.D, scale, ws.data_ptr(), wsb, S()));
+    q = k = v = o = lse = Tensor{};
+    return {dq, dk, dv};
+  }
+};
+
+}  // namespace
+
+Tensor causal_attention_impl(const Tensor& q, const Tensor& k, const Tensor& v, float scale,
+                             Tensor* lse_out) {
+  const AttnDims d = attn_dims(q, k, v);
+  Tensor o = empty_like(q);
+  Tensor lse = Tensor::empty({d.B, d.H, d.T}, DType::kFloat32, q.device());
+  CTD_CHECK(ember_attn_fwd(cfp(q), cfp(k), cfp(v), fp(o), fp(lse), d.B, d.T, d.H, d.Hk, d.D,
+                           scale, S()));
+  if (lse_out) *lse_out = lse;
+  return o;
+}
+
+Tensor causal_attention(const Tensor& q, const Tensor& k, const Tensor& v, float scale) {
+  Tensor lse;
+  Tensor o = causal_attention_impl(q, k, v, scale, &lse);
+  if (autograd::any_requires_grad({q, k, v})) {
+    auto node = std::make_shared<CausalAttentionBackward>();
+    node->q = q.detach();
+    node->k = k.detach();
+    node->v = v.detach();
+    node->o = o.detach();
+    node->lse = lse;
+    node->scale = scale;
+    node->next_edges = autograd::collect_next_edges({q, k, v});
+    autograd::set_history(o, std::move(node));
+  }
+  return o;
+}
+
+}  // namespace ctd::ops

@@ -1,0 +1,322 @@
+// Runtime glue, allocators and Storage.
+//
+// Reference: src/core/allocator.cpp:14-57 (raw cudaMalloc/cudaFree per tensor,
+// malloc CPU allocator, cudaMallocHost pinned allocator) and
+// src/core/storage.cpp.  The device allocator here caches freed blocks per
+// rounded size so the training loop never reaches the driver after its first
+// step (hipFree would also synchronise the device), and it keeps the
+// high-water mark of live bytes that the peak-HBM figure is read from.
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "ctd/allocator.h"
+#include "ctd/runtime.h"
+#include "ctd/storage.h"
+
+namespace ctd {
+
+namespace runtime {
+
+void check(int status, const char* what) {
+  if (status != EMBER_OK)
+    throw std::runtime_error(std::string(what) + ": " + ember_status_string(status));
+}
+
+namespace {
+struct Streams {
+  ember_stream_t compute = nullptr, h2d = nullptr, d2h = nullptr;
+  Streams() {
+    check(ember_stream_create(&compute), "create compute stream");
+    check(ember_stream_create(&h2d), "create h2d stream");
+    check(ember_stream_create(&d2h), "create d2h stream");
+  }
+};
+Streams& streams() {
+  static Streams s;
+  return s;
+}
+}  // namespace
+
+ember_stream_t compute_stream() { return streams().compute; }
+ember_stream_t h2d_stream() { return streams().h2d; }
+ember_stream_t d2h_stream() { return streams().d2h; }
+
+void synchronize() { check(ember_stream_synchronize(compute_stream()), "synchronize"); }
+
+bool device_available() {
+  int n = 0;
+  return ember_get_device_count(&n) == EMBER_OK && n > 0;
+}
+
+namespace {
+struct GemmProfiler {
+  std::mutex mu;
+  bool on = false;
+  std::vector<ember_event_t> pool;                       // free events
+  std::vector<std::pair<ember_event_t, ember_event_t>> spans;
+  std::vector<double> flops;
+  ember_event_t get() {
+    if (!pool.empty()) {
+      ember_event_t e = pool.back();
+      pool.pop_back();
+      return e;
+    }
+    ember_event_t e = nullptr;
+    check(ember_event_create(&e), "gemm profiler event");
+    return e;
+  }
+};
+GemmProfiler& prof() {
+  static GemmProfiler* p = new GemmProfiler();
+  return *p;
+}
+}  // namespace
+
+void gemm_profile_enable(bool on) {
+  std::lock_guard<std::mutex> lk(prof().mu);
+  prof().on = on;
+}
+bool gemm_profiling() { return prof().on; }
+
+void* gemm_profile_begin() {
+  auto& p = prof();
+  if (!p.on) return nullptr;
+  std::lock_guard<std::mutex> lk(p.mu);
+  ember_event_t e = p.get();
+  check(ember_event_record(e, compute_stream()), "gemm profiler record");
+  return e;
+}
+
+void gemm_profile_end(void* begin, double flops) {
+  if (!begin) return;
+  auto& p = prof();
+  std::lock_guard<std::mutex> lk(p.mu);
+  ember_event_t e = p.get();
+  check(ember_event_record(e, compute_stream()), "gemm profiler record");
+  p.spans.emplace_back(begin, e);
+  p.flops.push_back(flops);
+}
+
+void gemm_profile_collect(int64_t* launches, double* flops, double* total_ms) {
+  auto& p = prof();
+  std::lock_guard<std::mutex> lk(p.mu);
+  synchronize();
+  double ms = 0.0, fl = 0.0;
+  for (size_t i = 0; i < p.spans.size(); ++i) {
+    float t = 0.f;
+    check(ember_event_elapsed_ms(&t, p.spans[i].first, p.spans[i].second), "gemm profiler elapsed");
+    ms += t;
+    fl += p.flops[i];
+    p.pool.push_back(p.spans[i].first);
+    p.pool.push_back(p.spans[i].second);
+  }
+  if (launches) *launches = static_cast<int64_t>(p.spans.size());
+  if (flops) *flops = fl;
+  if (total_ms) *total_ms = ms;
+  p.spans.clear();
+  p.flops.clear();
+}
+
+}  // namespace runtime
+
+namespace {
+
+class HipCachingAllocator final : public Allocator {
+ public:
+  void* allocate(size_t nbytes) override {
+    if (nbytes == 0) return nullptr;
+    const size_t r = round_up(nbytes);
+    std::lock_guard<std::mutex> lk(mu_);
+    void* p = nullptr;
+    auto it = free_.find(r);
+    if (it != free_.end() && !it->second.empty()) {
+      p = it->second.back();
+      it->second.pop_back();
+    } else {
+      int rc = ember_device_malloc(&p, r);
+      if (rc != EMBER_OK) {  // give cached blocks back and retry once
+        release_cached_locked();
+        rc = ember_device_malloc(&p, r);
+      }
+      if (rc != EMBER_OK)
+        throw std::runtime_error("hip_allocator: out of device memory allocating " +
+                                 std::to_string(r) + " bytes (" + ember_status_string(rc) + ")");
+      stats_.reserved_bytes += r;
+      stats_.num_device_mallocs += 1;
+      if (stats_.reserved_bytes > stats_.peak_reserved_bytes)
+        stats_.peak_reserved_bytes = stats_.reserved_bytes;
+    }
+    live_[p] = r;
+    stats_.allocated_bytes += r;
+    if (stats_.allocated_bytes > stats_.peak_allocated_bytes)
+      stats_.peak_allocated_bytes = stats_.allocated_bytes;
+    return p;
+  }
+
+  void deallocate(void* ptr) noexcept override {
+    if (!ptr) return;
+    std::lock_guard<std::mutex> lk(mu_);
+    auto it = live_.find(ptr);
+    if (it == live_.end()) return;
+    const size_t r = it->second;
+    live_.erase(it);
+    stats_.allocated_bytes -= r;
+    free_[r].push_back(ptr);
+  }
+
+  Device device() const override { return kHIP0; }
+
+  DeviceMemoryStats stats() {
+    std::lock_guard<std::mutex> lk(mu_);
+    return stats_;
+  }
+  void reset_peak() {
+    std::lock_guard<std::mutex> lk(mu_);
+    stats_.peak_allocated_bytes = stats_.allocated_bytes;
+    stats_.peak_reserved_bytes = stats_.reserved_bytes;
+  }
+  void empty_cache() {
+    std::lock_guard<std::mutex> lk(mu_);
+    release_cached_locked();
+  }
+
+ private:
+  // 512-byte granules below 1 MiB, 2 MiB granules above.
+  static size_t round_up(size_t n) {
+    if (n <= (size_t{1} << 20)) return (n + 511) & ~size_t{511};
+    const size_t g = size_t{2} << 20;
+    return (n + g - 1) / g * g;
+  }
+  void release_cached_locked() {
+    ember_device_synchronize();
+    for (auto& [r, v] : free_) {
+      for (void* p : v) {
+        ember_device_free(p);
+        stats_.reserved_bytes -= r;
+      }
+      v.clear();
+    }
+  }
+
+  std::mutex mu_;
+  std::unordered_map<size_t, std::vector<void*>> free_;
+  std::unordered_map<void*, size_t> live_;
+  DeviceMemoryStats stats_;
+};
+
+class CpuAllocator final : public Allocator {
+ public:
+  void* allocate(size_t nbytes) override {
+    if (nbytes == 0) return nullptr;
+    void* p = std::aligned_alloc(64, (nbytes + 63) & ~size_t{63});
+    if (!p) throw std::runtime_error("cpu_allocator: out of memory");
+    return p;
+  }
+  void deallocate(void* ptr) noexcept override { std::free(ptr); }
+  Device device() const override { return kCPU; }
+};
+
+class PinnedCpuAllocator final : public Allocator {
+ public:
+  void* allocate(size_t nbytes) override {
+    if (nbytes == 0) return nullptr;
+    void* p = nullptr;
+    runtime::check(ember_host_malloc_pinned(&p, nbytes), "pinned_cpu_allocator");
+    std::lock_guard<std::mutex> lk(mu_);
+    sizes_[p] = nbytes;
+    bytes_ += nbytes;
+    return p;
+  }
+  void deallocate(void* ptr) noexcept override {
+    if (!ptr) return;
+    {
+      std::lock_guard<std::mutex> lk(mu_);
+      auto it = sizes_.find(ptr);
+      if (it != sizes_.end()) {
+        bytes_ -= it->second;
+        sizes_.erase(it);
+      }
+    }
+    ember_host_free_pinned(ptr);
+  }
+  Device device() const override { return kCPU; }
+  size_t bytes() {
+    std::lock_guard<std::mutex> lk(mu_);
+    return bytes_;
+  }
+
+ private:
+  std::mutex mu_;
+  std::unordered_map<void*, size_t> sizes_;
+  size_t bytes_ = 0;
+};
+
+HipCachingAllocator& hip_cache() {
+  static HipCachingAllocator* a = new HipCachingAllocator();  // outlives static tensors
+  return *a;
+}
+PinnedCpuAllocator& pinned() {
+  static PinnedCpuAllocator* a = new PinnedCpuAllocator();
+  return *a;
+}
+
+}  // namespace
+
+Allocator& hip_allocator() { return hip_cache(); }
+Allocator& cpu_allocator() {
+  static CpuAllocator a;
+  return a;
+}
+Allocator& pinned_cpu_allocator() { return pinned(); }
+Allocator& allocator_for(const Device& device) {
+  return device.is_hip() ? hip_allocator() : cpu_allocator();
+}
+
+DeviceMemoryStats device_memory_stats() { return hip_cache().stats(); }
+void reset_peak_device_memory() { hip_cache().reset_peak(); }
+void empty_device_cache() { hip_cache().empty_cache(); }
+size_t pinned_host_bytes() { return pinned().bytes(); }
+
+// ------------------------------------------------------------------ Storage
+Storage::Storage(size_t nbytes, Allocator& allocator)
+    : allocator_(&allocator), nbytes_(nbytes), device_(allocator.device()) {
+  data_ = allocator_->allocate(nbytes);
+  pinned_ = (&allocator == &pinned_cpu_allocator());
+}
+
+Storage::Storage(Storage&& o) noexcept
+    : allocator_(o.allocator_), data_(o.data_), nbytes_(o.nbytes_), device_(o.device_),
+      pinned_(o.pinned_) {
+  o.allocator_ = nullptr;
+  o.data_ = nullptr;
+  o.nbytes_ = 0;
+}
+
+Storage& Storage::operator=(Storage&& o) noexcept {
+  if (this != &o) {
+    release_();
+    allocator_ = o.allocator_;
+    data_ = o.data_;
+    nbytes_ = o.nbytes_;
+    device_ = o.device_;
+    pinned_ = o.pinned_;
+    o.allocator_ = nullptr;
+    o.data_ = nullptr;
+    o.nbytes_ = 0;
+  }
+  return *this;
+}
+
+Storage::~Storage() { release_(); }
+
+void Storage::release_() noexcept {
+  if (allocator_ && data_) allocator_->deallocate(data_);
+  data_ = nullptr;
+}
+
+}  // namespace ctd

@@ -1,0 +1,556 @@
+// C entry points (include/ctd_capi.h) over the C++ layer: model construction
+// with seeded synthetic weights, the ctd_train step, memory statistics and
+// checkpoint save/load.  The step follows tools/ctd_train/main.cpp:348-398 of
+// the reference (forward_train_masked, backward, clip_grad_norm_, step,
+// zero_grad); the optimizer-state file follows main.cpp:208-271 (m then v per
+// parameter, decay group first, plus optimizer.step), loading straight into
+// the pinned host state when m/v are offloaded.
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "ctd/allocator.h"
+#include "ctd/nn/model.h"
+#include "ctd/optim.h"
+#include "ctd/runtime.h"
+#include "ctd_capi.h"
+
+using namespace ctd;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+template <typename F>
+int guarded(F&& f) {
+  try {
+    f();
+    return 0;
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+  } catch (...) {
+    g_last_error = "unknown C++ exception";
+  }
+  return CTD_EXCEPTION;
+}
+
+uint64_t splitmix(uint64_t& s) {
+  uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+nn::LlamaConfig to_llama(const ctd_model_config& c) {
+  nn::LlamaConfig l{};
+  l.vocab_size = c.vocab_size;
+  l.hidden_size = c.hidden_size;
+  l.intermediate_size = c.intermediate_size;
+  l.num_hidden_layers = c.num_layers;
+  l.num_attention_heads = c.num_heads;
+  l.num_key_value_heads = c.num_kv_heads;
+  l.head_dim = c.head_dim;
+  l.max_position_embeddings = 1 << 20;
+  l.rms_norm_eps = c.rms_norm_eps;
+  l.rope_theta = c.rope_theta;
+  l.tie_word_embeddings = true;
+  l.qk_norm = c.qk_norm != 0;
+  l.rope_scaling_factor = c.rope_factor;
+  l.rope_scaling_low_freq_factor = c.rope_low_freq_factor;
+  l.rope_scaling_high_freq_factor = c.rope_high_freq_factor;
+  l.rope_scaling_original_max_pos = c.rope_original_max_pos;
+  return l;
+}
+
+ctd_model_config from_llama(const nn::LlamaConfig& l) {
+  ctd_model_config c{};
+  c.vocab_size = l.vocab_size;
+  c.hidden_size = l.hidden_size;
+  c.intermediate_size = l.intermediate_size;
+  c.num_layers = l.num_hidden_layers;
+  c.num_heads = l.num_attention_heads;
+  c.num_kv_heads = l.num_key_value_heads;
+  c.head_dim = l.head_dim;
+  c.qk_norm = l.qk_norm ? 1 : 0;
+  c.rms_norm_eps = l.rms_norm_eps;
+  c.rope_theta = l.rope_theta;
+  c.rope_factor = l.rope_scaling_factor;
+  c.rope_low_freq_factor = l.rope_scaling_low_freq_factor;
+  c.rope_high_freq_factor = l.rope_scaling_high_freq_factor;
+  c.rope_original_max_pos = l.rope_scaling_original_max_pos;
+  return c;
+}
+
+struct Trainer {
+  nn::Model model;
+  nn::Model::NamedParameters named;
+  std::vector<int32_t> decay;  // per entry of named.all
+  std::vector<std::pair<size_t, size_t>> opt_index;  // named.all index -> (group, position)
+  Tensor ids, targets, mask;
+  int64_t B = 0, T = 0;
+  float mask_sum = 0.f;
+  std::unique_ptr<optim::AdamW> opt;
+};
+
+Trainer* as_trainer(ctd_trainer_t t) {
+  if (!t) throw std::runtime_error("null trainer handle");
+  return static_cast<Trainer*>(t);
+}
+
+Tensor& param_at(Trainer* tr, int64_t i) {
+  if (i < 0 || i >= static_cast<int64_t>(tr->named.all.size()))
+    throw std::runtime_error("parameter index out of range");
+  return tr->named.all[static_cast<size_t>(i)].second;
+}
+
+void check_numel(const Tensor& t, int64_t numel) {
+  if (t.numel() != numel) throw std::runtime_error("numel mismatch");
+}
+
+// Uninitialised device tensors under the HF names build_model expects.
+TensorDict weight_shapes(const nn::LlamaConfig& c) {
+  TensorDict w;
+  const int64_t d = c.hidden_size, I = c.intermediate_size, H = c.num_attention_heads,
+                Hk = c.num_key_value_heads, D = c.head_dim, V = c.vocab_size;
+  auto mk = [&](const std::string& name, std::vector<int64_t> shape) {
+    w.emplace(name, Tensor::empty(std::move(shape), DType::kFloat32, kHIP0));
+  };
+  mk("model.embed_tokens.weight", {V, d});
+  mk("model.norm.weight", {d});
+  for (int l = 0; l < c.num_hidden_layers; ++l) {
+    const std::string p = "model.layers." + std::to_string(l) + ".";
+    mk(p + "input_layernorm.weight", {d});
+    mk(p + "post_attention_layernorm.weight", {d});
+    mk(p + "self_attn.q_proj.weight", {H * D, d});
+    mk(p + "self_attn.k_proj.weight", {Hk * D, d});
+    mk(p + "self_attn.v_proj.weight", {Hk * D, d});
+    mk(p + "self_attn.o_proj.weight", {d, H * D});
+    if (c.qk_norm) {
+      mk(p + "self_attn.q_norm.weight", {D});
+      mk(p + "self_attn.k_norm.weight", {D});
+    }
+    mk(p + "mlp.gate_proj.weight", {I, d});
+    mk(p + "mlp.up_proj.weight", {I, d});
+    mk(p + "mlp.down_proj.weight", {d, I});
+  }
+  return w;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ctd_last_error(void) { return g_last_error.c_str(); }
+
+int ctd_preset_config(const char* name, ctd_model_config* out) {
+  return guarded([&] {
+    if (!name || !out) throw std::runtime_error("null argument");
+    const std::string n(name);
+    nn::LlamaConfig l;
+    if (n == "smollm2-135m") l = nn::smollm2_135m_config();
+    else if (n == "smollm2-360m") l = nn::smollm2_360m_config();
+    else if (n == "qwen3-0.6b") l = nn::qwen3_0_6b_config();
+    else if (n == "qwen3-1.7b") l = nn::qwen3_1_7b_config();
+    else if (n == "llama3.2-1b") l = nn::llama3_2_1b_config();
+    else throw std::runtime_error("unknown preset " + n);
+    *out = from_llama(l);
+  });
+}
+
+int ctd_trainer_create(const ctd_model_config* cfg, uint64_t seed, float init_std,
+                       float norm_value, ctd_trainer_t* out) {
+  return guarded([&] {
+    if (!cfg || !out) throw std::runtime_error("null argument");
+    auto tr = std::make_unique<Trainer>();
+    const nn::LlamaConfig l = to_llama(*cfg);
+    TensorDict w = weight_shapes(l);
+    tr->model = nn::build_model(w, l);
+    tr->named = tr->model.collect_parameters();
+    // Seeded init over the parameter list in collect_parameters order: one
+    // counter stream, element offset = running parameter offset.
+    uint64_t offset = 0;
+    size_t di = 0, ni = 0;
+    for (auto& [name, p] : tr->named.all) {
+      const bool is_norm = p.dim() == 1;
+      const bool dec = di < tr->named.decay_names.size() && tr->named.decay_names[di] == name;
+      if (dec) {
+        tr->opt_index.emplace_back(0, di++);
+      } else {
+        tr->opt_index.emplace_back(1, ni++);
+      }
+      tr->decay.push_back(dec ? 1 : 0);
+      if (is_norm && !std::isnan(norm_value)) {
+        CTD_CHECK(ember_fill(static_cast<float*>(p.data_ptr()), p.numel(), norm_value,
+                             runtime::compute_stream()));
+      } else {
+        CTD_CHECK(ember_fill_normal(static_cast<float*>(p.data_ptr()), p.numel(), seed, offset,
+                                    0.0f, init_std, runtime::compute_stream()));
+      }
+      offset += static_cast<uint64_t>(p.numel());
+    }
+    runtime::synchronize();
+    *out = tr.release();
+  });
+}
+
+int ctd_trainer_destroy(ctd_trainer_t t) {
+  return guarded([&] {
+    runtime::synchronize();
+    delete static_cast<Trainer*>(t);
+  });
+}
+
+int ctd_trainer_num_params(ctd_trainer_t t, int64_t* n) {
+  return guarded([&] { *n = static_cast<int64_t>(as_trainer(t)->named.all.size()); });
+}
+
+int ctd_trainer_param_info(ctd_trainer_t t, int64_t i, char* name, size_t cap, int64_t* numel,
+                           int32_t* decay) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    Tensor& p = param_at(tr, i);
+    const std::string& nm = tr->named.all[static_cast<size_t>(i)].first;
+    if (name && cap) {
+      std::strncpy(name, nm.c_str(), cap - 1);
+      name[cap - 1] = '\0';
+    }
+    if (numel) *numel = p.numel();
+    if (decay) *decay = tr->decay[static_cast<size_t>(i)];
+  });
+}
+
+int ctd_trainer_set_param(ctd_trainer_t t, int64_t i, const float* host, int64_t numel) {
+  return guarded([&] {
+    Tensor& p = param_at(as_trainer(t), i);
+    check_numel(p, numel);
+    CTD_CHECK(ember_memcpy_async(p.data_ptr(), host, p.nbytes(), 0, runtime::compute_stream()));
+    runtime::synchronize();
+  });
+}
+
+int ctd_trainer_get_param(ctd_trainer_t t, int64_t i, float* host, int64_t numel) {
+  return guarded([&] {
+    Tensor& p = param_at(as_trainer(t), i);
+    check_numel(p, numel);
+    p.copy_to_host(host);
+  });
+}
+
+int ctd_trainer_get_grad(ctd_trainer_t t, int64_t i, float* host, int64_t numel) {
+  try {
+    Tensor g = param_at(as_trainer(t), i).grad();
+    if (!g.storage()) return -1;
+    check_numel(g, numel);
+    g.copy_to_host(host);
+    return 0;
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+    return CTD_EXCEPTION;
+  }
+}
+
+int ctd_trainer_set_checkpointing(ctd_trainer_t t, int32_t on) {
+  return guarded([&] { as_trainer(t)->model.gradient_checkpointing = on != 0; });
+}
+
+int ctd_trainer_set_batch(ctd_trainer_t t, const int64_t* ids, const int64_t* targets,
+                          const float* mask, int64_t B, int64_t T) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    if (B <= 0 || T <= 0 || !ids || !targets) throw std::runtime_error("bad batch");
+    std::vector<float> ones;
+    if (!mask) {
+      ones.assign(static_cast<size_t>(B * T), 1.0f);
+      mask = ones.data();
+    }
+    double ms = 0.0;
+    for (int64_t i = 0; i < B * T; ++i) ms += mask[i];
+    tr->ids = Tensor::from_host(ids, {B, T}, DType::kInt64, kHIP0);
+    tr->targets = Tensor::from_host(targets, {B, T}, DType::kInt64, kHIP0);
+    tr->mask = Tensor::from_host(mask, {B, T}, DType::kFloat32, kHIP0);
+    tr->B = B;
+    tr->T = T;
+    tr->mask_sum = static_cast<float>(ms);
+  });
+}
+
+int ctd_trainer_synthetic_batch(ctd_trainer_t t, int64_t B, int64_t T, uint64_t seed,
+                                int32_t masked) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    const uint64_t V = static_cast<uint64_t>(tr->model.config.vocab_size);
+    uint64_t s = seed * 0x2545F4914F6CDD1Dull + 1;
+    std::vector<int64_t> ids(static_cast<size_t>(B * T)), tg(static_cast<size_t>(B * T));
+    std::vector<float> mask(static_cast<size_t>(B * T), 1.0f);
+    for (int64_t b = 0; b < B; ++b) {
+      std::vector<int64_t> row(static_cast<size_t>(T + 1));
+      for (auto& x : row) x = static_cast<int64_t>(splitmix(s) % V);
+      for (int64_t i = 0; i < T; ++i) {
+        ids[static_cast<size_t>(b * T + i)] = row[static_cast<size_t>(i)];
+        tg[static_cast<size_t>(b * T + i)] = row[static_cast<size_t>(i + 1)];
+      }
+      if (masked) {
+        const double u = 0.2 + 0.4 * (static_cast<double>(splitmix(s) >> 11) / 9007199254740992.0);
+        const int64_t cut = static_cast<int64_t>(std::floor(u * static_cast<double>(T)));
+        for (int64_t i = 0; i < cut; ++i) mask[static_cast<size_t>(b * T + i)] = 0.0f;
+      }
+    }
+    if (ctd_trainer_set_batch(t, ids.data(), tg.data(), mask.data(), B, T) != 0)
+      throw std::runtime_error(g_last_error);
+  });
+}
+
+int ctd_trainer_forward_backward(ctd_trainer_t t, int32_t backward, float* loss) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    if (!tr->ids.defined()) throw std::runtime_error("no batch set");
+    Tensor l = tr->model.forward_train_masked(tr->ids, tr->targets, tr->mask);
+    if (backward) l.backward();
+    if (loss) l.copy_to_host(loss);
+  });
+}
+
+int ctd_trainer_hidden(ctd_trainer_t t, float* host, int64_t numel) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    autograd::NoGradGuard ng;
+    Tensor h = tr->model.embed_tokens.forward(tr->ids);
+    for (const auto& layer : tr->model.layers) h = layer.forward_train(h);
+    h = tr->model.norm.forward(h);
+    check_numel(h, numel);
+    h.copy_to_host(host);
+  });
+}
+
+int ctd_trainer_block_step(ctd_trainer_t t, int64_t layer, const float* x, const float* dy,
+                           int64_t B, int64_t T, int32_t checkpoint, float* y_out, float* dx_out) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    if (layer < 0 || layer >= static_cast<int64_t>(tr->model.layers.size()))
+      throw std::runtime_error("layer index out of range");
+    const auto& blk = tr->model.layers[static_cast<size_t>(layer)];
+    const int64_t d = tr->model.config.hidden_size;
+    Tensor xin = Tensor::from_host(x, {B, T, d}, DType::kFloat32, kHIP0);
+    xin.requires_grad_(true);
+    Tensor y = checkpoint ? autograd::checkpoint(
+                                [&blk](const Tensor& v) { return blk.forward_train(v); }, xin)
+                          : blk.forward_train(xin);
+    if (y_out) y.copy_to_host(y_out);
+    Tensor g = Tensor::from_host(dy, {B, T, d}, DType::kFloat32, kHIP0);
+    y.backward(g);
+    if (dx_out) {
+      Tensor dx = xin.grad();
+      if (!dx.storage()) throw std::runtime_error("block_step: input received no gradient");
+      dx.copy_to_host(dx_out);
+    }
+  });
+}
+
+int ctd_trainer_make_optimizer(ctd_trainer_t t, float lr, float weight_decay, float beta1,
+                               float beta2, float eps, int32_t offload, int64_t chunk_elems) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    // Two groups like ctd_train (main.cpp:299-311): decay, then no_decay with wd 0.
+    std::vector<optim::ParamGroup> groups{{tr->named.decay, lr, weight_decay},
+                                          {tr->named.no_decay, lr, 0.0f}};
+    tr->opt = std::make_unique<optim::AdamW>(std::move(groups), beta1, beta2, eps, offload != 0);
+    if (chunk_elems > 0) tr->opt->set_offload_chunk(chunk_elems);
+    tr->opt->ensure_state_initialized();
+  });
+}
+
+int ctd_trainer_clip(ctd_trainer_t t, float max_norm, float* total_norm) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    std::vector<Tensor> ps;
+    for (auto& [n, p] : tr->named.all) ps.push_back(p);
+    const float v = optim::clip_grad_norm_(ps, max_norm);
+    if (total_norm) *total_norm = v;
+  });
+}
+
+int ctd_trainer_opt_step(ctd_trainer_t t) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    if (!tr->opt) throw std::runtime_error("no optimizer");
+    tr->opt->step();
+  });
+}
+
+int ctd_trainer_zero_grad(ctd_trainer_t t) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    for (auto& [n, p] : tr->named.all) p.zero_grad_();
+  });
+}
+
+int ctd_trainer_get_opt_state(ctd_trainer_t t, int64_t i, float* m, float* v, int64_t numel) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    if (!tr->opt) throw std::runtime_error("no optimizer");
+    param_at(tr, i);
+    const auto [gi, pi] = tr->opt_index[static_cast<size_t>(i)];
+    runtime::synchronize();
+    Tensor& tm = tr->opt->m_tensor(gi, pi);
+    Tensor& tv = tr->opt->v_tensor(gi, pi);
+    check_numel(tm, numel);
+    if (m) tm.copy_to_host(m);
+    if (v) tv.copy_to_host(v);
+  });
+}
+
+int ctd_trainer_step_count(ctd_trainer_t t, int64_t* steps) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    *steps = tr->opt ? tr->opt->step_count() : 0;
+  });
+}
+
+int ctd_trainer_train_step(ctd_trainer_t t, float max_norm, ctd_step_times* times) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    if (!tr->opt) throw std::runtime_error("no optimizer");
+    if (!tr->ids.defined()) throw std::runtime_error("no batch set");
+    ember_stream_t cs = runtime::compute_stream();
+    ember_event_t ev[5];
+    for (auto& e : ev) CTD_CHECK(ember_event_create(&e));
+    CTD_CHECK(ember_event_record(ev[0], cs));
+    Tensor loss = tr->model.forward_train_masked(tr->ids, tr->targets, tr->mask);
+    CTD_CHECK(ember_event_record(ev[1], cs));
+    loss.backward();
+    CTD_CHECK(ember_event_record(ev[2], cs));
+    float gn = 0.f;
+    if (max_norm > 0.f) {
+      std::vector<Tensor> ps;
+      for (auto& [n, p] : tr->named.all) ps.push_back(p);
+      gn = optim::clip_grad_norm_(ps, max_norm);
+    }
+    CTD_CHECK(ember_event_record(ev[3], cs));
+    tr->opt->step();
+    CTD_CHECK(ember_event_record(ev[4], cs));
+    for (auto& [n, p] : tr->named.all) p.zero_grad_();
+    float lv = 0.f;
+    loss.copy_to_host(&lv);
+    CTD_CHECK(ember_event_synchronize(ev[4]));
+    if (times) {
+      CTD_CHECK(ember_event_elapsed_ms(&times->forward_ms, ev[0], ev[1]));
+      CTD_CHECK(ember_event_elapsed_ms(&times->backward_ms, ev[1], ev[2]));
+      CTD_CHECK(ember_event_elapsed_ms(&times->clip_ms, ev[2], ev[3]));
+      CTD_CHECK(ember_event_elapsed_ms(&times->optimizer_ms, ev[3], ev[4]));
+      CTD_CHECK(ember_event_elapsed_ms(&times->total_ms, ev[0], ev[4]));
+      times->loss = lv;
+      times->grad_norm = gn;
+      times->mask_sum = tr->mask_sum;
+    }
+    for (auto& e : ev) ember_event_destroy(e);
+  });
+}
+
+int ctd_trainer_synchronize(ctd_trainer_t t) {
+  return guarded([&] {
+    (void)t;
+    runtime::synchronize();
+    CTD_CHECK(ember_stream_synchronize(runtime::d2h_stream()));
+    CTD_CHECK(ember_stream_synchronize(runtime::h2d_stream()));
+  });
+}
+
+int ctd_memory_stats(ctd_memory* out) {
+  return guarded([&] {
+    const DeviceMemoryStats s = device_memory_stats();
+    out->allocated = s.allocated_bytes;
+    out->peak_allocated = s.peak_allocated_bytes;
+    out->reserved = s.reserved_bytes;
+    out->peak_reserved = s.peak_reserved_bytes;
+    out->pinned_host = pinned_host_bytes();
+    size_t fr = 0, tot = 0;
+    CTD_CHECK(ember_mem_get_info(&fr, &tot));
+    out->device_used = tot - fr;
+    out->device_total = tot;
+  });
+}
+
+int ctd_reset_peak_memory(void) {
+  return guarded([] { reset_peak_device_memory(); });
+}
+
+int ctd_gemm_profile_enable(int32_t on) {
+  return guarded([&] { runtime::gemm_profile_enable(on != 0); });
+}
+
+int ctd_gemm_profile_collect(ctd_gemm_profile* out) {
+  return guarded([&] {
+    runtime::gemm_profile_collect(&out->launches, &out->flops, &out->total_ms);
+  });
+}
+
+int ctd_trainer_save(ctd_trainer_t t, const char* path) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    save_safetensors(tr->named.all, path);
+    if (!tr->opt) return;
+    std::vector<std::pair<std::string, Tensor>> items;
+    for (size_t i = 0; i < tr->named.decay_names.size(); ++i) {
+      items.emplace_back("optimizer.m." + tr->named.decay_names[i], tr->opt->m_tensor(0, i));
+      items.emplace_back("optimizer.v." + tr->named.decay_names[i], tr->opt->v_tensor(0, i));
+    }
+    for (size_t i = 0; i < tr->named.no_decay_names.size(); ++i) {
+      items.emplace_back("optimizer.m." + tr->named.no_decay_names[i], tr->opt->m_tensor(1, i));
+      items.emplace_back("optimizer.v." + tr->named.no_decay_names[i], tr->opt->v_tensor(1, i));
+    }
+    runtime::synchronize();
+    const float step_f = static_cast<float>(tr->opt->step_count());
+    items.emplace_back("optimizer.step", Tensor::from_host(&step_f, {1}, DType::kFloat32, kCPU));
+    save_safetensors(items, std::string(path) + ".opt.safetensors");
+  });
+}
+
+int ctd_trainer_load(ctd_trainer_t t, const char* path) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    TensorDict w = load_safetensors(path, kCPU);
+    for (auto& [name, p] : tr->named.all) {
+      auto it = w.find(name);
+      if (it == w.end()) throw std::runtime_error("load: missing " + name);
+      if (it->second.shape() != p.shape()) throw std::runtime_error("load: shape mismatch " + name);
+      CTD_CHECK(ember_memcpy_async(p.data_ptr(), it->second.data_ptr(), p.nbytes(), 0,
+                                   runtime::compute_stream()));
+    }
+    runtime::synchronize();
+    if (!tr->opt) return;
+    TensorDict o = load_safetensors(std::string(path) + ".opt.safetensors", kCPU);
+    tr->opt->ensure_state_initialized();
+    auto load_into = [&](Tensor& dst, const std::string& key) {
+      auto it = o.find(key);
+      if (it == o.end()) throw std::runtime_error("resume: missing " + key);
+      if (it->second.shape() != dst.shape()) throw std::runtime_error("resume: shape " + key);
+      // Offloaded state is host memory: a plain copy (the reference copied
+      // device-to-device here, tools/ctd_train/main.cpp:236-243).
+      if (dst.device().is_hip()) {
+        CTD_CHECK(ember_memcpy_async(dst.data_ptr(), it->second.data_ptr(), dst.nbytes(), 0,
+                                     runtime::compute_stream()));
+        runtime::synchronize();
+      } else {
+        std::memcpy(dst.data_ptr(), it->second.data_ptr(), dst.nbytes());
+      }
+    };
+    for (size_t i = 0; i < tr->named.decay_names.size(); ++i) {
+      load_into(tr->opt->m_tensor(0, i), "optimizer.m." + tr->named.decay_names[i]);
+      load_into(tr->opt->v_tensor(0, i), "optimizer.v." + tr->named.decay_names[i]);
+    }
+    for (size_t i = 0; i < tr->named.no_decay_names.size(); ++i) {
+      load_into(tr->opt->m_tensor(1, i), "optimizer.m." + tr->named.no_decay_names[i]);
+      load_into(tr->opt->v_tensor(1, i), "optimizer.v." + tr->named.no_decay_names[i]);
+    }
+    auto it = o.find("optimizer.step");
+    if (it == o.end()) throw std::runtime_error("resume: missing optimizer.step");
+    float step_f = 0.f;
+    std::memcpy(&step_f, it->second.data_ptr(), sizeof(float));
+    tr->opt->set_step_count(static_cast<int64_t>(step_f));
+  });
+}
+
+}  // extern "C"

@@ -45,7 +45,8 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_vec(const float* __restr
   if (live)
     for (int64_t c = sub; c < nc; c += LPR) {
       const f32x4 v = xr[c];
-      ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ss = fmaf(v[e], v[e], ss);
     }
   ss = group_sum(ss, LPR);
   if (!live) return;
@@ -72,7 +73,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_scalar(const float* __re
   const int64_t row = blockIdx.x;
   const float* xr = x + row * H;
   float ss = 0.f;
-  for (int64_t i = threadIdx.x; i < H; i += kThreads) ss += xr[i] * xr[i];
+  for (int64_t i = threadIdx.x; i < H; i += kThreads) ss = fmaf(xr[i], xr[i], ss);
   ss = block_sum(ss, red);
   const float s = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
   if (rstd && threadIdx.x == 0) rstd[row] = s;
@@ -112,7 +113,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
           const f32x4 v = xr[ci], g = gr[ci], ww = wv[ci];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            ss += v[e] * v[e];
+            ss = fmaf(v[e], v[e], ss);
             c += g[e] * ww[e] * v[e];
           }
         }
@@ -120,7 +121,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
     ss = group_sum(ss, LPR);
     c = group_sum(c, LPR);
     if (!live) continue;
-    const float s = rstd ? rstd[row] : 1.0f / sqrtf(ss * invH + eps);
+    const float s = rstd ? rstd[row] : 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
     const float k = s * s * c * invH;
 #pragma unroll
     for (int j = 0; j < MAXC; ++j) {
@@ -168,12 +169,12 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_scalar(
     const float* gr = dy + row * H;
     float ss = 0.f, c = 0.f;
     for (int64_t i = threadIdx.x; i < H; i += kThreads) {
-      ss += xr[i] * xr[i];
+      ss = fmaf(xr[i], xr[i], ss);
       c += gr[i] * w[i] * xr[i];
     }
     ss = block_sum(ss, red);
     c = block_sum(c, red);
-    const float s = rstd ? rstd[row] : 1.0f / sqrtf(ss * invH + eps);
+    const float s = rstd ? rstd[row] : 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
     for (int64_t i = threadIdx.x; i < H; i += kThreads) {
       if (dx) dx[row * H + i] = s * (gr[i] * w[i] - xr[i] * s * s * c * invH);
       if (dw_part) dw_part[blockIdx.x * H + i] += gr[i] * xr[i] * s;

@@ -7,6 +7,11 @@
 // clip norm is reproducible.
 #include "common.h"
 
+// No FMA contraction in this file: the float4 and scalar paths (taken for
+// chunks that start off a 16-byte boundary) must round identically, so an
+// offloaded, chunked update equals the on-device one bit for bit.
+#pragma clang fp contract(off)
+
 using namespace ember;
 
 namespace {

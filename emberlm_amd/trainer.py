@@ -1,0 +1,278 @@
+"""ctypes front end of include/ctd_capi.h (libctd.so): the C++ Model/AdamW layer.
+
+Used by bench.py and the model-level parity tests.  The library is loaded from
+emberlm_amd/lib/ and there is no fallback: a missing build raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+import os
+
+import numpy as np
+
+from . import capi
+
+LIB_PATH = os.path.join(capi.LIB_DIR, "libctd.so")
+
+
+class ModelConfig(C.Structure):
+    _fields_ = [
+        ("vocab_size", C.c_int32), ("hidden_size", C.c_int32), ("intermediate_size", C.c_int32),
+        ("num_layers", C.c_int32), ("num_heads", C.c_int32), ("num_kv_heads", C.c_int32),
+        ("head_dim", C.c_int32), ("qk_norm", C.c_int32), ("rms_norm_eps", C.c_float),
+        ("rope_theta", C.c_float), ("rope_factor", C.c_float),
+        ("rope_low_freq_factor", C.c_float), ("rope_high_freq_factor", C.c_float),
+        ("rope_original_max_pos", C.c_int32),
+    ]
+
+
+class StepTimes(C.Structure):
+    _fields_ = [(n, C.c_float) for n in ("forward_ms", "backward_ms", "clip_ms", "optimizer_ms",
+                                         "total_ms", "loss", "grad_norm", "mask_sum")]
+
+
+class Memory(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("allocated", "peak_allocated", "reserved",
+                                          "peak_reserved", "pinned_host", "device_used",
+                                          "device_total")]
+
+
+class GemmProfile(C.Structure):
+    _fields_ = [("launches", C.c_int64), ("flops", C.c_double), ("total_ms", C.c_double)]
+
+
+_lib = None
+vp, i64, i32, f32, u64 = C.c_void_p, C.c_int64, C.c_int32, C.c_float, C.c_uint64
+fptr = C.POINTER(C.c_float)
+lptr = C.POINTER(C.c_int64)
+
+_SIGS = {
+    "ctd_last_error": (C.c_char_p, []),
+    "ctd_preset_config": (i32, [C.c_char_p, C.POINTER(ModelConfig)]),
+    "ctd_trainer_create": (i32, [C.POINTER(ModelConfig), u64, f32, f32, C.POINTER(vp)]),
+    "ctd_trainer_destroy": (i32, [vp]),
+    "ctd_trainer_num_params": (i32, [vp, lptr]),
+    "ctd_trainer_param_info": (i32, [vp, i64, C.c_char_p, C.c_size_t, lptr, C.POINTER(i32)]),
+    "ctd_trainer_set_param": (i32, [vp, i64, fptr, i64]),
+    "ctd_trainer_get_param": (i32, [vp, i64, fptr, i64]),
+    "ctd_trainer_get_grad": (i32, [vp, i64, fptr, i64]),
+    "ctd_trainer_set_checkpointing": (i32, [vp, i32]),
+    "ctd_trainer_set_batch": (i32, [vp, lptr, lptr, fptr, i64, i64]),
+    "ctd_trainer_synthetic_batch": (i32, [vp, i64, i64, u64, i32]),
+    "ctd_trainer_forward_backward": (i32, [vp, i32, fptr]),
+    "ctd_trainer_hidden": (i32, [vp, fptr, i64]),
+    "ctd_trainer_block_step": (i32, [vp, i64, fptr, fptr, i64, i64, i32, fptr, fptr]),
+    "ctd_trainer_make_optimizer": (i32, [vp, f32, f32, f32, f32, f32, i32, i64]),
+    "ctd_trainer_clip": (i32, [vp, f32, fptr]),
+    "ctd_trainer_opt_step": (i32, [vp]),
+    "ctd_trainer_zero_grad": (i32, [vp]),
+    "ctd_trainer_get_opt_state": (i32, [vp, i64, fptr, fptr, i64]),
+    "ctd_trainer_step_count": (i32, [vp, lptr]),
+    "ctd_trainer_train_step": (i32, [vp, f32, C.POINTER(StepTimes)]),
+    "ctd_trainer_synchronize": (i32, [vp]),
+    "ctd_memory_stats": (i32, [C.POINTER(Memory)]),
+    "ctd_reset_peak_memory": (i32, []),
+    "ctd_gemm_profile_enable": (i32, [i32]),
+    "ctd_gemm_profile_collect": (i32, [C.POINTER(GemmProfile)]),
+    "ctd_trainer_save": (i32, [vp, C.c_char_p]),
+    "ctd_trainer_load": (i32, [vp, C.c_char_p]),
+}
+
+
+class CtdError(RuntimeError):
+    pass
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        capi.lib()  # the kernel library first (libctd links against it)
+        if not os.path.exists(LIB_PATH):
+            raise CtdError(f"{LIB_PATH} is missing: run `python -m emberlm_amd.build` first")
+        l = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(l, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = l
+    return _lib
+
+
+def _ck(rc, what):
+    if rc != 0:
+        raise CtdError(f"{what}: {lib().ctd_last_error().decode()} (status {rc})")
+
+
+def _f32(a):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return a, a.ctypes.data_as(fptr)
+
+
+def preset(name: str) -> ModelConfig:
+    c = ModelConfig()
+    _ck(lib().ctd_preset_config(name.encode(), C.byref(c)), "preset")
+    return c
+
+
+def make_config(**kw) -> ModelConfig:
+    c = ModelConfig()
+    d = dict(qk_norm=0, rms_norm_eps=1e-5, rope_theta=1e4, rope_factor=0.0,
+             rope_low_freq_factor=1.0, rope_high_freq_factor=4.0, rope_original_max_pos=8192)
+    d.update(kw)
+    for k, v in d.items():
+        setattr(c, k, v)
+    return c
+
+
+def memory() -> Memory:
+    m = Memory()
+    _ck(lib().ctd_memory_stats(C.byref(m)), "memory")
+    return m
+
+
+def reset_peak_memory():
+    _ck(lib().ctd_reset_peak_memory(), "reset_peak_memory")
+
+
+def gemm_profile(enable=None):
+    if enable is not None:
+        _ck(lib().ctd_gemm_profile_enable(int(enable)), "gemm_profile_enable")
+        return None
+    g = GemmProfile()
+    _ck(lib().ctd_gemm_profile_collect(C.byref(g)), "gemm_profile_collect")
+    return g
+
+
+class Trainer:
+    """Model + AdamW on the GPU (C++ layer), seeded synthetic weights."""
+
+    def __init__(self, cfg: ModelConfig, seed=0, init_std=0.02, norm_value=1.0):
+        self.cfg = cfg
+        h = vp()
+        _ck(lib().ctd_trainer_create(C.byref(cfg), seed, init_std,
+                                     float("nan") if norm_value is None else norm_value,
+                                     C.byref(h)), "create")
+        self.h = h
+        n = C.c_int64()
+        _ck(lib().ctd_trainer_num_params(h, C.byref(n)), "num_params")
+        self.names, self.numels, self.decay = [], [], []
+        buf = C.create_string_buffer(256)
+        for i in range(n.value):
+            ne, dc = C.c_int64(), C.c_int32()
+            _ck(lib().ctd_trainer_param_info(h, i, buf, 256, C.byref(ne), C.byref(dc)), "info")
+            self.names.append(buf.value.decode())
+            self.numels.append(ne.value)
+            self.decay.append(bool(dc.value))
+
+    def close(self):
+        if self.h:
+            _ck(lib().ctd_trainer_destroy(self.h), "destroy")
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_param(self, i, arr):
+        a, p = _f32(arr)
+        _ck(lib().ctd_trainer_set_param(self.h, i, p, a.size), "set_param")
+
+    def get_param(self, i):
+        out = np.empty(self.numels[i], np.float32)
+        _ck(lib().ctd_trainer_get_param(self.h, i, out.ctypes.data_as(fptr), out.size), "get_param")
+        return out
+
+    def get_grad(self, i):
+        out = np.empty(self.numels[i], np.float32)
+        rc = lib().ctd_trainer_get_grad(self.h, i, out.ctypes.data_as(fptr), out.size)
+        if rc == -1:
+            return None
+        _ck(rc, "get_grad")
+        return out
+
+    def set_checkpointing(self, on):
+        _ck(lib().ctd_trainer_set_checkpointing(self.h, int(on)), "set_checkpointing")
+
+    def set_batch(self, ids, targets, mask=None):
+        ids = np.ascontiguousarray(ids, dtype=np.int64)
+        tg = np.ascontiguousarray(targets, dtype=np.int64)
+        B, T = ids.shape
+        mp = None
+        if mask is not None:
+            m, mp = _f32(mask)
+            self._mask_keep = m
+        _ck(lib().ctd_trainer_set_batch(self.h, ids.ctypes.data_as(lptr), tg.ctypes.data_as(lptr),
+                                        mp, B, T), "set_batch")
+
+    def synthetic_batch(self, B, T, seed=0, masked=True):
+        _ck(lib().ctd_trainer_synthetic_batch(self.h, B, T, seed, int(masked)), "synthetic_batch")
+
+    def forward_backward(self, backward=True):
+        loss = C.c_float()
+        _ck(lib().ctd_trainer_forward_backward(self.h, int(backward), C.byref(loss)), "fwd/bwd")
+        return loss.value
+
+    def block_step(self, layer, x, dy, checkpoint=False):
+        x, px = _f32(x)
+        dy, pdy = _f32(dy)
+        B, T, d = x.shape
+        y = np.empty_like(x)
+        dx = np.empty_like(x)
+        _ck(lib().ctd_trainer_block_step(self.h, layer, px, pdy, B, T, int(checkpoint),
+                                         y.ctypes.data_as(fptr), dx.ctypes.data_as(fptr)),
+            "block_step")
+        return y, dx
+
+    def make_optimizer(self, lr=1e-4, weight_decay=0.1, beta1=0.9, beta2=0.95, eps=1e-8,
+                       offload=False, chunk_elems=0):
+        _ck(lib().ctd_trainer_make_optimizer(self.h, lr, weight_decay, beta1, beta2, eps,
+                                             int(offload), chunk_elems), "make_optimizer")
+
+    def clip(self, max_norm):
+        n = C.c_float()
+        _ck(lib().ctd_trainer_clip(self.h, max_norm, C.byref(n)), "clip")
+        return n.value
+
+    def opt_step(self):
+        _ck(lib().ctd_trainer_opt_step(self.h), "opt_step")
+
+    def zero_grad(self):
+        _ck(lib().ctd_trainer_zero_grad(self.h), "zero_grad")
+
+    def opt_state(self, i):
+        m = np.empty(self.numels[i], np.float32)
+        v = np.empty(self.numels[i], np.float32)
+        _ck(lib().ctd_trainer_get_opt_state(self.h, i, m.ctypes.data_as(fptr),
+                                            v.ctypes.data_as(fptr), m.size), "opt_state")
+        return m, v
+
+    def train_step(self, max_norm=1.0) -> StepTimes:
+        t = StepTimes()
+        _ck(lib().ctd_trainer_train_step(self.h, max_norm, C.byref(t)), "train_step")
+        return t
+
+    def synchronize(self):
+        _ck(lib().ctd_trainer_synchronize(self.h), "synchronize")
+
+    def save(self, path):
+        _ck(lib().ctd_trainer_save(self.h, str(path).encode()), "save")
+
+    def load(self, path):
+        _ck(lib().ctd_trainer_load(self.h, str(path).encode()), "load")
+
+    def num_params(self):
+        return len(self.names)
+
+
+def param_count(cfg: ModelConfig) -> int:
+    d, I, H, Hk, D, V, L = (cfg.hidden_size, cfg.intermediate_size, cfg.num_heads,
+                            cfg.num_kv_heads, cfg.head_dim, cfg.vocab_size, cfg.num_layers)
+    per = 2 * d + 2 * H * D * d + 2 * Hk * D * d + 3 * I * d + (2 * D if cfg.qk_norm else 0)
+    return V * d + d + L * per
+
+
+__all__ = ["ModelConfig", "Trainer", "preset", "make_config", "memory", "reset_peak_memory",
+           "gemm_profile", "param_count", "StepTimes", "math"]

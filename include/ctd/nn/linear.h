@@ -1,0 +1,26 @@
+#pragma once
+// Linear layer without bias: y = x W^T (mirrors nn/linear.h of the reference).
+#include <stdexcept>
+
+#include "ctd/ops/matmul.h"
+#include "ctd/tensor.h"
+
+namespace ctd::nn {
+
+struct Linear {
+  Tensor weight;  // [out, in]
+
+  Tensor forward(const Tensor& x) const {
+    const int64_t in = weight.shape()[1];
+    const int64_t out = weight.shape()[0];
+    const auto& sh = x.shape();
+    if (sh.back() != in) throw std::runtime_error("Linear: in_features mismatch");
+    const int64_t leading = x.numel() / in;
+    Tensor y2d = ops::matmul(x.reshape({leading, in}), weight, /*transa=*/false, /*transb=*/true);
+    std::vector<int64_t> out_shape(sh.begin(), sh.end());
+    out_shape.back() = out;
+    return y2d.reshape(out_shape);
+  }
+};
+
+}  // namespace ctd::nn

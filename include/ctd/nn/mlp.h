@@ -1,0 +1,22 @@
+#pragma once
+// SwiGLU feed-forward: y = down(silu(gate(x)) * up(x)) (mirrors nn/mlp.h of the
+// reference); silu and the product run as one fused op.
+#include "ctd/nn/linear.h"
+#include "ctd/ops/elementwise.h"
+#include "ctd/tensor.h"
+
+namespace ctd::nn {
+
+struct MLP {
+  Linear gate_proj;
+  Linear up_proj;
+  Linear down_proj;
+
+  Tensor forward(const Tensor& x) const {
+    Tensor g = gate_proj.forward(x);
+    Tensor u = up_proj.forward(x);
+    return down_proj.forward(ops::swiglu(g, u));
+  }
+};
+
+}  // namespace ctd::nn

@@ -1,0 +1,38 @@
+#pragma once
+// Device runtime glue over the C ABI (include/ember_hip.h): error checking,
+// the compute stream every op is enqueued on, and the copy streams used by
+// the offloaded optimizer.  Replaces the reference's cuda_utils.h /
+// cublas_utils.h (CTD_CUDA_CHECK*, the call_once cuBLAS handle).
+
+#include <string>
+
+#include "ember_hip.h"
+
+namespace ctd::runtime {
+
+// Throws std::runtime_error("<what>: <status text>") when status != 0.
+void check(int status, const char* what);
+
+// Process-wide streams, created on first use at the default priority.
+ember_stream_t compute_stream();
+ember_stream_t h2d_stream();
+ember_stream_t d2h_stream();
+
+// Blocks until all work on the compute stream is done.
+void synchronize();
+
+// Whether a HIP device is present (without creating a context on failure).
+bool device_available();
+
+// GEMM timing for the roofline figure: while enabled, the ops layer brackets
+// every GEMM launch with HIP events on the compute stream.
+void gemm_profile_enable(bool on);
+bool gemm_profiling();
+void* gemm_profile_begin();                     // null when disabled
+void gemm_profile_end(void* begin, double flops);
+// Resolves the recorded events (synchronises) and resets the record.
+void gemm_profile_collect(int64_t* launches, double* flops, double* total_ms);
+
+}  // namespace ctd::runtime
+
+#define CTD_CHECK(expr) ::ctd::runtime::check((expr), #expr)

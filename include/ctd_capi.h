@@ -1,0 +1,123 @@
+/*
+ * ctd_capi.h -- C entry points of the C++ training layer (libctd.so).
+ *
+ * A thin handle-based wrapper over ctd::nn::Model + ctd::optim::AdamW that
+ * runs the ctd_train step (tools/ctd_train/main.cpp:348-398 of the reference:
+ * forward_train_masked -> backward -> clip_grad_norm_ -> AdamW::step ->
+ * zero_grad) for harnesses that are not C++ (the Python bench and parity
+ * tests).  Every function returns 0 or a negative status; after a failure
+ * ctd_last_error() holds the exception text of the C++ layer.
+ */
+#ifndef CTD_CAPI_H
+#define CTD_CAPI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CTD_EXCEPTION (-10)
+
+typedef struct ctd_model_config {
+  int32_t vocab_size, hidden_size, intermediate_size, num_layers;
+  int32_t num_heads, num_kv_heads, head_dim, qk_norm;
+  float rms_norm_eps, rope_theta;
+  float rope_factor, rope_low_freq_factor, rope_high_freq_factor;
+  int32_t rope_original_max_pos;
+} ctd_model_config;
+
+typedef struct ctd_step_times {
+  float forward_ms, backward_ms, clip_ms, optimizer_ms, total_ms;
+  float loss, grad_norm, mask_sum;
+} ctd_step_times;
+
+typedef struct ctd_memory {
+  uint64_t allocated, peak_allocated, reserved, peak_reserved, pinned_host;
+  uint64_t device_used, device_total; /* hipMemGetInfo: total - free, total */
+} ctd_memory;
+
+typedef struct ctd_gemm_profile {
+  int64_t launches;
+  double flops;     /* algorithmic 2*M*N*K summed over launches */
+  double total_ms;  /* summed HIP-event durations of those launches */
+} ctd_gemm_profile;
+
+typedef void* ctd_trainer_t;
+
+const char* ctd_last_error(void);
+
+/* Presets by name: "smollm2-135m", "smollm2-360m", "qwen3-0.6b", "qwen3-1.7b",
+ * "llama3.2-1b" (include/ctd/nn/model.h:39-124 of the reference). */
+int ctd_preset_config(const char* name, ctd_model_config* out);
+
+/* Builds a model with seeded synthetic weights on the device: every matrix
+ * (and the embedding) ~ N(0, init_std); norm weights = norm_value, or
+ * ~ N(0, init_std) when norm_value is NaN.  The parameter list follows
+ * Model::collect_parameters. */
+int ctd_trainer_create(const ctd_model_config* cfg, uint64_t seed, float init_std,
+                       float norm_value, ctd_trainer_t* out);
+int ctd_trainer_destroy(ctd_trainer_t t);
+
+int ctd_trainer_num_params(ctd_trainer_t t, int64_t* n);
+/* name (NUL-terminated, truncated to cap), numel, decay group (1) or not (0). */
+int ctd_trainer_param_info(ctd_trainer_t t, int64_t i, char* name, size_t cap, int64_t* numel,
+                           int32_t* decay);
+int ctd_trainer_set_param(ctd_trainer_t t, int64_t i, const float* host, int64_t numel);
+int ctd_trainer_get_param(ctd_trainer_t t, int64_t i, float* host, int64_t numel);
+/* Copies the accumulated gradient; returns -1 if the parameter has none. */
+int ctd_trainer_get_grad(ctd_trainer_t t, int64_t i, float* host, int64_t numel);
+
+int ctd_trainer_set_checkpointing(ctd_trainer_t t, int32_t on);
+/* Batch: ids/targets int64 [B,T], mask fp32 [B,T] (NULL = all ones), host memory. */
+int ctd_trainer_set_batch(ctd_trainer_t t, const int64_t* ids, const int64_t* targets,
+                          const float* mask, int64_t B, int64_t T);
+/* Synthetic batch generated on the host: ids uniform in [0,V) from `seed`,
+ * targets = ids shifted by one, and (masked != 0) a zero prefix of
+ * 20-60% of each row (assistant-turn masking). */
+int ctd_trainer_synthetic_batch(ctd_trainer_t t, int64_t B, int64_t T, uint64_t seed,
+                                int32_t masked);
+
+/* loss = Model::forward_train_masked(...); backward too when `backward`. */
+int ctd_trainer_forward_backward(ctd_trainer_t t, int32_t backward, float* loss);
+/* Final hidden states before the LM head for the current batch, [B*T*d] floats. */
+int ctd_trainer_hidden(ctd_trainer_t t, float* host, int64_t numel);
+
+/* One decoder block in isolation (TransformerBlock::forward_train): x and dy
+ * are host [B,T,d]; y = block(x) (wrapped in autograd::checkpoint when
+ * `checkpoint`), then y.backward(dy); y_out and dx_out (host, may be NULL)
+ * receive y and dL/dx, and the block's parameter grads accumulate. */
+int ctd_trainer_block_step(ctd_trainer_t t, int64_t layer, const float* x, const float* dy,
+                           int64_t B, int64_t T, int32_t checkpoint, float* y_out, float* dx_out);
+
+int ctd_trainer_make_optimizer(ctd_trainer_t t, float lr, float weight_decay, float beta1,
+                               float beta2, float eps, int32_t offload, int64_t chunk_elems);
+int ctd_trainer_clip(ctd_trainer_t t, float max_norm, float* total_norm);
+int ctd_trainer_opt_step(ctd_trainer_t t);
+int ctd_trainer_zero_grad(ctd_trainer_t t);
+int ctd_trainer_get_opt_state(ctd_trainer_t t, int64_t i, float* m, float* v, int64_t numel);
+int ctd_trainer_step_count(ctd_trainer_t t, int64_t* steps);
+
+/* One full training step (forward, backward, clip to max_norm when > 0,
+ * optimizer step, zero_grad) with HIP-event phase times. */
+int ctd_trainer_train_step(ctd_trainer_t t, float max_norm, ctd_step_times* times);
+
+int ctd_trainer_synchronize(ctd_trainer_t t);
+int ctd_memory_stats(ctd_memory* out);
+int ctd_reset_peak_memory(void);
+
+/* GEMM timing: while enabled, every ember_gemm_f32 launched by the ops layer
+ * is bracketed by HIP events on the compute stream; collect resolves them. */
+int ctd_gemm_profile_enable(int32_t on);
+int ctd_gemm_profile_collect(ctd_gemm_profile* out);
+
+/* Weights (HF names) to `path` and optimizer state to `path`.opt.safetensors
+ * (tools/ctd_train/main.cpp:208-234 layout); load restores both. */
+int ctd_trainer_save(ctd_trainer_t t, const char* path);
+int ctd_trainer_load(ctd_trainer_t t, const char* path);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CTD_CAPI_H */

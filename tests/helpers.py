@@ -6,20 +6,22 @@ import numpy as np
 from emberlm_amd import capi
 
 
-def assert_close(got, ref, rtol=1e-4, name=""):
-    """|a-b| <= rtol*|b| + rtol*max|b| elementwise, and relative L2 <= rtol."""
+def assert_close(got, ref, rtol=1e-4, name="", atol=0.0):
+    """|a-b| <= rtol*|b| + rtol*max|b| + atol elementwise, and relative L2 <= rtol
+    (the L2 check is skipped when the reference is all zero)."""
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     assert got.shape == ref.shape, (name, got.shape, ref.shape)
     scale = float(np.max(np.abs(ref))) if ref.size else 0.0
     err = np.abs(got - ref)
-    bound = rtol * np.abs(ref) + rtol * scale
+    bound = rtol * np.abs(ref) + rtol * scale + atol
     bad = err > bound
     assert not bad.any(), (f"{name}: {int(bad.sum())} of {ref.size} outside tolerance; "
                            f"max err {err.max():.3e} at {np.unravel_index(err.argmax(), err.shape)}, "
                            f"scale {scale:.3e}")
-    l2 = np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-300)
-    assert l2 <= rtol, f"{name}: relative L2 {l2:.3e} > {rtol}"
+    if scale > 0:
+        l2 = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+        assert l2 <= rtol, f"{name}: relative L2 {l2:.3e} > {rtol}"
 
 
 def dev(a, dtype=None):

@@ -122,10 +122,13 @@ def test_rmsnorm_fwd_bwd_vs_oracle(rows, H, eps):
     dx_ref, dw_ref = O.rmsnorm_bwd(dy, x, w, eps)
     assert_close(host(DX), dx_ref, name="rms dx")
     assert_close(host(DW), dw_ref, name="rms dw")
-    # recompute rstd path and bitwise determinism
+    # bitwise determinism, and the recomputed-rstd path gives the same bits as the
+    # saved-rstd path (forward and backward accumulate sum(x^2) in the same order)
     DX2, DW2 = empty((rows, H)), empty((H,))
+    call("ember_rmsnorm_bwd", p(DY), p(X), p(W), p(RS), p(DX2), p(DW2), rows, H, eps, p(WS), ws_n, None)
+    assert torch.equal(DW, DW2) and torch.equal(DX, DX2)
     call("ember_rmsnorm_bwd", p(DY), p(X), p(W), None, p(DX2), p(DW2), rows, H, eps, p(WS), ws_n, None)
-    assert torch.equal(DW, DW2)
+    assert torch.equal(DW, DW2) and torch.equal(DX, DX2)
     Y2 = empty((rows, H))
     call("ember_rmsnorm_fwd", p(X), p(W), p(Y2), None, rows, H, eps, None)
     assert torch.equal(Y, Y2)
@@ -289,9 +292,14 @@ def test_adamw_vs_oracle():
     call("ember_adamw", p(P), p(G), p(Mt), p(Vt), n, lr, b1, b2, eps, wd, float(bc1), float(bc2), None)
     rp, rm, rv = O.adamw(pp, g, m, v, np.float32(lr), np.float32(b1), np.float32(b2), np.float32(eps),
                          np.float32(wd), bc1, bc2)
+    # Per element: rtol 1e-5 plus an absolute floor of 1e-6 * max|ref| for entries that
+    # cancel to ~0 (m = b1*m + (1-b1)*g); the reference's own KAT uses 1e-5 absolute
+    # on p ~ 1 (tests/test_autograd.cpp:560).
     for got, ref, name in [(P, rp, "p"), (Mt, rm, "m"), (Vt, rv, "v")]:
         err = np.abs(host(got) - ref)
-        assert (err <= 1e-5 * np.abs(ref) + 1e-12).all(), name
+        bound = 1e-5 * np.abs(ref) + 1e-6 * np.abs(ref).max()
+        i = int(np.argmax(err - bound))
+        assert (err <= bound).all(), (name, i, float(host(got)[i]), float(ref[i]), float(err[i]))
 
 
 def test_sumsq_multi():
@@ -341,8 +349,10 @@ def test_attention_fwd_bwd_vs_oracle(B, T, H, Hk, D):
     call("ember_attn_bwd", p(Q), p(K), p(Vv), p(Ot), p(L), p(DO), p(DQ), p(DK), p(DV), B, T, H, Hk,
          D, scale, p(WS), wsb, None)
     dq_ref, dk_ref, dv_ref = O.attention_bwd(q, k, v, do, scale)
-    assert_close(host(DQ), dq_ref, name="dq")
-    assert_close(host(DK), dk_ref, name="dk")
+    # at T = 1 dq and dk are exactly 0 in exact arithmetic (softmax of one score);
+    # fp32 leaves rounding residue of order 1e-7, hence the absolute floor
+    assert_close(host(DQ), dq_ref, name="dq", atol=1e-5)
+    assert_close(host(DK), dk_ref, name="dk", atol=1e-5)
     assert_close(host(DV), dv_ref, name="dv")
     # bitwise run-to-run determinism (forward and backward)
     O2, L2 = empty((B, T, H, D)), empty((B, H, T))

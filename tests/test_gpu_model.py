@@ -1,0 +1,238 @@
+"""Model-level GPU parity: the C++ Tensor/autograd/Module/AdamW layer (libctd.so)
+against the CPU oracle, plus the checkpointing and offload invariants.
+
+- c1: one SmolLM2-135M-shaped decoder block, B1 T256, seed 0,
+  weights ~N(0,0.02), x and dy ~N(0,1): forward/backward vs the oracle, then the
+  same with gradient checkpointing (bitwise equal), then one AdamW step with m/v
+  offloaded (lr 1e-4, betas 0.9/0.95, eps 1e-8, wd 0.1 on 2-D weights).
+- tiny full models (embedding + blocks + tied head + masked CE) vs the oracle's
+  loss and every gradient, with QK-Norm and with llama3 RoPE scaling.
+- c2 full SmolLM2-135M step at B4 T512: checkpoint on/off bitwise identical.
+Tolerance: |a-b| <= 1e-4|b| + 1e-4 max|b| and relative L2 <= 1e-4; AdamW 1e-5.
+"""
+import json
+import math
+import struct
+
+import numpy as np
+import pytest
+
+import oracle as O
+from tests.helpers import assert_close
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+from emberlm_amd import trainer as TR  # noqa: E402
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+BLOCK_ORDER = ["input_layernorm", "q_proj", "k_proj", "v_proj", "o_proj", "q_norm", "k_norm",
+               "post_attention_layernorm", "gate_proj", "up_proj", "down_proj"]
+
+
+def oracle_cfg(c: TR.ModelConfig):
+    return O.make_cfg(vocab=c.vocab_size, hidden=c.hidden_size, inter=c.intermediate_size,
+                      layers=c.num_layers, heads=c.num_heads, kv_heads=c.num_kv_heads,
+                      head_dim=c.head_dim, eps=float(np.float32(c.rms_norm_eps)),
+                      theta=c.rope_theta, rope_factor=c.rope_factor,
+                      rope_low_freq=c.rope_low_freq_factor, rope_high_freq=c.rope_high_freq_factor,
+                      rope_orig_max_pos=c.rope_original_max_pos, qk_norm=c.qk_norm)
+
+
+def shapes(c):
+    d, I, H, Hk, D = c.hidden_size, c.intermediate_size, c.num_heads, c.num_kv_heads, c.head_dim
+    return {"input_layernorm": (d,), "q_proj": (H * D, d), "k_proj": (Hk * D, d),
+            "v_proj": (Hk * D, d), "o_proj": (d, H * D), "q_norm": (D,), "k_norm": (D,),
+            "post_attention_layernorm": (d,), "gate_proj": (I, d), "up_proj": (I, d),
+            "down_proj": (d, I)}
+
+
+def layer_params(tr, c, layer):
+    sh = shapes(c)
+    out = {}
+    for i, name in enumerate(tr.names):
+        pre = f"model.layers.{layer}."
+        if name.startswith(pre):
+            key = name[len(pre):].split(".")[-2]
+            out[key] = (i, tr.get_param(i).reshape(sh[key]))
+    return out
+
+
+C1 = dict(vocab_size=256, hidden_size=576, intermediate_size=1536, num_layers=1, num_heads=9,
+          num_kv_heads=3, head_dim=64, rms_norm_eps=1e-5, rope_theta=1e5)
+
+
+def test_c1_block_fwd_bwd_checkpoint_and_offloaded_adamw():
+    c = TR.make_config(**C1)
+    tr = TR.Trainer(c, seed=0, init_std=0.02, norm_value=None)  # all weights ~N(0,0.02)
+    rng = np.random.default_rng(0)
+    B, T, d = 1, 256, 576
+    x = rng.standard_normal((B, T, d)).astype(np.float32)
+    dy = rng.standard_normal((B, T, d)).astype(np.float32)
+    lp = layer_params(tr, c, 0)
+    w = {k: v[1] for k, v in lp.items()}
+    oc = oracle_cfg(c)
+
+    y, dx = tr.block_step(0, x, dy, checkpoint=False)
+    grads_off = {k: tr.get_grad(i).reshape(w[k].shape) for k, (i, _) in lp.items()}
+    assert_close(y, O.block_fwd(oc, w, x), name="c1 y")
+    dx_ref, dw_ref = O.block_bwd(oc, w, x, dy)
+    assert_close(dx, dx_ref, name="c1 dx")
+    for k in w:
+        assert_close(grads_off[k], dw_ref[k], name=f"c1 d{k}")
+
+    # Gradient checkpointing: recomputed activations and every gradient bitwise equal.
+    tr.zero_grad()
+    y2, dx2 = tr.block_step(0, x, dy, checkpoint=True)
+    assert np.array_equal(y, y2) and np.array_equal(dx, dx2)
+    for k, (i, _) in lp.items():
+        assert np.array_equal(tr.get_grad(i).reshape(w[k].shape), grads_off[k]), k
+
+    # One AdamW step with m/v offloaded to pinned host memory, checked per element
+    # against the oracle update from the same gradients.
+    tr.make_optimizer(lr=1e-4, weight_decay=0.1, beta1=0.9, beta2=0.95, eps=1e-8, offload=True)
+    tr.opt_step()
+    bc1, bc2 = np.float32(1 - np.float32(0.9)), np.float32(1 - np.float32(0.95))
+    for k, (i, p0) in lp.items():
+        g = grads_off[k]
+        wd = 0.1 if tr.decay[i] else 0.0
+        rp, rm, rv = O.adamw(p0.reshape(-1), g.reshape(-1), np.zeros(g.size), np.zeros(g.size),
+                             np.float32(1e-4), np.float32(0.9), np.float32(0.95), np.float32(1e-8),
+                             np.float32(wd), bc1, bc2)
+        m, v = tr.opt_state(i)
+        for got, ref, nm in [(tr.get_param(i), rp, "p"), (m, rm, "m"), (v, rv, "v")]:
+            err = np.abs(got - ref)
+            bound = 1e-5 * np.abs(ref) + 1e-6 * np.abs(ref).max()
+            assert (err <= bound).all(), (k, nm, float(err.max()))
+    tr.close()
+
+
+def tiny_cfg(qk_norm=False, llama3=False, D=64):
+    return TR.make_config(vocab_size=1000, hidden_size=128, intermediate_size=256, num_layers=2,
+                          num_heads=4, num_kv_heads=2, head_dim=D, qk_norm=int(qk_norm),
+                          rms_norm_eps=1e-6 if qk_norm else 1e-5,
+                          rope_theta=5e5 if llama3 else 1e4, rope_factor=32.0 if llama3 else 0.0,
+                          rope_original_max_pos=64 if llama3 else 8192)
+
+
+def batch(c, B, T, seed):
+    rng = np.random.default_rng(seed)
+    row = rng.integers(0, c.vocab_size, (B, T + 1))
+    mask = np.ones((B, T), np.float32)
+    for b in range(B):
+        mask[b, : int(rng.uniform(0.2, 0.6) * T)] = 0
+    return row[:, :T], row[:, 1:], mask
+
+
+@pytest.mark.parametrize("qk_norm,llama3,D", [(False, False, 64), (True, False, 128),
+                                              (False, True, 64)])
+def test_tiny_model_loss_and_grads_vs_oracle(qk_norm, llama3, D):
+    c = tiny_cfg(qk_norm, llama3, D)
+    tr = TR.Trainer(c, seed=1, init_std=0.1, norm_value=None)
+    ids, tg, mask = batch(c, 2, 96, seed=2)
+    tr.set_batch(ids, tg, mask)
+    loss = tr.forward_backward(True)
+    params = [tr.get_param(i) for i in range(tr.num_params())]
+    sh = shapes(c)
+    shaped = []
+    for name, p in zip(tr.names, params):
+        if name == "model.embed_tokens.weight":
+            shaped.append(p.reshape(c.vocab_size, c.hidden_size))
+        elif name == "model.norm.weight":
+            shaped.append(p)
+        else:
+            shaped.append(p.reshape(sh[name.split(".")[-2]]))
+    ref_loss, ref_grads = O.model_loss(oracle_cfg(c), shaped, ids, tg, mask)
+    assert abs(loss - ref_loss) <= 1e-4 * abs(ref_loss), (loss, ref_loss)
+    grads_off = []
+    for i, name in enumerate(tr.names):
+        g = tr.get_grad(i)
+        assert g is not None, name
+        assert_close(g, ref_grads[i].reshape(-1), name=name)
+        grads_off.append(g)
+    # checkpointing on: same loss bits, same gradient bits
+    tr.zero_grad()
+    tr.set_checkpointing(True)
+    loss2 = tr.forward_backward(True)
+    assert loss2 == loss
+    for i, name in enumerate(tr.names):
+        assert np.array_equal(tr.get_grad(i), grads_off[i]), name
+    tr.close()
+
+
+def test_offload_equals_on_device_over_steps():
+    c = tiny_cfg(qk_norm=True, D=128)
+    a = TR.Trainer(c, seed=3, init_std=0.05)
+    b = TR.Trainer(c, seed=3, init_std=0.05)
+    a.make_optimizer(lr=1e-3, weight_decay=0.1, offload=True, chunk_elems=4099)  # many chunks
+    b.make_optimizer(lr=1e-3, weight_decay=0.1, offload=False)
+    for step in range(3):
+        for t in (a, b):
+            t.synthetic_batch(2, 64, seed=step, masked=True)
+            t.forward_backward(True)
+            t.clip(1.0)
+            t.opt_step()
+            t.zero_grad()
+    for i in range(a.num_params()):
+        assert np.array_equal(a.get_param(i), b.get_param(i)), a.names[i]
+        ma, va = a.opt_state(i)
+        mb, vb = b.opt_state(i)
+        assert np.array_equal(ma, mb) and np.array_equal(va, vb), a.names[i]
+    a.close()
+    b.close()
+
+
+def test_train_step_and_checkpoint_roundtrip(tmp_path):
+    c = tiny_cfg()
+    a = TR.Trainer(c, seed=4)
+    a.make_optimizer(lr=1e-3, offload=True)
+    a.synthetic_batch(2, 64, seed=5)
+    t = a.train_step(1.0)
+    assert math.isfinite(t.loss) and t.loss > 0 and t.total_ms > 0
+    path = tmp_path / "ckpt.safetensors"
+    a.save(path)
+    # header: u64 length, compact key-sorted JSON, space padded to 8 bytes
+    def header(p):
+        raw = open(p, "rb").read()
+        (hl,) = struct.unpack("<Q", raw[:8])
+        assert hl % 8 == 0
+        return raw[8: 8 + hl].decode()
+    head = header(path)
+    keys = list(json.loads(head).keys())
+    assert keys == sorted(keys) and '"data_offsets":' in head and ", " not in head
+    b = TR.Trainer(c, seed=99)
+    b.make_optimizer(lr=1e-3, offload=True)
+    b.load(path)
+    for i in range(a.num_params()):
+        assert np.array_equal(a.get_param(i), b.get_param(i))
+        ma, va = a.opt_state(i)
+        mb, vb = b.opt_state(i)
+        assert np.array_equal(ma, mb) and np.array_equal(va, vb)
+    opt_keys = json.loads(header(str(path) + ".opt.safetensors"))
+    assert "optimizer.step" in opt_keys and f"optimizer.m.{a.names[0]}" in opt_keys
+    a.close()
+    b.close()
+
+
+def test_c2_smollm2_full_step_checkpoint_bitwise():
+    c = TR.preset("smollm2-135m")
+    tr = TR.Trainer(c, seed=0, init_std=0.02)
+    tr.synthetic_batch(4, 512, seed=0, masked=True)
+    loss_off = tr.forward_backward(True)
+    g_off = [tr.get_grad(i) for i in (0, 1, 5, tr.num_params() - 1)]
+    tr.zero_grad()
+    tr.set_checkpointing(True)
+    loss_on = tr.forward_backward(True)
+    assert loss_on == loss_off
+    # At init the logits are ~N(0, s^2) with s^2 = d * 0.02^2 (unit-RMS hidden states
+    # times N(0, 0.02) embeddings), so E[loss] ~ ln V + s^2 / 2.
+    assert abs(loss_off - (math.log(c.vocab_size) + c.hidden_size * 0.02 ** 2 / 2)) < 0.05
+    for j, i in enumerate((0, 1, 5, tr.num_params() - 1)):
+        assert np.array_equal(tr.get_grad(i), g_off[j])
+    tr.close()
