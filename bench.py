@@ -1,0 +1,276 @@
+#!/usr/bin/env python3
+"""Headline benchmark: Qwen3-1.7B-shaped fp32 training step with gradient
+checkpointing (block recompute) and AdamW m/v offloaded to pinned host memory,
+batch 8 x seq 4096 on one MI355X.
+
+One step = forward_train_masked -> backward (each block recomputed) ->
+clip_grad_norm_(1.0) -> offloaded AdamW step -> zero_grad, i.e. the reference's
+ctd_train step (tools/ctd_train/main.cpp:348-398), run through the C++ layer
+(libctd.so) on the gfx950 kernels (libember_hip.so).  Inputs are seeded
+synthetic token ids (uniform in [0,V)) with an assistant-prefix loss mask;
+weights ~N(0,0.02), norm weights 1.
+
+Prints ONE JSON line: tokens/s (B*T per second), peak HBM, the GEMM roofline
+(HIP events around every GEMM launch of the timed steps) and a CPU baseline
+(the scalar CPU oracle timed on a bounded sample of the same workload and
+extrapolated; 1 core).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "train tokens/s + peak HBM GB, Qwen3-1.7B recompute+offload seq4096, 1 GPU"
+FP32_MFMA_PEAK_TFLOPS = 157.3
+PCIE_GEN5_X16_GBPS = 63.0
+
+WORKLOADS = {
+    # name: (preset, B, T, masked)
+    "qwen3-1.7b": ("qwen3-1.7b", 8, 4096, True),      # configs[4], the metric's config
+    "llama3.2-1b": ("llama3.2-1b", 4, 2048, False),   # configs[3]
+    "qwen3-0.6b": ("qwen3-0.6b", 4, 1024, True),      # configs[2]
+    "smollm2-135m": ("smollm2-135m", 4, 512, True),   # configs[1]
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(cfg, B, T, budget_s=20.0):
+    """Scalar CPU oracle (double, 1 thread) on a bounded sample, extrapolated to one step.
+
+    Sample: one decoder block forward+backward (the backward recomputes the block,
+    as checkpointing does) on s tokens at full hidden width; one attention head
+    forward+backward at T_s; the tied LM head for r rows.  Per-token costs scale
+    linearly to B*T tokens and L layers, attention by (T/T_s)^2 * H * B * L, the
+    head by B*T rows x 3 GEMMs (forward, dX, dW)."""
+    import numpy as np
+    import oracle as O
+
+    rng = np.random.default_rng(0)
+    d, I, H, Hk, D, V, L = (cfg.hidden_size, cfg.intermediate_size, cfg.num_heads,
+                            cfg.num_kv_heads, cfg.head_dim, cfg.vocab_size, cfg.num_layers)
+    oc = O.make_cfg(vocab=V, hidden=d, inter=I, layers=1, heads=H, kv_heads=Hk, head_dim=D,
+                    eps=cfg.rms_norm_eps, theta=cfg.rope_theta, rope_factor=cfg.rope_factor,
+                    qk_norm=cfg.qk_norm)
+    w = {"input_layernorm": np.ones(d), "post_attention_layernorm": np.ones(d),
+         "q_proj": 0.02 * rng.standard_normal((H * D, d)),
+         "k_proj": 0.02 * rng.standard_normal((Hk * D, d)),
+         "v_proj": 0.02 * rng.standard_normal((Hk * D, d)),
+         "o_proj": 0.02 * rng.standard_normal((d, H * D)),
+         "gate_proj": 0.02 * rng.standard_normal((I, d)),
+         "up_proj": 0.02 * rng.standard_normal((I, d)),
+         "down_proj": 0.02 * rng.standard_normal((d, I))}
+    if cfg.qk_norm:
+        w["q_norm"] = np.ones(D)
+        w["k_norm"] = np.ones(D)
+    s = 12
+    x = rng.standard_normal((1, s, d))
+    t0 = time.perf_counter()
+    O.block_bwd(oc, w, x, rng.standard_normal((1, s, d)))  # forward + recompute + backward
+    t_block = time.perf_counter() - t0
+    Ts = 256
+    q = rng.standard_normal((1, Ts, 1, D))
+    t0 = time.perf_counter()
+    O.attention_fwd(q, q, q)
+    O.attention_bwd(q, q, q, q)
+    t_attn = time.perf_counter() - t0
+    r, Vs = 1, min(V, 16384)  # head cost is linear in the vocabulary rows
+    hn = rng.standard_normal((r, d))
+    E = 0.02 * rng.standard_normal((Vs, d))
+    t0 = time.perf_counter()
+    O.matmul(hn, E, False, True)
+    t_head = (time.perf_counter() - t0) * V / Vs
+    sample_s = t_block + t_attn + t_head
+    N = B * T
+    step_s = (t_block / s * N * L
+              + t_attn * (T / Ts) ** 2 * H * B * L
+              + t_head / r * N * 3)
+    return {
+        "value": N / step_s,
+        "unit": "tokens/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"scalar fp64 CPU oracle, 1 thread: one block fwd+recompute+bwd on {s} tokens "
+                   f"({t_block:.2f}s), one head attention fwd+bwd at T={Ts} ({t_attn:.2f}s), "
+                   f"tied LM head for {r} row x {Vs} vocab rows (scaled to V: {t_head:.2f}s); "
+                   f"extrapolated linearly in tokens "
+                   f"and layers, attention by T^2; sample {sample_s:.1f}s, extrapolated step "
+                   f"{step_s:.0f}s"),
+        "cpu_model": _cpu_model(),
+        "nproc": os.cpu_count(),
+    }
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--workload", default="qwen3-1.7b", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-checkpointing", action="store_true")
+    ap.add_argument("--no-offload", action="store_true")
+    ap.add_argument("--nockpt-steps", type=int, default=1,
+                    help="extra steps without checkpointing for the recompute overhead and "
+                         "the no-checkpoint peak HBM (0 = skip)")
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--max-norm", type=float, default=1.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported "
+                          "(multi-GPU data parallelism is a design note only)"}))
+        sys.exit(2)
+
+    from emberlm_amd import trainer as TR
+
+    preset, B, T, masked = WORKLOADS[args.workload]
+    cfg = TR.preset(preset)
+    ckpt = not args.no_checkpointing
+    offload = not args.no_offload
+    n_params = TR.param_count(cfg)
+    log(f"[bench] {args.workload}: {n_params / 1e9:.4f} B params, B={B} T={T}, "
+        f"checkpointing={ckpt}, offload={offload}")
+
+    t0 = time.time()
+    tr = TR.Trainer(cfg, seed=0, init_std=0.02, norm_value=1.0)
+    tr.set_checkpointing(ckpt)
+    tr.make_optimizer(lr=1e-4, weight_decay=0.1, beta1=0.9, beta2=0.95, eps=1e-8, offload=offload)
+    tr.synthetic_batch(B, T, seed=0, masked=masked)
+    log(f"[bench] setup {time.time() - t0:.1f}s")
+
+    for i in range(args.warmup):
+        st = tr.train_step(args.max_norm)
+        log(f"[bench] warmup {i}: {st.total_ms:.0f} ms loss {st.loss:.4f}")
+
+    TR.reset_peak_memory()
+    TR.gemm_profile(True)
+    tr.synchronize()
+    times = []
+    t_wall = time.perf_counter()
+    for i in range(args.steps):
+        st = tr.train_step(args.max_norm)
+        times.append(st)
+        log(f"[bench] step {i}: total {st.total_ms:.0f} ms (fwd {st.forward_ms:.0f}, bwd "
+            f"{st.backward_ms:.0f}, clip {st.clip_ms:.0f}, opt {st.optimizer_ms:.0f}) "
+            f"loss {st.loss:.4f}")
+    tr.synchronize()
+    wall = time.perf_counter() - t_wall
+    TR.gemm_profile(False)
+    prof = TR.gemm_profile()
+    mem = TR.memory()
+
+    ms_step = wall / args.steps * 1e3
+    tokens = B * T
+    value = tokens / (ms_step / 1e3)
+    avg = lambda f: sum(getattr(s, f) for s in times) / len(times)  # noqa: E731
+    opt_ms = avg("optimizer_ms")
+    bytes_dir = 8.0 * n_params if offload else 0.0
+    mask_sum = times[-1].mask_sum
+
+    # Dominant GEMM instantiation (largest summed time) for the roofline line.
+    kname = {"NT": "gemm_f32_mfma<A K-contig, B K-contig> (Linear forward, NT)",
+             "NN": "gemm_f32_mfma<A K-contig, B N-contig> (dX, NN)",
+             "TN": "gemm_f32_mfma<A M-contig, B N-contig> (dW, TN)",
+             "TT": "gemm_f32_mfma<A M-contig, B K-contig> (TT)"}
+    dom = max(prof, key=lambda k: prof[k].total_ms)
+    p = prof[dom]
+    per_launch_flops = p.flops / max(p.launches, 1)
+    avg_ms = p.total_ms / max(p.launches, 1)
+    achieved = per_launch_flops / (avg_ms / 1e3) / 1e12 if avg_ms > 0 else 0.0
+    all_fl = sum(v.flops for v in prof.values())
+    all_ms = sum(v.total_ms for v in prof.values())
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded uniform token ids, assistant-prefix loss mask (20-60% of each "
+                "row), weights ~N(0,0.02), norm weights 1",
+        "config": {"workload": f"{args.workload} B{B} T{T} "
+                               f"{'recompute' if ckpt else 'no-recompute'}"
+                               f"{'+offload' if offload else ''}",
+                   "model": preset, "global_batch": B, "seq_len": T, "parallelism": "none (1 GPU)",
+                   "gradient_checkpointing": ckpt, "offload_optimizer": offload,
+                   "params": n_params},
+        "peak_hbm_gb": round(mem.peak_allocated / 1e9, 3),
+        "peak_hbm_reserved_gb": round(mem.peak_reserved / 1e9, 3),
+        "hbm_device_used_gb": round(mem.device_used / 1e9, 3),
+        "pinned_host_gb": round(mem.pinned_host / 1e9, 3),
+        "active_tokens_per_s": round(mask_sum / (ms_step / 1e3), 2),
+        "phase_ms": {k: round(avg(k + "_ms"), 2) for k in
+                     ("forward", "backward", "clip", "optimizer")},
+        "loss": round(times[-1].loss, 5),
+        "offload": {"bytes_per_direction": bytes_dir,
+                    "optimizer_phase_gbps_per_direction":
+                        round(bytes_dir / (opt_ms / 1e3) / 1e9, 2) if offload and opt_ms > 0 else None,
+                    "pcie_gen5_x16_gbps": PCIE_GEN5_X16_GBPS},
+        "gemm_all": {"launches": sum(v.launches for v in prof.values()),
+                     "tflops": round(all_fl / (all_ms / 1e3) / 1e12, 2) if all_ms else None,
+                     "frac_of_fp32_mfma_peak":
+                         round(all_fl / (all_ms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)
+                         if all_ms else None,
+                     "ms_per_step": round(all_ms / args.steps, 2)},
+        "roofline": {"kernel": kname[dom], "bound": "mfma", "achieved": round(achieved, 2),
+                     "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
+                     "launches": p.launches, "avg_launch_ms": round(avg_ms, 4),
+                     "flops_per_launch": per_launch_flops, "traffic": None},
+    }
+
+    if args.nockpt_steps > 0 and ckpt:
+        tr.set_checkpointing(False)
+        st = tr.train_step(args.max_norm)  # warm the allocator for the larger footprint
+        TR.reset_peak_memory()
+        nts = [tr.train_step(args.max_norm) for _ in range(args.nockpt_steps)]
+        mem2 = TR.memory()
+        base = sum(s.total_ms for s in nts) / len(nts)
+        fb = sum(s.forward_ms + s.backward_ms for s in nts) / len(nts)
+        fb_ck = avg("forward_ms") + avg("backward_ms")
+        result["no_checkpointing"] = {
+            "ms_per_step": round(base, 2),
+            "peak_hbm_gb": round(mem2.peak_allocated / 1e9, 3),
+            "recompute_overhead_step": round(avg("total_ms") / base - 1.0, 4),
+            "recompute_overhead_fwd_bwd": round(fb_ck / fb - 1.0, 4),
+        }
+        tr.set_checkpointing(True)
+    tr.close()
+
+    if not args.skip_cpu:
+        t0 = time.time()
+        result["cpu_baseline"] = cpu_baseline(cfg, B, T)
+        log(f"[bench] cpu baseline {time.time() - t0:.1f}s")
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

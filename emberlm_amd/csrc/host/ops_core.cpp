@@ -97,7 +97,7 @@ Tensor matmul_impl(const Tensor& a, const Tensor& b, bool transa, bool transb) {
   void* ev = runtime::gemm_profile_begin();
   CTD_CHECK(ember_gemm_f32(transa, transb, d.M, d.N, d.K, 1.0f, cfp(a), d.lda, 0, cfp(b), d.ldb,
                            0, 0.0f, fp(c), d.N, 0, 1, S()));
-  runtime::gemm_profile_end(ev, 2.0 * d.M * d.N * d.K);
+  runtime::gemm_profile_end(ev, 2.0 * d.M * d.N * d.K, 2 * transa + transb);
   return c;
 }
 
@@ -131,7 +131,7 @@ Tensor bmm_impl(const Tensor& a, const Tensor& b, bool transa, bool transb) {
   CTD_CHECK(ember_gemm_f32(transa, transb, M, N, K, 1.0f, cfp(a), a.shape()[2],
                            a.shape()[1] * a.shape()[2], cfp(b), b.shape()[2],
                            b.shape()[1] * b.shape()[2], 0.0f, fp(c), N, M * N, Bt, S()));
-  runtime::gemm_profile_end(ev, 2.0 * Bt * M * N * K);
+  runtime::gemm_profile_end(ev, 2.0 * Bt * M * N * K, 2 * transa + transb);
   return c;
 }
 

@@ -60,6 +60,7 @@ struct GemmProfiler {
   std::vector<ember_event_t> pool;                       // free events
   std::vector<std::pair<ember_event_t, ember_event_t>> spans;
   std::vector<double> flops;
+  std::vector<int> variant;
   ember_event_t get() {
     if (!pool.empty()) {
       ember_event_t e = pool.back();
@@ -92,7 +93,7 @@ void* gemm_profile_begin() {
   return e;
 }
 
-void gemm_profile_end(void* begin, double flops) {
+void gemm_profile_end(void* begin, double flops, int variant) {
   if (!begin) return;
   auto& p = prof();
   std::lock_guard<std::mutex> lk(p.mu);
@@ -100,26 +101,31 @@ void gemm_profile_end(void* begin, double flops) {
   check(ember_event_record(e, compute_stream()), "gemm profiler record");
   p.spans.emplace_back(begin, e);
   p.flops.push_back(flops);
+  p.variant.push_back(variant & 3);
 }
 
 void gemm_profile_collect(int64_t* launches, double* flops, double* total_ms) {
   auto& p = prof();
   std::lock_guard<std::mutex> lk(p.mu);
   synchronize();
-  double ms = 0.0, fl = 0.0;
+  for (int v = 0; v < 4; ++v) {
+    launches[v] = 0;
+    flops[v] = 0.0;
+    total_ms[v] = 0.0;
+  }
   for (size_t i = 0; i < p.spans.size(); ++i) {
     float t = 0.f;
     check(ember_event_elapsed_ms(&t, p.spans[i].first, p.spans[i].second), "gemm profiler elapsed");
-    ms += t;
-    fl += p.flops[i];
+    const int v = p.variant[i];
+    launches[v] += 1;
+    flops[v] += p.flops[i];
+    total_ms[v] += t;
     p.pool.push_back(p.spans[i].first);
     p.pool.push_back(p.spans[i].second);
   }
-  if (launches) *launches = static_cast<int64_t>(p.spans.size());
-  if (flops) *flops = fl;
-  if (total_ms) *total_ms = ms;
   p.spans.clear();
   p.flops.clear();
+  p.variant.clear();
 }
 
 }  // namespace runtime

@@ -139,9 +139,9 @@ def gemm_profile(enable=None):
     if enable is not None:
         _ck(lib().ctd_gemm_profile_enable(int(enable)), "gemm_profile_enable")
         return None
-    g = GemmProfile()
-    _ck(lib().ctd_gemm_profile_collect(C.byref(g)), "gemm_profile_collect")
-    return g
+    g = (GemmProfile * 4)()
+    _ck(lib().ctd_gemm_profile_collect(g), "gemm_profile_collect")
+    return {name: g[i] for i, name in enumerate(("NN", "NT", "TN", "TT"))}
 
 
 class Trainer:

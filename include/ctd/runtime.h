@@ -29,8 +29,10 @@ bool device_available();
 void gemm_profile_enable(bool on);
 bool gemm_profiling();
 void* gemm_profile_begin();                     // null when disabled
-void gemm_profile_end(void* begin, double flops);
-// Resolves the recorded events (synchronises) and resets the record.
+// variant = 2*transa + transb of the launch (which kernel instantiation ran).
+void gemm_profile_end(void* begin, double flops, int variant);
+// Resolves the recorded events (synchronises) and resets the record; the
+// arrays have 4 entries, one per variant.
 void gemm_profile_collect(int64_t* launches, double* flops, double* total_ms);
 
 }  // namespace ctd::runtime

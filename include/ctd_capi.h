@@ -108,7 +108,9 @@ int ctd_memory_stats(ctd_memory* out);
 int ctd_reset_peak_memory(void);
 
 /* GEMM timing: while enabled, every ember_gemm_f32 launched by the ops layer
- * is bracketed by HIP events on the compute stream; collect resolves them. */
+ * is bracketed by HIP events on the compute stream; collect resolves them
+ * into out[4], indexed by 2*transa + transb (one entry per kernel
+ * instantiation: NN, NT, TN, TT). */
 int ctd_gemm_profile_enable(int32_t on);
 int ctd_gemm_profile_collect(ctd_gemm_profile* out);
 
