@@ -73,7 +73,7 @@ def cpu_baseline(cfg, B, T, budget_s=20.0):
     if cfg.qk_norm:
         w["q_norm"] = np.ones(D)
         w["k_norm"] = np.ones(D)
-    s = 12
+    s = 48
     x = rng.standard_normal((1, s, d))
     t0 = time.perf_counter()
     O.block_bwd(oc, w, x, rng.standard_normal((1, s, d)))  # forward + recompute + backward
@@ -133,6 +133,9 @@ def main():
                     help="extra steps without checkpointing for the recompute overhead and "
                          "the no-checkpoint peak HBM (0 = skip)")
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="launch one ember_scale over 1 GiB (reads 1 GiB, writes 1 GiB) first: "
+                         "the known-size copy that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE")
     ap.add_argument("--max-norm", type=float, default=1.0)
     args = ap.parse_args()
 
@@ -142,6 +145,18 @@ def main():
         sys.exit(2)
 
     from emberlm_amd import trainer as TR
+
+    if args.copy_probe:
+        from emberlm_amd import capi
+        n = (1 << 30) // 4
+        buf = C.c_void_p()
+        capi.check(capi.lib().ember_device_malloc(C.byref(buf), 2 * n * 4), "malloc")
+        src, dst = buf.value, buf.value + n * 4
+        capi.check(capi.lib().ember_fill(src, n, 1.0, None), "fill")
+        capi.check(capi.lib().ember_scale(src, 1.0, dst, n, None), "copy probe")
+        capi.check(capi.lib().ember_device_synchronize(), "sync")
+        capi.check(capi.lib().ember_device_free(buf), "free")
+        log("[bench] copy probe: ember_scale over 1 GiB done")
 
     preset, B, T, masked = WORKLOADS[args.workload]
     cfg = TR.preset(preset)
