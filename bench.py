@@ -111,6 +111,22 @@ def cpu_baseline(cfg, B, T, budget_s=20.0):
     }
 
 
+def profiled_traffic(workload, variant):
+    """HBM bytes per launch of the dominant GEMM from the committed rocprofv3 PMC
+    summary of this workload (FETCH_SIZE/WRITE_SIZE scaled by a known-size copy), or None."""
+    key = {"NT": "gemm_nt", "NN": "gemm_nn", "TN": "gemm_tn"}.get(variant)
+    pdir = os.path.join(ROOT, "profiles")
+    if not key or not os.path.isdir(pdir):
+        return None, None
+    for fn in sorted(os.listdir(pdir)):
+        if workload in fn and fn.endswith(".md"):
+            for line in open(os.path.join(pdir, fn)):
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "TRAFFIC_BYTES_PER_LAUNCH" and parts[1] == key:
+                    return float(parts[2]), "profiles/" + fn
+    return None, None
+
+
 def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -259,6 +275,10 @@ def main():
                      "launches": p.launches, "avg_launch_ms": round(avg_ms, 4),
                      "flops_per_launch": per_launch_flops, "traffic": None},
     }
+    traffic, src = profiled_traffic(args.workload, dom)
+    if traffic is not None:
+        result["roofline"]["traffic"] = traffic
+        result["roofline"]["traffic_source"] = src
 
     if args.nockpt_steps > 0 and ckpt:
         tr.set_checkpointing(False)
