@@ -18,8 +18,10 @@
 // pair (g = 0/1) and the probabilities come out exactly in the B-operand
 // layout of O^T += V^T P^T: accumulator register e of S^T is the B value of
 // the MFMA step that contracts over keys {8*(e/4)+(e%4), 8*(e/4)+4+(e%4)}.
-// Q stays in registers (pre-multiplied by scale*log2(e)), K and V tiles of 64
-// keys are staged through LDS and shared by the block's 4 waves.
+// Q stays in registers (pre-multiplied by scale*log2(e)).  K/V tiles of 32
+// keys are double-buffered in LDS: the global loads of tile i+1 are issued
+// into registers before the MFMAs of tile i and written to the other buffer
+// after them, so one barrier per tile remains and load latency is hidden.
 //
 // Backward (no atomics, so dK/dV/dQ are bitwise reproducible):
 //   attn_delta:  delta = rowsum(dO * O);
@@ -29,6 +31,7 @@
 //                lane, so dV^T += dO^T P and dK^T += Q^T dS accumulate in
 //                registers across every query tile and every query head of
 //                the KV head's group, in a fixed order.
+// Both backward kernels double-buffer their streamed tiles the same way.
 #include "common.h"
 
 using namespace ember;
@@ -37,10 +40,14 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr int kThreads = 256;
 
 __device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
+
+// 2^x on the transcendental unit (inputs here are <= 0 or -inf).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ int acc_row(int e, int g) { return 8 * (e >> 2) + 4 * g + (e & 3); }
 
@@ -49,26 +56,58 @@ __device__ __forceinline__ void zero16(f32x16& a) {
   for (int e = 0; e < 16; ++e) a[e] = 0.f;
 }
 
-// Copy `rows` rows of D floats (row stride `gstride` floats) into LDS rows of
-// stride `ls`, zero rows at or beyond `valid`.
-template <int D>
-__device__ __forceinline__ void stage_rows(float* __restrict__ lds, int ls,
-                                           const float* __restrict__ src, int64_t gstride,
-                                           int rows, int valid) {
-  for (int c = threadIdx.x; c < rows * (D / 4); c += blockDim.x) {
-    const int row = c / (D / 4), c4 = c % (D / 4);
-    f32x4 v = {0.f, 0.f, 0.f, 0.f};
-    if (row < valid) v = reinterpret_cast<const f32x4*>(src + row * gstride)[c4];
-    *reinterpret_cast<f32x4*>(lds + row * ls + 4 * c4) = v;
-  }
+// Block order.  Every attention kernel runs a 1-D grid of (tile, row) work
+// items, row = (b, head).  Blocks are dispatched in index order and dealt
+// round-robin over the 8 XCDs (block i runs on XCD i % 8), so the index puts
+// the heaviest tiles first (the causal triangle makes tile cost vary 32x) and
+// gives every XCD the same mix of tiles; when the row count is a multiple of 8
+// the rows are regrouped so that each XCD owns a contiguous range of (b, head)
+// rows and the K/V of a GQA group stays in one L2.
+struct WorkItem {
+  int tile, row;
+};
+__device__ __forceinline__ WorkItem work_item(int ntiles) {
+  const int L = static_cast<int>(blockIdx.x);
+  const int rows = static_cast<int>(gridDim.x) / ntiles;
+  int rr = L % rows;
+  if (rows % 8 == 0) rr = (rr % 8) * (rows / 8) + rr / 8;
+  return {L / rows, rr};
 }
+
+// ROWS rows of D floats staged global -> registers -> LDS.  All loads of a
+// tile are issued before the first wait; rows at or beyond `valid` are zero.
+template <int D, int ROWS>
+struct RowTile {
+  static constexpr int kChunks = ROWS * D / 4;
+  static constexpr int kPer = kChunks / kThreads;
+  static_assert(kChunks % kThreads == 0, "tile does not split evenly over the block");
+  f32x4 r[kPer];
+
+  __device__ __forceinline__ void load(const float* __restrict__ src, int64_t gstride, int valid) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = threadIdx.x + i * kThreads;
+      const int row = c / (D / 4), c4 = c % (D / 4);
+      r[i] = row < valid ? reinterpret_cast<const f32x4*>(src + row * gstride)[c4]
+                         : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  __device__ __forceinline__ void store(float* __restrict__ lds, int ls) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = threadIdx.x + i * kThreads;
+      const int row = c / (D / 4), c4 = c % (D / 4);
+      *reinterpret_cast<f32x4*>(lds + row * ls + 4 * c4) = r[i];
+    }
+  }
+};
 
 // Write LDS rows [rows][D] (stride ls) to global rows, skipping rows >= valid.
 template <int D>
 __device__ __forceinline__ void unstage_rows(const float* __restrict__ lds, int ls,
                                              float* __restrict__ dst, int64_t gstride, int rows,
                                              int valid) {
-  for (int c = threadIdx.x; c < rows * (D / 4); c += blockDim.x) {
+  for (int c = threadIdx.x; c < rows * (D / 4); c += kThreads) {
     const int row = c / (D / 4), c4 = c % (D / 4);
     if (row < valid)
       reinterpret_cast<f32x4*>(dst + row * gstride)[c4] =
@@ -95,31 +134,58 @@ __device__ __forceinline__ void load_half(float (&reg)[HALF], const float* __res
   }
 }
 
+// Transposes a wave's 32-column accumulator block through LDS into rows
+// [32*w + r][D] of `lds` (stride ls), scaled by `mul`.  The D index is
+// interleaved over the NDT accumulator tiles: row m of tile dt is d = NDT*m + dt,
+// so the A operand of every D-tiled MFMA is one b128 LDS read of NDT
+// consecutive d values (NDT = 4 at D = 128, 2 at D = 64).
+template <int NDT>
+__device__ __forceinline__ void acc_to_rows(float* __restrict__ lds, int ls,
+                                            const f32x16 (&acc)[NDT], int w, int g, int r,
+                                            float mul) {
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      lds[(32 * w + r) * ls + NDT * acc_row(e, g) + dt] = acc[dt][e] * mul;
+}
+
+// NDT consecutive floats of an LDS row (the interleaved A operand above).
+template <int NDT>
+struct DVec;
+template <>
+struct DVec<4> {
+  using T = f32x4;
+};
+template <>
+struct DVec<2> {
+  typedef float T __attribute__((ext_vector_type(2)));
+};
+
 // ------------------------------------------------------------------ forward
 template <int D>
 struct FwdCfg {
-  static constexpr int kBQ = 128, kBK = 64, kKS = D + 4, kVS = D + 8, kOS = D + 4;
-  static constexpr int kTile = kBK * (kKS + kVS);
+  static constexpr int kBQ = 128, kBK = 32, kKS = D + 4, kVS = D + 8, kOS = D + 4;
+  static constexpr int kBuf = kBK * (kKS + kVS);  // one K+V stage
   static constexpr int kOut = kBQ * kOS;
-  static constexpr int kSmem = kTile > kOut ? kTile : kOut;
+  static constexpr int kSmem = 2 * kBuf > kOut ? 2 * kBuf : kOut;
 };
 
 template <int D>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(const float* __restrict__ q,
-                                                       const float* __restrict__ k,
-                                                       const float* __restrict__ v,
-                                                       float* __restrict__ o,
-                                                       float* __restrict__ lse, int T, int H,
-                                                       int Hk, float scale_log2) {
+__global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const float* __restrict__ q,
+                                                               const float* __restrict__ k,
+                                                               const float* __restrict__ v,
+                                                               float* __restrict__ o,
+                                                               float* __restrict__ lse, int T,
+                                                               int H, int Hk, float scale_log2) {
   using C = FwdCfg<D>;
   constexpr int HALF = D / 2, NDT = D / 32;
   __shared__ __attribute__((aligned(16))) float smem[C::kSmem];
-  float* Ks = smem;
-  float* Vs = smem + C::kBK * C::kKS;
 
   const int nqb = (T + C::kBQ - 1) / C::kBQ;
-  const int qb = nqb - 1 - static_cast<int>(blockIdx.x);  // longest rows first
-  const int h = blockIdx.y, b = blockIdx.z;
+  const WorkItem wi = work_item(nqb);
+  const int qb = nqb - 1 - wi.tile;  // longest rows first
+  const int h = wi.row % H, b = wi.row / H;
   const int hk = h / (H / Hk);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 5, r = lane & 31;
   const int q0 = qb * C::kBQ, qw0 = q0 + 32 * w, myq = qw0 + r;
@@ -138,89 +204,92 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const float* __restrict__
 
   const int kend = min(T, q0 + C::kBQ);
   const int nkb = (kend + C::kBK - 1) / C::kBK;
+  RowTile<D, C::kBK> tk, tv;
+  tk.load(kbase, ks, T);
+  tv.load(vbase, ks, T);
+  tk.store(smem, C::kKS);
+  tv.store(smem + C::kBK * C::kKS, C::kVS);
+  __syncthreads();
+
   for (int kb = 0; kb < nkb; ++kb) {
     const int k0 = kb * C::kBK;
-    stage_rows<D>(Ks, C::kKS, kbase + static_cast<int64_t>(k0) * ks, ks, C::kBK, T - k0);
-    stage_rows<D>(Vs, C::kVS, vbase + static_cast<int64_t>(k0) * ks, ks, C::kBK, T - k0);
-    __syncthreads();
+    const bool more = kb + 1 < nkb;
+    if (more) {
+      tk.load(kbase + static_cast<int64_t>(k0 + C::kBK) * ks, ks, T - k0 - C::kBK);
+      tv.load(vbase + static_cast<int64_t>(k0 + C::kBK) * ks, ks, T - k0 - C::kBK);
+    }
+    const float* Ks = smem + (kb & 1) * C::kBuf;
+    const float* Vs = Ks + C::kBK * C::kKS;
     if (k0 <= qw0 + 31) {
-      f32x16 s[2];
-      zero16(s[0]);
-      zero16(s[1]);
+      f32x16 s;
+      zero16(s);
 #pragma unroll
       for (int s4 = 0; s4 < HALF / 4; ++s4) {
+        const f32x4 kf = *reinterpret_cast<const f32x4*>(Ks + r * C::kKS + HALF * g + 4 * s4);
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-          const f32x4 kf =
-              *reinterpret_cast<const f32x4*>(Ks + (mt * 32 + r) * C::kKS + HALF * g + 4 * s4);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) s[mt] = mfma32(kf[j], qreg[4 * s4 + j], s[mt]);
-        }
+        for (int j = 0; j < 4; ++j) s = mfma32(kf[j], qreg[4 * s4 + j], s);
       }
       const bool need_mask = (k0 + C::kBK - 1 > qw0) || (k0 + C::kBK > T);
       float tmax = -INFINITY;
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int key = k0 + mt * 32 + acc_row(e, g);
-          if (need_mask && (key > myq || key >= T)) s[mt][e] = -INFINITY;
-          tmax = fmaxf(tmax, s[mt][e]);
-        }
+      for (int e = 0; e < 16; ++e) {
+        const int key = k0 + acc_row(e, g);
+        if (need_mask && (key > myq || key >= T)) s[e] = -INFINITY;
+        tmax = fmaxf(tmax, s[e]);
+      }
       tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
       const float m_new = fmaxf(m_run, tmax);
-      const float alpha = exp2f(m_run - m_new);
+      const float alpha = fast_exp2(m_run - m_new);
       float psum = 0.f;
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float p = exp2f(s[mt][e] - m_new);
-          s[mt][e] = p;
-          psum += p;
-        }
+      for (int e = 0; e < 16; ++e) {
+        const float pv = fast_exp2(s[e] - m_new);
+        s[e] = pv;
+        psum += pv;
+      }
       l_run = l_run * alpha + psum;
       m_run = m_new;
+      if (__any(alpha != 1.0f)) {  // the running max moved for some query of the wave
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
+        for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) acc[dt][e] *= alpha;
+          for (int e = 0; e < 16; ++e) acc[dt][e] *= alpha;
+      }
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      for (int e = 0; e < 16; ++e) {
+        const auto vv = *reinterpret_cast<const typename DVec<NDT>::T*>(
+            Vs + acc_row(e, g) * C::kVS + NDT * r);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float* vrow = Vs + (mt * 32 + acc_row(e, g)) * C::kVS + r;
-#pragma unroll
-          for (int dt = 0; dt < NDT; ++dt) acc[dt] = mfma32(vrow[dt * 32], s[mt][e], acc[dt]);
-        }
+        for (int dt = 0; dt < NDT; ++dt) acc[dt] = mfma32(vv[dt], s[e], acc[dt]);
+      }
+    }
+    if (more) {
+      float* nb = smem + ((kb + 1) & 1) * C::kBuf;
+      tk.store(nb, C::kKS);
+      tv.store(nb + C::kBK * C::kKS, C::kVS);
     }
     __syncthreads();
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
-  const float inv = 1.0f / l_tot;
   if (g == 0 && myq < T)
     lse[(static_cast<int64_t>(b) * H + h) * T + myq] = (m_run + log2f(l_tot)) * kLn2;
-  float* Os = smem;
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int e = 0; e < 16; ++e)
-      Os[(32 * w + r) * C::kOS + dt * 32 + acc_row(e, g)] = acc[dt][e] * inv;
+  acc_to_rows<NDT>(smem, C::kOS, acc, w, g, r, 1.0f / l_tot);
   __syncthreads();
-  unstage_rows<D>(Os, C::kOS, o + static_cast<int64_t>(b) * T * qs + static_cast<int64_t>(q0) * qs +
-                                  static_cast<int64_t>(h) * D,
+  unstage_rows<D>(smem, C::kOS,
+                  o + static_cast<int64_t>(b) * T * qs + static_cast<int64_t>(q0) * qs +
+                      static_cast<int64_t>(h) * D,
                   qs, C::kBQ, T - q0);
 }
 
 // --------------------------------------------------------------- backward
 // delta[b,h,t] = sum_d dO[b,t,h,d] * O[b,t,h,d]; LPR = D/4 lanes per row.
 template <int D>
-__global__ __launch_bounds__(256) void attn_delta_kernel(const float* __restrict__ o,
-                                                         const float* __restrict__ dout,
-                                                         float* __restrict__ delta, int64_t rows,
-                                                         int T, int H) {
-  constexpr int LPR = D / 4, RPB = 256 / LPR;
+__global__ __launch_bounds__(kThreads) void attn_delta_kernel(const float* __restrict__ o,
+                                                              const float* __restrict__ dout,
+                                                              float* __restrict__ delta,
+                                                              int64_t rows, int T, int H) {
+  constexpr int LPR = D / 4, RPB = kThreads / LPR;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
   const int sub = threadIdx.x % LPR;
   float a = 0.f;
@@ -241,25 +310,24 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(const float* __restrict
 template <int D>
 struct DqCfg {
   static constexpr int kBQ = 128, kBK = 32, kKS = D + 4, kVS = D + 4, kOS = D + 4;
-  static constexpr int kTile = kBK * (kKS + kVS);
+  static constexpr int kBuf = kBK * (kKS + kVS);
   static constexpr int kOut = kBQ * kOS;
-  static constexpr int kSmem = kTile > kOut ? kTile : kOut;
+  static constexpr int kSmem = 2 * kBuf > kOut ? 2 * kBuf : kOut;
 };
 
 template <int D>
-__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
+__global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta,
     float* __restrict__ dq, int T, int H, int Hk, float scale_log2, float scale) {
   using C = DqCfg<D>;
   constexpr int HALF = D / 2, NDT = D / 32;
   __shared__ __attribute__((aligned(16))) float smem[C::kSmem];
-  float* Ks = smem;
-  float* Vs = smem + C::kBK * C::kKS;
 
   const int nqb = (T + C::kBQ - 1) / C::kBQ;
-  const int qb = nqb - 1 - static_cast<int>(blockIdx.x);
-  const int h = blockIdx.y, b = blockIdx.z;
+  const WorkItem wi = work_item(nqb);
+  const int qb = nqb - 1 - wi.tile;  // longest rows first
+  const int h = wi.row % H, b = wi.row / H;
   const int hk = h / (H / Hk);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 5, r = lane & 31;
   const int q0 = qb * C::kBQ, qw0 = q0 + 32 * w, myq = qw0 + r;
@@ -281,11 +349,22 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
 
   const int kend = min(T, q0 + C::kBQ);
   const int nkb = (kend + C::kBK - 1) / C::kBK;
+  RowTile<D, C::kBK> tk, tv;
+  tk.load(kbase, ks, T);
+  tv.load(vbase, ks, T);
+  tk.store(smem, C::kKS);
+  tv.store(smem + C::kBK * C::kKS, C::kVS);
+  __syncthreads();
+
   for (int kb = 0; kb < nkb; ++kb) {
     const int k0 = kb * C::kBK;
-    stage_rows<D>(Ks, C::kKS, kbase + static_cast<int64_t>(k0) * ks, ks, C::kBK, T - k0);
-    stage_rows<D>(Vs, C::kVS, vbase + static_cast<int64_t>(k0) * ks, ks, C::kBK, T - k0);
-    __syncthreads();
+    const bool more = kb + 1 < nkb;
+    if (more) {
+      tk.load(kbase + static_cast<int64_t>(k0 + C::kBK) * ks, ks, T - k0 - C::kBK);
+      tv.load(vbase + static_cast<int64_t>(k0 + C::kBK) * ks, ks, T - k0 - C::kBK);
+    }
+    const float* Ks = smem + (kb & 1) * C::kBuf;
+    const float* Vs = Ks + C::kBK * C::kKS;
     if (k0 <= qw0 + 31) {
       f32x16 s, dp;
       zero16(s);
@@ -303,39 +382,40 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int key = k0 + acc_row(e, g);
-        const float p = (key > myq || key >= T) ? 0.f : exp2f(s[e] - lse2);
+        const float p = (key > myq || key >= T) ? 0.f : fast_exp2(s[e] - lse2);
         s[e] = p * (dp[e] - dlt);
       }
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const float* krow = Ks + acc_row(e, g) * C::kKS + r;
+        const auto kv = *reinterpret_cast<const typename DVec<NDT>::T*>(
+            Ks + acc_row(e, g) * C::kKS + NDT * r);
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) acc[dt] = mfma32(krow[dt * 32], s[e], acc[dt]);
+        for (int dt = 0; dt < NDT; ++dt) acc[dt] = mfma32(kv[dt], s[e], acc[dt]);
       }
+    }
+    if (more) {
+      float* nb = smem + ((kb + 1) & 1) * C::kBuf;
+      tk.store(nb, C::kKS);
+      tv.store(nb + C::kBK * C::kKS, C::kVS);
     }
     __syncthreads();
   }
 
-  float* Os = smem;
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int e = 0; e < 16; ++e)
-      Os[(32 * w + r) * C::kOS + dt * 32 + acc_row(e, g)] = acc[dt][e] * scale;
+  acc_to_rows<NDT>(smem, C::kOS, acc, w, g, r, scale);
   __syncthreads();
-  unstage_rows<D>(Os, C::kOS, dq + qoff + static_cast<int64_t>(q0) * qs, qs, C::kBQ, T - q0);
+  unstage_rows<D>(smem, C::kOS, dq + qoff + static_cast<int64_t>(q0) * qs, qs, C::kBQ, T - q0);
 }
 
 template <int D>
 struct DkvCfg {
   static constexpr int kBKeys = 128, kBQ = 32, kQS = D + 4, kOS = D + 4;
-  static constexpr int kTile = 2 * kBQ * kQS + 2 * kBQ;
+  static constexpr int kBuf = 2 * kBQ * kQS + 2 * kBQ;  // Q, dO, lse, delta
   static constexpr int kOut = kBKeys * kOS;
-  static constexpr int kSmem = kTile > kOut ? kTile : kOut;
+  static constexpr int kSmem = 2 * kBuf > kOut ? 2 * kBuf : kOut;
 };
 
 template <int D>
-__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(
+__global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta,
     float* __restrict__ dk, float* __restrict__ dv, int T, int H, int Hk, float scale_log2,
@@ -343,13 +423,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(
   using C = DkvCfg<D>;
   constexpr int HALF = D / 2, NDT = D / 32;
   __shared__ __attribute__((aligned(16))) float smem[C::kSmem];
-  float* Qs = smem;
-  float* Ds = smem + C::kBQ * C::kQS;
-  float* Ls = smem + 2 * C::kBQ * C::kQS;
-  float* Es = Ls + C::kBQ;
 
-  const int kb = blockIdx.x;  // small key blocks see the most queries: launched first
-  const int hk = blockIdx.y, b = blockIdx.z;
+  const WorkItem wi = work_item((T + C::kBKeys - 1) / C::kBKeys);
+  const int kb = wi.tile;  // small key blocks see the most queries: launched first
+  const int hk = wi.row % Hk, b = wi.row / Hk;
   const int group = H / Hk;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 5, r = lane & 31;
   const int key0 = kb * C::kBKeys, kw0 = key0 + 32 * w, mykey = kw0 + r;
@@ -367,78 +444,100 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(
     zero16(adv[dt]);
   }
 
-  for (int hh = 0; hh < group; ++hh) {
+  // The streamed sequence: for each query head of the group, the query tiles
+  // key0, key0 + 32, ... below T.
+  const int ntile = (T - key0 + C::kBQ - 1) / C::kBQ;
+  const int nsteps = group * ntile;
+  RowTile<D, C::kBQ> tq, tdo;
+  float tl = 0.f, te = 0.f;
+  auto issue = [&](int step) {
+    const int hh = step / ntile, qt0 = key0 + (step % ntile) * C::kBQ;
     const int h = hk * group + hh;
-    const int64_t qoff = static_cast<int64_t>(b) * T * qs + static_cast<int64_t>(h) * D;
-    const int64_t srow = (static_cast<int64_t>(b) * H + h) * T;
-    for (int qt0 = key0; qt0 < T; qt0 += C::kBQ) {
-      stage_rows<D>(Qs, C::kQS, q + qoff + static_cast<int64_t>(qt0) * qs, qs, C::kBQ, T - qt0);
-      stage_rows<D>(Ds, C::kQS, dout + qoff + static_cast<int64_t>(qt0) * qs, qs, C::kBQ, T - qt0);
-      if (threadIdx.x < C::kBQ) {
-        const int t = qt0 + threadIdx.x;
-        Ls[threadIdx.x] = t < T ? lse[srow + t] * kLog2e : 0.f;
-        Es[threadIdx.x] = t < T ? delta[srow + t] : 0.f;
-      }
-      __syncthreads();
-      if (qt0 + C::kBQ - 1 >= kw0) {
-        f32x16 s, dp;
-        zero16(s);
-        zero16(dp);
-#pragma unroll
-        for (int s4 = 0; s4 < HALF / 4; ++s4) {
-          const f32x4 qf = *reinterpret_cast<const f32x4*>(Qs + r * C::kQS + HALF * g + 4 * s4);
-          const f32x4 of = *reinterpret_cast<const f32x4*>(Ds + r * C::kQS + HALF * g + 4 * s4);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            s = mfma32(qf[j], kreg[4 * s4 + j], s);
-            dp = mfma32(of[j], vreg[4 * s4 + j], dp);
-          }
-        }
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int ql = acc_row(e, g);
-          const int qq = qt0 + ql;
-          const float p = (qq < mykey || qq >= T) ? 0.f : exp2f(s[e] - Ls[ql]);
-          s[e] = p;
-          dp[e] = p * (dp[e] - Es[ql]);
-        }
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int ql = acc_row(e, g);
-          const float* orow = Ds + ql * C::kQS + r;
-          const float* qrow = Qs + ql * C::kQS + r;
-#pragma unroll
-          for (int dt = 0; dt < NDT; ++dt) {
-            adv[dt] = mfma32(orow[dt * 32], s[e], adv[dt]);
-            adk[dt] = mfma32(qrow[dt * 32], dp[e], adk[dt]);
-          }
-        }
-      }
-      __syncthreads();
+    const int64_t qoff = static_cast<int64_t>(b) * T * qs + static_cast<int64_t>(h) * D +
+                         static_cast<int64_t>(qt0) * qs;
+    tq.load(q + qoff, qs, T - qt0);
+    tdo.load(dout + qoff, qs, T - qt0);
+    if (threadIdx.x < C::kBQ) {
+      const int t = qt0 + static_cast<int>(threadIdx.x);
+      const int64_t srow = (static_cast<int64_t>(b) * H + h) * T;
+      tl = t < T ? lse[srow + t] * kLog2e : 0.f;
+      te = t < T ? delta[srow + t] : 0.f;
     }
+  };
+  auto commit = [&](float* buf) {
+    tq.store(buf, C::kQS);
+    tdo.store(buf + C::kBQ * C::kQS, C::kQS);
+    if (threadIdx.x < C::kBQ) {
+      buf[2 * C::kBQ * C::kQS + threadIdx.x] = tl;
+      buf[2 * C::kBQ * C::kQS + C::kBQ + threadIdx.x] = te;
+    }
+  };
+  issue(0);
+  commit(smem);
+  __syncthreads();
+
+  for (int step = 0; step < nsteps; ++step) {
+    const int qt0 = key0 + (step % ntile) * C::kBQ;
+    const bool more = step + 1 < nsteps;
+    if (more) issue(step + 1);
+    const float* Qs = smem + (step & 1) * C::kBuf;
+    const float* Ds = Qs + C::kBQ * C::kQS;
+    const float* Ls = Qs + 2 * C::kBQ * C::kQS;
+    const float* Es = Ls + C::kBQ;
+    if (qt0 + C::kBQ - 1 >= kw0) {
+      f32x16 s, dp;
+      zero16(s);
+      zero16(dp);
+#pragma unroll
+      for (int s4 = 0; s4 < HALF / 4; ++s4) {
+        const f32x4 qf = *reinterpret_cast<const f32x4*>(Qs + r * C::kQS + HALF * g + 4 * s4);
+        const f32x4 of = *reinterpret_cast<const f32x4*>(Ds + r * C::kQS + HALF * g + 4 * s4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          s = mfma32(qf[j], kreg[4 * s4 + j], s);
+          dp = mfma32(of[j], vreg[4 * s4 + j], dp);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int ql = acc_row(e, g);
+        const int qq = qt0 + ql;
+        const float p = (qq < mykey || qq >= T) ? 0.f : fast_exp2(s[e] - Ls[ql]);
+        s[e] = p;
+        dp[e] = p * (dp[e] - Es[ql]);
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int ql = acc_row(e, g);
+        const auto ov = *reinterpret_cast<const typename DVec<NDT>::T*>(Ds + ql * C::kQS + NDT * r);
+        const auto qv = *reinterpret_cast<const typename DVec<NDT>::T*>(Qs + ql * C::kQS + NDT * r);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          adv[dt] = mfma32(ov[dt], s[e], adv[dt]);
+          adk[dt] = mfma32(qv[dt], dp[e], adk[dt]);
+        }
+      }
+    }
+    if (more) commit(smem + ((step + 1) & 1) * C::kBuf);
+    __syncthreads();
   }
 
-  float* Os = smem;
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int e = 0; e < 16; ++e)
-      Os[(32 * w + r) * C::kOS + dt * 32 + acc_row(e, g)] = adk[dt][e] * scale;
+  acc_to_rows<NDT>(smem, C::kOS, adk, w, g, r, scale);
   __syncthreads();
-  unstage_rows<D>(Os, C::kOS, dk + koff + static_cast<int64_t>(key0) * ks, ks, C::kBKeys, T - key0);
+  unstage_rows<D>(smem, C::kOS, dk + koff + static_cast<int64_t>(key0) * ks, ks, C::kBKeys,
+                  T - key0);
   __syncthreads();
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) Os[(32 * w + r) * C::kOS + dt * 32 + acc_row(e, g)] = adv[dt][e];
+  acc_to_rows<NDT>(smem, C::kOS, adv, w, g, r, 1.0f);
   __syncthreads();
-  unstage_rows<D>(Os, C::kOS, dv + koff + static_cast<int64_t>(key0) * ks, ks, C::kBKeys, T - key0);
+  unstage_rows<D>(smem, C::kOS, dv + koff + static_cast<int64_t>(key0) * ks, ks, C::kBKeys,
+                  T - key0);
 }
 
 int check_shapes(int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D) {
   if (B < 0 || T < 0 || H <= 0 || Hk <= 0 || H % Hk != 0) return EMBER_EINVAL;
   if (D != 64 && D != 128) return EMBER_EINVAL;
   if (T > 0x7fffffff / 2 || H > 65535 || Hk > 65535 || B > 65535) return EMBER_EINVAL;
+  if ((T + 127) / 128 * H * B > 0x7fffffff) return EMBER_EINVAL;  // 1-D grid
   return EMBER_OK;
 }
 
@@ -452,14 +551,13 @@ extern "C" int ember_attn_fwd(const float* q, const float* k, const float* v, fl
   if (B == 0 || T == 0) return EMBER_OK;
   if (!q || !k || !v || !o || !lse) return EMBER_EINVAL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return EMBER_EALIGN;
-  const dim3 grid(static_cast<unsigned>((T + 127) / 128), static_cast<unsigned>(H),
-                  static_cast<unsigned>(B));
+  const dim3 grid(static_cast<unsigned>((T + 127) / 128 * H * B));
   const float sl = scale * kLog2e;
   const int Ti = static_cast<int>(T), Hi = static_cast<int>(H), Hki = static_cast<int>(Hk);
   if (D == 64)
-    attn_fwd_kernel<64><<<grid, 256, 0, as_stream(s)>>>(q, k, v, o, lse, Ti, Hi, Hki, sl);
+    attn_fwd_kernel<64><<<grid, kThreads, 0, as_stream(s)>>>(q, k, v, o, lse, Ti, Hi, Hki, sl);
   else
-    attn_fwd_kernel<128><<<grid, 256, 0, as_stream(s)>>>(q, k, v, o, lse, Ti, Hi, Hki, sl);
+    attn_fwd_kernel<128><<<grid, kThreads, 0, as_stream(s)>>>(q, k, v, o, lse, Ti, Hi, Hki, sl);
   return launch_status();
 }
 
@@ -486,28 +584,26 @@ extern "C" int ember_attn_bwd(const float* q, const float* k, const float* v, co
   const int64_t rows = B * T * H;
   const int Ti = static_cast<int>(T), Hi = static_cast<int>(H), Hki = static_cast<int>(Hk);
   const float sl = scale * kLog2e;
-  const dim3 gq(static_cast<unsigned>((T + 127) / 128), static_cast<unsigned>(H),
-                static_cast<unsigned>(B));
-  const dim3 gk(static_cast<unsigned>((T + 127) / 128), static_cast<unsigned>(Hk),
-                static_cast<unsigned>(B));
+  const dim3 gq(static_cast<unsigned>((T + 127) / 128 * H * B));
+  const dim3 gk(static_cast<unsigned>((T + 127) / 128 * Hk * B));
   if (D == 64) {
-    attn_delta_kernel<64><<<static_cast<unsigned>((rows + 15) / 16), 256, 0, st>>>(o, dout, delta,
-                                                                                  rows, Ti, Hi);
+    attn_delta_kernel<64><<<static_cast<unsigned>((rows + 15) / 16), kThreads, 0, st>>>(
+        o, dout, delta, rows, Ti, Hi);
     if ((rc = launch_status())) return rc;
-    attn_bwd_dq_kernel<64><<<gq, 256, 0, st>>>(q, k, v, dout, lse, delta, dq, Ti, Hi, Hki, sl,
-                                               scale);
+    attn_bwd_dq_kernel<64><<<gq, kThreads, 0, st>>>(q, k, v, dout, lse, delta, dq, Ti, Hi, Hki,
+                                                    sl, scale);
     if ((rc = launch_status())) return rc;
-    attn_bwd_dkdv_kernel<64><<<gk, 256, 0, st>>>(q, k, v, dout, lse, delta, dk, dv, Ti, Hi, Hki,
-                                                 sl, scale);
+    attn_bwd_dkdv_kernel<64><<<gk, kThreads, 0, st>>>(q, k, v, dout, lse, delta, dk, dv, Ti, Hi,
+                                                      Hki, sl, scale);
   } else {
-    attn_delta_kernel<128><<<static_cast<unsigned>((rows + 7) / 8), 256, 0, st>>>(o, dout, delta,
-                                                                                 rows, Ti, Hi);
+    attn_delta_kernel<128><<<static_cast<unsigned>((rows + 7) / 8), kThreads, 0, st>>>(
+        o, dout, delta, rows, Ti, Hi);
     if ((rc = launch_status())) return rc;
-    attn_bwd_dq_kernel<128><<<gq, 256, 0, st>>>(q, k, v, dout, lse, delta, dq, Ti, Hi, Hki, sl,
-                                                scale);
+    attn_bwd_dq_kernel<128><<<gq, kThreads, 0, st>>>(q, k, v, dout, lse, delta, dq, Ti, Hi, Hki,
+                                                     sl, scale);
     if ((rc = launch_status())) return rc;
-    attn_bwd_dkdv_kernel<128><<<gk, 256, 0, st>>>(q, k, v, dout, lse, delta, dk, dv, Ti, Hi, Hki,
-                                                  sl, scale);
+    attn_bwd_dkdv_kernel<128><<<gk, kThreads, 0, st>>>(q, k, v, dout, lse, delta, dk, dv, Ti, Hi,
+                                                       Hki, sl, scale);
   }
   return launch_status();
 }
