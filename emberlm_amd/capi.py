@@ -44,6 +44,9 @@ SIGNATURES = {
     "ember_fill": (i32, [vp, i64, f32, vp]),
     "ember_gemm_f32": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, i64, vp, i64, i64, f32, vp,
                              i64, i64, i64, vp]),
+    "ember_gemm_f32_workspace_bytes": (sz, [i64, i64, i64, i64]),
+    "ember_gemm_f32_ws": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, i64, vp, i64, i64, f32, vp,
+                                i64, i64, i64, vp, sz, vp]),
     "ember_rmsnorm_fwd": (i32, [vp, vp, vp, vp, i64, i64, f32, vp]),
     "ember_rmsnorm_bwd_workspace_bytes": (sz, [i64, i64]),
     "ember_rmsnorm_bwd": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, f32, vp, sz, vp]),

@@ -94,9 +94,13 @@ struct BmmBackward : autograd::Node {
 Tensor matmul_impl(const Tensor& a, const Tensor& b, bool transa, bool transb) {
   const MM d = mm_dims(a, b, transa, transb, "matmul");
   Tensor c = Tensor::empty({d.M, d.N}, DType::kFloat32, a.device());
+  // Weight-gradient shapes (few output tiles, K = tokens) split K into partials.
+  const size_t wsb = ember_gemm_f32_workspace_bytes(d.M, d.N, d.K, 1);
+  Tensor ws = wsb ? workspace(wsb) : Tensor{};
   void* ev = runtime::gemm_profile_begin();
-  CTD_CHECK(ember_gemm_f32(transa, transb, d.M, d.N, d.K, 1.0f, cfp(a), d.lda, 0, cfp(b), d.ldb,
-                           0, 0.0f, fp(c), d.N, 0, 1, S()));
+  CTD_CHECK(ember_gemm_f32_ws(transa, transb, d.M, d.N, d.K, 1.0f, cfp(a), d.lda, 0, cfp(b),
+                              d.ldb, 0, 0.0f, fp(c), d.N, 0, 1, wsb ? ws.data_ptr() : nullptr,
+                              wsb, S()));
   runtime::gemm_profile_end(ev, 2.0 * d.M * d.N * d.K, 2 * transa + transb);
   return c;
 }

@@ -9,22 +9,31 @@
 // lane group g = lane/32 owns k = 8*slab + 4*g + j for step j; A and B use the
 // same permutation, so the contraction is unchanged.
 //
-// Block tile 128x128, 256 threads = 4 waves in 2x2, wave tile 64x64 = 2x2
-// MFMA tiles of 32x32 (64 accumulator registers per lane).  Global loads for
-// stage k+1 are issued before the MFMAs of stage k (double-buffered LDS, one
-// barrier per stage).  Tiles are ordered so that tiles sharing A rows land
-// on the same XCD (block b runs on XCD b % 8) and, within it, in groups of 8
-// tile rows for L2 reuse.
+// Block tiles 128x128 (three blocks per CU) or 256x128 (two per CU), 256
+// threads = 4 waves in 2x2, wave tile (BM/2)x(BN/2) of 32x32 MFMA tiles held
+// in accumulation registers.  A stage is BK = 16 = two k slabs, software
+// pipelined inside one wave so the matrix core never waits on LDS:
+//   global loads of stage k+1 -> registers (issued first),
+//   slab 0 MFMAs interleaved with the LDS reads of slab 1,
+//   slab 1 MFMAs interleaved with the LDS stores of stage k+1,
+//   barrier, then the reads of stage k+1's slab 0 under the last MFMAs.
+// One barrier per stage; LDS is double-buffered.  Tiles are ordered so that
+// tiles sharing A rows land on the same XCD (block b runs on XCD b % 8) and,
+// within it, in groups of 8 tile rows for L2 reuse.
+//
+// Small output grids with a long K (weight gradients: M, N = features,
+// K = tokens) are split along K into a workspace of partial products that a
+// second kernel sums in a fixed order, so results stay bitwise reproducible.
 #include "common.h"
 
 using namespace ember;
 
 namespace {
 
-constexpr int kBM = 128;
-constexpr int kBN = 128;
 constexpr int kThreads = 256;
+constexpr int kBK = 16;
 constexpr int kGroupM = 8;
+constexpr int kCUs = 256;
 
 struct GemmArgs {
   const float* A;
@@ -33,6 +42,7 @@ struct GemmArgs {
   int64_t M, N, K;
   int64_t lda, ldb, ldc;
   int64_t sA, sB, sC;
+  int64_t kchunk;  // > 0: blockIdx.y is a K split of this many k (last one clipped)
   float alpha, beta;
   int tiles_m, tiles_n;
 };
@@ -119,6 +129,7 @@ struct Stage {
   }
 };
 
+template <int BM, int BN>
 __device__ __forceinline__ void tile_coords(const GemmArgs& a, int& tm, int& tn) {
   const int tiles = a.tiles_m * a.tiles_n;
   int t = blockIdx.x;
@@ -132,88 +143,133 @@ __device__ __forceinline__ void tile_coords(const GemmArgs& a, int& tm, int& tn)
   tn = in / gsz;
 }
 
-template <bool A_KC, bool B_KC, bool VEC, int BK>
-__global__ __launch_bounds__(kThreads) void gemm_f32_mfma(GemmArgs a) {
-  using SA = Stage<A_KC, kBM, BK>;
-  using SB = Stage<B_KC, kBN, BK>;
+// Schedules NM MFMAs of the current region with NX instructions of class
+// `mask` spread evenly among them (0x100 LDS read, 0x200 LDS write, 0x008 MFMA).
+template <int NX, int NM, int MASK>
+__device__ __forceinline__ void interleave() {
+  constexpr int per = NM / NX > 0 ? NM / NX : 1;
+#pragma unroll
+  for (int t = 0; t < NX; ++t) {
+    __builtin_amdgcn_sched_group_barrier(MASK, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, per, 0);
+  }
+  if (NM > NX * per) __builtin_amdgcn_sched_group_barrier(0x008, NM - NX * per, 0);
+}
+
+template <bool A_KC, bool B_KC, bool VEC, int BM, int BN, int OCC>
+__global__ __launch_bounds__(kThreads, OCC) void gemm_f32_mfma(GemmArgs a) {
+  using SA = Stage<A_KC, BM, kBK>;
+  using SB = Stage<B_KC, BN, kBK>;
+  constexpr int FI = BM / 64, FJ = BN / 64;             // 32x32 tiles per wave
+  constexpr int NR = FI * (A_KC ? 1 : 4) + FJ * (B_KC ? 1 : 4);  // LDS reads per slab
+  constexpr int NW = SA::kPerThread + SB::kPerThread;   // LDS stores per stage
+  constexpr int NM = 4 * FI * FJ;                       // MFMAs per slab
   __shared__ __attribute__((aligned(16))) float lds_a[2][SA::kSize];
   __shared__ __attribute__((aligned(16))) float lds_b[2][SB::kSize];
 
   int tm, tn;
-  tile_coords(a, tm, tn);
+  tile_coords<BM, BN>(a, tm, tn);
   const int64_t bz = blockIdx.y;
   const float* __restrict__ A = a.A + bz * a.sA;
   const float* __restrict__ B = a.B + bz * a.sB;
   float* __restrict__ C = a.C + bz * a.sC;
-  const int64_t m0 = static_cast<int64_t>(tm) * kBM;
-  const int64_t n0 = static_cast<int64_t>(tn) * kBN;
+  const int64_t K = a.kchunk > 0 ? min(a.kchunk, a.K - bz * a.kchunk) : a.K;
+  const int64_t m0 = static_cast<int64_t>(tm) * BM;
+  const int64_t n0 = static_cast<int64_t>(tn) * BN;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int g = lane >> 5, r = lane & 31;
+  const int arow = wm * (BM / 2) + r, brow = wn * (BN / 2) + r;
 
-  f32x16 acc[2][2];
+  f32x16 acc[FI][FJ];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < FI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < FJ; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   SA sa;
   SB sb;
-  const int64_t nk = (a.K + BK - 1) / BK;
+  const int64_t nk = (K + kBK - 1) / kBK;
   if (nk > 0) {
-    sa.template load<VEC>(A, a.lda, a.M, a.K, m0, 0);
-    sb.template load<VEC>(B, a.ldb, a.N, a.K, n0, 0);
+    sa.template load<VEC>(A, a.lda, a.M, K, m0, 0);
+    sb.template load<VEC>(B, a.ldb, a.N, K, n0, 0);
     sa.store(lds_a[0]);
     sb.store(lds_b[0]);
   }
   __syncthreads();
 
+  f32x4 fa0[FI], fb0[FJ], fa1[FI], fb1[FJ];
+#pragma unroll
+  for (int i = 0; i < FI; ++i) fa0[i] = SA::frag(lds_a[0], arow + i * 32, 0, g);
+#pragma unroll
+  for (int j = 0; j < FJ; ++j) fb0[j] = SB::frag(lds_b[0], brow + j * 32, 0, g);
+
   for (int64_t kt = 0; kt < nk; ++kt) {
     const int cur = static_cast<int>(kt & 1);
-    const bool more = kt + 1 < nk;
-    if (more) {
-      sa.template load<VEC>(A, a.lda, a.M, a.K, m0, (kt + 1) * BK);
-      sb.template load<VEC>(B, a.ldb, a.N, a.K, n0, (kt + 1) * BK);
-    }
+    // Stage kt+1; the last iteration reloads its own stage into the idle
+    // buffer, which nothing reads afterwards.
+    const int64_t knext = (kt + 1 < nk ? kt + 1 : kt) * kBK;
+    sa.template load<VEC>(A, a.lda, a.M, K, m0, knext);
+    sb.template load<VEC>(B, a.ldb, a.N, K, n0, knext);
     const float* la = lds_a[cur];
     const float* lb = lds_b[cur];
+    float* na = lds_a[cur ^ 1];
+    float* nb = lds_b[cur ^ 1];
+
 #pragma unroll
-    for (int slab = 0; slab < BK / 8; ++slab) {
-      f32x4 fa[2], fb[2];
+    for (int i = 0; i < FI; ++i) fa1[i] = SA::frag(la, arow + i * 32, 1, g);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) fa[i] = SA::frag(la, wm * 64 + i * 32 + r, slab, g);
+    for (int j = 0; j < FJ; ++j) fb1[j] = SB::frag(lb, brow + j * 32, 1, g);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) fb[j] = SB::frag(lb, wn * 64 + j * 32 + r, slab, g);
+    for (int s = 0; s < 4; ++s)
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
+      for (int i = 0; i < FI; ++i)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int j = 0; j < FJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa0[i][s], fb0[j][s], acc[i][j], 0, 0, 0);
+    interleave<NR, NM, 0x100>();
+
+    sa.store(na);
+    sb.store(nb);
 #pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
-    }
-    if (more) {
-      sa.store(lds_a[cur ^ 1]);
-      sb.store(lds_b[cur ^ 1]);
-    }
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int i = 0; i < FI; ++i)
+#pragma unroll
+        for (int j = 0; j < FJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[i][s], fb1[j][s], acc[i][j], 0, 0, 0);
+    interleave<NW, NM / 2, 0x200>();
     __syncthreads();
+
+#pragma unroll
+    for (int i = 0; i < FI; ++i) fa0[i] = SA::frag(na, arow + i * 32, 0, g);
+#pragma unroll
+    for (int j = 0; j < FJ; ++j) fb0[j] = SB::frag(nb, brow + j * 32, 0, g);
+#pragma unroll
+    for (int s = 2; s < 4; ++s)
+#pragma unroll
+      for (int i = 0; i < FI; ++i)
+#pragma unroll
+        for (int j = 0; j < FJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[i][s], fb1[j][s], acc[i][j], 0, 0, 0);
+    interleave<NR, NM / 2, 0x100>();
   }
 
   // Accumulator layout of a 32x32 MFMA tile: lane (g, r), register e holds
   // row 8*(e/4) + 4*g + (e%4), column r.
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < FI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t col = n0 + wn * 64 + j * 32 + r;
+    for (int j = 0; j < FJ; ++j) {
+      const int64_t col = n0 + wn * (BN / 2) + j * 32 + r;
       if (col >= a.N) continue;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int64_t row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+        const int64_t row = m0 + wm * (BM / 2) + i * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
         if (row < a.M) {
           float* dst = C + row * a.ldc + col;
           const float v = a.alpha * acc[i][j][e];
@@ -223,36 +279,157 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_mfma(GemmArgs a) {
     }
 }
 
-template <bool A_KC, bool B_KC>
-int launch(const GemmArgs& a, int64_t batch, bool vec, hipStream_t st) {
-  dim3 grid(static_cast<unsigned>(a.tiles_m) * a.tiles_n, static_cast<unsigned>(batch));
+// C = alpha * sum_{s<S} P[s] + beta * C, the split partials summed in order.
+// P is [S][M][N] dense; four columns per thread when the rows allow it.
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void splitk_reduce(const float* __restrict__ P, float* C,
+                                                          int64_t M, int64_t N, int64_t ldc,
+                                                          int S, float alpha, float beta) {
+  const int64_t per = VEC ? 4 : 1;
+  const int64_t cols = N / per;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= M * cols) return;
+  const int64_t m = i / cols, n = (i % cols) * per;
+  const int64_t plane = M * N;
+  if (VEC) {
+    f32x4 s = *reinterpret_cast<const f32x4*>(P + m * N + n);
+    for (int k = 1; k < S; ++k) {
+      const f32x4 t = *reinterpret_cast<const f32x4*>(P + k * plane + m * N + n);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s[e] += t[e];
+    }
+    f32x4* dst = reinterpret_cast<f32x4*>(C + m * ldc + n);
+    f32x4 out;
+    const f32x4 old = beta != 0.f ? *dst : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[e] = beta != 0.f ? alpha * s[e] + beta * old[e] : alpha * s[e];
+    *dst = out;
+  } else {
+    float s = P[m * N + n];
+    for (int k = 1; k < S; ++k) s += P[k * plane + m * N + n];
+    float* dst = C + m * ldc + n;
+    *dst = beta != 0.f ? alpha * s + beta * *dst : alpha * s;
+  }
+}
+
+// Launch plan for one call.
+struct Plan {
+  bool big;         // 256x128 tiles (else 128x128)
+  int64_t splits;   // 1 = no K split
+  int64_t kchunk;   // k per split (multiple of kBK)
+};
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch) {
+  Plan p{false, 1, 0};
+  const int64_t big_tiles = cdiv(M, 256) * cdiv(N, 128) * batch;
+  if (big_tiles >= 4 * kCUs) {  // at least two full waves of 2 blocks per CU
+    p.big = true;
+    return p;
+  }
+  const int64_t tiles = cdiv(M, 128) * cdiv(N, 128) * batch;
+  const int64_t target = 6 * kCUs;  // two waves of 3 blocks per CU
+  if (batch == 1 && tiles < target && K >= 4096) {
+    int64_t s = std::min<int64_t>(16, cdiv(target, tiles));
+    s = std::min<int64_t>(s, K / 1024);
+    if (s >= 2) {
+      p.kchunk = cdiv(cdiv(K, s), kBK) * kBK;
+      p.splits = cdiv(K, p.kchunk);
+    }
+  }
+  return p;
+}
+
+template <bool A_KC, bool B_KC, int BM, int BN, int OCC>
+int launch(const GemmArgs& a, int64_t ny, bool vec, hipStream_t st) {
+  dim3 grid(static_cast<unsigned>(a.tiles_m) * a.tiles_n, static_cast<unsigned>(ny));
   if (vec)
-    gemm_f32_mfma<A_KC, B_KC, true, 16><<<grid, kThreads, 0, st>>>(a);
+    gemm_f32_mfma<A_KC, B_KC, true, BM, BN, OCC><<<grid, kThreads, 0, st>>>(a);
   else
-    gemm_f32_mfma<A_KC, B_KC, false, 16><<<grid, kThreads, 0, st>>>(a);
+    gemm_f32_mfma<A_KC, B_KC, false, BM, BN, OCC><<<grid, kThreads, 0, st>>>(a);
   return launch_status();
 }
 
+template <int BM, int BN, int OCC>
+int launch_t(GemmArgs a, bool a_kc, bool b_kc, int64_t ny, bool vec, hipStream_t st) {
+  a.tiles_m = static_cast<int>(cdiv(a.M, BM));
+  a.tiles_n = static_cast<int>(cdiv(a.N, BN));
+  if (a_kc && b_kc) return launch<true, true, BM, BN, OCC>(a, ny, vec, st);
+  if (a_kc && !b_kc) return launch<true, false, BM, BN, OCC>(a, ny, vec, st);
+  if (!a_kc && !b_kc) return launch<false, false, BM, BN, OCC>(a, ny, vec, st);
+  return launch<false, true, BM, BN, OCC>(a, ny, vec, st);
+}
+
+int check_args(int transa, int transb, int64_t M, int64_t N, int64_t K, const float* A,
+               int64_t lda, const float* B, int64_t ldb, const float* C, int64_t ldc,
+               int64_t batch) {
+  if (M < 0 || N < 0 || K < 0 || batch < 1) return EMBER_EINVAL;
+  if (M == 0 || N == 0) return EMBER_OK;
+  if (!C || (K > 0 && (!A || !B))) return EMBER_EINVAL;
+  if (lda < (transa ? M : K) || ldb < (transb ? K : N) || ldc < N) return EMBER_EINVAL;
+  if (cdiv(M, 128) * cdiv(N, 128) > 0x7fffffff || batch > 65535) return EMBER_EINVAL;
+  return EMBER_OK;
+}
+
 }  // namespace
+
+extern "C" size_t ember_gemm_f32_workspace_bytes(int64_t M, int64_t N, int64_t K,
+                                                 int64_t batch) {
+  if (M <= 0 || N <= 0 || K <= 0 || batch < 1) return 0;
+  const Plan p = make_plan(M, N, K, batch);
+  return p.splits > 1 ? static_cast<size_t>(p.splits * M * N) * sizeof(float) : 0;
+}
+
+extern "C" int ember_gemm_f32_ws(int transa, int transb, int64_t M, int64_t N, int64_t K,
+                                 float alpha, const float* A, int64_t lda, int64_t sA,
+                                 const float* B, int64_t ldb, int64_t sB, float beta, float* C,
+                                 int64_t ldc, int64_t sC, int64_t batch, void* workspace,
+                                 size_t workspace_bytes, ember_stream_t s) {
+  int rc = check_args(transa, transb, M, N, K, A, lda, B, ldb, C, ldc, batch);
+  if (rc || M == 0 || N == 0) return rc;
+  GemmArgs a{A, B, C, M, N, K, lda, ldb, ldc, sA, sB, sC, 0, alpha, beta, 0, 0};
+  const bool vec = aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0) &&
+                   (batch == 1 || (sA % 4 == 0 && sB % 4 == 0));
+  hipStream_t st = as_stream(s);
+  const bool a_kc = !transa, b_kc = transb != 0;
+  Plan p = make_plan(M, N, K, batch);
+  if (p.splits > 1 &&
+      (!workspace || workspace_bytes < static_cast<size_t>(p.splits * M * N) * sizeof(float)))
+    p.splits = 1;  // no room for partials: one pass over K
+  if (p.splits > 1) {
+    // Split s computes A[:, s*kchunk ...] B[s*kchunk ..., :] into plane s.
+    GemmArgs sp = a;
+    sp.C = static_cast<float*>(workspace);
+    sp.ldc = N;
+    sp.sA = a_kc ? p.kchunk : p.kchunk * lda;
+    sp.sB = b_kc ? p.kchunk : p.kchunk * ldb;
+    sp.sC = M * N;
+    sp.kchunk = p.kchunk;
+    sp.alpha = 1.f;
+    sp.beta = 0.f;
+    if ((rc = launch_t<128, 128, 3>(sp, a_kc, b_kc, p.splits, vec, st))) return rc;
+    const bool rvec = (N % 4 == 0) && (ldc % 4 == 0) && aligned16(C);
+    const int64_t items = M * (rvec ? N / 4 : N);
+    const unsigned blocks = static_cast<unsigned>(cdiv(items, kThreads));
+    if (rvec)
+      splitk_reduce<true><<<blocks, kThreads, 0, st>>>(static_cast<const float*>(workspace), C, M,
+                                                       N, ldc, static_cast<int>(p.splits),
+                                                       alpha, beta);
+    else
+      splitk_reduce<false><<<blocks, kThreads, 0, st>>>(static_cast<const float*>(workspace), C,
+                                                        M, N, ldc, static_cast<int>(p.splits),
+                                                        alpha, beta);
+    return launch_status();
+  }
+  if (p.big) return launch_t<256, 128, 2>(a, a_kc, b_kc, batch, vec, st);
+  return launch_t<128, 128, 3>(a, a_kc, b_kc, batch, vec, st);
+}
 
 extern "C" int ember_gemm_f32(int transa, int transb, int64_t M, int64_t N, int64_t K,
                               float alpha, const float* A, int64_t lda, int64_t sA,
                               const float* B, int64_t ldb, int64_t sB, float beta, float* C,
                               int64_t ldc, int64_t sC, int64_t batch, ember_stream_t s) {
-  if (M < 0 || N < 0 || K < 0 || batch < 1) return EMBER_EINVAL;
-  if (M == 0 || N == 0) return EMBER_OK;
-  if (!C || (K > 0 && (!A || !B))) return EMBER_EINVAL;
-  if (lda < (transa ? M : K) || ldb < (transb ? K : N) || ldc < N) return EMBER_EINVAL;
-  const int64_t tm = (M + kBM - 1) / kBM, tn = (N + kBN - 1) / kBN;
-  if (tm * tn > 0x7fffffff || batch > 65535) return EMBER_EINVAL;
-  GemmArgs a{A, B, C, M, N, K, lda, ldb, ldc, sA, sB, sC, alpha, beta,
-             static_cast<int>(tm), static_cast<int>(tn)};
-  const bool vec = aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0) &&
-                   (batch == 1 || (sA % 4 == 0 && sB % 4 == 0));
-  hipStream_t st = as_stream(s);
-  const bool a_kc = !transa, b_kc = transb != 0;
-  if (a_kc && b_kc) return launch<true, true>(a, batch, vec, st);
-  if (a_kc && !b_kc) return launch<true, false>(a, batch, vec, st);
-  if (!a_kc && !b_kc) return launch<false, false>(a, batch, vec, st);
-  return launch<false, true>(a, batch, vec, st);
+  return ember_gemm_f32_ws(transa, transb, M, N, K, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc,
+                           sC, batch, nullptr, 0, s);
 }

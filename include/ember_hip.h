@@ -90,6 +90,17 @@ int ember_gemm_f32(int transa, int transb, int64_t M, int64_t N, int64_t K, floa
                    const float* A, int64_t lda, int64_t sA, const float* B, int64_t ldb,
                    int64_t sB, float beta, float* C, int64_t ldc, int64_t sC, int64_t batch,
                    ember_stream_t s);
+/* The same product with a workspace: when the output grid is too small to fill
+ * the GPU and K is long (weight gradients, K = tokens), K is split into partial
+ * products in `workspace` that are then summed in a fixed order, so results are
+ * reproducible run to run.  ember_gemm_f32_workspace_bytes gives the size this
+ * call can use (0: no split for this shape); a smaller or NULL workspace runs
+ * the unsplit kernel.  ember_gemm_f32 is this call with no workspace. */
+size_t ember_gemm_f32_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t batch);
+int ember_gemm_f32_ws(int transa, int transb, int64_t M, int64_t N, int64_t K, float alpha,
+                      const float* A, int64_t lda, int64_t sA, const float* B, int64_t ldb,
+                      int64_t sB, float beta, float* C, int64_t ldc, int64_t sC, int64_t batch,
+                      void* workspace, size_t workspace_bytes, ember_stream_t s);
 
 /* -------------------------------------------------------------- RMSNorm
  * y = x * rsqrt(mean(x^2) + eps) * w over rows of length H; rstd[rows] (may be
