@@ -37,6 +37,7 @@ SIGNATURES = {
     "ember_event_destroy": (i32, [vp]),
     "ember_event_record": (i32, [vp, vp]),
     "ember_event_synchronize": (i32, [vp]),
+    "ember_event_query": (i32, [vp]),
     "ember_stream_wait_event": (i32, [vp, vp]),
     "ember_event_elapsed_ms": (i32, [C.POINTER(f32), vp, vp]),
     "ember_device_info": (i32, [C.c_char_p, sz, C.POINTER(i32), C.POINTER(sz)]),
@@ -78,6 +79,7 @@ SIGNATURES = {
     "ember_embedding_bwd_workspace_bytes": (sz, [i64, i64]),
     "ember_embedding_bwd": (i32, [vp, vp, vp, i64, i64, i64, i32, vp, sz, vp]),
     "ember_adamw": (i32, [vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, f32, f32, vp]),
+    "ember_adamw_bounded": (i32, [vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, f32, f32, i32, vp]),
     "ember_sumsq_workspace_bytes": (sz, [i32]),
     "ember_sumsq_multi": (i32, [C.POINTER(vp), C.POINTER(i64), i32, vp, vp, sz, vp]),
 }

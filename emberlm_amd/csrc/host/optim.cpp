@@ -3,17 +3,28 @@
 // Reference: src/core/optim.cu:77-293.  The offloaded path there keeps m/v in
 // pageable host memory and runs, per parameter, two synchronous H2D copies,
 // the kernel and two synchronous D2H copies (optim.cu:176-210).  Here m/v are
-// page-locked, every parameter is cut into chunks of chunk_elems_ floats, and
-// chunk i flows through a ring of kSlots device buffers:
+// page-locked and laid out as one flat buffer each, parameters back to back in
+// streaming order (each starting on a 256-byte boundary), and the buffer is
+// cut into chunks of chunk_elems_ floats that may span several parameters --
+// a per-parameter cut would send hundreds of tiny norm-weight transfers,
+// whose fixed cost halves the link rate.  Chunk i flows through a ring of
+// kSlots device buffers:
 //
-//   h2d stream:     wait drained[s] -> copy m,v chunk i in  -> record loaded[s]
-//   compute stream: wait loaded[s]  -> AdamW on chunk i      -> record updated[s]
-//   d2h stream:     wait updated[s] -> copy m,v chunk i out -> record drained[s]
+//   h2d stream: wait drained[s] -> copy m,v chunk i in -> record loaded[s]
+//   d2h stream: wait loaded[s]  -> AdamW on each parameter piece of chunk i
+//               -> copy m,v chunk i out -> record drained[s]
 //
-// with s = i % kSlots, so the copies in of chunk i+1, the update of chunk i
-// and the copies out of chunk i-1 run at the same time, and both link
-// directions stay busy.  The compute stream finally waits for the last copy
-// out, so anything ordered after step() sees the finished state.
+// with s = i % kSlots, so the copies in of chunks i+1.. run while chunk i is
+// updated and copied out, and both link directions stay busy.  The update
+// kernels start after everything the compute stream has enqueued so far
+// (backward, clipping).  The compute
+// stream is not made to wait for the whole step: each parameter's storage
+// (and its gradient's) gets the event recorded after its last chunk's update,
+// and the first data_ptr() of that storage makes the compute stream wait for
+// exactly that event.  The next forward therefore starts as soon as its first
+// parameters are updated and the remaining transfers hide behind it.  Each
+// gradient stays alive until its parameter's update has run (release_after),
+// since zero_grad() lets go of it while the update may still be reading it.
 #include <algorithm>
 #include <chrono>
 #include <cmath>
@@ -25,6 +36,13 @@
 namespace ctd::optim {
 
 using namespace ctd::ops::detail;
+
+namespace {
+// Workgroups of one chunk update: one per CU.  A chunk is 448 MB of HBM
+// traffic per 2.6 ms of link time, far below what 256 resident workgroups
+// stream, and they fit next to the forward's GEMM blocks.
+constexpr int kUpdateBlocks = 256;
+}  // namespace
 
 AdamW::AdamW(std::vector<Tensor> params, float lr, float weight_decay, float beta1, float beta2,
              float eps, bool offload)
@@ -43,7 +61,19 @@ AdamW::AdamW(std::vector<ParamGroup> groups, float beta1, float beta2, float eps
 }
 
 AdamW::~AdamW() {
-  if (ev_done_) ember_event_synchronize(ev_done_);
+  if (in_flight_ && ev_done_) ember_event_synchronize(ev_done_);
+  runtime::collect_released();
+  // Our events die with us: no storage may keep pointing at them.
+  for (size_t gi = 0; gi < ev_param_.size(); ++gi)
+    for (size_t pi = 0; pi < ev_param_[gi].size(); ++pi) {
+      Tensor& p = groups_[gi].params[pi];
+      if (p.storage() && p.storage()->ready_event() == ev_param_[gi][pi])
+        p.storage()->set_ready_event(nullptr);
+      Tensor g = p.grad();
+      if (g.storage() && g.storage()->ready_event() == ev_param_[gi][pi])
+        g.storage()->set_ready_event(nullptr);
+      ember_event_destroy(ev_param_[gi][pi]);
+    }
   for (int s = 0; s < kSlots; ++s) {
     ember_device_free(d_m_[s]);
     ember_device_free(d_v_[s]);
@@ -52,9 +82,47 @@ AdamW::~AdamW() {
     ember_event_destroy(ev_drained_[s]);
   }
   ember_event_destroy(ev_done_);
+  ember_event_destroy(ev_begin_);
+  ember_event_destroy(ev_start_);
 }
 
+Tensor& AdamW::m_tensor(size_t gi, size_t pi) {
+  wait_idle();
+  return state_.at(gi).at(pi).m;
+}
+
+Tensor& AdamW::v_tensor(size_t gi, size_t pi) {
+  wait_idle();
+  return state_.at(gi).at(pi).v;
+}
+
+void AdamW::set_update_order(std::vector<std::pair<size_t, size_t>> order) {
+  for (const auto& [gi, pi] : order)
+    if (gi >= groups_.size() || pi >= groups_[gi].params.size())
+      throw std::runtime_error("AdamW::set_update_order: index out of range");
+  if (!layout_.empty() && order != order_)
+    throw std::runtime_error("AdamW::set_update_order: optimizer state already laid out");
+  order_ = std::move(order);
+}
+
+void AdamW::wait_idle() {
+  if (in_flight_) {
+    CTD_CHECK(ember_event_synchronize(ev_done_));
+    float ms = 0.f;
+    CTD_CHECK(ember_event_elapsed_ms(&ms, ev_begin_, ev_done_));
+    stats_.last_stream_ms = ms;
+    in_flight_ = false;
+  }
+  runtime::collect_released();
+}
+
+const OffloadStats& AdamW::offload_stats() { return stats_; }
+
 void AdamW::ensure_state_initialized() {
+  if (offload_) {
+    init_offload_state();
+    return;
+  }
   for (size_t gi = 0; gi < groups_.size(); ++gi) init_state_for_group(gi);
 }
 
@@ -64,22 +132,46 @@ void AdamW::init_state_for_group(size_t gi) {
   if (st.size() == g.params.size()) return;
   st.clear();
   st.reserve(g.params.size());
-  int64_t largest = 0;
   for (const auto& p : g.params) {
     State s;
-    if (offload_) {
-      s.m = Tensor::zeros_pinned(p.shape(), p.dtype());
-      s.v = Tensor::zeros_pinned(p.shape(), p.dtype());
-    } else {
-      s.m = Tensor::zeros(p.shape(), p.dtype(), p.device());
-      s.v = Tensor::zeros(p.shape(), p.dtype(), p.device());
-    }
-    largest = std::max(largest, p.numel());
+    s.m = Tensor::zeros(p.shape(), p.dtype(), p.device());
+    s.v = Tensor::zeros(p.shape(), p.dtype(), p.device());
     st.push_back(std::move(s));
   }
-  if (offload_ && !d_m_[0]) {
-    // Slots never need to be larger than the largest parameter of the group.
-    chunk_elems_ = std::max<int64_t>(1, std::min(chunk_elems_, largest));
+}
+
+void AdamW::init_offload_state() {
+  if (!layout_.empty() || groups_.empty()) return;
+  // Streaming order: the requested one, then whatever it left out.
+  std::vector<std::vector<bool>> seen(groups_.size());
+  for (size_t gi = 0; gi < groups_.size(); ++gi) seen[gi].assign(groups_[gi].params.size(), false);
+  std::vector<std::pair<size_t, size_t>> items;
+  for (const auto& it : order_)
+    if (!seen[it.first][it.second]) {
+      seen[it.first][it.second] = true;
+      items.push_back(it);
+    }
+  for (size_t gi = 0; gi < groups_.size(); ++gi)
+    for (size_t pi = 0; pi < groups_[gi].params.size(); ++pi)
+      if (!seen[gi][pi]) items.emplace_back(gi, pi);
+  int64_t off = 0;
+  for (const auto& [gi, pi] : items) {
+    const int64_t n = groups_[gi].params[pi].numel();
+    layout_.push_back({gi, pi, off, n});
+    off += (n + 63) / 64 * 64;
+  }
+  flat_n_ = off;
+  flat_m_ = Tensor::zeros_pinned({std::max<int64_t>(flat_n_, 1)}, DType::kFloat32);
+  flat_v_ = Tensor::zeros_pinned({std::max<int64_t>(flat_n_, 1)}, DType::kFloat32);
+  for (size_t gi = 0; gi < groups_.size(); ++gi) state_[gi].assign(groups_[gi].params.size(), {});
+  for (const auto& sg : layout_) {
+    const Tensor& p = groups_[sg.gi].params[sg.pi];
+    state_[sg.gi][sg.pi].m = flat_m_.view_at(sg.off, p.shape());
+    state_[sg.gi][sg.pi].v = flat_v_.view_at(sg.off, p.shape());
+  }
+  if (!d_m_[0]) {
+    // Slots never need to be larger than the whole state.
+    chunk_elems_ = std::max<int64_t>(64, std::min(chunk_elems_, flat_n_));
     for (int s = 0; s < kSlots; ++s) {
       void* pm = nullptr;
       void* pv = nullptr;
@@ -92,7 +184,16 @@ void AdamW::init_state_for_group(size_t gi) {
       CTD_CHECK(ember_event_create(&ev_drained_[s]));
     }
     CTD_CHECK(ember_event_create(&ev_done_));
+    CTD_CHECK(ember_event_create(&ev_begin_));
+    CTD_CHECK(ember_event_create(&ev_start_));
   }
+  ev_param_.resize(groups_.size());
+  for (size_t gi = 0; gi < groups_.size(); ++gi)
+    while (ev_param_[gi].size() < groups_[gi].params.size()) {
+      void* e = nullptr;
+      CTD_CHECK(ember_event_create(&e));
+      ev_param_[gi].push_back(e);
+    }
 }
 
 void AdamW::step() {
@@ -126,50 +227,87 @@ void AdamW::step_offloaded() {
   const auto t0 = std::chrono::steady_clock::now();
   const float bc1 = 1.0f - std::pow(beta1_, static_cast<float>(step_));
   const float bc2 = 1.0f - std::pow(beta2_, static_cast<float>(step_));
-  for (size_t gi = 0; gi < groups_.size(); ++gi) init_state_for_group(gi);
+  init_offload_state();
+  // The previous step has long finished by now (the forward and backward in
+  // between waited for every parameter it updated); this also frees its ring
+  // slots and hands back the gradients it kept.
+  wait_idle();
+  // The update kernels share the d2h stream: each chunk's kernels then its
+  // copies out, in order.  A separate kernel stream would cost one more
+  // hardware queue, and with more streams than queues the runtime makes
+  // streams share queues, which serialises them against the compute stream.
   ember_stream_t cs = S(), hs = runtime::h2d_stream(), ds = runtime::d2h_stream();
+  CTD_CHECK(ember_event_record(ev_start_, cs));
+  CTD_CHECK(ember_stream_wait_event(ds, ev_start_));
+  CTD_CHECK(ember_event_record(ev_begin_, hs));
 
-  // Grads and params are produced on the compute stream; the copy streams only
-  // touch the pinned host state and the ring buffers, so they need no wait for
-  // the backward pass.  The previous step's last copy out must be finished
-  // before this step overwrites the same host buffers' device copies.
-  if (step_ > 1) CTD_CHECK(ember_stream_wait_event(hs, ev_done_));
+  // Device pointers of every parameter with a gradient, in layout order
+  // (taken before any storage gets this step's ready event).
+  struct Work {
+    float* p = nullptr;
+    const float* g = nullptr;
+  };
+  std::vector<Work> work(layout_.size());
+  for (size_t k = 0; k < layout_.size(); ++k) {
+    const Segment& sg = layout_[k];
+    Tensor& p = groups_[sg.gi].params[sg.pi];
+    Tensor g = p.grad();
+    if (!g.storage()) continue;
+    if (g.shape() != p.shape()) throw std::runtime_error("AdamW: param/grad shape mismatch");
+    work[k] = {fp(p), cfp(g)};
+  }
 
+  float* hm = static_cast<float*>(flat_m_.data_ptr());
+  float* hv = static_cast<float*>(flat_v_.data_ptr());
+  size_t k = 0;  // first segment not yet finished
   int64_t chunk = 0;
   double bytes = 0.0;
-  for (size_t gi = 0; gi < groups_.size(); ++gi) {
-    auto& group = groups_[gi];
-    auto& st = state_[gi];
-    for (size_t pi = 0; pi < group.params.size(); ++pi) {
-      Tensor& p = group.params[pi];
-      Tensor g = p.grad();
-      if (!g.storage()) continue;
-      if (g.shape() != p.shape()) throw std::runtime_error("AdamW: param/grad shape mismatch");
-      float* hm = static_cast<float*>(st[pi].m.data_ptr());
-      float* hv = static_cast<float*>(st[pi].v.data_ptr());
-      const int64_t n = p.numel();
-      for (int64_t off = 0; off < n; off += chunk_elems_, ++chunk) {
-        const int64_t len = std::min(chunk_elems_, n - off);
-        const size_t nb = static_cast<size_t>(len) * sizeof(float);
-        const int s = static_cast<int>(chunk % kSlots);
-        if (chunk >= kSlots) CTD_CHECK(ember_stream_wait_event(hs, ev_drained_[s]));
-        CTD_CHECK(ember_memcpy_async(d_m_[s], hm + off, nb, 0, hs));
-        CTD_CHECK(ember_memcpy_async(d_v_[s], hv + off, nb, 0, hs));
-        CTD_CHECK(ember_event_record(ev_loaded_[s], hs));
-        CTD_CHECK(ember_stream_wait_event(cs, ev_loaded_[s]));
-        CTD_CHECK(ember_adamw(fp(p) + off, cfp(g) + off, d_m_[s], d_v_[s], len, group.lr, beta1_,
-                              beta2_, eps_, group.weight_decay, bc1, bc2, cs));
-        CTD_CHECK(ember_event_record(ev_updated_[s], cs));
-        CTD_CHECK(ember_stream_wait_event(ds, ev_updated_[s]));
-        CTD_CHECK(ember_memcpy_async(hm + off, d_m_[s], nb, 1, ds));
-        CTD_CHECK(ember_memcpy_async(hv + off, d_v_[s], nb, 1, ds));
-        CTD_CHECK(ember_event_record(ev_drained_[s], ds));
-        bytes += 2.0 * static_cast<double>(nb);
+  for (int64_t c0 = 0; c0 < flat_n_; c0 += chunk_elems_, ++chunk) {
+    const int64_t len = std::min(chunk_elems_, flat_n_ - c0);
+    const size_t nb = static_cast<size_t>(len) * sizeof(float);
+    const int s = static_cast<int>(chunk % kSlots);
+    if (chunk >= kSlots) CTD_CHECK(ember_stream_wait_event(hs, ev_drained_[s]));
+    CTD_CHECK(ember_memcpy_async(d_m_[s], hm + c0, nb, 0, hs));
+    CTD_CHECK(ember_memcpy_async(d_v_[s], hv + c0, nb, 0, hs));
+    CTD_CHECK(ember_event_record(ev_loaded_[s], hs));
+    CTD_CHECK(ember_stream_wait_event(ds, ev_loaded_[s]));
+    // Update every parameter piece inside [c0, c0 + len).
+    while (k < layout_.size() && layout_[k].off < c0 + len) {
+      const Segment& sg = layout_[k];
+      const int64_t lo = std::max(sg.off, c0), hi = std::min(sg.off + sg.n, c0 + len);
+      if (work[k].p && hi > lo) {
+        const ParamGroup& group = groups_[sg.gi];
+        CTD_CHECK(ember_adamw_bounded(work[k].p + (lo - sg.off), work[k].g + (lo - sg.off),
+                                      d_m_[s] + (lo - c0), d_v_[s] + (lo - c0), hi - lo, group.lr,
+                                      beta1_, beta2_, eps_, group.weight_decay, bc1, bc2,
+                                      kUpdateBlocks, ds));
       }
+      if (sg.off + sg.n > c0 + len) break;  // continues in the next chunk
+      if (work[k].p) {
+        CTD_CHECK(ember_event_record(ev_param_[sg.gi][sg.pi], ds));
+        // The gradient is dead once its update has run: hand its block back
+        // then, not at the end of the step, so the next forward does not
+        // carry it.
+        runtime::release_after(ev_param_[sg.gi][sg.pi],
+                               {groups_[sg.gi].params[sg.pi].grad().storage()});
+      }
+      ++k;
     }
+    CTD_CHECK(ember_memcpy_async(hm + c0, d_m_[s], nb, 1, ds));
+    CTD_CHECK(ember_memcpy_async(hv + c0, d_v_[s], nb, 1, ds));
+    CTD_CHECK(ember_event_record(ev_drained_[s], ds));
+    bytes += 2.0 * static_cast<double>(nb);
   }
   CTD_CHECK(ember_event_record(ev_done_, ds));
-  CTD_CHECK(ember_stream_wait_event(cs, ev_done_));
+  // Only now, after the last data_ptr() above: later users of a parameter or
+  // its gradient on the compute stream wait for that parameter's update.
+  for (size_t j = 0; j < layout_.size(); ++j) {
+    if (!work[j].p) continue;
+    Tensor& p = groups_[layout_[j].gi].params[layout_[j].pi];
+    p.storage()->set_ready_event(ev_param_[layout_[j].gi][layout_[j].pi]);
+    p.grad().storage()->set_ready_event(ev_param_[layout_[j].gi][layout_[j].pi]);
+  }
+  in_flight_ = true;
   stats_.last_h2d_bytes = bytes;
   stats_.last_d2h_bytes = bytes;
   stats_.last_step_ms =

@@ -48,6 +48,63 @@ ember_stream_t d2h_stream() { return streams().d2h; }
 
 void synchronize() { check(ember_stream_synchronize(compute_stream()), "synchronize"); }
 
+void wait_ready(Storage& s) {
+  if (void* e = s.take_ready_event()) check(ember_stream_wait_event(compute_stream(), e), "wait_ready");
+}
+
+namespace {
+struct Deferred {
+  std::mutex mu;
+  std::vector<std::pair<ember_event_t, std::vector<StoragePtr>>> items;
+};
+Deferred& deferred() {
+  static Deferred d;
+  return d;
+}
+}  // namespace
+
+void release_after(ember_event_t done, std::vector<StoragePtr> keep) {
+  Deferred& d = deferred();
+  std::lock_guard<std::mutex> lk(d.mu);
+  d.items.emplace_back(done, std::move(keep));
+}
+
+size_t collect_released() {
+  Deferred& d = deferred();
+  std::vector<std::vector<StoragePtr>> drop;
+  size_t left = 0;
+  {
+    std::lock_guard<std::mutex> lk(d.mu);
+    if (d.items.empty()) return 0;
+    auto it = d.items.begin();
+    while (it != d.items.end()) {
+      const int rc = ember_event_query(it->first);
+      if (rc == EMBER_OK) {
+        drop.push_back(std::move(it->second));
+        it = d.items.erase(it);
+      } else {
+        if (rc != EMBER_NOTREADY) check(rc, "release_after event");
+        ++it;
+      }
+    }
+    left = d.items.size();
+  }
+  return left;  // `drop` releases its storages here, outside the lock
+}
+
+void drain_released() {
+  Deferred& d = deferred();
+  std::vector<std::pair<ember_event_t, std::vector<StoragePtr>>> items;
+  {
+    std::lock_guard<std::mutex> lk(d.mu);
+    items.swap(d.items);
+  }
+  for (auto& [e, keep] : items) {
+    check(ember_event_synchronize(e), "drain_released");
+    keep.clear();
+  }
+}
+
 bool device_available() {
   int n = 0;
   return ember_get_device_count(&n) == EMBER_OK && n > 0;
@@ -137,6 +194,19 @@ class HipCachingAllocator final : public Allocator {
   void* allocate(size_t nbytes) override {
     if (nbytes == 0) return nullptr;
     const size_t r = round_up(nbytes);
+    // Blocks a side stream has finished with go back first.  If some are
+    // still in use and this request would set a new lifetime high-water
+    // mark, wait for them instead: the host runs ahead of the GPU, and the side stream's
+    // buffers (gradients the offloaded update still reads) would otherwise
+    // count on top of the next forward's own peak.
+    if (runtime::collect_released() > 0) {
+      bool over;
+      {
+        std::lock_guard<std::mutex> lk(mu_);
+        over = stats_.allocated_bytes + r > high_water_;
+      }
+      if (over) runtime::drain_released();
+    }
     std::lock_guard<std::mutex> lk(mu_);
     void* p = nullptr;
     auto it = free_.find(r);
@@ -161,6 +231,7 @@ class HipCachingAllocator final : public Allocator {
     stats_.allocated_bytes += r;
     if (stats_.allocated_bytes > stats_.peak_allocated_bytes)
       stats_.peak_allocated_bytes = stats_.allocated_bytes;
+    if (stats_.allocated_bytes > high_water_) high_water_ = stats_.allocated_bytes;
     return p;
   }
 
@@ -213,6 +284,7 @@ class HipCachingAllocator final : public Allocator {
   std::unordered_map<size_t, std::vector<void*>> free_;
   std::unordered_map<void*, size_t> live_;
   DeviceMemoryStats stats_;
+  size_t high_water_ = 0;  // like peak_allocated_bytes, but never reset
 };
 
 class CpuAllocator final : public Allocator {

@@ -143,17 +143,33 @@ Tensor Tensor::reshape(std::vector<int64_t> new_shape) const {
   return t;
 }
 
+Tensor Tensor::view_at(int64_t offset, std::vector<int64_t> shape) const {
+  if (!is_contiguous()) throw std::runtime_error("view_at: tensor must be contiguous");
+  if (offset < 0 || offset + shape_numel(shape) > numel())
+    throw std::runtime_error("view_at: view out of range");
+  Tensor t;
+  t.storage_ = storage_;
+  t.storage_offset_ = storage_offset_ + offset;
+  t.strides_ = contiguous_strides(shape);
+  t.shape_ = std::move(shape);
+  t.dtype_ = dtype_;
+  t.device_ = device_;
+  return t;
+}
+
 int64_t Tensor::numel() const { return shape_numel(shape_); }
 
 bool Tensor::is_contiguous() const { return strides_ == contiguous_strides(shape_); }
 
 void* Tensor::data_ptr() {
   if (!storage_) return nullptr;
+  if (storage_->ready_event()) runtime::wait_ready(*storage_);
   return static_cast<char*>(storage_->data()) + storage_offset_ * dtype_size(dtype_);
 }
 
 const void* Tensor::data_ptr() const {
   if (!storage_) return nullptr;
+  if (storage_->ready_event()) runtime::wait_ready(*storage_);
   return static_cast<const char*>(storage_->data()) + storage_offset_ * dtype_size(dtype_);
 }
 

@@ -358,6 +358,9 @@ int ctd_trainer_make_optimizer(ctd_trainer_t t, float lr, float weight_decay, fl
                                           {tr->named.no_decay, lr, 0.0f}};
     tr->opt = std::make_unique<optim::AdamW>(std::move(groups), beta1, beta2, eps, offload != 0);
     if (chunk_elems > 0) tr->opt->set_offload_chunk(chunk_elems);
+    // Stream parameters in model order (collect_parameters), the order in
+    // which the forward reads them, so it can overlap the offloaded update.
+    tr->opt->set_update_order(tr->opt_index);
     tr->opt->ensure_state_initialized();
   });
 }
@@ -399,6 +402,20 @@ int ctd_trainer_get_opt_state(ctd_trainer_t t, int64_t i, float* m, float* v, in
     check_numel(tm, numel);
     if (m) tm.copy_to_host(m);
     if (v) tv.copy_to_host(v);
+  });
+}
+
+int ctd_trainer_offload_stats(ctd_trainer_t t, double* stream_ms, double* bytes_per_direction) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    double ms = 0.0, b = 0.0;
+    if (tr->opt && tr->opt->is_offloaded()) {
+      tr->opt->wait_idle();
+      ms = tr->opt->offload_stats().last_stream_ms;
+      b = tr->opt->offload_stats().last_h2d_bytes;
+    }
+    if (stream_ms) *stream_ms = ms;
+    if (bytes_per_direction) *bytes_per_direction = b;
   });
 }
 
@@ -444,6 +461,7 @@ int ctd_trainer_train_step(ctd_trainer_t t, float max_norm, ctd_step_times* time
       times->loss = lv;
       times->grad_norm = gn;
       times->mask_sum = tr->mask_sum;
+      times->optimizer_stream_ms = static_cast<float>(tr->opt->offload_stats().last_stream_ms);
     }
     for (auto& e : ev) ember_event_destroy(e);
   });
@@ -451,7 +469,8 @@ int ctd_trainer_train_step(ctd_trainer_t t, float max_norm, ctd_step_times* time
 
 int ctd_trainer_synchronize(ctd_trainer_t t) {
   return guarded([&] {
-    (void)t;
+    Trainer* tr = as_trainer(t);
+    if (tr->opt) tr->opt->wait_idle();
     runtime::synchronize();
     CTD_CHECK(ember_stream_synchronize(runtime::d2h_stream()));
     CTD_CHECK(ember_stream_synchronize(runtime::h2d_stream()));

@@ -97,11 +97,20 @@ __global__ __launch_bounds__(kThreads) void sum_parts(const float* __restrict__ 
 extern "C" int ember_adamw(float* p, const float* g, float* m, float* v, int64_t n, float lr,
                            float beta1, float beta2, float eps, float wd, float bc1, float bc2,
                            ember_stream_t s) {
-  if (n < 0) return EMBER_EINVAL;
+  return ember_adamw_bounded(p, g, m, v, n, lr, beta1, beta2, eps, wd, bc1, bc2, 0, s);
+}
+
+extern "C" int ember_adamw_bounded(float* p, const float* g, float* m, float* v, int64_t n,
+                                   float lr, float beta1, float beta2, float eps, float wd,
+                                   float bc1, float bc2, int max_blocks, ember_stream_t s) {
+  if (n < 0 || max_blocks < 0) return EMBER_EINVAL;
   if (n == 0) return EMBER_OK;
   if (!p || !g || !m || !v) return EMBER_EINVAL;
-  const bool vec = aligned16(p) && aligned16(g) && aligned16(m) && aligned16(v);
-  const unsigned grid = grid_1d(vec ? (n + 3) / 4 : n, kThreads, 8192);
+  // A bounded launch shares the GPU with another kernel, so it takes the
+  // scalar form: 22 registers per lane instead of 62 lets its waves sit next
+  // to a GEMM's or the attention forward's on the same SIMD.
+  const bool vec = max_blocks == 0 && aligned16(p) && aligned16(g) && aligned16(m) && aligned16(v);
+  const unsigned grid = grid_1d(vec ? (n + 3) / 4 : n, kThreads, max_blocks > 0 ? max_blocks : 8192);
   if (vec)
     adamw_kernel<true><<<grid, kThreads, 0, as_stream(s)>>>(p, g, m, v, n, lr, beta1, beta2, eps,
                                                             wd, bc1, bc2);

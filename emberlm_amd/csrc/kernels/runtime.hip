@@ -112,6 +112,12 @@ extern "C" int ember_event_synchronize(ember_event_t e) {
   if (!e) return EMBER_EINVAL;
   return status_of(hipEventSynchronize(reinterpret_cast<hipEvent_t>(e)));
 }
+extern "C" int ember_event_query(ember_event_t e) {
+  if (!e) return EMBER_EINVAL;
+  const hipError_t rc = hipEventQuery(reinterpret_cast<hipEvent_t>(e));
+  if (rc == hipErrorNotReady) return EMBER_NOTREADY;
+  return status_of(rc);
+}
 extern "C" int ember_stream_wait_event(ember_stream_t s, ember_event_t e) {
   if (!e) return EMBER_EINVAL;
   return status_of(hipStreamWaitEvent(as_stream(s), reinterpret_cast<hipEvent_t>(e), 0));

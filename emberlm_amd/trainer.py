@@ -29,7 +29,8 @@ class ModelConfig(C.Structure):
 
 class StepTimes(C.Structure):
     _fields_ = [(n, C.c_float) for n in ("forward_ms", "backward_ms", "clip_ms", "optimizer_ms",
-                                         "total_ms", "loss", "grad_norm", "mask_sum")]
+                                         "total_ms", "loss", "grad_norm", "mask_sum",
+                                         "optimizer_stream_ms")]
 
 
 class Memory(C.Structure):
@@ -69,6 +70,7 @@ _SIGS = {
     "ctd_trainer_zero_grad": (i32, [vp]),
     "ctd_trainer_get_opt_state": (i32, [vp, i64, fptr, fptr, i64]),
     "ctd_trainer_step_count": (i32, [vp, lptr]),
+    "ctd_trainer_offload_stats": (i32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "ctd_trainer_train_step": (i32, [vp, f32, C.POINTER(StepTimes)]),
     "ctd_trainer_synchronize": (i32, [vp]),
     "ctd_memory_stats": (i32, [C.POINTER(Memory)]),
@@ -253,6 +255,12 @@ class Trainer:
         t = StepTimes()
         _ck(lib().ctd_trainer_train_step(self.h, max_norm, C.byref(t)), "train_step")
         return t
+
+    def offload_stats(self):
+        """(stream_ms, bytes_per_direction) of the last offloaded step, after it finished."""
+        ms, b = C.c_double(), C.c_double()
+        _ck(lib().ctd_trainer_offload_stats(self.h, C.byref(ms), C.byref(b)), "offload_stats")
+        return ms.value, b.value
 
     def synchronize(self):
         _ck(lib().ctd_trainer_synchronize(self.h), "synchronize")

@@ -5,12 +5,20 @@
 //   m = b1 m + (1-b1) g;  v = b2 v + (1-b2) g^2
 //   p <- p - lr ( (m/(1-b1^t)) / (sqrt(v/(1-b2^t)) + eps) + wd p )
 //
-// With offload = true, m and v live in page-locked host memory and step()
-// streams them through a ring of device buffers in fixed-size chunks: the
-// host->device copies, the fused update on the compute stream and the
-// device->host copies of neighbouring chunks overlap on two copy streams.
+// With offload = true, m and v live in page-locked host memory, one flat
+// buffer each with the parameters laid out in streaming order, and step()
+// streams them through a ring of device buffers in fixed-size chunks that may
+// span several (small) parameters: the
+// host->device copies, the fused update and the device->host copies of
+// neighbouring chunks overlap on two copy streams and an optimizer stream.
+// step() returns once the work is enqueued; the compute stream is not held
+// back by it.  Each parameter's storage carries the event of its own update,
+// so the next forward waits only for the parameters it touches, in the order
+// it touches them (set_update_order), and the host link stays busy while the
+// next step computes.
 
 #include <cstdint>
+#include <utility>
 #include <vector>
 
 #include "ctd/tensor.h"
@@ -24,9 +32,12 @@ struct ParamGroup {
 };
 
 struct OffloadStats {
-  double last_step_ms = 0.0;       // wall time of the last offloaded step()
+  double last_step_ms = 0.0;       // host time to enqueue the last offloaded step()
   double last_h2d_bytes = 0.0;
   double last_d2h_bytes = 0.0;
+  // Device time from the first copy in to the last copy out of the most
+  // recent offloaded step that has finished (0 until one has).
+  double last_stream_ms = 0.0;
 };
 
 class AdamW {
@@ -53,13 +64,24 @@ class AdamW {
   void set_step_count(int64_t s) { step_ = s; }
   size_t num_groups() const { return groups_.size(); }
   size_t num_params(size_t gi) const { return groups_.at(gi).params.size(); }
-  Tensor& m_tensor(size_t gi, size_t pi) { return state_.at(gi).at(pi).m; }
-  Tensor& v_tensor(size_t gi, size_t pi) { return state_.at(gi).at(pi).v; }
+  // Optimizer state; with offload these are host tensors that an in-flight
+  // step() still writes, so both accessors first wait for it to finish.
+  Tensor& m_tensor(size_t gi, size_t pi);
+  Tensor& v_tensor(size_t gi, size_t pi);
 
   // Elements per streamed chunk (default 16M floats = 64 MB per buffer).
   // Rounded up to 64 elements so every chunk starts on a 256-byte boundary.
   void set_offload_chunk(int64_t elems) { chunk_elems_ = elems <= 0 ? 64 : (elems + 63) / 64 * 64; }
-  const OffloadStats& offload_stats() const { return stats_; }
+  // Order in which the offloaded step streams parameters, as (group, index)
+  // pairs; parameters not listed follow in group order.  Give the order in
+  // which the forward pass first reads them, so it can start on the first
+  // parameters while the rest are still in flight.  It fixes the host layout
+  // of m and v, so it must come before the state exists (first step(),
+  // ensure_state_initialized()).
+  void set_update_order(std::vector<std::pair<size_t, size_t>> order);
+  // Blocks until the last offloaded step() has finished on every stream.
+  void wait_idle();
+  const OffloadStats& offload_stats();
 
  private:
   struct State {
@@ -67,7 +89,14 @@ class AdamW {
     Tensor v;
   };
 
+  // One parameter's place in the flat offloaded state (streaming order).
+  struct Segment {
+    size_t gi, pi;
+    int64_t off, n;
+  };
+
   void init_state_for_group(size_t gi);
+  void init_offload_state();
   void step_ondevice();
   void step_offloaded();
 
@@ -87,6 +116,14 @@ class AdamW {
   void* ev_updated_[kSlots] = {nullptr, nullptr, nullptr};
   void* ev_drained_[kSlots] = {nullptr, nullptr, nullptr};
   void* ev_done_ = nullptr;
+  void* ev_begin_ = nullptr;   // on the h2d stream before the first copy in
+  void* ev_start_ = nullptr;   // on the compute stream: grads and params final
+  bool in_flight_ = false;     // an offloaded step was enqueued and not yet waited on
+  std::vector<std::vector<void*>> ev_param_;  // per parameter: its update is done
+  std::vector<std::pair<size_t, size_t>> order_;
+  std::vector<Segment> layout_;  // offloaded state, in streaming order
+  Tensor flat_m_, flat_v_;       // pinned host buffers the per-parameter m/v view
+  int64_t flat_n_ = 0;
   OffloadStats stats_;
 };
 

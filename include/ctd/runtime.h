@@ -5,7 +5,9 @@
 // cublas_utils.h (CTD_CUDA_CHECK*, the call_once cuBLAS handle).
 
 #include <string>
+#include <vector>
 
+#include "ctd/storage.h"
 #include "ember_hip.h"
 
 namespace ctd::runtime {
@@ -20,6 +22,21 @@ ember_stream_t d2h_stream();
 
 // Blocks until all work on the compute stream is done.
 void synchronize();
+
+// Makes the compute stream wait for the storage's pending writer event (see
+// Storage::set_ready_event) and clears it.
+void wait_ready(Storage& s);
+
+// Keeps `keep` alive until `done` has completed, then drops the references
+// (their device blocks return to the cache).  Used for buffers that a side
+// stream still reads after their owner let go of them, e.g. gradients the
+// offloaded optimizer consumes while zero_grad() has already released them.
+// Pending entries are checked on every device allocation.
+void release_after(ember_event_t done, std::vector<StoragePtr> keep);
+// Drops every pending entry whose event has completed; returns how many remain.
+size_t collect_released();
+// Waits for every pending entry's event and drops them all.
+void drain_released();
 
 // Whether a HIP device is present (without creating a context on failure).
 bool device_available();

@@ -25,6 +25,18 @@ class Storage {
   const Device& device() const { return device_; }
   bool pinned() const { return pinned_; }
 
+  // An event (ember_event_t) recorded on another stream after work that
+  // writes this buffer, e.g. the offloaded optimizer's update of a parameter.
+  // Tensor::data_ptr() makes the compute stream wait for it on first access
+  // and clears it, so the buffer's next user is ordered after that writer.
+  void set_ready_event(void* ev) { ready_event_ = ev; }
+  void* ready_event() const { return ready_event_; }
+  void* take_ready_event() {
+    void* e = ready_event_;
+    ready_event_ = nullptr;
+    return e;
+  }
+
  private:
   void release_() noexcept;
 
@@ -33,6 +45,7 @@ class Storage {
   size_t nbytes_ = 0;
   Device device_{};
   bool pinned_ = false;
+  void* ready_event_ = nullptr;
 };
 
 using StoragePtr = std::shared_ptr<Storage>;

@@ -31,6 +31,9 @@ class Tensor {
 
   // Zero-copy view with a new shape. Tensor must be contiguous.
   Tensor reshape(std::vector<int64_t> new_shape) const;
+  // Contiguous view of prod(shape) elements starting `offset` elements into
+  // this contiguous tensor; shares the storage, carries no autograd history.
+  Tensor view_at(int64_t offset, std::vector<int64_t> shape) const;
 
   const std::vector<int64_t>& shape() const { return shape_; }
   const std::vector<int64_t>& strides() const { return strides_; }

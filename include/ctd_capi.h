@@ -31,6 +31,10 @@ typedef struct ctd_model_config {
 typedef struct ctd_step_times {
   float forward_ms, backward_ms, clip_ms, optimizer_ms, total_ms;
   float loss, grad_norm, mask_sum;
+  /* Offloaded AdamW: device time of the most recent finished step's
+   * transfers and updates (first copy in to last copy out), which run behind
+   * the next step's forward; 0 before one has finished or without offload. */
+  float optimizer_stream_ms;
 } ctd_step_times;
 
 typedef struct ctd_memory {
@@ -98,6 +102,10 @@ int ctd_trainer_opt_step(ctd_trainer_t t);
 int ctd_trainer_zero_grad(ctd_trainer_t t);
 int ctd_trainer_get_opt_state(ctd_trainer_t t, int64_t i, float* m, float* v, int64_t numel);
 int ctd_trainer_step_count(ctd_trainer_t t, int64_t* steps);
+/* Offloaded AdamW: waits for the last step() to finish, then reports its
+ * device time from first copy in to last copy out and the bytes it moved per
+ * direction (zeros without offload). */
+int ctd_trainer_offload_stats(ctd_trainer_t t, double* stream_ms, double* bytes_per_direction);
 
 /* One full training step (forward, backward, clip to max_norm when > 0,
  * optimizer step, zero_grad) with HIP-event phase times. */

@@ -35,7 +35,8 @@ enum {
   EMBER_EINVAL = -1,     /* bad size, shape, null pointer or flag */
   EMBER_EWORKSPACE = -2, /* workspace missing or too small */
   EMBER_EALIGN = -3,     /* pointer alignment the kernel requires is not met */
-  EMBER_EMASKSUM = -4    /* sum(loss_mask) == 0 in cross-entropy backward */
+  EMBER_EMASKSUM = -4,   /* sum(loss_mask) == 0 in cross-entropy backward */
+  EMBER_NOTREADY = 600   /* ember_event_query: work before the event still pending */
 };
 
 /* Human-readable text for a status code (static storage). */
@@ -66,6 +67,8 @@ int ember_event_create(ember_event_t* e);
 int ember_event_destroy(ember_event_t e);
 int ember_event_record(ember_event_t e, ember_stream_t s);
 int ember_event_synchronize(ember_event_t e);
+/* EMBER_OK once the work recorded before e has finished, EMBER_NOTREADY before. */
+int ember_event_query(ember_event_t e);
 int ember_stream_wait_event(ember_stream_t s, ember_event_t e);
 int ember_event_elapsed_ms(float* ms, ember_event_t start, ember_event_t stop);
 /* Device name / CU count / HBM bytes of the current device. */
@@ -226,6 +229,14 @@ int ember_embedding_bwd(const int64_t* ids, const float* dy, float* dw, int64_t 
  * (adamw_step_kernel_f32, src/core/optim.cu:54-73). */
 int ember_adamw(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1,
                 float beta2, float eps, float wd, float bc1, float bc2, ember_stream_t s);
+/* The same update on at most max_blocks workgroups (0: ember_adamw; each
+ * workgroup strides over the array), in a low-register form whose waves fit
+ * next to a GEMM's or the attention forward's on one SIMD.  The offloaded
+ * optimizer runs its chunk updates this way while the next step's forward
+ * holds the GPU.  Results equal ember_adamw's bitwise. */
+int ember_adamw_bounded(float* p, const float* g, float* m, float* v, int64_t n, float lr,
+                        float beta1, float beta2, float eps, float wd, float bc1, float bc2,
+                        int max_blocks, ember_stream_t s);
 
 /* ------------------------------------------------------- grad-norm clip
  * out[0] = sum over tensors of sum(g^2), fixed-order two-stage reduction.
