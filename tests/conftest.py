@@ -12,6 +12,21 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (HIP) device")
 
 
+@pytest.fixture(autouse=True)
+def _torch_float32_default():
+    """Every test starts from torch's float32 default, whatever an earlier
+    module or test set (the oracle tests switch to float64 for themselves)."""
+    try:
+        import torch
+    except ImportError:
+        yield
+        return
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float32)
+    yield
+    torch.set_default_dtype(old)
+
+
 def pytest_collection_modifyitems(config, items):
     # GPU tests run in the order written; nothing is reordered.
     return None

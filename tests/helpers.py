@@ -48,7 +48,16 @@ def p(t):
 
 
 def call(name, *args):
+    """C-ABI call on its own stream argument, ordered after and before torch's
+    work: torch fills the inputs on its current stream, which need not be the
+    stream the call runs on, so the device is synchronised on both sides."""
+    import torch
+    sync = torch.cuda.is_available()
+    if sync:
+        torch.cuda.synchronize()
     capi.call(name, *args)
+    if sync:
+        torch.cuda.synchronize()
 
 
 def f32ptr(arr):

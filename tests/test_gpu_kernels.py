@@ -97,7 +97,8 @@ def test_gemm_full_size_vs_torch_and_deterministic():
     ref = x @ w.t()
     torch.cuda.synchronize()
     rel = ((out - ref).norm() / ref.norm()).item()
-    assert rel < 1e-5, rel
+    assert rel < 1e-5, (rel, int((~torch.isfinite(out)).sum()), int((~torch.isfinite(ref)).sum()),
+                        int((~torch.isfinite(x)).sum()), int((~torch.isfinite(w)).sum()))
     out2 = empty((M, N))
     call("ember_gemm_f32", 0, 1, M, N, K, 1.0, p(x), K, 0, p(w), K, 0, 0.0, p(out2), N, 0, 1, None)
     assert torch.equal(out, out2)
@@ -360,6 +361,29 @@ def test_adamw_vs_oracle():
         bound = 1e-5 * np.abs(ref) + 1e-6 * np.abs(ref).max()
         i = int(np.argmax(err - bound))
         assert (err <= bound).all(), (name, i, float(host(got)[i]), float(ref[i]), float(err[i]))
+
+
+@pytest.mark.parametrize("max_blocks,offset", [(256, 0), (7, 0), (256, 3), (1, 1)])
+def test_adamw_bounded_equals_adamw_bitwise(max_blocks, offset):
+    # The offloaded optimizer's low-register, bounded-grid update must round
+    # exactly like ember_adamw (float4 path), also off a 16-byte boundary.
+    r = rng(8)
+    n = 70001
+    pp, g = r.standard_normal(n + 4).astype(np.float32), r.standard_normal(n + 4).astype(np.float32)
+    m, v = (0.1 * r.standard_normal(n + 4)).astype(np.float32), r.random(n + 4).astype(np.float32)
+    args = (1e-3, 0.9, 0.95, 1e-8, 0.1, 0.271, 0.1426)
+    A = [dev(x) for x in (pp, g, m, v)]
+    B = [dev(x) for x in (pp, g, m, v)]
+    call("ember_adamw", *[p(t) for t in A], n + 4, *args, None)
+    off = 4 * offset
+    call("ember_adamw_bounded", *[C.c_void_p(t.data_ptr() + off) for t in B], n, *args,
+         max_blocks, None)
+    for a, b, name in zip(A, B, ("p", "g", "m", "v")):
+        ha, hb = host(a), host(b)
+        assert np.array_equal(ha[offset:offset + n], hb[offset:offset + n]), name
+        # nothing outside [offset, offset + n) was touched
+        assert np.array_equal(hb[:offset], (pp, g, m, v)[("p", "g", "m", "v").index(name)][:offset])
+        assert np.array_equal(hb[offset + n:], (pp, g, m, v)[("p", "g", "m", "v").index(name)][offset + n:])
 
 
 def test_sumsq_multi():

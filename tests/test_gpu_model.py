@@ -188,6 +188,32 @@ def test_offload_equals_on_device_over_steps():
     b.close()
 
 
+def test_overlapped_offload_train_steps_equal_on_device():
+    # train_step returns while the offloaded update still streams; the next
+    # forward must see every updated parameter, and the host reads below must
+    # see the final state without an explicit synchronize.
+    c = tiny_cfg(qk_norm=True, D=64)
+    a = TR.Trainer(c, seed=5, init_std=0.05)
+    b = TR.Trainer(c, seed=5, init_std=0.05)
+    a.make_optimizer(lr=1e-3, weight_decay=0.1, offload=True, chunk_elems=3000)
+    b.make_optimizer(lr=1e-3, weight_decay=0.1, offload=False)
+    losses = {id(a): [], id(b): []}
+    for step in range(4):
+        for t in (a, b):
+            t.synthetic_batch(2, 96, seed=10 + step, masked=True)
+            losses[id(t)].append(t.train_step(1.0).loss)
+    assert losses[id(a)] == losses[id(b)]
+    for i in range(a.num_params()):
+        assert np.array_equal(a.get_param(i), b.get_param(i)), a.names[i]
+        ma, va = a.opt_state(i)
+        mb, vb = b.opt_state(i)
+        assert np.array_equal(ma, mb) and np.array_equal(va, vb), a.names[i]
+    ms, nbytes = a.offload_stats()
+    assert ms > 0 and nbytes >= 8 * sum(a.numels)
+    a.close()
+    b.close()
+
+
 def test_train_step_and_checkpoint_roundtrip(tmp_path):
     c = tiny_cfg()
     a = TR.Trainer(c, seed=4)

@@ -14,7 +14,16 @@ import torch.nn.functional as F
 
 import oracle as O
 
-torch.set_default_dtype(torch.float64)
+
+
+@pytest.fixture(autouse=True)
+def _float64_default():
+    # float64 torch defaults for this module only: a process-wide change made
+    # at import would leak into the GPU tests collected with it.
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    yield
+    torch.set_default_dtype(old)
 
 
 def rng(seed=0):
