@@ -112,6 +112,24 @@ def build_cpp_tests(verbose=False):
     return out
 
 
+def build_tools(verbose=False):
+    """Command-line tools (emberlm_amd/csrc/tools/*.cpp), one executable each in lib/."""
+    srcs = sorted(glob.glob(os.path.join(ROOT, "emberlm_amd", "csrc", "tools", "*.cpp")))
+    if not srcs or not os.path.exists(os.path.join(LIB, "libctd.so")):
+        return []
+    cxx = shutil.which("g++") or "g++"
+    outs = []
+    for src in srcs:
+        out = os.path.join(LIB, os.path.splitext(os.path.basename(src))[0])
+        _run([cxx, *CXX_FLAGS, "-o", out + ".tmp", src, "-L" + LIB, "-lctd", "-lember_hip",
+              "-Wl,-rpath,$ORIGIN"])
+        os.replace(out + ".tmp", out)
+        outs.append(out)
+        if verbose:
+            print("built", out)
+    return outs
+
+
 def build_oracle():
     subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=True)
 
@@ -120,6 +138,7 @@ def build_all(verbose=False):
     build_oracle()
     build_hip(verbose)
     build_host(verbose)
+    build_tools(verbose)
     build_cpp_tests(verbose)
 
 

@@ -19,6 +19,7 @@
 
 #include "ctd/runtime.h"
 #include "ctd/safetensors.h"
+#include "json.h"
 
 namespace ctd {
 
@@ -31,166 +32,9 @@ struct FileCloser {
 };
 using FilePtr = std::unique_ptr<std::FILE, FileCloser>;
 
-// ---- minimal JSON value / parser (objects, arrays, strings, numbers, literals)
-struct JVal {
-  enum Kind { kNull, kBool, kNum, kStr, kArr, kObj } kind = kNull;
-  double num = 0;
-  std::string str;
-  std::vector<JVal> arr;
-  std::vector<std::pair<std::string, JVal>> obj;
-  const JVal& at(const std::string& k) const {
-    for (const auto& [key, v] : obj)
-      if (key == k) return v;
-    throw std::runtime_error("safetensors: header entry missing '" + k + "'");
-  }
-};
+using json::JVal;
 
-class Parser {
- public:
-  explicit Parser(const std::string& s) : s_(s) {}
-  JVal parse() {
-    JVal v = value();
-    ws();
-    if (i_ != s_.size()) fail("trailing characters");
-    return v;
-  }
-
- private:
-  [[noreturn]] void fail(const char* m) {
-    throw std::runtime_error(std::string("safetensors: bad header JSON (") + m + ") at byte " +
-                             std::to_string(i_));
-  }
-  void ws() {
-    while (i_ < s_.size() && (s_[i_] == ' ' || s_[i_] == '\n' || s_[i_] == '\t' || s_[i_] == '\r'))
-      ++i_;
-  }
-  char peek() {
-    ws();
-    if (i_ >= s_.size()) fail("unexpected end");
-    return s_[i_];
-  }
-  void expect(char c) {
-    if (peek() != c) fail("unexpected character");
-    ++i_;
-  }
-  JVal value() {
-    const char c = peek();
-    if (c == '{') return object();
-    if (c == '[') return array();
-    if (c == '"') {
-      JVal v;
-      v.kind = JVal::kStr;
-      v.str = string();
-      return v;
-    }
-    if (c == 't' || c == 'f' || c == 'n') return literal();
-    return number();
-  }
-  JVal object() {
-    JVal v;
-    v.kind = JVal::kObj;
-    expect('{');
-    if (peek() == '}') {
-      ++i_;
-      return v;
-    }
-    for (;;) {
-      std::string k = string();
-      expect(':');
-      v.obj.emplace_back(std::move(k), value());
-      const char c = peek();
-      ++i_;
-      if (c == '}') break;
-      if (c != ',') fail("expected , or }");
-    }
-    return v;
-  }
-  JVal array() {
-    JVal v;
-    v.kind = JVal::kArr;
-    expect('[');
-    if (peek() == ']') {
-      ++i_;
-      return v;
-    }
-    for (;;) {
-      v.arr.push_back(value());
-      const char c = peek();
-      ++i_;
-      if (c == ']') break;
-      if (c != ',') fail("expected , or ]");
-    }
-    return v;
-  }
-  std::string string() {
-    expect('"');
-    std::string out;
-    while (i_ < s_.size() && s_[i_] != '"') {
-      char c = s_[i_++];
-      if (c == '\\') {
-        if (i_ >= s_.size()) fail("bad escape");
-        const char e = s_[i_++];
-        switch (e) {
-          case 'n': out += '\n'; break;
-          case 't': out += '\t'; break;
-          case 'r': out += '\r'; break;
-          case 'b': out += '\b'; break;
-          case 'f': out += '\f'; break;
-          case 'u': {
-            if (i_ + 4 > s_.size()) fail("bad \\u escape");
-            const unsigned cp = static_cast<unsigned>(std::stoul(s_.substr(i_, 4), nullptr, 16));
-            i_ += 4;
-            if (cp < 0x80) {
-              out += static_cast<char>(cp);
-            } else if (cp < 0x800) {
-              out += static_cast<char>(0xC0 | (cp >> 6));
-              out += static_cast<char>(0x80 | (cp & 0x3F));
-            } else {
-              out += static_cast<char>(0xE0 | (cp >> 12));
-              out += static_cast<char>(0x80 | ((cp >> 6) & 0x3F));
-              out += static_cast<char>(0x80 | (cp & 0x3F));
-            }
-            break;
-          }
-          default: out += e;
-        }
-      } else {
-        out += c;
-      }
-    }
-    if (i_ >= s_.size()) fail("unterminated string");
-    ++i_;
-    return out;
-  }
-  JVal number() {
-    const size_t b = i_;
-    while (i_ < s_.size() && (std::strchr("+-0123456789.eE", s_[i_]) != nullptr)) ++i_;
-    if (b == i_) fail("expected a value");
-    JVal v;
-    v.kind = JVal::kNum;
-    v.num = std::stod(s_.substr(b, i_ - b));
-    v.str = s_.substr(b, i_ - b);
-    return v;
-  }
-  JVal literal() {
-    JVal v;
-    if (s_.compare(i_, 4, "true") == 0) {
-      v.kind = JVal::kBool;
-      v.num = 1;
-      i_ += 4;
-    } else if (s_.compare(i_, 5, "false") == 0) {
-      v.kind = JVal::kBool;
-      i_ += 5;
-    } else if (s_.compare(i_, 4, "null") == 0) {
-      i_ += 4;
-    } else {
-      fail("bad literal");
-    }
-    return v;
-  }
-  const std::string& s_;
-  size_t i_ = 0;
-};
+JVal parse_header(const std::string& text) { return json::Parser(text, "safetensors: bad header JSON").parse(); }
 
 uint64_t as_u64(const JVal& v) {
   if (v.kind != JVal::kNum) throw std::runtime_error("safetensors: expected an integer");
@@ -242,7 +86,7 @@ TensorDict load_safetensors(const std::filesystem::path& path, Device device) {
   std::string header(header_size, '\0');
   if (std::fread(header.data(), 1, header_size, fp.get()) != header_size)
     throw std::runtime_error("safetensors: short read on header");
-  const JVal json = Parser(header).parse();
+  const JVal json = parse_header(header);
   if (json.kind != JVal::kObj) throw std::runtime_error("safetensors: header is not an object");
   const int64_t data_origin = static_cast<int64_t>(8 + header_size);
 

@@ -14,8 +14,10 @@
 
 #include "ctd/allocator.h"
 #include "ctd/nn/model.h"
+#include "ctd/ops/repeat_kv.h"
 #include "ctd/optim.h"
 #include "ctd/runtime.h"
+#include "ctd/train.h"
 #include "ctd_capi.h"
 
 using namespace ctd;
@@ -94,6 +96,15 @@ struct Trainer {
   float mask_sum = 0.f;
   std::unique_ptr<optim::AdamW> opt;
 };
+
+// Decay group, then no-decay group: the order ctd_train hands the parameters
+// to clip_grad_norm_ (tools/ctd_train/main.cpp:296-299), which fixes the order
+// of the norm's reduction.
+std::vector<Tensor> clip_order(const Trainer& tr) {
+  std::vector<Tensor> ps(tr.named.decay.begin(), tr.named.decay.end());
+  ps.insert(ps.end(), tr.named.no_decay.begin(), tr.named.no_decay.end());
+  return ps;
+}
 
 Trainer* as_trainer(ctd_trainer_t t) {
   if (!t) throw std::runtime_error("null trainer handle");
@@ -368,9 +379,7 @@ int ctd_trainer_make_optimizer(ctd_trainer_t t, float lr, float weight_decay, fl
 int ctd_trainer_clip(ctd_trainer_t t, float max_norm, float* total_norm) {
   return guarded([&] {
     Trainer* tr = as_trainer(t);
-    std::vector<Tensor> ps;
-    for (auto& [n, p] : tr->named.all) ps.push_back(p);
-    const float v = optim::clip_grad_norm_(ps, max_norm);
+    const float v = optim::clip_grad_norm_(clip_order(*tr), max_norm);
     if (total_norm) *total_norm = v;
   });
 }
@@ -441,9 +450,7 @@ int ctd_trainer_train_step(ctd_trainer_t t, float max_norm, ctd_step_times* time
     CTD_CHECK(ember_event_record(ev[2], cs));
     float gn = 0.f;
     if (max_norm > 0.f) {
-      std::vector<Tensor> ps;
-      for (auto& [n, p] : tr->named.all) ps.push_back(p);
-      gn = optim::clip_grad_norm_(ps, max_norm);
+      gn = optim::clip_grad_norm_(clip_order(*tr), max_norm);
     }
     CTD_CHECK(ember_event_record(ev[3], cs));
     tr->opt->step();
@@ -512,21 +519,9 @@ int ctd_gemm_profile_collect(ctd_gemm_profile* out) {
 int ctd_trainer_save(ctd_trainer_t t, const char* path) {
   return guarded([&] {
     Trainer* tr = as_trainer(t);
-    save_safetensors(tr->named.all, path);
-    if (!tr->opt) return;
-    std::vector<std::pair<std::string, Tensor>> items;
-    for (size_t i = 0; i < tr->named.decay_names.size(); ++i) {
-      items.emplace_back("optimizer.m." + tr->named.decay_names[i], tr->opt->m_tensor(0, i));
-      items.emplace_back("optimizer.v." + tr->named.decay_names[i], tr->opt->v_tensor(0, i));
-    }
-    for (size_t i = 0; i < tr->named.no_decay_names.size(); ++i) {
-      items.emplace_back("optimizer.m." + tr->named.no_decay_names[i], tr->opt->m_tensor(1, i));
-      items.emplace_back("optimizer.v." + tr->named.no_decay_names[i], tr->opt->v_tensor(1, i));
-    }
     runtime::synchronize();
-    const float step_f = static_cast<float>(tr->opt->step_count());
-    items.emplace_back("optimizer.step", Tensor::from_host(&step_f, {1}, DType::kFloat32, kCPU));
-    save_safetensors(items, std::string(path) + ".opt.safetensors");
+    save_safetensors(tr->named.all, path);
+    if (tr->opt) train::save_optimizer_state(*tr->opt, tr->named, train::opt_path_for(path));
   });
 }
 
@@ -542,36 +537,74 @@ int ctd_trainer_load(ctd_trainer_t t, const char* path) {
                                    runtime::compute_stream()));
     }
     runtime::synchronize();
-    if (!tr->opt) return;
-    TensorDict o = load_safetensors(std::string(path) + ".opt.safetensors", kCPU);
-    tr->opt->ensure_state_initialized();
-    auto load_into = [&](Tensor& dst, const std::string& key) {
-      auto it = o.find(key);
-      if (it == o.end()) throw std::runtime_error("resume: missing " + key);
-      if (it->second.shape() != dst.shape()) throw std::runtime_error("resume: shape " + key);
-      // Offloaded state is host memory: a plain copy (the reference copied
-      // device-to-device here, tools/ctd_train/main.cpp:236-243).
-      if (dst.device().is_hip()) {
-        CTD_CHECK(ember_memcpy_async(dst.data_ptr(), it->second.data_ptr(), dst.nbytes(), 0,
-                                     runtime::compute_stream()));
-        runtime::synchronize();
-      } else {
-        std::memcpy(dst.data_ptr(), it->second.data_ptr(), dst.nbytes());
-      }
-    };
-    for (size_t i = 0; i < tr->named.decay_names.size(); ++i) {
-      load_into(tr->opt->m_tensor(0, i), "optimizer.m." + tr->named.decay_names[i]);
-      load_into(tr->opt->v_tensor(0, i), "optimizer.v." + tr->named.decay_names[i]);
-    }
-    for (size_t i = 0; i < tr->named.no_decay_names.size(); ++i) {
-      load_into(tr->opt->m_tensor(1, i), "optimizer.m." + tr->named.no_decay_names[i]);
-      load_into(tr->opt->v_tensor(1, i), "optimizer.v." + tr->named.no_decay_names[i]);
-    }
-    auto it = o.find("optimizer.step");
-    if (it == o.end()) throw std::runtime_error("resume: missing optimizer.step");
-    float step_f = 0.f;
-    std::memcpy(&step_f, it->second.data_ptr(), sizeof(float));
-    tr->opt->set_step_count(static_cast<int64_t>(step_f));
+    if (tr->opt) train::load_optimizer_state(*tr->opt, tr->named, train::opt_path_for(path));
+  });
+}
+
+int ctd_trainer_set_lr(ctd_trainer_t t, float lr) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    if (!tr->opt) throw std::runtime_error("no optimizer");
+    tr->opt->set_lr(lr);
+  });
+}
+
+int ctd_trainer_accumulate(ctd_trainer_t t, float scale, float* loss) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    if (!tr->ids.defined()) throw std::runtime_error("no batch set");
+    Tensor l = tr->model.forward_train_masked(tr->ids, tr->targets, tr->mask);
+    ops::mul_scalar(l, scale).backward();
+    if (loss) l.copy_to_host(loss);
+  });
+}
+
+int ctd_train_run(const char* config_path) {
+  return guarded([&] {
+    if (!config_path) throw std::runtime_error("null config path");
+    train::run(train::load_config(config_path));
+  });
+}
+
+int ctd_train_lr_at_step(int32_t step, int32_t warmup_steps, int32_t total_steps, float lr,
+                         float min_lr_ratio, float* out) {
+  return guarded([&] {
+    if (!out) throw std::runtime_error("null argument");
+    train::Config c;
+    c.warmup_steps = warmup_steps;
+    c.total_steps = total_steps;
+    c.lr = lr;
+    c.min_lr_ratio = min_lr_ratio;
+    *out = train::lr_at_step(step, c);
+  });
+}
+
+int ctd_train_host_batch(const char* tok_path, const char* mask_path, int32_t seq_len,
+                         const int64_t* docs, int64_t B, int64_t* ids, int64_t* targets,
+                         float* mask, float* sum_mask, int64_t* num_docs) {
+  return guarded([&] {
+    if (!tok_path || !mask_path) throw std::runtime_error("null path");
+    const train::DataSplit s = train::load_split(tok_path, mask_path, seq_len);
+    if (num_docs) *num_docs = s.num_docs;
+    if (B <= 0) return;
+    if (!docs || !ids || !targets || !mask) throw std::runtime_error("null argument");
+    const train::HostBatch h =
+        train::make_host_batch(s, std::vector<int64_t>(docs, docs + B), seq_len);
+    std::memcpy(ids, h.input_ids.data(), h.input_ids.size() * sizeof(int64_t));
+    std::memcpy(targets, h.targets.data(), h.targets.size() * sizeof(int64_t));
+    std::memcpy(mask, h.loss_mask.data(), h.loss_mask.size() * sizeof(float));
+    if (sum_mask) *sum_mask = h.sum_mask;
+  });
+}
+
+int ctd_train_event_json(int32_t step, float loss, float lr, float grad_norm,
+                         double tokens_per_sec, double wall_s, int32_t val, char* buf,
+                         size_t cap) {
+  return guarded([&] {
+    const std::string e = val ? train::val_event(step, loss, wall_s)
+                              : train::train_event(step, loss, lr, grad_norm, tokens_per_sec, wall_s);
+    if (!buf || cap < e.size() + 1) throw std::runtime_error("buffer too small");
+    std::memcpy(buf, e.c_str(), e.size() + 1);
   });
 }
 

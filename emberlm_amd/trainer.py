@@ -79,6 +79,14 @@ _SIGS = {
     "ctd_gemm_profile_collect": (i32, [C.POINTER(GemmProfile)]),
     "ctd_trainer_save": (i32, [vp, C.c_char_p]),
     "ctd_trainer_load": (i32, [vp, C.c_char_p]),
+    "ctd_trainer_accumulate": (i32, [vp, f32, fptr]),
+    "ctd_trainer_set_lr": (i32, [vp, f32]),
+    "ctd_train_run": (i32, [C.c_char_p]),
+    "ctd_train_lr_at_step": (i32, [i32, i32, i32, f32, f32, fptr]),
+    "ctd_train_host_batch": (i32, [C.c_char_p, C.c_char_p, i32, lptr, i64, lptr, lptr, fptr, fptr,
+                                   lptr]),
+    "ctd_train_event_json": (i32, [i32, f32, f32, f32, C.c_double, C.c_double, i32, C.c_char_p,
+                                   C.c_size_t]),
 }
 
 
@@ -251,6 +259,15 @@ class Trainer:
                                             v.ctypes.data_as(fptr), m.size), "opt_state")
         return m, v
 
+    def accumulate(self, scale):
+        """Forward + backward of loss * scale, gradients accumulating; returns the loss."""
+        loss = C.c_float()
+        _ck(lib().ctd_trainer_accumulate(self.h, scale, C.byref(loss)), "accumulate")
+        return loss.value
+
+    def set_lr(self, lr):
+        _ck(lib().ctd_trainer_set_lr(self.h, lr), "set_lr")
+
     def train_step(self, max_norm=1.0) -> StepTimes:
         t = StepTimes()
         _ck(lib().ctd_trainer_train_step(self.h, max_norm, C.byref(t)), "train_step")
@@ -275,6 +292,40 @@ class Trainer:
         return len(self.names)
 
 
+def train_run(config_path):
+    """Runs the ctd_train driver in this process (include/ctd/train.h)."""
+    _ck(lib().ctd_train_run(str(config_path).encode()), "ctd_train")
+
+
+def lr_at_step(step, warmup_steps, total_steps, lr, min_lr_ratio):
+    out = C.c_float()
+    _ck(lib().ctd_train_lr_at_step(step, warmup_steps, total_steps, lr, min_lr_ratio,
+                                   C.byref(out)), "lr_at_step")
+    return out.value
+
+
+def host_batch(tok_path, mask_path, seq_len, docs):
+    """(ids, targets, mask, sum_mask, num_docs) of the driver's batch of `docs`."""
+    docs = np.ascontiguousarray(docs, dtype=np.int64)
+    B, T = docs.size, seq_len - 1
+    ids = np.zeros((B, T), np.int64)
+    tgt = np.zeros((B, T), np.int64)
+    mask = np.zeros((B, T), np.float32)
+    sm, nd = C.c_float(), C.c_int64()
+    _ck(lib().ctd_train_host_batch(str(tok_path).encode(), str(mask_path).encode(), seq_len,
+                                   docs.ctypes.data_as(lptr), B, ids.ctypes.data_as(lptr),
+                                   tgt.ctypes.data_as(lptr), mask.ctypes.data_as(fptr),
+                                   C.byref(sm), C.byref(nd)), "host_batch")
+    return ids, tgt, mask, sm.value, nd.value
+
+
+def event_json(step, loss, lr=0.0, grad_norm=0.0, tokens_per_sec=0.0, wall_s=0.0, val=False):
+    buf = C.create_string_buffer(512)
+    _ck(lib().ctd_train_event_json(step, loss, lr, grad_norm, tokens_per_sec, wall_s, int(val), buf,
+                                   512), "event_json")
+    return buf.value.decode()
+
+
 def param_count(cfg: ModelConfig) -> int:
     d, I, H, Hk, D, V, L = (cfg.hidden_size, cfg.intermediate_size, cfg.num_heads,
                             cfg.num_kv_heads, cfg.head_dim, cfg.vocab_size, cfg.num_layers)
@@ -283,4 +334,5 @@ def param_count(cfg: ModelConfig) -> int:
 
 
 __all__ = ["ModelConfig", "Trainer", "preset", "make_config", "memory", "reset_peak_memory",
-           "gemm_profile", "param_count", "StepTimes", "math"]
+           "gemm_profile", "param_count", "StepTimes", "train_run", "lr_at_step", "host_batch",
+           "event_json", "math"]

@@ -127,6 +127,31 @@ int ctd_gemm_profile_collect(ctd_gemm_profile* out);
 int ctd_trainer_save(ctd_trainer_t t, const char* path);
 int ctd_trainer_load(ctd_trainer_t t, const char* path);
 
+/* Forward + backward of (loss * scale) into the gradients, which accumulate
+ * (ctd_train's micro-batch step, main.cpp:354-365); loss receives the
+ * unscaled loss. */
+int ctd_trainer_accumulate(ctd_trainer_t t, float scale, float* loss);
+/* Learning rate of every group for the next opt_step (AdamW::set_lr). */
+int ctd_trainer_set_lr(ctd_trainer_t t, float lr);
+
+/* ---- the ctd_train driver (include/ctd/train.h) */
+/* Runs ctd_train with the JSON config at config_path (its directory is the run
+ * directory: loss.jsonl, checkpoints). */
+int ctd_train_run(const char* config_path);
+/* Learning rate of a step: linear warmup, then cosine to lr * min_lr_ratio. */
+int ctd_train_lr_at_step(int32_t step, int32_t warmup_steps, int32_t total_steps, float lr,
+                         float min_lr_ratio, float* out);
+/* Loads a split (int32 tokens, int8 mask; seq_len per document) and assembles
+ * the batch of the B documents `docs` into host buffers of B*(seq_len-1)
+ * entries; num_docs receives the split size.  B = 0 only loads. */
+int ctd_train_host_batch(const char* tok_path, const char* mask_path, int32_t seq_len,
+                         const int64_t* docs, int64_t B, int64_t* ids, int64_t* targets,
+                         float* mask, float* sum_mask, int64_t* num_docs);
+/* One loss.jsonl line (val != 0: a validation record) into buf. */
+int ctd_train_event_json(int32_t step, float loss, float lr, float grad_norm,
+                         double tokens_per_sec, double wall_s, int32_t val, char* buf,
+                         size_t cap);
+
 #ifdef __cplusplus
 }
 #endif
