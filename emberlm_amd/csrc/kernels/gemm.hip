@@ -1,26 +1,30 @@
 // fp32 GEMM on the gfx950 matrix cores (v_mfma_f32_32x32x2_f32).
 //
 // Replaces cublasSgemm / cublasSgemmStridedBatched behind ops::matmul and
-// ops::bmm (reference src/ops/matmul.cpp:13-93).  One kernel template covers
-// the four transpose cases: each operand is staged through LDS either
-// K-contiguous ([rows][BK+4], read as b128 so one LDS read feeds four MFMA
-// k-steps) or MN-contiguous ([BK][rows+8], read as b32 with consecutive lanes
-// on consecutive rows).  The k index an MFMA step consumes is permuted so that
-// lane group g = lane/32 owns k = 8*slab + 4*g + j for step j; A and B use the
-// same permutation, so the contraction is unchanged.
+// ops::bmm (reference src/ops/matmul.cpp:13-93).  Kernel templates cover the
+// four transpose cases: each operand tile is K-contiguous (read as b128, one
+// LDS read feeds four MFMA k-steps) or MN-contiguous (read as b32 with
+// consecutive lanes on consecutive rows).  The k index an MFMA step consumes
+// is permuted so that lane group g = lane/32 owns k = 8*slab + 4*g + j for
+// step j; A and B use the same permutation, so the contraction is unchanged.
 //
 // Block tiles 128x128 (three blocks per CU) or 256x128 (two per CU), 256
 // threads = 4 waves in 2x2, wave tile (BM/2)x(BN/2) of 32x32 MFMA tiles held
 // in accumulation registers.  A stage is BK = 16 = two k slabs, software
-// pipelined inside one wave so the matrix core never waits on LDS:
-//   global loads of stage k+1 -> registers (issued first),
-//   slab 0 MFMAs interleaved with the LDS reads of slab 1,
-//   slab 1 MFMAs interleaved with the LDS stores of stage k+1,
-//   barrier, then the reads of stage k+1's slab 0 under the last MFMAs.
-// One barrier per stage; LDS is double-buffered.  Tiles are ordered so that
-// tiles sharing A rows land on the same XCD (block b runs on XCD b % 8) and,
-// within it, in groups of 8 tile rows for L2 reuse.
+// pipelined inside one wave so the matrix core never waits on LDS (ordering
+// fixed with sched_group_barrier): slab-0 MFMAs under the LDS reads of slab 1,
+// one barrier, the next stage's slab-0 reads under the last slab-1 MFMAs.
 //
+// Main path, gemm_f32_dma: tiles are copied global -> LDS by
+// global_load_lds_dwordx4 (no register staging, no LDS store instructions)
+// into a 3-stage ring, two stages ahead of the MFMAs, with swizzled layouts
+// instead of padding.  Fallback, gemm_f32_mfma (K % 16 != 0, unaligned or
+// odd-width operands): global -> registers -> LDS, double-buffered, the
+// stores interleaved with the MFMAs.  Both accumulate in the same k order,
+// so they give identical bits.
+//
+// Tiles are ordered so that tiles sharing A rows land on the same XCD (block
+// b runs on XCD b % 8) and, within it, in groups of 8 tile rows for L2 reuse.
 // Small output grids with a long K (weight gradients: M, N = features,
 // K = tokens) are split along K into a workspace of partial products that a
 // second kernel sums in a fixed order, so results stay bitwise reproducible.
@@ -279,6 +283,229 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_mfma(GemmArgs a) {
     }
 }
 
+
+// ---------------------------------------------------------------- LDS DMA
+// Operand tiles go global -> LDS with global_load_lds_dwordx4: lane L of a
+// wave-instruction writes 16 bytes at LDS base + 16 L, so one instruction
+// fills a contiguous 1 KB block and the choice of which global 16 bytes each
+// lane fetches sets the layout.  No registers stage the tile and no LDS store
+// instruction runs.
+//   K-contiguous tile [ROWS][16]: 16-row blocks of 64 16-byte units; row x's
+//     k-chunk c sits at unit 4 (x % 16) + (c ^ swz(x % 16)).
+//   MN-contiguous tile [16][ROWS]: k-row k's chunk q (4 floats) sits at
+//     chunk position q ^ (8 ((k >> 2) & 1)).
+// Both keep the fragment reads free of bank conflicts without padding.
+__device__ __forceinline__ int swz(int x) { return ((x >> 1) ^ (x >> 3)) & 3; }
+
+template <bool KC, int ROWS>
+struct DmaTile {
+  static constexpr int kFloats = ROWS * 16;   // one stage
+  static constexpr int kInsts = ROWS / 64;    // wave-instructions per wave per stage
+  const float* src[kInsts];                    // this lane's 16 bytes, stage 0
+  int64_t step;                                // element stride between stages
+
+  __device__ __forceinline__ void init(const float* X, int64_t ld, int64_t R, int64_t row0,
+                                       int w, int lane) {
+#pragma unroll
+    for (int q = 0; q < kInsts; ++q) {
+      const int t = w + 4 * q;  // 1 KB block of the tile
+      if (KC) {
+        const int x = lane >> 2;
+        const int64_t row = min(row0 + 16 * t + x, R - 1);  // rows past R: never stored
+        src[q] = X + row * ld + 4 * ((lane & 3) ^ swz(x));
+      } else {
+        constexpr int kRowsPer = 256 / ROWS;   // k-rows per 1 KB block
+        constexpr int kLanesPer = 64 / kRowsPer;
+        const int k = t * kRowsPer + lane / kLanesPer;
+        const int q4 = (lane % kLanesPer) ^ (8 * ((k >> 2) & 1));
+        const int64_t col = min(row0 + 4 * q4, R - 4);      // R % 4 == 0 on this path
+        src[q] = X + k * ld + col;
+      }
+    }
+    step = KC ? 16 : 16 * ld;
+  }
+  // Stage kt of this lane's loads into the stage buffer `dst` (LDS).
+  __device__ __forceinline__ void issue(float* dst, int64_t kt, int w) const {
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass would drop the kernel's launch stub
+#pragma unroll
+    for (int q = 0; q < kInsts; ++q)
+      __builtin_amdgcn_global_load_lds(src[q] + kt * step, dst + 256 * (w + 4 * q), 16, 0, 0);
+#endif
+  }
+};
+
+// Fragment of 32-row tile `i` for MFMA steps j = 0..3 of slab s: one b128
+// read at the lane's precomputed offset (K-contiguous), or four b32 reads of
+// k-rows 8 s + 4 g + j at column position ((mb4 + 8 i) ^ 8 g) * 4 + r
+// (MN-contiguous; mb4 = the wave's first column / 4).
+template <bool KC, int ROWS>
+__device__ __forceinline__ f32x4 dma_frag(const float* st, int off, int i, int s, int g, int r,
+                                          int mb4) {
+  if (KC) return *reinterpret_cast<const f32x4*>(st + off + i * 32 * 16);
+  f32x4 v;
+  const int q = (mb4 + 8 * i) ^ (8 * g);
+  const float* p = st + (8 * s + 4 * g) * ROWS + (q << 2) + r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = p[j * ROWS];
+  return v;
+}
+
+// s_waitcnt with vmcnt <= N (loads still in flight: the newest N) and
+// lgkmcnt = 0; expcnt left alone.  gfx9 encoding: vmcnt bits 3:0 and 15:14,
+// expcnt 6:4, lgkmcnt 11:8.
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (0 << 8));
+}
+// Workgroup barrier with no implied memory wait (the waits above are explicit);
+// the empty asm keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void block_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <bool A_KC, bool B_KC, int BM, int BN, int OCC>
+__global__ __launch_bounds__(kThreads, OCC) void gemm_f32_dma(GemmArgs a) {
+  using TA = DmaTile<A_KC, BM>;
+  using TB = DmaTile<B_KC, BN>;
+  constexpr int FI = BM / 64, FJ = BN / 64;
+  constexpr int NR = FI * (A_KC ? 1 : 4) + FJ * (B_KC ? 1 : 4);
+  constexpr int NM = 4 * FI * FJ;
+  constexpr int kStage = TA::kFloats + TB::kFloats;
+  __shared__ __attribute__((aligned(1024))) float lds[3 * kStage];  // 3-stage ring
+  constexpr int NI = TA::kInsts + TB::kInsts;  // DMA instructions per wave per stage
+
+  int tm, tn;
+  tile_coords<BM, BN>(a, tm, tn);
+  const int64_t bz = blockIdx.y;
+  const float* __restrict__ A = a.A + bz * a.sA;
+  const float* __restrict__ B = a.B + bz * a.sB;
+  float* __restrict__ C = a.C + bz * a.sC;
+  const int64_t K = a.kchunk > 0 ? min(a.kchunk, a.K - bz * a.kchunk) : a.K;
+  const int64_t m0 = static_cast<int64_t>(tm) * BM;
+  const int64_t n0 = static_cast<int64_t>(tn) * BN;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int g = lane >> 5, r = lane & 31;
+
+  TA ta;
+  TB tb;
+  ta.init(A, a.lda, a.M, m0, wave, lane);
+  tb.init(B, a.ldb, a.N, n0, wave, lane);
+
+  // Per-lane fragment offsets (floats) inside a stage's A / B tile.
+  // K-contiguous: slab s reads unit 4 (r % 16) + ((2 s + g) ^ swz(r % 16)) of
+  // 16-row block (row / 16); MN-contiguous: k-row 8 s + 4 g + j, float
+  // ((mbase / 4) ^ 8 g) * 4 + r.
+  int offA[2], offB[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int u = 4 * (4 * (r & 15) + ((2 * s + g) ^ swz(r & 15))) + (r >> 4) * 256;
+    offA[s] = u + wm * (BM / 2) * 16;
+    offB[s] = u + wn * (BN / 2) * 16;
+  }
+  const int mbA = (wm * (BM / 2)) >> 2, mbB = (wn * (BN / 2)) >> 2;
+  f32x16 acc[FI][FJ];
+#pragma unroll
+  for (int i = 0; i < FI; ++i)
+#pragma unroll
+    for (int j = 0; j < FJ; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int64_t nk = K / 16;
+  if (nk > 0) {
+    ta.issue(lds, 0, wave);
+    tb.issue(lds + TA::kFloats, 0, wave);
+  }
+  if (nk > 1) {
+    ta.issue(lds + kStage, 1, wave);
+    tb.issue(lds + kStage + TA::kFloats, 1, wave);
+    wait_vm_lgkm0<NI>();
+  } else {
+    wait_vm_lgkm0<0>();
+  }
+  block_barrier();
+  float* st0 = lds;
+  f32x4 fa0[FI], fb0[FJ], fa1[FI], fb1[FJ];
+#pragma unroll
+  for (int i = 0; i < FI; ++i) fa0[i] = dma_frag<A_KC, BM>(st0, offA[0], i, 0, g, r, mbA);
+#pragma unroll
+  for (int j = 0; j < FJ; ++j) fb0[j] = dma_frag<B_KC, BN>(st0 + TA::kFloats, offB[0], j, 0, g, r, mbB);
+
+  int ic = 0;  // kt % 3
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    float* cur = lds + ic * kStage;
+    float* nxt = lds + (ic == 2 ? 0 : ic + 1) * kStage;
+    float* nx2 = lds + (ic == 0 ? 2 : ic - 1) * kStage;
+    const bool more2 = kt + 2 < nk;
+    if (more2) {
+      ta.issue(nx2, kt + 2, wave);
+      tb.issue(nx2 + TA::kFloats, kt + 2, wave);
+    }
+#pragma unroll
+    for (int i = 0; i < FI; ++i) fa1[i] = dma_frag<A_KC, BM>(cur, offA[1], i, 1, g, r, mbA);
+#pragma unroll
+    for (int j = 0; j < FJ; ++j) fb1[j] = dma_frag<B_KC, BN>(cur + TA::kFloats, offB[1], j, 1, g, r, mbB);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int i = 0; i < FI; ++i)
+#pragma unroll
+        for (int j = 0; j < FJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa0[i][s], fb0[j][s], acc[i][j], 0, 0, 0);
+    interleave<NR, NM, 0x100>();
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int i = 0; i < FI; ++i)
+#pragma unroll
+        for (int j = 0; j < FJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[i][s], fb1[j][s], acc[i][j], 0, 0, 0);
+    // Stage kt+1's DMA has landed (only stage kt+2's may still be in flight)
+    // and every wave is done reading stage kt's buffer.
+    if (more2)
+      wait_vm_lgkm0<NI>();
+    else
+      wait_vm_lgkm0<0>();
+    block_barrier();
+#pragma unroll
+    for (int i = 0; i < FI; ++i) fa0[i] = dma_frag<A_KC, BM>(nxt, offA[0], i, 0, g, r, mbA);
+#pragma unroll
+    for (int j = 0; j < FJ; ++j) fb0[j] = dma_frag<B_KC, BN>(nxt + TA::kFloats, offB[0], j, 0, g, r, mbB);
+#pragma unroll
+    for (int s = 2; s < 4; ++s)
+#pragma unroll
+      for (int i = 0; i < FI; ++i)
+#pragma unroll
+        for (int j = 0; j < FJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[i][s], fb1[j][s], acc[i][j], 0, 0, 0);
+    interleave<NR, NM / 2, 0x100>();
+    ic = ic == 2 ? 0 : ic + 1;
+  }
+
+#pragma unroll
+  for (int i = 0; i < FI; ++i)
+#pragma unroll
+    for (int j = 0; j < FJ; ++j) {
+      const int64_t col = n0 + wn * (BN / 2) + j * 32 + r;
+      if (col >= a.N) continue;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t row = m0 + wm * (BM / 2) + i * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+        if (row < a.M) {
+          float* dst = C + row * a.ldc + col;
+          const float v = a.alpha * acc[i][j][e];
+          *dst = (a.beta != 0.f) ? v + a.beta * *dst : v;
+        }
+      }
+    }
+}
+
 // C = alpha * sum_{s<S} P[s] + beta * C, the split partials summed in order.
 // P is [S][M][N] dense; four columns per thread when the rows allow it.
 template <bool VEC>
@@ -361,6 +588,23 @@ int launch_t(GemmArgs a, bool a_kc, bool b_kc, int64_t ny, bool vec, hipStream_t
   return launch<false, true, BM, BN, OCC>(a, ny, vec, st);
 }
 
+template <bool A_KC, bool B_KC, int BM, int BN, int OCC>
+int launch_dma_t(GemmArgs a, int64_t ny, hipStream_t st) {
+  a.tiles_m = static_cast<int>(cdiv(a.M, BM));
+  a.tiles_n = static_cast<int>(cdiv(a.N, BN));
+  dim3 grid(static_cast<unsigned>(a.tiles_m) * a.tiles_n, static_cast<unsigned>(ny));
+  gemm_f32_dma<A_KC, B_KC, BM, BN, OCC><<<grid, kThreads, 0, st>>>(a);
+  return launch_status();
+}
+
+template <int BM, int BN, int OCC>
+int launch_dma(const GemmArgs& a, bool a_kc, bool b_kc, int64_t ny, hipStream_t st) {
+  if (a_kc && b_kc) return launch_dma_t<true, true, BM, BN, OCC>(a, ny, st);
+  if (a_kc && !b_kc) return launch_dma_t<true, false, BM, BN, OCC>(a, ny, st);
+  if (!a_kc && !b_kc) return launch_dma_t<false, false, BM, BN, OCC>(a, ny, st);
+  return launch_dma_t<false, true, BM, BN, OCC>(a, ny, st);
+}
+
 int check_args(int transa, int transb, int64_t M, int64_t N, int64_t K, const float* A,
                int64_t lda, const float* B, int64_t ldb, const float* C, int64_t ldc,
                int64_t batch) {
@@ -408,7 +652,11 @@ extern "C" int ember_gemm_f32_ws(int transa, int transb, int64_t M, int64_t N, i
     sp.kchunk = p.kchunk;
     sp.alpha = 1.f;
     sp.beta = 0.f;
-    if ((rc = launch_t<128, 128, 3>(sp, a_kc, b_kc, p.splits, vec, st))) return rc;
+    const bool dma = vec && p.kchunk % 16 == 0 && K % 16 == 0 && (a_kc || M % 4 == 0) &&
+                     (b_kc || N % 4 == 0);
+    if ((rc = dma ? launch_dma<128, 128, 3>(sp, a_kc, b_kc, p.splits, st)
+                  : launch_t<128, 128, 3>(sp, a_kc, b_kc, p.splits, vec, st)))
+      return rc;
     const bool rvec = (N % 4 == 0) && (ldc % 4 == 0) && aligned16(C);
     const int64_t items = M * (rvec ? N / 4 : N);
     const unsigned blocks = static_cast<unsigned>(cdiv(items, kThreads));
@@ -422,6 +670,10 @@ extern "C" int ember_gemm_f32_ws(int transa, int transb, int64_t M, int64_t N, i
                                                         alpha, beta);
     return launch_status();
   }
+  const bool dma = vec && K % 16 == 0 && (a_kc || M % 4 == 0) && (b_kc || N % 4 == 0) &&
+                   (batch == 1 || (sA % 4 == 0 && sB % 4 == 0));
+  if (dma && p.big) return launch_dma<256, 128, 2>(a, a_kc, b_kc, batch, st);
+  if (dma) return launch_dma<128, 128, 3>(a, a_kc, b_kc, batch, st);
   if (p.big) return launch_t<256, 128, 2>(a, a_kc, b_kc, batch, vec, st);
   return launch_t<128, 128, 3>(a, a_kc, b_kc, batch, vec, st);
 }

@@ -75,13 +75,14 @@ def test_gemm_alpha_beta_and_kat():
     assert_close(got, 0.5 * O.matmul(a, b) + c, name="alpha/beta")
 
 
-def test_gemm_batched():
+@pytest.mark.parametrize("K", [40, 48])
+def test_gemm_batched(K):
     r = rng(4)
-    a = r.standard_normal((3, 64, 40)).astype(np.float32)
-    b = r.standard_normal((3, 72, 40)).astype(np.float32)
+    a = r.standard_normal((3, 64, K)).astype(np.float32)
+    b = r.standard_normal((3, 72, K)).astype(np.float32)
     A, B = dev(a), dev(b)
     Cm = empty((3, 64, 72))
-    call("ember_gemm_f32", 0, 1, 64, 72, 40, 1.0, p(A), 40, 64 * 40, p(B), 40, 72 * 40, 0.0, p(Cm),
+    call("ember_gemm_f32", 0, 1, 64, 72, K, 1.0, p(A), K, 64 * K, p(B), K, 72 * K, 0.0, p(Cm),
          72, 64 * 72, 3, None)
     assert_close(host(Cm), O.bmm(a, b, False, True), name="bmm")
 
@@ -119,10 +120,12 @@ def gemm_ws(a, b, ta, tb, alpha=1.0, beta=0.0, c=None, ws_bytes=None):
     return host(Cm), need
 
 
-@pytest.mark.parametrize("ta,tb", [(1, 0), (0, 0), (0, 1), (1, 1)])
-def test_gemm_split_k_vs_oracle(ta, tb):
-    # Few output tiles and a long, ragged K: the K-split path with partials.
-    M, N, K = 130, 200, 5003
+@pytest.mark.parametrize("ta,tb,K", [(1, 0, 5003), (0, 0, 5003), (0, 1, 5003), (1, 1, 5003),
+                                     (1, 0, 5008), (0, 1, 5008)])
+def test_gemm_split_k_vs_oracle(ta, tb, K):
+    # Few output tiles and a long K: the K-split path with partials (K % 16 == 0
+    # takes the LDS-DMA kernel, a ragged K the register-staged one).
+    M, N = 132, 200
     r = rng(11 + 2 * ta + tb)
     a = r.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
     b = r.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
@@ -154,10 +157,15 @@ def test_gemm_split_k_weight_gradient_shape_vs_torch():
     assert rel < 1e-5, rel
 
 
-@pytest.mark.parametrize("ta,tb", [(0, 1), (0, 0), (1, 0), (1, 1)])
-def test_gemm_large_tile_ragged_vs_oracle(ta, tb):
-    # Enough tiles for the 256x128 kernel, with M, N and K all off the tile grid.
-    M, N, K = 33000, 1000, 40
+@pytest.mark.parametrize("ta,tb,M,N,K", [
+    (0, 1, 33000, 1000, 40), (0, 0, 33000, 1000, 40), (1, 0, 33000, 1000, 40),
+    (1, 1, 33000, 1000, 40),                        # register-staged kernel (K % 16 != 0)
+    (0, 1, 33000, 1000, 48), (0, 0, 33000, 1000, 48), (1, 0, 33000, 1000, 48),
+    (1, 1, 33000, 1000, 48),                        # LDS-DMA kernel, M, N off the tile grid
+    (0, 1, 33001, 999, 48),                         # LDS-DMA, K-contiguous rows clamped
+])
+def test_gemm_large_tile_ragged_vs_oracle(ta, tb, M, N, K):
+    # Enough tiles for the 256x128 kernels, with M and N off the tile grid.
     r = rng(21 + 2 * ta + tb)
     a = r.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
     b = r.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
