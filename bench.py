@@ -222,10 +222,10 @@ def main():
     mask_sum = times[-1].mask_sum
 
     # Dominant GEMM instantiation (largest summed time) for the roofline line.
-    kname = {"NT": "gemm_f32_mfma<A K-contig, B K-contig> (Linear forward, NT)",
-             "NN": "gemm_f32_mfma<A K-contig, B N-contig> (dX, NN)",
-             "TN": "gemm_f32_mfma<A M-contig, B N-contig> (dW, TN)",
-             "TT": "gemm_f32_mfma<A M-contig, B K-contig> (TT)"}
+    kname = {"NT": "gemm_f32_dma<A K-contig, B K-contig> (Linear forward, NT)",
+             "NN": "gemm_f32_dma<A K-contig, B N-contig> (dX, NN)",
+             "TN": "gemm_f32_dma<A M-contig, B N-contig> (dW, TN)",
+             "TT": "gemm_f32_dma<A M-contig, B K-contig> (TT)"}
     dom = max(prof, key=lambda k: prof[k].total_ms)
     p = prof[dom]
     per_launch_flops = p.flops / max(p.launches, 1)
