@@ -1,0 +1,199 @@
+// Token generation behind the ctd_generate protocol.
+// Reference: tools/ctd_generate/main.cpp:52-192 (request fields and defaults,
+// stop reasons, budget forcing, reply lines).
+//
+// Differences that keep the protocol: the prefill runs the LM head on the last
+// position only (Model::forward_last_logits; the reference computes [1, T, V]
+// logits and copies all of them to the host to keep the last row), and greedy
+// steps take the argmax on the device.
+#include "ctd/generate.h"
+
+#include <algorithm>
+#include <chrono>
+#include <random>
+#include <stdexcept>
+#include <unordered_set>
+
+#include "ctd/nn/kv_cache.h"
+#include "ctd/nn/model.h"
+#include "ctd/safetensors.h"
+#include "ctd/train.h"
+#include "json.h"
+
+namespace ctd::generate {
+
+namespace {
+
+using json::JVal;
+
+double number(const JVal& v, const std::string& key) {
+  if (v.kind != JVal::kNum) throw std::runtime_error("request: " + key + " must be a number");
+  return v.num;
+}
+
+int64_t integer(const JVal& v, const std::string& key) {
+  if (v.kind != JVal::kNum) throw std::runtime_error("request: " + key + " must be an integer");
+  if (v.str.find_first_of(".eE") == std::string::npos) return std::stoll(v.str);
+  return static_cast<int64_t>(v.num);
+}
+
+std::vector<int64_t> ids(const JVal& v, const std::string& key) {
+  std::vector<int64_t> out;
+  if (v.kind == JVal::kNum) {  // a lone id counts as a one-element list
+    out.push_back(integer(v, key));
+    return out;
+  }
+  if (v.kind != JVal::kArr) throw std::runtime_error("request: " + key + " must be a list");
+  for (const JVal& e : v.arr) out.push_back(integer(e, key));
+  return out;
+}
+
+std::string line(const json::ObjectWriter& w) { return w.str() + "\n"; }
+
+double seconds_since(std::chrono::steady_clock::time_point t) {
+  return std::chrono::duration<double>(std::chrono::steady_clock::now() - t).count();
+}
+
+}  // namespace
+
+Request parse_request(const std::string& text) {
+  const JVal req = json::Parser(text, "request: bad JSON").parse();
+  if (req.kind != JVal::kObj) throw std::runtime_error("request: expected a JSON object");
+  Request r;
+  r.input_ids = ids(req.at("input_ids"), "input_ids");
+  if (const JVal* v = req.find("max_new_tokens"))
+    r.max_new_tokens = static_cast<int>(integer(*v, "max_new_tokens"));
+  if (const JVal* v = req.find("max_seq_len"))
+    r.max_seq_len = static_cast<int>(integer(*v, "max_seq_len"));
+  if (const JVal* v = req.find("temperature"))
+    r.sampler.temperature = static_cast<float>(number(*v, "temperature"));
+  if (const JVal* v = req.find("top_k")) r.sampler.top_k = static_cast<int>(integer(*v, "top_k"));
+  if (const JVal* v = req.find("top_p"))
+    r.sampler.top_p = static_cast<float>(number(*v, "top_p"));
+  if (const JVal* v = req.find("seed")) {
+    if (v->kind != JVal::kNum) throw std::runtime_error("request: seed must be an integer");
+    r.seed = v->str.find_first_of(".eE-") == std::string::npos
+                 ? std::stoull(v->str)
+                 : static_cast<uint64_t>(integer(*v, "seed"));
+  }
+  if (const JVal* v = req.find("eos_ids")) r.eos_ids = ids(*v, "eos_ids");
+  if (const JVal* v = req.find("thinking_token_budget"))
+    r.thinking_token_budget = static_cast<int>(integer(*v, "thinking_token_budget"));
+  if (const JVal* v = req.find("think_open_ids")) r.think_open_ids = ids(*v, "think_open_ids");
+  if (const JVal* v = req.find("think_close_ids")) r.think_close_ids = ids(*v, "think_close_ids");
+  return r;
+}
+
+ThinkBudget::ThinkBudget(const Request& r)
+    : active_(r.thinking_token_budget > 0 && !r.think_open_ids.empty() &&
+              !r.think_close_ids.empty()),
+      budget_(r.thinking_token_budget),
+      open_(r.think_open_ids),
+      close_(r.think_close_ids),
+      cap_(std::max(r.think_open_ids.size(), r.think_close_ids.size())) {}
+
+bool ThinkBudget::next_forced(int64_t* tok) {
+  if (!active_ || queue_.empty()) return false;
+  *tok = queue_.front();
+  queue_.erase(queue_.begin());
+  return true;
+}
+
+bool ThinkBudget::ends_with(const std::vector<int64_t>& seq) const {
+  return window_.size() >= seq.size() &&
+         std::equal(seq.begin(), seq.end(), window_.end() - static_cast<int64_t>(seq.size()));
+}
+
+void ThinkBudget::observe(int64_t tok) {
+  if (!active_) return;
+  window_.push_back(tok);
+  if (window_.size() > cap_) window_.erase(window_.begin());
+  if (ends_with(open_)) {
+    in_think_ = true;
+    count_ = 0;
+  } else if (ends_with(close_)) {
+    in_think_ = false;
+  } else if (in_think_) {
+    ++count_;
+  }
+  if (in_think_ && queue_.empty() && count_ >= budget_) queue_ = close_;
+}
+
+int run(const std::string& model_path, const std::string& request, std::ostream& out,
+        std::ostream& log, const std::string& model_config) {
+  try {
+    const Request req = parse_request(request);
+    const std::unordered_set<int64_t> eos(req.eos_ids.begin(), req.eos_ids.end());
+
+    const auto t0 = std::chrono::steady_clock::now();
+    log << "[ctd_generate] loading " << model_path << "\n";
+    const TensorDict weights = load_safetensors(model_path, kHIP0);
+    const nn::LlamaConfig cfg = model_config.empty() ? nn::autodetect_config(weights)
+                                                     : train::load_model_config(model_config);
+    log << "[ctd_generate] arch: hidden=" << cfg.hidden_size
+        << " layers=" << cfg.num_hidden_layers << "\n";
+    const nn::Model model = nn::build_model(weights, cfg);
+    const auto t1 = std::chrono::steady_clock::now();
+    log << "[ctd_generate] model ready in " << seconds_since(t0) << " s\n";
+
+    const int prompt_len = static_cast<int>(req.input_ids.size());
+    if (prompt_len == 0) {
+      out << line(json::ObjectWriter().field("done", true).field("reason", "empty_prompt"))
+          << std::flush;
+      return 0;
+    }
+    if (prompt_len >= req.max_seq_len) {
+      out << line(json::ObjectWriter().field("done", true).field("reason", "max_seq_len"))
+          << std::flush;
+      return 0;
+    }
+    nn::KVCache cache = nn::KVCache::allocate(cfg.num_hidden_layers, cfg.num_key_value_heads,
+                                              cfg.head_dim, /*batch=*/1, req.max_seq_len, kHIP0);
+    Tensor prompt = Tensor::from_host(req.input_ids.data(), {1, prompt_len}, DType::kInt64, kHIP0);
+    Tensor last = model.forward_last_logits(prompt, &cache, 0);
+    log << "[ctd_generate] prefill (" << prompt_len << " tok) in " << seconds_since(t1)
+        << " s\n";
+
+    std::mt19937_64 rng(req.seed);
+    ThinkBudget think(req);
+    int generated = 0;
+    const char* reason = "max_tokens";
+    const auto t2 = std::chrono::steady_clock::now();
+    while (generated < req.max_new_tokens) {
+      int64_t tok;
+      if (!think.next_forced(&tok)) tok = sample(last, req.sampler, rng)[0];
+      out << line(json::ObjectWriter().field("token", tok)) << std::flush;
+      ++generated;
+      think.observe(tok);
+      if (eos.count(tok)) {
+        reason = "eos";
+        break;
+      }
+      if (cache.current_len + 1 > req.max_seq_len) {
+        reason = "max_seq_len";
+        break;
+      }
+      Tensor next = Tensor::from_host(&tok, {1, 1}, DType::kInt64, kHIP0);
+      last = model.forward_last_logits(next, &cache, static_cast<int>(cache.current_len));
+    }
+    const double dt = seconds_since(t2);
+    log << "[ctd_generate] generated " << generated << " tok in " << dt << " s  ("
+        << generated / std::max(dt, 1e-9) << " tok/s)\n";
+    out << line(json::ObjectWriter()
+                    .field("done", true)
+                    .field("generated_tokens", generated)
+                    .field("reason", reason))
+        << std::flush;
+    return 0;
+  } catch (const std::exception& e) {
+    log << "[ctd_generate] error: " << e.what() << "\n";
+    out << line(json::ObjectWriter()
+                    .field("done", true)
+                    .field("error", e.what())
+                    .field("reason", "error"))
+        << std::flush;
+    return 1;
+  }
+}
+
+}  // namespace ctd::generate

@@ -197,10 +197,30 @@ class ObjectWriter {
     key(k);
     out_ += '"';
     for (char c : v) {
-      if (c == '"' || c == '\\') out_ += '\\';
-      out_ += c;
+      switch (c) {
+        case '"': out_ += "\\\""; break;
+        case '\\': out_ += "\\\\"; break;
+        case '\b': out_ += "\\b"; break;
+        case '\f': out_ += "\\f"; break;
+        case '\n': out_ += "\\n"; break;
+        case '\r': out_ += "\\r"; break;
+        case '\t': out_ += "\\t"; break;
+        default:
+          if (static_cast<unsigned char>(c) < 0x20) {
+            char buf[8];
+            std::snprintf(buf, sizeof(buf), "\\u%04x", static_cast<unsigned>(c));
+            out_ += buf;
+          } else {
+            out_ += c;
+          }
+      }
     }
     out_ += '"';
+    return *this;
+  }
+  ObjectWriter& field(const std::string& k, bool v) {
+    key(k);
+    out_ += v ? "true" : "false";
     return *this;
   }
   ObjectWriter& field(const std::string& k, const char* v) { return field(k, std::string(v)); }

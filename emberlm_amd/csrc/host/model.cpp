@@ -6,6 +6,8 @@
 #include <string>
 
 #include "ctd/ops/loss.h"
+#include "ctd/runtime.h"
+#include "ember_hip.h"
 
 namespace ctd::nn {
 
@@ -94,9 +96,56 @@ LlamaConfig autodetect_config(const TensorDict& w) {
                            " vocab_size=" + std::to_string(vocab));
 }
 
-Tensor Model::forward(const Tensor& input_ids) const {
+namespace {
+
+// Final hidden states [B, T, H] of the inference forward (model.h:152-163 of
+// the reference, without the LM head).
+Tensor hidden_states(const Model& m, const Tensor& input_ids, KVCache* cache,
+                     int position_start) {
+  if (input_ids.dim() != 2) throw std::runtime_error("Model::forward: input_ids must be [B, T]");
+  if (cache) {
+    if (cache->layers.size() != m.layers.size())
+      throw std::runtime_error("Model::forward: KV cache has " +
+                               std::to_string(cache->layers.size()) + " layers, model has " +
+                               std::to_string(m.layers.size()));
+    if (cache->batch != input_ids.shape()[0])
+      throw std::runtime_error("Model::forward: KV cache batch != input batch");
+  }
+  Tensor h = m.embed_tokens.forward(input_ids);
+  for (size_t i = 0; i < m.layers.size(); ++i) {
+    KVLayer* kv = cache ? &cache->layers[i] : nullptr;
+    h = m.layers[i].forward(h, kv, position_start);
+  }
+  if (cache) cache->current_len = position_start + input_ids.shape()[1];
+  return m.norm.forward(h);
+}
+
+}  // namespace
+
+Tensor Model::forward(const Tensor& input_ids, KVCache* cache, int position_start) const {
   autograd::NoGradGuard ng;
-  return forward_train_logits(input_ids);
+  Tensor h = hidden_states(*this, input_ids, cache, position_start);
+  Linear lm_head{embed_tokens.weight};  // tied head
+  return lm_head.forward(h);
+}
+
+Tensor Model::forward_last_logits(const Tensor& input_ids, KVCache* cache,
+                                  int position_start) const {
+  autograd::NoGradGuard ng;
+  Tensor h = hidden_states(*this, input_ids, cache, position_start);
+  const int64_t B = h.shape()[0], T = h.shape()[1], H = h.shape()[2];
+  Tensor last;
+  if (B == 1) {
+    last = h.view_at((T - 1) * H, {1, 1, H});
+  } else {
+    last = Tensor::empty({B, 1, H}, DType::kFloat32, h.device());
+    for (int64_t b = 0; b < B; ++b)
+      CTD_CHECK(ember_memcpy_async(static_cast<float*>(last.data_ptr()) + b * H,
+                                   static_cast<const float*>(h.data_ptr()) + (b * T + T - 1) * H,
+                                   H * sizeof(float), 2, runtime::compute_stream()));
+  }
+  Linear lm_head{embed_tokens.weight};
+  return lm_head.forward(last);
 }
 
 Tensor Model::forward_train_logits(const Tensor& input_ids) const {

@@ -80,7 +80,40 @@ std::string get_string(const json::JVal& j, const char* k) {
   return v.str;
 }
 
+// LlamaConfig from a JSON object with the HF config field names.
+nn::LlamaConfig model_config(const json::JVal& m) {
+  if (m.kind != json::JVal::kObj) throw std::runtime_error("config: model must be an object");
+  nn::LlamaConfig a{};
+  a.vocab_size = get_int(m, "vocab_size", 0);
+  a.hidden_size = get_int(m, "hidden_size", 0);
+  a.intermediate_size = get_int(m, "intermediate_size", 0);
+  a.num_hidden_layers = get_int(m, "num_hidden_layers", 0);
+  a.num_attention_heads = get_int(m, "num_attention_heads", 0);
+  a.num_key_value_heads = get_int(m, "num_key_value_heads", a.num_attention_heads);
+  a.head_dim = get_int(m, "head_dim",
+                       a.num_attention_heads ? a.hidden_size / a.num_attention_heads : 0);
+  a.max_position_embeddings = get_int(m, "max_position_embeddings", 8192);
+  a.rms_norm_eps = get_float(m, "rms_norm_eps", 1e-5f);
+  a.rope_theta = get_float(m, "rope_theta", 1e4f);
+  a.tie_word_embeddings = get_bool(m, "tie_word_embeddings", true);
+  a.qk_norm = get_bool(m, "qk_norm", false);
+  a.rope_scaling_factor = get_float(m, "rope_scaling_factor", 0.0f);
+  a.rope_scaling_low_freq_factor = get_float(m, "rope_scaling_low_freq_factor", 1.0f);
+  a.rope_scaling_high_freq_factor = get_float(m, "rope_scaling_high_freq_factor", 4.0f);
+  a.rope_scaling_original_max_pos = get_int(m, "rope_scaling_original_max_pos", 8192);
+  if (a.vocab_size <= 0 || a.hidden_size <= 0 || a.num_hidden_layers <= 0 ||
+      a.num_attention_heads <= 0 || a.intermediate_size <= 0)
+    throw std::runtime_error("config: model needs vocab_size, hidden_size, intermediate_size, "
+                             "num_hidden_layers and num_attention_heads");
+  return a;
+}
+
 }  // namespace
+
+nn::LlamaConfig load_model_config(const fs::path& path) {
+  const std::string text = read_text(path);
+  return model_config(json::Parser(text, "model config: bad JSON").parse());
+}
 
 Config load_config(const fs::path& cfg_path) {
   const std::string text = read_text(cfg_path);
@@ -114,28 +147,7 @@ Config load_config(const fs::path& cfg_path) {
   c.offload_optimizer = get_bool(j, "offload_optimizer", c.offload_optimizer);
   c.gradient_checkpointing = get_bool(j, "gradient_checkpointing", c.gradient_checkpointing);
   if (const json::JVal* m = key(j, "model")) {
-    if (m->kind != json::JVal::kObj) throw std::runtime_error("config: model must be an object");
-    nn::LlamaConfig& a = c.model;
-    a.vocab_size = get_int(*m, "vocab_size", 0);
-    a.hidden_size = get_int(*m, "hidden_size", 0);
-    a.intermediate_size = get_int(*m, "intermediate_size", 0);
-    a.num_hidden_layers = get_int(*m, "num_hidden_layers", 0);
-    a.num_attention_heads = get_int(*m, "num_attention_heads", 0);
-    a.num_key_value_heads = get_int(*m, "num_key_value_heads", a.num_attention_heads);
-    a.head_dim = get_int(*m, "head_dim", a.num_attention_heads ? a.hidden_size / a.num_attention_heads : 0);
-    a.max_position_embeddings = get_int(*m, "max_position_embeddings", 8192);
-    a.rms_norm_eps = get_float(*m, "rms_norm_eps", 1e-5f);
-    a.rope_theta = get_float(*m, "rope_theta", 1e4f);
-    a.tie_word_embeddings = get_bool(*m, "tie_word_embeddings", true);
-    a.qk_norm = get_bool(*m, "qk_norm", false);
-    a.rope_scaling_factor = get_float(*m, "rope_scaling_factor", 0.0f);
-    a.rope_scaling_low_freq_factor = get_float(*m, "rope_scaling_low_freq_factor", 1.0f);
-    a.rope_scaling_high_freq_factor = get_float(*m, "rope_scaling_high_freq_factor", 4.0f);
-    a.rope_scaling_original_max_pos = get_int(*m, "rope_scaling_original_max_pos", 8192);
-    if (a.vocab_size <= 0 || a.hidden_size <= 0 || a.num_hidden_layers <= 0 ||
-        a.num_attention_heads <= 0 || a.intermediate_size <= 0)
-      throw std::runtime_error("config: model needs vocab_size, hidden_size, intermediate_size, "
-                               "num_hidden_layers and num_attention_heads");
+    c.model = model_config(*m);
     c.has_model = true;
   }
   if (c.seq_len < 2 || c.batch_size < 1 || c.grad_accum_steps < 1)

@@ -5,9 +5,11 @@
 // zero_grad); the optimizer-state file follows main.cpp:208-271 (m then v per
 // parameter, decay group first, plus optimizer.step), loading straight into
 // the pinned host state when m/v are offloaded.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <memory>
+#include <random>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -17,6 +19,7 @@
 #include "ctd/ops/repeat_kv.h"
 #include "ctd/optim.h"
 #include "ctd/runtime.h"
+#include "ctd/sampling.h"
 #include "ctd/train.h"
 #include "ctd_capi.h"
 
@@ -605,6 +608,56 @@ int ctd_train_event_json(int32_t step, float loss, float lr, float grad_norm,
                               : train::train_event(step, loss, lr, grad_norm, tokens_per_sec, wall_s);
     if (!buf || cap < e.size() + 1) throw std::runtime_error("buffer too small");
     std::memcpy(buf, e.c_str(), e.size() + 1);
+  });
+}
+
+int ctd_kvcache_create(ctd_trainer_t t, int64_t batch, int64_t max_seq, ctd_kvcache_t* out) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    if (!out) throw std::runtime_error("null output handle");
+    if (batch < 1 || max_seq < 1) throw std::runtime_error("kv cache: batch, max_seq >= 1");
+    const nn::LlamaConfig& c = tr->model.config;
+    *out = new nn::KVCache(nn::KVCache::allocate(c.num_hidden_layers, c.num_key_value_heads,
+                                                 c.head_dim, batch, max_seq, kHIP0));
+  });
+}
+
+int ctd_kvcache_destroy(ctd_kvcache_t c) {
+  return guarded([&] { delete static_cast<nn::KVCache*>(c); });
+}
+
+int ctd_kvcache_len(ctd_kvcache_t c, int64_t* current_len) {
+  return guarded([&] {
+    if (!c) throw std::runtime_error("null kv cache handle");
+    *current_len = static_cast<nn::KVCache*>(c)->current_len;
+  });
+}
+
+int ctd_trainer_forward_cached(ctd_trainer_t t, ctd_kvcache_t cache, const int64_t* ids,
+                               int64_t B, int64_t T, int32_t position_start, int32_t last_only,
+                               float* logits, int64_t numel) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    Tensor x = Tensor::from_host(ids, {B, T}, DType::kInt64, kHIP0);
+    auto* kv = static_cast<nn::KVCache*>(cache);
+    Tensor y = last_only ? tr->model.forward_last_logits(x, kv, position_start)
+                         : tr->model.forward(x, kv, position_start);
+    check_numel(y, numel);
+    y.copy_to_host(logits);
+  });
+}
+
+int ctd_sample(const float* logits, int64_t B, int64_t V, float temperature, int32_t top_k,
+               float top_p, uint64_t seed, int32_t draws, int32_t on_device, int64_t* out) {
+  return guarded([&] {
+    if (B < 0 || V < 1 || draws < 0) throw std::runtime_error("sample: bad sizes");
+    Tensor x = Tensor::from_host(logits, {B, 1, V}, DType::kFloat32, on_device ? kHIP0 : kCPU);
+    SamplerConfig cfg{temperature, top_k, top_p};
+    std::mt19937_64 rng(seed);
+    for (int32_t d = 0; d < draws; ++d) {
+      const std::vector<int64_t> tok = sample(x, cfg, rng);
+      std::copy(tok.begin(), tok.end(), out + static_cast<int64_t>(d) * B);
+    }
   });
 }
 

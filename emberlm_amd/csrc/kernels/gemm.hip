@@ -539,6 +539,102 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce(const float* __restric
   }
 }
 
+// Skinny NT product for M <= 8 rows (decode: one token per sequence):
+// C[M,N] = alpha * A[M,K] B[N,K]^T + beta * C.  The MFMA tiles would run
+// 1/128 full and only N/128 workgroups wide; this kernel is bound by streaming
+// B from HBM (4*N*K bytes) instead.  A workgroup owns kSkinnyRows consecutive
+// rows of B; its 4 waves take one K quarter each, every lane streams float4s of
+// those rows (1 KB per row per wave load) and dots them with the M rows of A
+// (a few KB, served by L1/L2).  Partial sums are reduced across the wave by
+// shuffles and across the 4 waves through LDS in wave order.
+constexpr int kSkinnyRows = 4;
+constexpr int kSkinnyMaxM = 8;
+
+template <int MR>
+__global__ __launch_bounds__(kThreads) void gemm_skinny_nt(const float* __restrict__ A,
+                                                           int64_t lda,
+                                                           const float* __restrict__ B,
+                                                           int64_t ldb, float* __restrict__ C,
+                                                           int64_t ldc, int M, int64_t N,
+                                                           int64_t K, float alpha, float beta) {
+  constexpr int NR = kSkinnyRows;
+  __shared__ float red[kThreads / kWave][NR * MR];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = threadIdx.x / kWave;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * NR;
+  const int64_t K4 = K / 4;
+  const int64_t quarter = (K4 + 3) / 4;
+  const int64_t kb = w * quarter;
+  const int64_t ke = kb + quarter < K4 ? kb + quarter : K4;
+  const f32x4* brow[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int64_t n = n0 + r < N ? n0 + r : N - 1;  // rows past N re-read the last one
+    brow[r] = reinterpret_cast<const f32x4*>(B + n * ldb);
+  }
+  float acc[NR][MR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[r][m] = 0.f;
+
+  for (int64_t i = kb + lane; i < ke; i += 2 * kWave) {
+    const int64_t i1 = i + kWave;
+    const bool two = i1 < ke;
+    f32x4 b0[NR], b1[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      b0[r] = brow[r][i];
+      b1[r] = two ? brow[r][i1] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      if (m < M) {
+        const f32x4* arow = reinterpret_cast<const f32x4*>(A + m * lda);
+        const f32x4 x0 = arow[i];
+        const f32x4 x1 = two ? arow[i1] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          acc[r][m] += b0[r].x * x0.x + b0[r].y * x0.y + b0[r].z * x0.z + b0[r].w * x0.w;
+          acc[r][m] += b1[r].x * x1.x + b1[r].y * x1.y + b1[r].z * x1.z + b1[r].w * x1.w;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; ++r)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      if (m < M) {
+        const float s = wave_sum(acc[r][m]);
+        if (lane == 0) red[w][r * MR + m] = s;
+      }
+    }
+  __syncthreads();
+  const int idx = threadIdx.x;
+  if (idx < NR * MR) {
+    const int r = idx / MR, m = idx % MR;
+    const int64_t n = n0 + r;
+    if (m < M && n < N) {
+      float s = 0.f;
+#pragma unroll
+      for (int q = 0; q < kThreads / kWave; ++q) s += red[q][idx];
+      float* c = C + m * ldc + n;
+      *c = beta != 0.f ? alpha * s + beta * *c : alpha * s;
+    }
+  }
+}
+
+template <int MR>
+int launch_skinny(const float* A, int64_t lda, const float* B, int64_t ldb, float* C,
+                  int64_t ldc, int64_t M, int64_t N, int64_t K, float alpha, float beta,
+                  hipStream_t st) {
+  const unsigned grid = static_cast<unsigned>((N + kSkinnyRows - 1) / kSkinnyRows);
+  gemm_skinny_nt<MR><<<grid, kThreads, 0, st>>>(A, lda, B, ldb, C, ldc, static_cast<int>(M), N,
+                                                 K, alpha, beta);
+  return launch_status();
+}
+
 // Launch plan for one call.
 struct Plan {
   bool big;         // 256x128 tiles (else 128x128)
@@ -637,6 +733,13 @@ extern "C" int ember_gemm_f32_ws(int transa, int transb, int64_t M, int64_t N, i
                    (batch == 1 || (sA % 4 == 0 && sB % 4 == 0));
   hipStream_t st = as_stream(s);
   const bool a_kc = !transa, b_kc = transb != 0;
+  if (batch == 1 && M <= kSkinnyMaxM && a_kc && b_kc && vec && K > 0 && K % 4 == 0 &&
+      N <= int64_t{kSkinnyRows} * 0x7fffffff) {
+    if (M == 1) return launch_skinny<1>(A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, st);
+    if (M == 2) return launch_skinny<2>(A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, st);
+    if (M <= 4) return launch_skinny<4>(A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, st);
+    return launch_skinny<8>(A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, st);
+  }
   Plan p = make_plan(M, N, K, batch);
   if (p.splits > 1 &&
       (!workspace || workspace_bytes < static_cast<size_t>(p.splits * M * N) * sizeof(float)))

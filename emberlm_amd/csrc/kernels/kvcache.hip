@@ -1,0 +1,372 @@
+// KV cache and cached (decode) attention for the inference forward.
+//
+// Reference: write_kv_kernel / read_kv_expanded_kernel (src/ops/kv_cache.cu:13-48)
+// and the chain Attention::forward runs over the cache
+// (include/ctd/nn/attention.h:43-97): read_kv_expanded -> bmm -> mul_scalar ->
+// apply_causal_mask(position_start) -> softmax -> bmm.
+//
+// The cache keeps the reference's layout [B, Hk, S, D]: one KV head's keys are
+// contiguous, which is what a decode step streams.  ember_attn_decode reads it
+// in place (no GQA expansion, no [B*H, T, L] scores): a workgroup owns one
+// (batch, KV head, key split) and every query row of that KV head's group, so
+// each key and value row is read from HBM once per step whatever the group
+// size.  Inside the workgroup a row of D floats is spread over D/4 lanes
+// (one float4 each), so a wave covers 64*4/D keys per load; each lane group
+// runs its own online softmax (exp2 domain, queries pre-scaled by
+// scale*log2(e)), the groups and the 4 waves are merged through LDS in a fixed
+// order, and the key splits are merged by a second kernel in split order, so
+// results are reproducible bit for bit.
+#include <cmath>
+
+#include "common.h"
+
+using namespace ember;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kRowTile = 4;        // query rows per pass over the split's keys (a GQA group)
+constexpr int kUnroll = 4;         // key loads in flight per lane before use
+constexpr int kMinKeysPerSplit = 64;
+constexpr int kTargetBlocks = 2048;  // 8 workgroups per CU
+
+// ---------------------------------------------------------------- KV writes
+// src [B,T,Hk,D] -> cache [B,Hk,S,D] rows [pos, pos+T).  One thread per VEC
+// floats of src, in src order.
+template <int VEC>
+__global__ __launch_bounds__(kThreads) void kv_write_kernel(const float* __restrict__ src,
+                                                            float* __restrict__ cache, int64_t n,
+                                                            int64_t T, int64_t Hk, int64_t D,
+                                                            int64_t S, int64_t pos) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+       i += stride) {
+    const int64_t e = i * VEC;
+    const int64_t d = e % D;
+    const int64_t h = (e / D) % Hk;
+    const int64_t t = (e / (D * Hk)) % T;
+    const int64_t b = e / (D * Hk * T);
+    const int64_t dst = ((b * Hk + h) * S + pos + t) * D + d;
+    if (VEC == 4)
+      *reinterpret_cast<f32x4*>(cache + dst) = *reinterpret_cast<const f32x4*>(src + e);
+    else
+      cache[dst] = src[e];
+  }
+}
+
+// cache [B,Hk,S,D] rows [0,L) -> out [B, Hk*group, L, D], head h reading KV head h/group.
+template <int VEC>
+__global__ __launch_bounds__(kThreads) void kv_read_expanded_kernel(
+    const float* __restrict__ cache, float* __restrict__ out, int64_t n, int64_t Hk,
+    int64_t group, int64_t L, int64_t D, int64_t S) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  const int64_t H = Hk * group;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+       i += stride) {
+    const int64_t e = i * VEC;
+    const int64_t d = e % D;
+    const int64_t t = (e / D) % L;
+    const int64_t h = (e / (D * L)) % H;
+    const int64_t b = e / (D * L * H);
+    const int64_t src = ((b * Hk + h / group) * S + t) * D + d;
+    if (VEC == 4)
+      *reinterpret_cast<f32x4*>(out + e) = *reinterpret_cast<const f32x4*>(cache + src);
+    else
+      out[e] = cache[src];
+  }
+}
+
+// ------------------------------------------------------- decode attention
+struct DecodeArgs {
+  const float* q;    // [B, T, H, D]
+  const float* k;    // key row (b, hk, j) at k + b*kv_sb + hk*kv_sh + j*kv_st
+  const float* v;
+  float* o;          // [B, T, H, D] (written here when nsplit == 1)
+  float* part_o;     // [B*T*H, nsplit, D]   unnormalised split outputs
+  float* part_ml;    // [B*T*H, nsplit, 2]   split (max, sum) in log2 units
+  int64_t T, H, Hk, L, pos;
+  int64_t kv_sb, kv_sh, kv_st;
+  int64_t kps;       // keys per split
+  int nsplit;
+  float qscale;      // scale * log2(e)
+};
+
+// Sum over the LPK lanes of one key group (aligned blocks of LPK lanes).
+template <int LPK>
+__device__ __forceinline__ float group_sum(float x) {
+#pragma unroll
+  for (int o = LPK / 2; o > 0; o >>= 1) x += __shfl_xor(x, o, kWave);
+  return x;
+}
+
+__device__ __forceinline__ float dot4(f32x4 a, f32x4 b) {
+  return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
+  constexpr int LPK = D / 4;          // lanes per key row
+  constexpr int KPW = kWave / LPK;    // keys per wave load
+  constexpr int NG = kWaves * KPW;    // independent softmax groups per workgroup
+  __shared__ float s_ml[NG][kRowTile][2];
+  __shared__ f32x4 s_o[NG][kRowTile][LPK];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = threadIdx.x / kWave;
+  const int sub = lane / LPK;
+  const int d4 = lane % LPK;
+  const int g_id = w * KPW + sub;
+
+  const int64_t G = a.H / a.Hk;
+  const int64_t split = blockIdx.x % a.nsplit;
+  const int64_t bh = blockIdx.x / a.nsplit;
+  const int64_t hk = bh % a.Hk;
+  const int64_t b = bh / a.Hk;
+  const int64_t ks = split * a.kps;
+  const int64_t ke = ks + a.kps < a.L ? ks + a.kps : a.L;
+  const float* kbase = a.k + b * a.kv_sb + hk * a.kv_sh + 4 * d4;
+  const float* vbase = a.v + b * a.kv_sb + hk * a.kv_sh + 4 * d4;
+  const int64_t R = G * a.T;  // query rows of this KV head: r -> (t = r / G, h = hk*G + r % G)
+
+  for (int64_t r0 = 0; r0 < R; r0 += kRowTile) {
+    const int nr = static_cast<int>(R - r0 < kRowTile ? R - r0 : kRowTile);
+    f32x4 q[kRowTile], acc[kRowTile];
+    float m[kRowTile], l[kRowTile];
+    int lim[kRowTile];  // keys j < lim[r] are visible to row r
+    int jend = static_cast<int>(ks);
+#pragma unroll
+    for (int r = 0; r < kRowTile; ++r) {
+      acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+      m[r] = -INFINITY;
+      l[r] = 0.f;
+      q[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+      lim[r] = static_cast<int>(ks);
+      if (r < nr) {
+        const int64_t row = r0 + r;
+        const int64_t t = row / G;
+        const int64_t h = hk * G + row % G;
+        q[r] = *reinterpret_cast<const f32x4*>(a.q + ((b * a.T + t) * a.H + h) * D + 4 * d4) *
+               a.qscale;
+        const int64_t c = a.pos + t + 1;  // causal: key j <= pos + t
+        lim[r] = static_cast<int>(c < ke ? c : ke);
+        jend = lim[r] > jend ? lim[r] : jend;
+      }
+    }
+    // Keys of this lane group: ks + (it*kWaves + w)*KPW + sub.
+    for (int j0 = static_cast<int>(ks) + w * KPW + sub; j0 < jend; j0 += kUnroll * kWaves * KPW) {
+      f32x4 kf[kUnroll], vf[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int j = j0 + u * kWaves * KPW;
+        if (j < jend) {
+          kf[u] = *reinterpret_cast<const f32x4*>(kbase + static_cast<int64_t>(j) * a.kv_st);
+          vf[u] = *reinterpret_cast<const f32x4*>(vbase + static_cast<int64_t>(j) * a.kv_st);
+        } else {
+          kf[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+          vf[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int j = j0 + u * kWaves * KPW;
+#pragma unroll
+        for (int r = 0; r < kRowTile; ++r) {
+          if (r < nr) {
+            const float s = group_sum<LPK>(dot4(q[r], kf[u]));
+            if (j < lim[r]) {
+              const float mn = fmaxf(m[r], s);
+              const float c = exp2f(m[r] - mn);
+              const float p = exp2f(s - mn);
+              l[r] = l[r] * c + p;
+              acc[r] = acc[r] * c + vf[u] * p;
+              m[r] = mn;
+            }
+          }
+        }
+      }
+    }
+    // Merge the NG groups: publish, then each thread finishes (row, float4) items.
+    __syncthreads();  // previous row tile's readers are done with LDS
+#pragma unroll
+    for (int r = 0; r < kRowTile; ++r) {
+      if (r < nr) {
+        s_o[g_id][r][d4] = acc[r];
+        if (d4 == 0) {
+          s_ml[g_id][r][0] = m[r];
+          s_ml[g_id][r][1] = l[r];
+        }
+      }
+    }
+    __syncthreads();
+    for (int it = threadIdx.x; it < nr * LPK; it += kThreads) {
+      const int r = it / LPK;
+      const int c4 = it % LPK;
+      float M = -INFINITY;
+      for (int g = 0; g < NG; ++g) M = fmaxf(M, s_ml[g][r][0]);
+      float lsum = 0.f;
+      f32x4 osum = {0.f, 0.f, 0.f, 0.f};
+      if (M != -INFINITY) {
+        for (int g = 0; g < NG; ++g) {
+          const float e = exp2f(s_ml[g][r][0] - M);
+          lsum += s_ml[g][r][1] * e;
+          osum += s_o[g][r][c4] * e;
+        }
+      }
+      const int64_t row = r0 + r;
+      const int64_t t = row / G;
+      const int64_t h = hk * G + row % G;
+      const int64_t orow = (b * a.T + t) * a.H + h;
+      if (a.nsplit == 1) {
+        // Split 0 holds key 0, which every row sees: lsum >= 1.
+        *reinterpret_cast<f32x4*>(a.o + orow * D + 4 * c4) = osum * (1.0f / lsum);
+      } else {
+        *reinterpret_cast<f32x4*>(a.part_o + (orow * a.nsplit + split) * D + 4 * c4) = osum;
+        if (c4 == 0) {
+          a.part_ml[(orow * a.nsplit + split) * 2 + 0] = M;
+          a.part_ml[(orow * a.nsplit + split) * 2 + 1] = lsum;
+        }
+      }
+    }
+  }
+}
+
+// One wave per output row: merge the splits in split order.
+template <int D>
+__global__ __launch_bounds__(kThreads) void attn_decode_combine(const float* __restrict__ part_o,
+                                                                const float* __restrict__ part_ml,
+                                                                float* __restrict__ o,
+                                                                int64_t rows, int nsplit) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  if (row >= rows) return;
+  const float* ml = part_ml + row * nsplit * 2;
+  float M = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ml[2 * s]);
+  constexpr int PER = D / kWave;
+  float acc[PER] = {};
+  float lsum = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    const float ms = ml[2 * s];
+    if (ms == -INFINITY) continue;  // no key of this split is visible to the row
+    const float e = exp2f(ms - M);
+    lsum += ml[2 * s + 1] * e;
+#pragma unroll
+    for (int p = 0; p < PER; ++p) acc[p] += part_o[(row * nsplit + s) * D + p * kWave + lane] * e;
+  }
+  const float inv = 1.0f / lsum;
+#pragma unroll
+  for (int p = 0; p < PER; ++p) o[row * D + p * kWave + lane] = acc[p] * inv;
+}
+
+struct DecodePlan {
+  int nsplit;
+  int64_t kps;
+};
+
+DecodePlan decode_plan(int64_t B, int64_t Hk, int64_t L) {
+  const int64_t heads = B * Hk;
+  int64_t want = (kTargetBlocks + heads - 1) / heads;
+  const int64_t most = (L + kMinKeysPerSplit - 1) / kMinKeysPerSplit;
+  if (want > most) want = most;
+  if (want < 1) want = 1;
+  const int64_t kps = (L + want - 1) / want;
+  return DecodePlan{static_cast<int>((L + kps - 1) / kps), kps};
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace
+
+extern "C" int ember_kv_write(const float* src, float* cache, int64_t B, int64_t T, int64_t Hk,
+                              int64_t D, int64_t S, int64_t pos, ember_stream_t s) {
+  if (B < 0 || T < 0 || Hk < 0 || D < 0 || pos < 0 || pos + T > S) return EMBER_EINVAL;
+  const int64_t n = B * T * Hk * D;
+  if (n == 0) return EMBER_OK;
+  if (!src || !cache) return EMBER_EINVAL;
+  hipStream_t st = as_stream(s);
+  if (D % 4 == 0 && aligned16(src) && aligned16(cache))
+    kv_write_kernel<4><<<grid_1d(n / 4, kThreads), kThreads, 0, st>>>(src, cache, n / 4, T, Hk,
+                                                                       D, S, pos);
+  else
+    kv_write_kernel<1><<<grid_1d(n, kThreads), kThreads, 0, st>>>(src, cache, n, T, Hk, D, S,
+                                                                   pos);
+  return launch_status();
+}
+
+extern "C" int ember_kv_read_expanded(const float* cache, float* out, int64_t B, int64_t Hk,
+                                      int64_t group, int64_t L, int64_t D, int64_t S,
+                                      ember_stream_t s) {
+  if (B < 0 || Hk < 0 || group <= 0 || L < 0 || L > S || D < 0) return EMBER_EINVAL;
+  const int64_t n = B * Hk * group * L * D;
+  if (n == 0) return EMBER_OK;
+  if (!cache || !out) return EMBER_EINVAL;
+  hipStream_t st = as_stream(s);
+  if (D % 4 == 0 && aligned16(cache) && aligned16(out))
+    kv_read_expanded_kernel<4><<<grid_1d(n / 4, kThreads), kThreads, 0, st>>>(
+        cache, out, n / 4, Hk, group, L, D, S);
+  else
+    kv_read_expanded_kernel<1><<<grid_1d(n, kThreads), kThreads, 0, st>>>(cache, out, n, Hk,
+                                                                           group, L, D, S);
+  return launch_status();
+}
+
+extern "C" size_t ember_attn_decode_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t Hk,
+                                                    int64_t D, int64_t L) {
+  if (B <= 0 || T <= 0 || H <= 0 || Hk <= 0 || D <= 0 || L <= 0) return 0;
+  const DecodePlan p = decode_plan(B, Hk, L);
+  if (p.nsplit == 1) return 0;
+  return static_cast<size_t>(B * T * H) * p.nsplit * (D + 2) * sizeof(float);
+}
+
+extern "C" int ember_attn_decode(const float* q, const float* k, const float* v, float* o,
+                                 int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D,
+                                 int64_t L, int64_t pos, int64_t kv_sb, int64_t kv_sh,
+                                 int64_t kv_st, float scale, void* workspace,
+                                 size_t workspace_bytes, ember_stream_t s) {
+  if (B < 0 || T < 0 || H <= 0 || Hk <= 0 || H % Hk != 0 || pos < 0) return EMBER_EINVAL;
+  if (D != 64 && D != 128) return EMBER_EINVAL;
+  if (B == 0 || T == 0) return EMBER_OK;
+  if (L < 1 || !q || !k || !v || !o) return EMBER_EINVAL;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || kv_sb % 4 ||
+      kv_sh % 4 || kv_st % 4)
+    return EMBER_EINVAL;
+  const DecodePlan p = decode_plan(B, Hk, L);
+  const int64_t blocks = B * Hk * p.nsplit;
+  if (blocks > 0x7fffffff) return EMBER_EINVAL;
+  const size_t need = ember_attn_decode_workspace_bytes(B, T, H, Hk, D, L);
+  if (need && (!workspace || workspace_bytes < need)) return EMBER_EINVAL;
+  DecodeArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  const int64_t rows = B * T * H;
+  a.part_o = static_cast<float*>(workspace);
+  a.part_ml = need ? a.part_o + rows * p.nsplit * D : nullptr;
+  a.T = T;
+  a.H = H;
+  a.Hk = Hk;
+  a.L = L;
+  a.pos = pos;
+  a.kv_sb = kv_sb;
+  a.kv_sh = kv_sh;
+  a.kv_st = kv_st;
+  a.kps = p.kps;
+  a.nsplit = p.nsplit;
+  a.qscale = scale * 1.4426950408889634f;
+  hipStream_t st = as_stream(s);
+  const unsigned grid = static_cast<unsigned>(blocks);
+  if (D == 128)
+    attn_decode_kernel<128><<<grid, kThreads, 0, st>>>(a);
+  else
+    attn_decode_kernel<64><<<grid, kThreads, 0, st>>>(a);
+  int rc = launch_status();
+  if (rc || p.nsplit == 1) return rc;
+  const unsigned cgrid = static_cast<unsigned>(cdiv(rows, kWaves));
+  if (D == 128)
+    attn_decode_combine<128><<<cgrid, kThreads, 0, st>>>(a.part_o, a.part_ml, o, rows, p.nsplit);
+  else
+    attn_decode_combine<64><<<cgrid, kThreads, 0, st>>>(a.part_o, a.part_ml, o, rows, p.nsplit);
+  return launch_status();
+}

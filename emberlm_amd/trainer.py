@@ -87,6 +87,11 @@ _SIGS = {
                                    lptr]),
     "ctd_train_event_json": (i32, [i32, f32, f32, f32, C.c_double, C.c_double, i32, C.c_char_p,
                                    C.c_size_t]),
+    "ctd_kvcache_create": (i32, [vp, i64, i64, C.POINTER(vp)]),
+    "ctd_kvcache_destroy": (i32, [vp]),
+    "ctd_kvcache_len": (i32, [vp, lptr]),
+    "ctd_trainer_forward_cached": (i32, [vp, vp, lptr, i64, i64, i32, i32, fptr, i64]),
+    "ctd_sample": (i32, [fptr, i64, i64, f32, i32, f32, u64, i32, i32, lptr]),
 }
 
 
@@ -291,6 +296,57 @@ class Trainer:
     def num_params(self):
         return len(self.names)
 
+    def kv_cache(self, batch, max_seq):
+        return KVCache(self, batch, max_seq)
+
+    def forward(self, ids, cache=None, position_start=0, last_only=False):
+        """Model::forward (or forward_last_logits) of host int64 ids [B,T] -> logits."""
+        ids = np.ascontiguousarray(ids, dtype=np.int64)
+        B, T = ids.shape
+        out = np.empty((B, 1 if last_only else T, self.cfg.vocab_size), np.float32)
+        _ck(lib().ctd_trainer_forward_cached(self.h, cache.h if cache is not None else None,
+                                             ids.ctypes.data_as(lptr), B, T, position_start,
+                                             int(last_only), out.ctypes.data_as(fptr), out.size),
+            "forward")
+        return out
+
+
+class KVCache:
+    """nn::KVCache for a trainer's model (zero-filled, batch x max_seq rows)."""
+
+    def __init__(self, tr: Trainer, batch, max_seq):
+        h = vp()
+        _ck(lib().ctd_kvcache_create(tr.h, batch, max_seq, C.byref(h)), "kv_cache")
+        self.h = h
+
+    @property
+    def current_len(self):
+        n = C.c_int64()
+        _ck(lib().ctd_kvcache_len(self.h, C.byref(n)), "kv_cache_len")
+        return n.value
+
+    def close(self):
+        if self.h:
+            _ck(lib().ctd_kvcache_destroy(self.h), "kv_cache_destroy")
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def sample(logits, temperature=1.0, top_k=0, top_p=0.0, seed=0, draws=1, on_device=False):
+    """ctd::sample over host logits [B, V]: `draws` consecutive draws from one
+    mt19937_64(seed) -> int64 [draws, B]."""
+    x, p = _f32(logits)
+    B, V = x.shape
+    out = np.zeros((draws, B), np.int64)
+    _ck(lib().ctd_sample(p, B, V, temperature, top_k, top_p, seed, draws, int(on_device),
+                         out.ctypes.data_as(lptr)), "sample")
+    return out
+
 
 def train_run(config_path):
     """Runs the ctd_train driver in this process (include/ctd/train.h)."""
@@ -335,4 +391,4 @@ def param_count(cfg: ModelConfig) -> int:
 
 __all__ = ["ModelConfig", "Trainer", "preset", "make_config", "memory", "reset_peak_memory",
            "gemm_profile", "param_count", "StepTimes", "train_run", "lr_at_step", "host_batch",
-           "event_json", "math"]
+           "event_json", "KVCache", "sample", "math"]

@@ -5,6 +5,7 @@
 
 #include "ctd/autograd.h"
 #include "ctd/nn/embedding.h"
+#include "ctd/nn/kv_cache.h"
 #include "ctd/nn/linear.h"
 #include "ctd/nn/rms_norm.h"
 #include "ctd/nn/transformer_block.h"
@@ -50,8 +51,16 @@ struct Model {
   RMSNorm norm;
   bool gradient_checkpointing = false;
 
-  // Inference logits (no KV cache): the training forward under no-grad.
-  Tensor forward(const Tensor& input_ids) const;
+  // Inference: input_ids int64 [B, T] -> logits fp32 [B, T, vocab], positions
+  // from position_start.  With a cache, each layer's K/V are written at rows
+  // [position_start, position_start+T) and cache->current_len becomes
+  // position_start + T.
+  Tensor forward(const Tensor& input_ids, KVCache* cache = nullptr,
+                 int position_start = 0) const;
+  // The same forward, but the LM head runs on the last position of each row
+  // only: logits [B, 1, vocab] (what a sampler consumes).
+  Tensor forward_last_logits(const Tensor& input_ids, KVCache* cache = nullptr,
+                             int position_start = 0) const;
   // input_ids int64 [B, T] -> logits fp32 [B, T, vocab]
   Tensor forward_train_logits(const Tensor& input_ids) const;
   // Mean cross-entropy over all positions, shape [1].

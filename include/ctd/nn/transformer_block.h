@@ -15,6 +15,16 @@ struct TransformerBlock {
   Attention self_attn;
   MLP mlp;
 
+  Tensor forward(const Tensor& x, KVLayer* kv = nullptr, int position_start = 0) const {
+    autograd::NoGradGuard ng;
+    Tensor h1 = input_layernorm.forward(x);
+    Tensor a = self_attn.forward(h1, kv, position_start);
+    Tensor h = ops::add(x, a);
+    Tensor h2 = post_attention_layernorm.forward(h);
+    Tensor m = mlp.forward(h2);
+    return ops::add(h, m);
+  }
+
   Tensor forward_train(const Tensor& x) const {
     Tensor h1 = input_layernorm.forward(x);
     Tensor a = self_attn.forward_train(h1);

@@ -51,6 +51,10 @@ struct Config {
 // Parses the JSON config; init_weights and data_dir are required.
 Config load_config(const std::filesystem::path& cfg_path);
 
+// A model architecture from a JSON file holding the fields of the config's
+// "model" object (HF config names: vocab_size, hidden_size, ...).
+nn::LlamaConfig load_model_config(const std::filesystem::path& path);
+
 // One split of the pre-tokenised data (main.cpp:115-136): `<split>.bin` holds
 // int32 token ids, seq_len per document; `<split>_mask.bin` one int8 loss-mask
 // value per token.

@@ -152,6 +152,24 @@ int ctd_train_event_json(int32_t step, float loss, float lr, float grad_norm,
                          double tokens_per_sec, double wall_s, int32_t val, char* buf,
                          size_t cap);
 
+/* ---- inference (include/ctd/nn/kv_cache.h, Model::forward with a cache,
+ * include/ctd/sampling.h) */
+typedef void* ctd_kvcache_t;
+/* A zero-filled KV cache for the trainer's model: batch x max_seq rows. */
+int ctd_kvcache_create(ctd_trainer_t t, int64_t batch, int64_t max_seq, ctd_kvcache_t* out);
+int ctd_kvcache_destroy(ctd_kvcache_t c);
+int ctd_kvcache_len(ctd_kvcache_t c, int64_t* current_len);
+/* Model::forward(ids [B,T] host int64, cache (NULL: none), position_start)
+ * -> logits [B,T,V] into host memory; last_only: forward_last_logits, [B,1,V]. */
+int ctd_trainer_forward_cached(ctd_trainer_t t, ctd_kvcache_t cache, const int64_t* ids,
+                               int64_t B, int64_t T, int32_t position_start, int32_t last_only,
+                               float* logits, int64_t numel);
+/* ctd::sample over host logits [B,V] (copied to the device first when
+ * on_device), `draws` times in a row from one mt19937_64(seed):
+ * out[d*B + b] is draw d of row b. */
+int ctd_sample(const float* logits, int64_t B, int64_t V, float temperature, int32_t top_k,
+               float top_p, uint64_t seed, int32_t draws, int32_t on_device, int64_t* out);
+
 #ifdef __cplusplus
 }
 #endif

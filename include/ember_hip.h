@@ -99,6 +99,10 @@ int ember_gemm_f32(int transa, int transb, int64_t M, int64_t N, int64_t K, floa
  * reproducible run to run.  ember_gemm_f32_workspace_bytes gives the size this
  * call can use (0: no split for this shape); a smaller or NULL workspace runs
  * the unsplit kernel.  ember_gemm_f32 is this call with no workspace. */
+/* Both entry points run products with at most 8 rows (M <= 8, batch 1, A and
+ * B K-contiguous i.e. transa = 0 and transb = 1, 16-byte aligned, K % 4 == 0:
+ * Linear forward of a decode step) on a skinny kernel that streams B at HBM
+ * rate instead of on the MFMA tiles. */
 size_t ember_gemm_f32_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t batch);
 int ember_gemm_f32_ws(int transa, int transb, int64_t M, int64_t N, int64_t K, float alpha,
                       const float* A, int64_t lda, int64_t sA, const float* B, int64_t ldb,
@@ -192,6 +196,43 @@ int ember_attn_bwd(const float* q, const float* k, const float* v, const float* 
                    const float* lse, const float* dout, float* dq, float* dk, float* dv,
                    int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D, float scale,
                    void* workspace, size_t workspace_bytes, ember_stream_t s);
+
+/* ------------------------------------------------------ KV cache (inference)
+ * Cache layout [B, Hk, S, D] (S = max_seq_len), fp32, as nn::KVCache holds it.
+ * ember_kv_write copies src [B,T,Hk,D] into cache rows [pos, pos+T), folding
+ * the axis permute into the copy; EMBER_EINVAL unless 0 <= pos and pos+T <= S.
+ * Replaces write_kv_kernel / ops::write_kv_inplace (src/ops/kv_cache.cu:13-27,
+ * 50-82). */
+int ember_kv_write(const float* src, float* cache, int64_t B, int64_t T, int64_t Hk, int64_t D,
+                   int64_t S, int64_t pos, ember_stream_t s);
+/* out [B, Hk*group, L, D] = cache rows [0, L), KV head h/group for head h.
+ * Replaces read_kv_expanded_kernel / ops::read_kv_expanded (kv_cache.cu:29-48,
+ * 84-108); the inference attention below reads the cache without it. */
+int ember_kv_read_expanded(const float* cache, float* out, int64_t B, int64_t Hk, int64_t group,
+                           int64_t L, int64_t D, int64_t S, ember_stream_t s);
+/* Attention of q [B,T,H,D] over L keys/values, query t seeing keys
+ * j <= pos + t (and j < L); head h reads KV head h / (H/Hk).  Key/value row
+ * (b, hk, j) sits at k + b*kv_sb + hk*kv_sh + j*kv_st floats: [B,Hk,S,D] cache
+ * (kv_sb = Hk*S*D, kv_sh = S*D, kv_st = D) or [B,T,Hk,D] projections
+ * (T*Hk*D, D, Hk*D).  o [B,T,H,D].  D in {64,128}; pointers 16-byte aligned,
+ * strides multiples of 4.  Long key ranges are split over workgroups into
+ * `workspace` (>= ember_attn_decode_workspace_bytes, 0 = none needed) and
+ * merged in a fixed order: deterministic.  Replaces, for the inference
+ * forward, read_kv_expanded -> bmm -> mul_scalar -> apply_causal_mask(pos)
+ * -> softmax -> bmm (include/ctd/nn/attention.h:66-91). */
+size_t ember_attn_decode_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D,
+                                         int64_t L);
+int ember_attn_decode(const float* q, const float* k, const float* v, float* o, int64_t B,
+                      int64_t T, int64_t H, int64_t Hk, int64_t D, int64_t L, int64_t pos,
+                      int64_t kv_sb, int64_t kv_sh, int64_t kv_st, float scale, void* workspace,
+                      size_t workspace_bytes, ember_stream_t s);
+
+/* ------------------------------------------------------------- sampling
+ * out[r] = index of the largest value of row r of x [rows, n], the first such
+ * index on ties, NaNs skipped (0 when x[r,0] is NaN or the row is all NaN):
+ * exactly the host scan argmax_cpu (src/core/sampling.cpp:12-19) that greedy
+ * sampling (temperature <= 0) runs on the copied logits.  out is device int64. */
+int ember_argmax_rows(const float* x, int64_t rows, int64_t n, int64_t* out, ember_stream_t s);
 
 /* ---------------------------------------------------- masked cross-entropy
  * Per row r: lse[r] = log sum_v exp(logits[r,v]); loss[0] = sum_r mask[r]*(lse[r]

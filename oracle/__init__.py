@@ -257,6 +257,19 @@ def attention_bwd(q, k, v, do, scale=None):
     return dq, dk, dv
 
 
+def attention_offset(q, k, v, pos, scale=None):
+    """Inference attention with a position offset: q [B,T,H,D] over key rows k,v
+    [B,L,Hk,D]; query t sees keys j <= pos + t."""
+    q, k, v = _f64(q), _f64(k), _f64(v)
+    B, T, H, D = q.shape
+    L, Hk = k.shape[1], k.shape[2]
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    o = np.zeros_like(q)
+    lib().orc_attention_offset(_p(q), _p(k), _p(v), _p(o), I64(B), I64(T), I64(L), I64(H),
+                               I64(Hk), I64(D), I64(pos), C.c_double(scale))
+    return o
+
+
 # ---------------------------------------------------------- Block / Model
 BLOCK_KEYS = ["input_layernorm", "q_proj", "k_proj", "v_proj", "o_proj", "q_norm", "k_norm",
               "post_attention_layernorm", "gate_proj", "up_proj", "down_proj"]
@@ -324,3 +337,16 @@ def model_loss(cfg, params: list, ids, targets, mask, want_grads=True):
     B, T = ids.shape
     loss = lib().orc_model_loss(C.byref(cfg), pp, gp, _p(ids), _p(tg), _p(mk), I64(B), I64(T))
     return loss, grads
+
+
+def model_logits(cfg, params: list, ids):
+    """Logits [B,T,V] of Model::forward without a cache."""
+    arrs = [_f64(p) for p in params]
+    n = len(arrs)
+    assert n == lib().orc_model_num_params(C.byref(cfg))
+    pp = (_d * n)(*[_p(a) for a in arrs])
+    ids = np.ascontiguousarray(ids, dtype=np.int64)
+    B, T = ids.shape
+    out = np.zeros((B, T, cfg.vocab))
+    lib().orc_model_logits(C.byref(cfg), pp, _p(ids), _p(out), I64(B), I64(T))
+    return out

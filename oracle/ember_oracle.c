@@ -535,6 +535,44 @@ void orc_block_bwd(const orc_cfg* c, const double* const* w, const double* x,
   free(dqr); free(dkr); free(dv); free(dqn); free(dkn); free(dq); free(dk); free(dh1);
 }
 
+/* Scores over all L keys, the mask applied as a -FLT_MAX fill (which
+ * underflows to probability 0), then softmax and P V. */
+void orc_attention_offset(const double* q, const double* k, const double* v, double* o,
+                          int64_t B, int64_t T, int64_t L, int64_t H, int64_t Hk, int64_t D,
+                          int64_t pos, double scale) {
+  const int64_t group = H / Hk;
+  double* p = DALLOC(L);
+  for (int64_t b = 0; b < B; ++b)
+    for (int64_t h = 0; h < H; ++h) {
+      const int64_t kvh = h / group;
+      for (int64_t t = 0; t < T; ++t) {
+        const double* qt = q + ((b * T + t) * H + h) * D;
+        double m = -DBL_MAX;
+        for (int64_t j = 0; j < L; ++j) {
+          double s = 0.0;
+          const double* kj = k + ((b * L + j) * Hk + kvh) * D;
+          for (int64_t d = 0; d < D; ++d) s += qt[d] * kj[d];
+          s *= scale;
+          if (j > pos + t) s = -FLT_MAX;
+          p[j] = s;
+          m = s > m ? s : m;
+        }
+        double sum = 0.0;
+        for (int64_t j = 0; j < L; ++j) {
+          p[j] = exp(p[j] - m);
+          sum += p[j];
+        }
+        double* ot = o + ((b * T + t) * H + h) * D;
+        for (int64_t d = 0; d < D; ++d) {
+          double acc = 0.0;
+          for (int64_t j = 0; j < L; ++j) acc += p[j] * v[((b * L + j) * Hk + kvh) * D + d];
+          ot[d] = acc / sum;
+        }
+      }
+    }
+  free(p);
+}
+
 /* -------------------------------------------------------------- Model */
 static int64_t per_layer(const orc_cfg* c) { return c->qk_norm ? 11 : 9; }
 
@@ -618,4 +656,27 @@ double orc_model_loss(const orc_cfg* c, const double* const* params, double* con
   for (int64_t l = 0; l <= L; ++l) free(xs[l]);
   free(xs); free(hn); free(logits);
   return loss;
+}
+
+void orc_model_logits(const orc_cfg* c, const double* const* params, const int64_t* ids,
+                      double* logits, int64_t B, int64_t T) {
+  const int64_t N = B * T, d = c->hidden, L = c->layers;
+  const int64_t np = orc_model_num_params(c);
+  double* x = DALLOC(N * d);
+  double* y = DALLOC(N * d);
+  orc_embedding_fwd(ids, params[0], x, N, d);
+  for (int64_t l = 0; l < L; ++l) {
+    int64_t slot[ORC_W_COUNT];
+    const double* w[ORC_W_COUNT];
+    layer_slots(c, 1 + l * per_layer(c), slot);
+    for (int i = 0; i < ORC_W_COUNT; ++i) w[i] = slot[i] >= 0 ? params[slot[i]] : NULL;
+    orc_block_fwd(c, w, x, y, B, T);
+    double* tmp = x;
+    x = y;
+    y = tmp;
+  }
+  orc_rmsnorm_fwd(x, params[np - 1], y, N, d, c->eps);
+  orc_matmul(y, params[0], logits, N, c->vocab, d, 0, 1, 0.0);
+  free(x);
+  free(y);
 }

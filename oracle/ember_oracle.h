@@ -107,6 +107,14 @@ void orc_attention_bwd(const double* q, const double* k, const double* v,
                        const double* dout, double* dq, double* dk, double* dv, int64_t B,
                        int64_t T, int64_t H, int64_t Hk, int64_t D, double scale);
 
+/* The attention of Attention::forward with a KV cache (include/ctd/nn/attention.h:43-97):
+ * scores = (Q K^T) * scale over L keys, apply_causal_mask(q0 = pos) hides key
+ * j > pos + t (src/ops/mask.cu:15-37), softmax, P V.  q,o [B,T,H,D]; k,v
+ * [B,L,Hk,D] (key rows in projection layout); head h reads KV head h/(H/Hk). */
+void orc_attention_offset(const double* q, const double* k, const double* v, double* o,
+                          int64_t B, int64_t T, int64_t L, int64_t H, int64_t Hk, int64_t D,
+                          int64_t pos, double scale);
+
 /* Decoder block / model shapes (include/ctd/nn/model.h:19-37). */
 typedef struct {
   int64_t vocab;   /* V */
@@ -147,6 +155,11 @@ int64_t orc_model_num_params(const orc_cfg* cfg);
 double orc_model_loss(const orc_cfg* cfg, const double* const* params, double* const* grads,
                       const int64_t* ids, const int64_t* targets, const double* mask,
                       int64_t B, int64_t T);
+
+/* Logits [B,T,V] of Model::forward without a cache (include/ctd/nn/model.h:152-163):
+ * embedding, blocks, final RMSNorm, tied head. */
+void orc_model_logits(const orc_cfg* cfg, const double* const* params, const int64_t* ids,
+                      double* logits, int64_t B, int64_t T);
 
 #ifdef __cplusplus
 }

@@ -59,3 +59,26 @@ def test_argument_validation_without_gpu():
     assert lib.ember_rmsnorm_bwd_workspace_bytes(32768, 2048) > 0
     assert lib.ember_attn_bwd_workspace_bytes(8, 4096, 16) == 8 * 4096 * 16 * 4
     assert lib.ember_ce_masked_fwd_workspace_bytes(32768) == 32768 * 4
+
+
+def test_inference_entry_validation_without_gpu():
+    lib = capi.lib()
+    # cache rows [pos, pos+T) must fit in S
+    assert lib.ember_kv_write(None, None, 1, 3, 2, 64, 8, 6, None) == -1
+    assert lib.ember_kv_write(None, None, 1, 3, 2, 64, 8, -1, None) == -1
+    assert lib.ember_kv_write(None, None, 0, 3, 2, 64, 8, 5, None) == 0      # nothing to copy
+    assert lib.ember_kv_read_expanded(None, None, 1, 2, 0, 4, 64, 8, None) == -1
+    assert lib.ember_kv_read_expanded(None, None, 1, 2, 2, 9, 64, 8, None) == -1
+    # decode attention: D in {64,128}, H % Hk == 0, at least one key
+    args = (1, 1, 4, 2, 96, 10, 9, 0, 0, 0, 1.0, None, 0, None)
+    assert lib.ember_attn_decode(None, None, None, None, *args) == -1
+    args = (1, 1, 3, 2, 64, 10, 9, 0, 0, 0, 1.0, None, 0, None)
+    assert lib.ember_attn_decode(None, None, None, None, *args) == -1
+    args = (1, 1, 4, 2, 64, 0, 0, 0, 0, 0, 1.0, None, 0, None)
+    assert lib.ember_attn_decode(None, None, None, None, *args) == -1
+    # short key ranges need no workspace; long ones split into >= 64-key chunks
+    assert lib.ember_attn_decode_workspace_bytes(1, 1, 16, 8, 128, 10) == 0
+    ws = lib.ember_attn_decode_workspace_bytes(1, 1, 16, 8, 128, 4096)
+    assert ws == 1 * 1 * 16 * 64 * (128 + 2) * 4
+    assert lib.ember_argmax_rows(None, 0, 10, None, None) == 0
+    assert lib.ember_argmax_rows(None, 2, 0, None, None) == -1

@@ -462,3 +462,48 @@ def test_model_loss_finite_difference_and_tied_head():
         fd = fd_grad(f, ps[pi], idx=idx)
         np.testing.assert_allclose([grads[pi].reshape(-1)[i] for i in idx], [fd[i] for i in idx],
                                    rtol=1e-5, atol=1e-9, err_msg=f"param {pi}")
+
+
+# ------------------------------------------------ Inference (KV cache) oracle
+@pytest.mark.parametrize("H,Hk,T,L,pos", [(4, 4, 3, 12, 9), (6, 2, 5, 12, 7), (6, 3, 1, 9, 8),
+                                          (4, 2, 4, 4, 0), (2, 1, 3, 6, 40)])
+def test_attention_offset_vs_torch_sdpa_masked(H, Hk, T, L, pos):
+    """Query t sees keys j <= pos + t: torch SDPA with that explicit boolean mask."""
+    r = rng(31)
+    B, D = 2, 8
+    q = r.standard_normal((B, T, H, D))
+    k, v = (r.standard_normal((B, L, Hk, D)) for _ in range(2))
+    g = H // Hk
+    allow = torch.tensor([[j <= pos + t for j in range(L)] for t in range(T)])
+    ref = F.scaled_dot_product_attention(t64(q.transpose(0, 2, 1, 3)),
+                                         t64(k.transpose(0, 2, 1, 3)).repeat_interleave(g, 1),
+                                         t64(v.transpose(0, 2, 1, 3)).repeat_interleave(g, 1),
+                                         attn_mask=allow)
+    o = O.attention_offset(q, k, v, pos)
+    np.testing.assert_allclose(o, ref.numpy().transpose(0, 2, 1, 3), rtol=1e-10, atol=1e-12)
+    if pos == 0 and L == T:  # plain causal attention: the training oracle
+        np.testing.assert_allclose(o, O.attention_fwd(q, k, v)[0], rtol=1e-12, atol=1e-14)
+
+
+def test_model_logits_composition_and_loss():
+    """Logits = embedding -> blocks -> final RMSNorm -> h E^T (each piece pinned above),
+    and their masked CE is the model loss."""
+    cfg = tiny_cfg(True, llama3=True)
+    r = rng(32)
+    ps = model_params(cfg, r)
+    B, T = 2, 6
+    ids = r.integers(0, cfg.vocab, (B, T))
+    logits = O.model_logits(cfg, ps, ids)
+    h = O.embedding_fwd(ids.reshape(-1), ps[0]).reshape(B, T, -1)
+    keys = [k_ for k_ in O.BLOCK_KEYS if cfg.qk_norm or k_ not in ("q_norm", "k_norm")]
+    for l in range(cfg.layers):
+        w = dict(zip(keys, ps[1 + l * len(keys): 1 + (l + 1) * len(keys)]))
+        h = O.block_fwd(cfg, w, h)
+    hn = O.rmsnorm_fwd(h.reshape(B * T, -1), ps[-1], cfg.eps)
+    np.testing.assert_allclose(logits.reshape(B * T, -1), hn @ ps[0].T, rtol=1e-12, atol=1e-12)
+    tg = r.integers(0, cfg.vocab, (B, T))
+    mask = np.ones((B, T))
+    lse = np.log(np.exp(logits).sum(-1))
+    ce = float(np.mean(lse - np.take_along_axis(logits, tg[..., None], -1)[..., 0]))
+    assert math.isclose(ce, O.model_loss(cfg, ps, ids, tg, mask, want_grads=False)[0],
+                        rel_tol=1e-12)
