@@ -31,6 +31,7 @@ sys.path.insert(0, ROOT)
 METRIC = "train tokens/s + peak HBM GB, Qwen3-1.7B recompute+offload seq4096, 1 GPU"
 FP32_MFMA_PEAK_TFLOPS = 157.3
 PCIE_GEN5_X16_GBPS = 63.0
+HBM_PEAK_GBPS = 8000.0
 
 WORKLOADS = {
     # name: (preset, B, T, masked)
@@ -127,6 +128,30 @@ def profiled_traffic(workload, variant):
     return None, None
 
 
+def decode_point(tr, cfg, n_params, prompt_len, new_tokens):
+    """ctd_generate's loop (greedy, batch 1) on the benchmark's model: a prompt
+    of prompt_len seeded ids, then new_tokens tokens through the KV cache.
+    HBM bytes per decoded token: every weight once (the tied embedding as the
+    LM head) plus the K/V rows attended to."""
+    import numpy as np
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab_size, prompt_len)
+    tr.generate(prompt[:8], 4)                         # warm the allocator and kernels
+    toks, pf_ms, dc_ms = tr.generate(prompt, new_tokens)
+    steps = new_tokens - 1
+    ms_tok = dc_ms / steps
+    avg_len = prompt_len + new_tokens / 2
+    kv_bytes = 2.0 * cfg.num_layers * cfg.num_kv_heads * cfg.head_dim * 4 * avg_len
+    bytes_tok = 4.0 * n_params + kv_bytes
+    gbps = bytes_tok / (ms_tok / 1e3) / 1e9
+    log(f"[bench] decode P={prompt_len}: prefill {pf_ms:.1f} ms, {ms_tok:.3f} ms/token "
+        f"({1e3 / ms_tok:.1f} tok/s, {gbps:.0f} GB/s)")
+    return {"prompt_tokens": prompt_len, "new_tokens": new_tokens, "sampling": "greedy",
+            "prefill_ms": round(pf_ms, 2), "prefill_tokens_per_s": round(prompt_len / pf_ms * 1e3, 1),
+            "ms_per_token": round(ms_tok, 4), "tokens_per_s": round(1e3 / ms_tok, 2),
+            "hbm_bytes_per_token": bytes_tok, "achieved_gbps": round(gbps, 1),
+            "frac_of_hbm_peak": round(gbps / HBM_PEAK_GBPS, 4)}
+
+
 def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -153,6 +178,11 @@ def main():
                     help="launch one ember_scale over 1 GiB (reads 1 GiB, writes 1 GiB) first: "
                          "the known-size copy that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE")
     ap.add_argument("--max-norm", type=float, default=1.0)
+    ap.add_argument("--decode-tokens", type=int, default=64,
+                    help="tokens generated per inference measurement (0: skip)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the inference measurement (greedy ctd_generate loop on the "
+                         "workload's model): prints one JSON line with the decode points")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -176,6 +206,16 @@ def main():
 
     preset, B, T, masked = WORKLOADS[args.workload]
     cfg = TR.preset(preset)
+    if args.decode_only:
+        n_params = TR.param_count(cfg)
+        tr = TR.Trainer(cfg, seed=0, init_std=0.02, norm_value=1.0)
+        points = [decode_point(tr, cfg, n_params, P, max(args.decode_tokens, 2))
+                  for P in (128, T)]
+        tr.close()
+        print(json.dumps({"metric": "decode tokens/s (greedy, batch 1)", "model": preset,
+                          "params": n_params, "dtype": "f32", "data": "synthetic prompt ids, "
+                          "weights ~N(0,0.02)", "decode": points}), flush=True)
+        return
     ckpt = not args.no_checkpointing
     offload = not args.no_offload
     n_params = TR.param_count(cfg)
@@ -316,6 +356,9 @@ def main():
             "recompute_overhead_fwd_bwd": round(fb_ck / fb - 1.0, 4),
         }
         tr.set_checkpointing(True)
+    if args.decode_tokens > 1:
+        result["decode"] = [decode_point(tr, cfg, n_params, P, args.decode_tokens)
+                            for P in (128, T)]
     tr.close()
 
     if not args.skip_cpu:

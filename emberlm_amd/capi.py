@@ -88,6 +88,13 @@ SIGNATURES = {
     "ember_attn_decode": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64,
                                 f32, vp, sz, vp]),
     "ember_argmax_rows": (i32, [vp, i64, i64, vp, vp]),
+    "ember_argmax_rows_workspace_bytes": (sz, [i64, i64]),
+    "ember_argmax_rows_ws": (i32, [vp, i64, i64, vp, vp, sz, vp]),
+    "ember_decode_gemv": (i32, [vp, i64, i64, vp, f32, i32, C.POINTER(vp), C.POINTER(i64),
+                                C.POINTER(vp), C.POINTER(vp), vp]),
+    "ember_decode_gateup": (i32, [vp, i64, i64, vp, f32, vp, vp, i64, vp, vp]),
+    "ember_decode_qkv_post": (i32, [vp, vp, vp, i64, i64, i64, i64, i64, vp, vp, f32,
+                                    C.POINTER(f32), i64, vp, vp, vp, i64, vp]),
 }
 
 _lib = None

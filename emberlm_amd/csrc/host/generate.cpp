@@ -16,8 +16,10 @@
 
 #include "ctd/nn/kv_cache.h"
 #include "ctd/nn/model.h"
+#include "ctd/runtime.h"
 #include "ctd/safetensors.h"
 #include "ctd/train.h"
+#include "ember_hip.h"
 #include "json.h"
 
 namespace ctd::generate {
@@ -119,12 +121,125 @@ void ThinkBudget::observe(int64_t tok) {
   if (in_think_ && queue_.empty() && count_ >= budget_) queue_ = close_;
 }
 
+namespace {
+
+// Greedy token choice on the device into `out` (int64 [1]), no host sync.
+void device_argmax(const Tensor& last, Tensor& out) {
+  const int64_t V = last.shape().back();
+  const size_t wsb = ember_argmax_rows_workspace_bytes(1, V);
+  Tensor ws = wsb ? Tensor::empty({static_cast<int64_t>((wsb + 7) / 8)}, DType::kInt64, kHIP0)
+                  : Tensor{};
+  CTD_CHECK(ember_argmax_rows_ws(static_cast<const float*>(last.data_ptr()), 1, V,
+                                 static_cast<int64_t*>(out.data_ptr()),
+                                 wsb ? ws.data_ptr() : nullptr, wsb, runtime::compute_stream()));
+}
+
+class Event {
+ public:
+  Event() { CTD_CHECK(ember_event_create(&e_)); }
+  ~Event() { ember_event_destroy(e_); }
+  Event(const Event&) = delete;
+  Event& operator=(const Event&) = delete;
+  void record() { CTD_CHECK(ember_event_record(e_, runtime::compute_stream())); }
+  void wait() { CTD_CHECK(ember_event_synchronize(e_)); }
+
+ private:
+  ember_event_t e_ = nullptr;
+};
+
+}  // namespace
+
+LoopResult generate_loop(const nn::Model& model, const Request& req,
+                         const std::function<void(int64_t)>& emit) {
+  using clk = std::chrono::steady_clock;
+  const nn::LlamaConfig& cfg = model.config;
+  const int prompt_len = static_cast<int>(req.input_ids.size());
+  if (prompt_len < 1 || prompt_len >= req.max_seq_len)
+    throw std::runtime_error("generate: need 1 <= prompt length < max_seq_len");
+  const std::unordered_set<int64_t> eos(req.eos_ids.begin(), req.eos_ids.end());
+  nn::KVCache cache = nn::KVCache::allocate(cfg.num_hidden_layers, cfg.num_key_value_heads,
+                                            cfg.head_dim, /*batch=*/1, req.max_seq_len, kHIP0);
+  ThinkBudget think(req);
+  LoopResult res;
+  res.reason = "max_tokens";
+  const auto t0 = clk::now();
+  Tensor prompt =
+      Tensor::from_host(req.input_ids.data(), {1, prompt_len}, DType::kInt64, kHIP0);
+  Tensor last = model.forward_last_logits(prompt, &cache, 0);
+
+  if (req.sampler.temperature <= 0.0f && !think.active()) {
+    // Token t lives in dev[t % 2] and reaches pinned host slot t % 2 through an
+    // async copy whose event the host waits on; step t+1 is already queued.
+    Tensor dev[2] = {Tensor::empty({1, 1}, DType::kInt64, kHIP0),
+                     Tensor::empty({1, 1}, DType::kInt64, kHIP0)};
+    Tensor pinned = Tensor::zeros_pinned({2}, DType::kInt64);
+    auto* host = static_cast<int64_t*>(pinned.data_ptr());
+    Event ready[2];
+    auto pick = [&](int slot) {
+      device_argmax(last, dev[slot]);
+      CTD_CHECK(ember_memcpy_async(host + slot, dev[slot].data_ptr(), sizeof(int64_t), 1,
+                                   runtime::compute_stream()));
+      ready[slot].record();
+    };
+    pick(0);
+    ready[0].wait();
+    res.prefill_ms = std::chrono::duration<double, std::milli>(clk::now() - t0).count();
+    const auto t1 = clk::now();
+    for (int t = 0; t < req.max_new_tokens; ++t) {
+      const int slot = t % 2;
+      const int64_t len = cache.current_len;  // positions before token t's own step
+      const bool more = t + 1 < req.max_new_tokens && len + 1 <= req.max_seq_len;
+      if (more) {  // token t's step, from the device copy of token t
+        last = model.forward_last_logits(dev[slot], &cache, static_cast<int>(len));
+        pick(1 - slot);
+      }
+      ready[slot].wait();
+      const int64_t tok = host[slot];
+      emit(tok);
+      ++res.generated;
+      if (eos.count(tok)) {
+        res.reason = "eos";
+        break;
+      }
+      if (len + 1 > req.max_seq_len) {
+        res.reason = "max_seq_len";
+        break;
+      }
+    }
+    runtime::synchronize();  // a speculative step may still be running
+    res.decode_ms = std::chrono::duration<double, std::milli>(clk::now() - t1).count();
+    return res;
+  }
+
+  std::mt19937_64 rng(req.seed);
+  runtime::synchronize();
+  res.prefill_ms = std::chrono::duration<double, std::milli>(clk::now() - t0).count();
+  const auto t1 = clk::now();
+  while (res.generated < req.max_new_tokens) {
+    int64_t tok;
+    if (!think.next_forced(&tok)) tok = sample(last, req.sampler, rng)[0];
+    emit(tok);
+    ++res.generated;
+    think.observe(tok);
+    if (eos.count(tok)) {
+      res.reason = "eos";
+      break;
+    }
+    if (cache.current_len + 1 > req.max_seq_len) {
+      res.reason = "max_seq_len";
+      break;
+    }
+    Tensor next = Tensor::from_host(&tok, {1, 1}, DType::kInt64, kHIP0);
+    last = model.forward_last_logits(next, &cache, static_cast<int>(cache.current_len));
+  }
+  res.decode_ms = std::chrono::duration<double, std::milli>(clk::now() - t1).count();
+  return res;
+}
+
 int run(const std::string& model_path, const std::string& request, std::ostream& out,
         std::ostream& log, const std::string& model_config) {
   try {
     const Request req = parse_request(request);
-    const std::unordered_set<int64_t> eos(req.eos_ids.begin(), req.eos_ids.end());
-
     const auto t0 = std::chrono::steady_clock::now();
     log << "[ctd_generate] loading " << model_path << "\n";
     const TensorDict weights = load_safetensors(model_path, kHIP0);
@@ -133,7 +248,6 @@ int run(const std::string& model_path, const std::string& request, std::ostream&
     log << "[ctd_generate] arch: hidden=" << cfg.hidden_size
         << " layers=" << cfg.num_hidden_layers << "\n";
     const nn::Model model = nn::build_model(weights, cfg);
-    const auto t1 = std::chrono::steady_clock::now();
     log << "[ctd_generate] model ready in " << seconds_since(t0) << " s\n";
 
     const int prompt_len = static_cast<int>(req.input_ids.size());
@@ -147,42 +261,18 @@ int run(const std::string& model_path, const std::string& request, std::ostream&
           << std::flush;
       return 0;
     }
-    nn::KVCache cache = nn::KVCache::allocate(cfg.num_hidden_layers, cfg.num_key_value_heads,
-                                              cfg.head_dim, /*batch=*/1, req.max_seq_len, kHIP0);
-    Tensor prompt = Tensor::from_host(req.input_ids.data(), {1, prompt_len}, DType::kInt64, kHIP0);
-    Tensor last = model.forward_last_logits(prompt, &cache, 0);
-    log << "[ctd_generate] prefill (" << prompt_len << " tok) in " << seconds_since(t1)
-        << " s\n";
-
-    std::mt19937_64 rng(req.seed);
-    ThinkBudget think(req);
-    int generated = 0;
-    const char* reason = "max_tokens";
-    const auto t2 = std::chrono::steady_clock::now();
-    while (generated < req.max_new_tokens) {
-      int64_t tok;
-      if (!think.next_forced(&tok)) tok = sample(last, req.sampler, rng)[0];
+    const LoopResult r = generate_loop(model, req, [&](int64_t tok) {
       out << line(json::ObjectWriter().field("token", tok)) << std::flush;
-      ++generated;
-      think.observe(tok);
-      if (eos.count(tok)) {
-        reason = "eos";
-        break;
-      }
-      if (cache.current_len + 1 > req.max_seq_len) {
-        reason = "max_seq_len";
-        break;
-      }
-      Tensor next = Tensor::from_host(&tok, {1, 1}, DType::kInt64, kHIP0);
-      last = model.forward_last_logits(next, &cache, static_cast<int>(cache.current_len));
-    }
-    const double dt = seconds_since(t2);
-    log << "[ctd_generate] generated " << generated << " tok in " << dt << " s  ("
-        << generated / std::max(dt, 1e-9) << " tok/s)\n";
+    });
+    log << "[ctd_generate] prefill (" << prompt_len << " tok) in " << r.prefill_ms / 1e3
+        << " s\n";
+    const double dt = r.decode_ms / 1e3;
+    log << "[ctd_generate] generated " << r.generated << " tok in " << dt << " s  ("
+        << r.generated / std::max(dt, 1e-9) << " tok/s)\n";
     out << line(json::ObjectWriter()
                     .field("done", true)
-                    .field("generated_tokens", generated)
-                    .field("reason", reason))
+                    .field("generated_tokens", r.generated)
+                    .field("reason", r.reason))
         << std::flush;
     return 0;
   } catch (const std::exception& e) {

@@ -5,6 +5,7 @@
 #include <stdexcept>
 #include <string>
 
+#include "ctd/ops/decode.h"
 #include "ctd/ops/loss.h"
 #include "ctd/runtime.h"
 #include "ember_hip.h"
@@ -98,8 +99,8 @@ LlamaConfig autodetect_config(const TensorDict& w) {
 
 namespace {
 
-// Final hidden states [B, T, H] of the inference forward (model.h:152-163 of
-// the reference, without the LM head).
+// Hidden states [B, T, H] after the last block of the inference forward
+// (model.h:152-163 of the reference, before the final norm and the LM head).
 Tensor hidden_states(const Model& m, const Tensor& input_ids, KVCache* cache,
                      int position_start) {
   if (input_ids.dim() != 2) throw std::runtime_error("Model::forward: input_ids must be [B, T]");
@@ -117,14 +118,14 @@ Tensor hidden_states(const Model& m, const Tensor& input_ids, KVCache* cache,
     h = m.layers[i].forward(h, kv, position_start);
   }
   if (cache) cache->current_len = position_start + input_ids.shape()[1];
-  return m.norm.forward(h);
+  return h;
 }
 
 }  // namespace
 
 Tensor Model::forward(const Tensor& input_ids, KVCache* cache, int position_start) const {
   autograd::NoGradGuard ng;
-  Tensor h = hidden_states(*this, input_ids, cache, position_start);
+  Tensor h = norm.forward(hidden_states(*this, input_ids, cache, position_start));
   Linear lm_head{embed_tokens.weight};  // tied head
   return lm_head.forward(h);
 }
@@ -144,8 +145,10 @@ Tensor Model::forward_last_logits(const Tensor& input_ids, KVCache* cache,
                                    static_cast<const float*>(h.data_ptr()) + (b * T + T - 1) * H,
                                    H * sizeof(float), 2, runtime::compute_stream()));
   }
+  if (B <= ops::kDecodeMaxRows)  // final RMSNorm folded into the LM-head GEMV
+    return ops::decode_linear(last, norm.weight, norm.eps, {embed_tokens.weight})[0];
   Linear lm_head{embed_tokens.weight};
-  return lm_head.forward(last);
+  return lm_head.forward(norm.forward(last));
 }
 
 Tensor Model::forward_train_logits(const Tensor& input_ids) const {

@@ -4,6 +4,7 @@
 #include <cmath>
 
 #include "ctd/ops/attention.h"
+#include "ctd/ops/decode.h"
 #include "ctd/ops/kv_cache.h"
 #include "ember_hip.h"
 #include "op_util.h"
@@ -86,6 +87,119 @@ Tensor offset_attention(const Tensor& q, const Tensor& k, const Tensor& v, int p
           "offset_attention: q/k shape mismatch");
   return decode_attention(q, k, v, Hk, T, position_start, T * Hk * D, D, Hk * D, scale,
                           "offset_attention");
+}
+
+namespace {
+
+int64_t rows_of(const Tensor& x, int64_t K, const char* op) {
+  require(x.dim() >= 1 && x.shape().back() == K, std::string(op) + ": in_features mismatch");
+  const int64_t M = x.numel() / K;
+  require(M <= kDecodeMaxRows, std::string(op) + ": more than 8 token rows");
+  return M;
+}
+
+std::vector<int64_t> with_last(const Tensor& x, int64_t n) {
+  std::vector<int64_t> sh = x.shape();
+  sh.back() = n;
+  return sh;
+}
+
+}  // namespace
+
+std::vector<Tensor> decode_linear(const Tensor& x, const Tensor& norm_w, float eps,
+                                  const std::vector<Tensor>& weights,
+                                  const std::vector<Tensor>& residuals) {
+  check_f32(x, "decode_linear", "x");
+  require(!weights.empty() && weights.size() <= 3, "decode_linear: 1 to 3 weights");
+  require(residuals.empty() || residuals.size() == weights.size(),
+          "decode_linear: one residual per weight");
+  const int64_t K = weights[0].shape().at(1);
+  const int64_t M = rows_of(x, K, "decode_linear");
+  if (norm_w.defined()) {
+    check_f32(norm_w, "decode_linear", "norm weight");
+    require(norm_w.numel() == K, "decode_linear: norm weight size != in_features");
+  }
+  std::vector<Tensor> out;
+  const float* W[3] = {};
+  int64_t N[3] = {};
+  float* y[3] = {};
+  const float* res[3] = {};
+  for (size_t i = 0; i < weights.size(); ++i) {
+    check_f32(weights[i], "decode_linear", "weight");
+    require(weights[i].dim() == 2 && weights[i].shape()[1] == K,
+            "decode_linear: weights must be [N, K] with one K");
+    N[i] = weights[i].shape()[0];
+    out.push_back(Tensor::empty(with_last(x, N[i]), DType::kFloat32, x.device()));
+    W[i] = cfp(weights[i]);
+    y[i] = fp(out.back());
+    if (!residuals.empty()) {
+      check_f32(residuals[i], "decode_linear", "residual");
+      require(residuals[i].shape() == out.back().shape(), "decode_linear: residual shape");
+      res[i] = cfp(residuals[i]);
+    }
+  }
+  CTD_CHECK(ember_decode_gemv(cfp(x), M, K, norm_w.defined() ? cfp(norm_w) : nullptr, eps,
+                              static_cast<int>(weights.size()), W, N, y,
+                              residuals.empty() ? nullptr : res, S()));
+  return out;
+}
+
+Tensor decode_gate_up(const Tensor& x, const Tensor& norm_w, float eps, const Tensor& w_gate,
+                      const Tensor& w_up) {
+  check_f32(x, "decode_gate_up", "x");
+  check_f32(w_gate, "decode_gate_up", "gate weight");
+  check_f32(w_up, "decode_gate_up", "up weight");
+  require(w_gate.dim() == 2 && w_gate.shape() == w_up.shape(),
+          "decode_gate_up: gate and up weights differ");
+  const int64_t I = w_gate.shape()[0], K = w_gate.shape()[1];
+  const int64_t M = rows_of(x, K, "decode_gate_up");
+  if (norm_w.defined()) {
+    check_f32(norm_w, "decode_gate_up", "norm weight");
+    require(norm_w.numel() == K, "decode_gate_up: norm weight size != in_features");
+  }
+  Tensor out = Tensor::empty(with_last(x, I), DType::kFloat32, x.device());
+  CTD_CHECK(ember_decode_gateup(cfp(x), M, K, norm_w.defined() ? cfp(norm_w) : nullptr, eps,
+                                cfp(w_gate), cfp(w_up), I, fp(out), S()));
+  return out;
+}
+
+Tensor decode_qkv_post(const Tensor& q, const Tensor& k, const Tensor& v, int num_heads,
+                       int num_kv_heads, int head_dim, const Tensor& q_norm_w,
+                       const Tensor& k_norm_w, float eps, float theta, const RopeScaling& scaling,
+                       int position_start, Tensor& k_cache, Tensor& v_cache) {
+  check_f32(q, "decode_qkv_post", "q");
+  check_f32(k, "decode_qkv_post", "k");
+  check_f32(v, "decode_qkv_post", "v");
+  check_f32(k_cache, "decode_qkv_post", "k cache");
+  check_f32(v_cache, "decode_qkv_post", "v cache");
+  require(q.dim() == 3 && k.dim() == 3 && k.shape() == v.shape(),
+          "decode_qkv_post: expected q [B,T,H*D], k/v [B,T,Hk*D]");
+  const int64_t B = q.shape()[0], T = q.shape()[1];
+  const int64_t H = num_heads, Hk = num_kv_heads, D = head_dim;
+  require(q.shape()[2] == H * D && k.shape()[0] == B && k.shape()[1] == T &&
+              k.shape()[2] == Hk * D,
+          "decode_qkv_post: q/k/v widths != heads * head_dim");
+  require(k_cache.dim() == 4 && k_cache.shape() == v_cache.shape() && k_cache.shape()[0] == B &&
+              k_cache.shape()[1] == Hk && k_cache.shape()[3] == D,
+          "decode_qkv_post: cache / src dim mismatch");
+  const int64_t max_seq = k_cache.shape()[2];
+  require(position_start >= 0 && position_start + T <= max_seq,
+          "write_kv: write range out of cache bounds");
+  for (const Tensor* w : {&q_norm_w, &k_norm_w})
+    if (w->defined()) {
+      check_f32(*w, "decode_qkv_post", "norm weight");
+      require(w->numel() == D, "decode_qkv_post: QK-Norm weight size != head_dim");
+    }
+  std::vector<float> freqs(static_cast<size_t>(D / 2));
+  CTD_CHECK(ember_rope_freqs_host(freqs.data(), static_cast<int>(D), theta, scaling.factor,
+                                  scaling.low_freq_factor, scaling.high_freq_factor,
+                                  scaling.original_max_pos));
+  Tensor qo = Tensor::empty({B, T, H, D}, DType::kFloat32, q.device());
+  CTD_CHECK(ember_decode_qkv_post(cfp(q), cfp(k), cfp(v), B, T, H, Hk, D,
+                                  q_norm_w.defined() ? cfp(q_norm_w) : nullptr,
+                                  k_norm_w.defined() ? cfp(k_norm_w) : nullptr, eps, freqs.data(),
+                                  position_start, fp(qo), fp(k_cache), fp(v_cache), max_seq, S()));
+  return qo;
 }
 
 }  // namespace ctd::ops

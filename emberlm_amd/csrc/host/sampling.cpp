@@ -108,8 +108,14 @@ std::vector<int64_t> sample(const Tensor& logits_last, const SamplerConfig& cfg,
   if (V <= 0) throw std::runtime_error("sample: empty vocabulary");
   if (cfg.temperature <= 0.0f && logits_last.device().is_hip()) {
     Tensor idx = Tensor::empty({B}, DType::kInt64, logits_last.device());
-    CTD_CHECK(ember_argmax_rows(static_cast<const float*>(logits_last.data_ptr()), B, V,
-                                static_cast<int64_t*>(idx.data_ptr()), runtime::compute_stream()));
+    const size_t wsb = ember_argmax_rows_workspace_bytes(B, V);
+    Tensor ws = wsb ? Tensor::empty({static_cast<int64_t>((wsb + 7) / 8)}, DType::kInt64,
+                                    logits_last.device())
+                    : Tensor{};
+    CTD_CHECK(ember_argmax_rows_ws(static_cast<const float*>(logits_last.data_ptr()), B, V,
+                                   static_cast<int64_t*>(idx.data_ptr()),
+                                   wsb ? ws.data_ptr() : nullptr, wsb,
+                                   runtime::compute_stream()));
     idx.copy_to_host(out.data());
     return out;
   }

@@ -6,6 +6,7 @@
 // parameter, decay group first, plus optimizer.step), loading straight into
 // the pinned host state when m/v are offloaded.
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstring>
 #include <memory>
@@ -15,6 +16,7 @@
 #include <vector>
 
 #include "ctd/allocator.h"
+#include "ctd/generate.h"
 #include "ctd/nn/model.h"
 #include "ctd/ops/repeat_kv.h"
 #include "ctd/optim.h"
@@ -658,6 +660,29 @@ int ctd_sample(const float* logits, int64_t B, int64_t V, float temperature, int
       const std::vector<int64_t> tok = sample(x, cfg, rng);
       std::copy(tok.begin(), tok.end(), out + static_cast<int64_t>(d) * B);
     }
+  });
+}
+
+int ctd_trainer_generate(ctd_trainer_t t, const int64_t* prompt, int64_t P, int32_t max_new,
+                         float temperature, int32_t top_k, float top_p, uint64_t seed,
+                         int64_t max_seq, int64_t* tokens, double* prefill_ms,
+                         double* decode_ms) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    if (P < 1 || max_new < 0 || P + max_new > max_seq)
+      throw std::runtime_error("generate: need 1 <= P and P + max_new <= max_seq");
+    generate::Request req;
+    req.input_ids.assign(prompt, prompt + P);
+    req.max_new_tokens = max_new;
+    req.max_seq_len = static_cast<int>(max_seq);
+    req.sampler = SamplerConfig{temperature, top_k, top_p};
+    req.seed = seed;
+    runtime::synchronize();
+    int n = 0;
+    const generate::LoopResult r =
+        generate::generate_loop(tr->model, req, [&](int64_t tok) { tokens[n++] = tok; });
+    if (prefill_ms) *prefill_ms = r.prefill_ms;
+    if (decode_ms) *decode_ms = r.decode_ms;
   });
 }
 

@@ -28,8 +28,12 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kRowTile = 4;        // query rows per pass over the split's keys (a GQA group)
 constexpr int kUnroll = 4;         // key loads in flight per lane before use
-constexpr int kMinKeysPerSplit = 64;
-constexpr int kTargetBlocks = 2048;  // 8 workgroups per CU
+// Split plan (measured on MI355X, B=1, 8 KV heads, D=128): about 512
+// workgroups in all, and at least 32 keys each.  Fewer, longer splits leave
+// HBM idle at the start; more, shorter ones spend their time in the per-split
+// setup and the merge.
+constexpr int kMinKeysPerSplit = 32;
+constexpr int kTargetBlocks = 512;
 
 // ---------------------------------------------------------------- KV writes
 // src [B,T,Hk,D] -> cache [B,Hk,S,D] rows [pos, pos+T).  One thread per VEC
@@ -167,21 +171,33 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
           vf[u] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
       }
+      // The kUnroll keys' scores are independent (their shuffles overlap);
+      // the running max and the rescale are then updated once per batch.
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int j = j0 + u * kWaves * KPW;
+      for (int r = 0; r < kRowTile; ++r) {
+        if (r < nr) {
+          float sc[kUnroll];
+          float mx = m[r];
 #pragma unroll
-        for (int r = 0; r < kRowTile; ++r) {
-          if (r < nr) {
-            const float s = group_sum<LPK>(dot4(q[r], kf[u]));
-            if (j < lim[r]) {
-              const float mn = fmaxf(m[r], s);
-              const float c = exp2f(m[r] - mn);
-              const float p = exp2f(s - mn);
-              l[r] = l[r] * c + p;
-              acc[r] = acc[r] * c + vf[u] * p;
-              m[r] = mn;
+          for (int u = 0; u < kUnroll; ++u) {
+            sc[u] = group_sum<LPK>(dot4(q[r], kf[u]));
+            if (j0 + u * kWaves * KPW < lim[r]) mx = fmaxf(mx, sc[u]);
+          }
+          if (mx != -INFINITY) {  // else no key of this row seen yet, none in the batch
+            const float c = exp2f(m[r] - mx);
+            float ps = 0.f;
+            f32x4 pv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+              if (j0 + u * kWaves * KPW < lim[r]) {
+                const float pr = exp2f(sc[u] - mx);
+                ps += pr;
+                pv += vf[u] * pr;
+              }
             }
+            l[r] = l[r] * c + ps;
+            acc[r] = acc[r] * c + pv;
+            m[r] = mx;
           }
         }
       }
@@ -231,29 +247,55 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
   }
 }
 
-// One wave per output row: merge the splits in split order.
+// One wave per output row: merge the splits in split order.  The split
+// weights exp2(m_s - M) are computed lane-parallel and kept in LDS, so the
+// loop over splits only streams part_o with independent loads.
+constexpr int kMaxSplits = 2048;
+
 template <int D>
 __global__ __launch_bounds__(kThreads) void attn_decode_combine(const float* __restrict__ part_o,
                                                                 const float* __restrict__ part_ml,
                                                                 float* __restrict__ o,
                                                                 int64_t rows, int nsplit) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + threadIdx.x / kWave;
+  __shared__ float s_e[kWaves][kMaxSplits];
+  const int w = threadIdx.x / kWave;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + w;
   const int lane = threadIdx.x & (kWave - 1);
-  if (row >= rows) return;
+  if (row >= rows) return;  // whole waves leave; no block barrier follows
   const float* ml = part_ml + row * nsplit * 2;
   float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ml[2 * s]);
+  for (int s = lane; s < nsplit; s += kWave) M = fmaxf(M, ml[2 * s]);
+  M = wave_max(M);
+  float lpart = 0.f;
+  for (int s = lane; s < nsplit; s += kWave) {
+    const float ms = ml[2 * s];
+    // A split with no visible key has m = -inf and l = 0: weight 0.
+    const float e = ms == -INFINITY ? 0.f : exp2f(ms - M);
+    s_e[w][s] = e;
+    lpart += ml[2 * s + 1] * e;
+  }
+  const float lsum = wave_sum(lpart);
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   constexpr int PER = D / kWave;
   float acc[PER] = {};
-  float lsum = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float ms = ml[2 * s];
-    if (ms == -INFINITY) continue;  // no key of this split is visible to the row
-    const float e = exp2f(ms - M);
-    lsum += ml[2 * s + 1] * e;
+  const float* po = part_o + row * nsplit * D + lane;
+  int s = 0;
+  for (; s + 4 <= nsplit; s += 4) {
+    float x[4][PER];
 #pragma unroll
-    for (int p = 0; p < PER; ++p) acc[p] += part_o[(row * nsplit + s) * D + p * kWave + lane] * e;
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int p = 0; p < PER; ++p) x[u][p] = po[(s + u) * D + p * kWave];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int p = 0; p < PER; ++p) acc[p] += x[u][p] * s_e[w][s + u];
   }
+  for (; s < nsplit; ++s)
+#pragma unroll
+    for (int p = 0; p < PER; ++p) acc[p] += po[s * D + p * kWave] * s_e[w][s];
   const float inv = 1.0f / lsum;
 #pragma unroll
   for (int p = 0; p < PER; ++p) o[row * D + p * kWave + lane] = acc[p] * inv;
@@ -270,6 +312,7 @@ DecodePlan decode_plan(int64_t B, int64_t Hk, int64_t L) {
   const int64_t most = (L + kMinKeysPerSplit - 1) / kMinKeysPerSplit;
   if (want > most) want = most;
   if (want < 1) want = 1;
+  if (want > kMaxSplits) want = kMaxSplits;
   const int64_t kps = (L + want - 1) / want;
   return DecodePlan{static_cast<int>((L + kps - 1) / kps), kps};
 }

@@ -92,6 +92,8 @@ _SIGS = {
     "ctd_kvcache_len": (i32, [vp, lptr]),
     "ctd_trainer_forward_cached": (i32, [vp, vp, lptr, i64, i64, i32, i32, fptr, i64]),
     "ctd_sample": (i32, [fptr, i64, i64, f32, i32, f32, u64, i32, i32, lptr]),
+    "ctd_trainer_generate": (i32, [vp, lptr, i64, i32, f32, i32, f32, u64, i64, lptr,
+                                   C.POINTER(C.c_double), C.POINTER(C.c_double)]),
 }
 
 
@@ -295,6 +297,19 @@ class Trainer:
 
     def num_params(self):
         return len(self.names)
+
+    def generate(self, prompt, max_new, temperature=0.0, top_k=0, top_p=0.0, seed=0,
+                 max_seq=None):
+        """ctd_generate's loop (batch 1): (tokens, prefill_ms, decode_ms)."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.int64)
+        toks = np.zeros(max_new, np.int64)
+        pf, dc = C.c_double(), C.c_double()
+        _ck(lib().ctd_trainer_generate(self.h, prompt.ctypes.data_as(lptr), prompt.size, max_new,
+                                       temperature, top_k, top_p, seed,
+                                       max_seq or prompt.size + max_new,
+                                       toks.ctypes.data_as(lptr), C.byref(pf), C.byref(dc)),
+            "generate")
+        return toks, pf.value, dc.value
 
     def kv_cache(self, batch, max_seq):
         return KVCache(self, batch, max_seq)

@@ -13,10 +13,12 @@
 // or {"done":true,"reason":"empty_prompt"|"max_seq_len"} before any token, or
 // {"done":true,"error":"...","reason":"error"} on failure.  Keys are sorted.
 #include <cstdint>
+#include <functional>
 #include <ostream>
 #include <string>
 #include <vector>
 
+#include "ctd/nn/model.h"
 #include "ctd/sampling.h"
 
 namespace ctd::generate {
@@ -58,6 +60,21 @@ class ThinkBudget {
   bool in_think_ = false;
   int count_ = 0;
 };
+
+struct LoopResult {
+  int generated = 0;
+  std::string reason;       // "max_tokens", "eos" or "max_seq_len"
+  double prefill_ms = 0.0;  // host wall time: prompt in, first logits ready
+  double decode_ms = 0.0;   // host wall time of the token loop
+};
+
+// The generation loop of run() over a built model, batch 1: prefill the
+// prompt (req.input_ids non-empty, shorter than req.max_seq_len), then up to
+// max_new_tokens tokens, calling emit(token) for each in order.  Greedy
+// requests without budget forcing keep the token on the device: step t+1 is
+// enqueued before the host reads token t, which only decides whether to stop.
+LoopResult generate_loop(const nn::Model& model, const Request& req,
+                         const std::function<void(int64_t)>& emit);
 
 // Runs the protocol for one request text with the model at model_path:
 // writes the JSON reply lines to out and progress to log.  Returns the exit

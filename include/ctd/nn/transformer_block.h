@@ -4,6 +4,7 @@
 #include "ctd/nn/attention.h"
 #include "ctd/nn/mlp.h"
 #include "ctd/nn/rms_norm.h"
+#include "ctd/ops/decode.h"
 #include "ctd/ops/elementwise.h"
 #include "ctd/tensor.h"
 
@@ -15,14 +16,38 @@ struct TransformerBlock {
   Attention self_attn;
   MLP mlp;
 
+  // Inference forward.  With a KV cache and at most ops::kDecodeMaxRows token
+  // rows (a decode step), the fused decode kernels run the same functions in
+  // six launches; otherwise the module ops run one by one.
   Tensor forward(const Tensor& x, KVLayer* kv = nullptr, int position_start = 0) const {
     autograd::NoGradGuard ng;
+    if (kv != nullptr && x.dim() == 3 && x.shape()[0] * x.shape()[1] <= ops::kDecodeMaxRows)
+      return decode_step(x, *kv, position_start);
     Tensor h1 = input_layernorm.forward(x);
     Tensor a = self_attn.forward(h1, kv, position_start);
     Tensor h = ops::add(x, a);
     Tensor h2 = post_attention_layernorm.forward(h);
     Tensor m = mlp.forward(h2);
     return ops::add(h, m);
+  }
+
+  Tensor decode_step(const Tensor& x, KVLayer& kv, int position_start) const {
+    const int64_t B = x.shape()[0], T = x.shape()[1];
+    const Attention& at = self_attn;
+    const int H = at.num_heads, Hk = at.num_kv_heads, D = at.head_dim;
+    auto qkv = ops::decode_linear(x, input_layernorm.weight, input_layernorm.eps,
+                                  {at.q_proj.weight, at.k_proj.weight, at.v_proj.weight});
+    Tensor q = ops::decode_qkv_post(qkv[0], qkv[1], qkv[2], H, Hk, D, at.q_norm.weight,
+                                    at.k_norm.weight, at.q_norm.eps, at.rope_theta,
+                                    at.rope_scaling, position_start, kv.k, kv.v);
+    Tensor a = ops::cached_attention(q, kv.k, kv.v, position_start + T, position_start,
+                                     1.0f / std::sqrt(static_cast<float>(D)));
+    Tensor h = ops::decode_linear(a.reshape({B, T, static_cast<int64_t>(H) * D}), Tensor{}, 0.0f,
+                                  {at.o_proj.weight}, {x})[0];
+    Tensor m = ops::decode_gate_up(h, post_attention_layernorm.weight,
+                                   post_attention_layernorm.eps, mlp.gate_proj.weight,
+                                   mlp.up_proj.weight);
+    return ops::decode_linear(m, Tensor{}, 0.0f, {mlp.down_proj.weight}, {h})[0];
   }
 
   Tensor forward_train(const Tensor& x) const {

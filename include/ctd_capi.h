@@ -170,6 +170,16 @@ int ctd_trainer_forward_cached(ctd_trainer_t t, ctd_kvcache_t cache, const int64
 int ctd_sample(const float* logits, int64_t B, int64_t V, float temperature, int32_t top_k,
                float top_p, uint64_t seed, int32_t draws, int32_t on_device, int64_t* out);
 
+/* The generation loop of ctd_generate (ctd::generate::generate_loop) on the
+ * trainer's model, batch 1: prefill of prompt[P], then max_new tokens, each
+ * sampled from the last logits and fed back through the KV cache (max_seq
+ * rows).  tokens[max_new] receives them; prefill_ms / decode_ms are host wall
+ * times (prompt in to first token known; the token loop). */
+int ctd_trainer_generate(ctd_trainer_t t, const int64_t* prompt, int64_t P, int32_t max_new,
+                         float temperature, int32_t top_k, float top_p, uint64_t seed,
+                         int64_t max_seq, int64_t* tokens, double* prefill_ms,
+                         double* decode_ms);
+
 #ifdef __cplusplus
 }
 #endif

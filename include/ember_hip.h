@@ -227,12 +227,53 @@ int ember_attn_decode(const float* q, const float* k, const float* v, float* o, 
                       int64_t kv_sb, int64_t kv_sh, int64_t kv_st, float scale, void* workspace,
                       size_t workspace_bytes, ember_stream_t s);
 
+/* ------------------------------------------------------ fused decode step
+ * Kernels for calls of at most 8 token rows (decode), each streaming its
+ * weights once with the small ops around it folded in.  No counterpart kernel
+ * in the reference, which runs the per-module ops of
+ * TransformerBlock::forward (include/ctd/nn/transformer_block.h:17-24) one
+ * launch each; these compute the same functions.
+ *
+ * ember_decode_gemv: for s < nseg (1..3), y[s][M, N[s]] = W[s][N[s], K] xn
+ * (+ residual[s][M, N[s]] when residual and residual[s] are non-NULL), where
+ * xn = x [M, K] when norm_w is NULL, else RMSNorm(x) with weight norm_w [K] and
+ * eps (src/ops/norm.cu:17-49 then Linear::forward).  M <= 8, K % 4 == 0,
+ * x / W / norm_w 16-byte aligned.  Host arrays W, N, y, residual are read at
+ * the call. */
+int ember_decode_gemv(const float* x, int64_t M, int64_t K, const float* norm_w, float eps,
+                      int nseg, const float* const* W, const int64_t* N, float* const* y,
+                      const float* const* residual, ember_stream_t s);
+/* out[M, I] = silu(Wg xn) * (Wu xn), xn as above: MLP::forward's gate, up and
+ * silu*mul (include/ctd/nn/mlp.h:16-21) with the post-attention RMSNorm. */
+int ember_decode_gateup(const float* x, int64_t M, int64_t K, const float* norm_w, float eps,
+                        const float* Wg, const float* Wu, int64_t I, float* out,
+                        ember_stream_t s);
+/* Per token row (b, t) of q [B,T,H,D] and k, v [B,T,Hk,D]: per-head RMSNorm of
+ * q and k with q_norm_w / k_norm_w [D] (skipped when NULL), RoPE at position
+ * pos + t (freqs_host: D/2 values of ember_rope_freqs_host), rotated q to
+ * q_out [B,T,H,D], rotated k and v to cache rows pos + t of cache_k / cache_v
+ * [B,Hk,S,D].  Replaces Attention::forward's q_norm/k_norm, the two
+ * apply_rope_inplace and the two write_kv_inplace (attention.h:55-72);
+ * EMBER_EINVAL unless pos + T <= S. */
+int ember_decode_qkv_post(const float* q, const float* k, const float* v, int64_t B, int64_t T,
+                          int64_t H, int64_t Hk, int64_t D, const float* q_norm_w,
+                          const float* k_norm_w, float eps, const float* freqs_host, int64_t pos,
+                          float* q_out, float* cache_k, float* cache_v, int64_t S,
+                          ember_stream_t s);
+
 /* ------------------------------------------------------------- sampling
  * out[r] = index of the largest value of row r of x [rows, n], the first such
  * index on ties, NaNs skipped (0 when x[r,0] is NaN or the row is all NaN):
  * exactly the host scan argmax_cpu (src/core/sampling.cpp:12-19) that greedy
  * sampling (temperature <= 0) runs on the copied logits.  out is device int64. */
 int ember_argmax_rows(const float* x, int64_t rows, int64_t n, int64_t* out, ember_stream_t s);
+/* The same in two stages for long rows (a vocabulary of logits): slices of each
+ * row are reduced by separate workgroups into `workspace` (>=
+ * ember_argmax_rows_workspace_bytes; 0 = one stage suffices), then merged.  A
+ * smaller or NULL workspace runs ember_argmax_rows.  n < 2^32, rows <= 65535. */
+size_t ember_argmax_rows_workspace_bytes(int64_t rows, int64_t n);
+int ember_argmax_rows_ws(const float* x, int64_t rows, int64_t n, int64_t* out, void* workspace,
+                         size_t workspace_bytes, ember_stream_t s);
 
 /* ---------------------------------------------------- masked cross-entropy
  * Per row r: lse[r] = log sum_v exp(logits[r,v]); loss[0] = sum_r mask[r]*(lse[r]

@@ -82,3 +82,5 @@ def test_inference_entry_validation_without_gpu():
     assert ws == 1 * 1 * 16 * 64 * (128 + 2) * 4
     assert lib.ember_argmax_rows(None, 0, 10, None, None) == 0
     assert lib.ember_argmax_rows(None, 2, 0, None, None) == -1
+    assert lib.ember_argmax_rows_workspace_bytes(2, 5000) == 0          # one stage
+    assert lib.ember_argmax_rows_workspace_bytes(2, 151936) == 2 * 19 * 8

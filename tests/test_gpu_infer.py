@@ -59,8 +59,8 @@ def test_kv_write_and_read_expanded(B, T, Hk, D, S, pos):
     r = rng(B * T + D)
     src = r.standard_normal((B, T, Hk, D)).astype(np.float32)
     cache0 = r.standard_normal((B, Hk, S, D)).astype(np.float32)
-    cache = dev(cache0)
-    call("ember_kv_write", p(dev(src)), p(cache), B, T, Hk, D, S, pos, None)
+    cache, srcd = dev(cache0), dev(src)
+    call("ember_kv_write", p(srcd), p(cache), B, T, Hk, D, S, pos, None)
     ref = cache0.copy()
     ref[:, :, pos:pos + T, :] = src.transpose(0, 2, 1, 3)
     got = host(cache)
@@ -144,6 +144,84 @@ def test_skinny_gemm_vs_oracle(M, N, K):
     assert_close(host(Cm), O.matmul(a, b, transb=True), name="skinny beta0")
 
 
+# ------------------------------------------------------ fused decode kernels
+def ptr_array(ts):
+    return (C.c_void_p * 3)(*[t.data_ptr() if t is not None else None for t in ts])
+
+
+@pytest.mark.parametrize("M,K,Ns,norm,resid", [
+    (1, 2048, (2048, 1024, 1024), True, False),   # qwen3-1.7b RMSNorm + Q/K/V
+    (2, 2048, (2048,), False, True),              # O projection + residual
+    (1, 6144, (2048,), False, True),              # down projection + residual
+    (8, 576, (576, 192, 192), True, False),       # smollm2-135m, 8 rows
+    (3, 64, (5, 7, 9), True, True),               # ragged rows
+])
+def test_decode_gemv_vs_oracle(M, K, Ns, norm, resid):
+    r = rng(M * K)
+    x = r.standard_normal((M, K)).astype(np.float32)
+    nw = (1 + 0.1 * r.standard_normal(K)).astype(np.float32)
+    Ws = [(0.05 * r.standard_normal((n, K))).astype(np.float32) for n in Ns]
+    Rs = [r.standard_normal((M, n)).astype(np.float32) for n in Ns]
+    xd, nwd = dev(x), dev(nw)
+    Wd = [dev(w) for w in Ws]
+    Yd = [empty((M, n)) for n in Ns]
+    Rd = [dev(a) for a in Rs]
+    Nn = (C.c_int64 * 3)(*Ns)
+    call("ember_decode_gemv", p(xd), M, K, p(nwd) if norm else None, 1e-6, len(Ns),
+         C.cast(ptr_array(Wd), C.POINTER(C.c_void_p)), Nn,
+         C.cast(ptr_array(Yd), C.POINTER(C.c_void_p)),
+         C.cast(ptr_array(Rd), C.POINTER(C.c_void_p)) if resid else None, None)
+    xn = O.rmsnorm_fwd(x, nw, 1e-6) if norm else x
+    for w, y, res in zip(Ws, Yd, Rs):
+        ref = O.matmul(xn, w, transb=True) + (res if resid else 0.0)
+        assert_close(host(y), ref, name="decode_gemv")
+
+
+@pytest.mark.parametrize("M,K,I", [(1, 2048, 6144), (4, 576, 1536), (8, 128, 258)])
+def test_decode_gateup_vs_oracle(M, K, I):
+    r = rng(K + I)
+    x = r.standard_normal((M, K)).astype(np.float32)
+    nw = (1 + 0.1 * r.standard_normal(K)).astype(np.float32)
+    wg, wu = ((0.05 * r.standard_normal((I, K))).astype(np.float32) for _ in range(2))
+    out = empty((M, I))
+    xd, nwd, wgd, wud = dev(x), dev(nw), dev(wg), dev(wu)  # held until the call has run
+    call("ember_decode_gateup", p(xd), M, K, p(nwd), 1e-5, p(wgd), p(wud), I, p(out), None)
+    xn = O.rmsnorm_fwd(x, nw, 1e-5)
+    ref = O.silu(O.matmul(xn, wg, transb=True)) * O.matmul(xn, wu, transb=True)
+    assert_close(host(out), ref, name="decode_gateup")
+
+
+@pytest.mark.parametrize("B,T,H,Hk,D,pos,qk,factor", [(1, 1, 16, 8, 128, 300, True, 0.0),
+                                                      (2, 3, 8, 2, 64, 17, False, 32.0),
+                                                      (1, 2, 9, 3, 64, 0, False, 0.0)])
+def test_decode_qkv_post_vs_oracle(B, T, H, Hk, D, pos, qk, factor):
+    r = rng(H * D + pos)
+    S, theta, eps = pos + T + 5, 5e5, 1e-6
+    q = r.standard_normal((B, T, H, D)).astype(np.float32)
+    k = r.standard_normal((B, T, Hk, D)).astype(np.float32)
+    v = r.standard_normal((B, T, Hk, D)).astype(np.float32)
+    qn, kn = ((1 + 0.1 * r.standard_normal(D)).astype(np.float32) for _ in range(2))
+    ck0 = r.standard_normal((B, Hk, S, D)).astype(np.float32)
+    cv0 = r.standard_normal((B, Hk, S, D)).astype(np.float32)
+    ck, cv, qo = dev(ck0), dev(cv0), empty((B, T, H, D))
+    freqs = (C.c_float * (D // 2))()
+    capi.check(capi.lib().ember_rope_freqs_host(freqs, D, theta, factor, 1.0, 4.0, 64))
+    qd, kd, vd, qnd, knd = dev(q), dev(k), dev(v), dev(qn), dev(kn)
+    call("ember_decode_qkv_post", p(qd), p(kd), p(vd), B, T, H, Hk, D, p(qnd) if qk else None,
+         p(knd) if qk else None, eps, freqs, pos, p(qo), p(ck), p(cv), S, None)
+    rope = dict(theta=theta, pos0=pos, factor=factor, low=1.0, high=4.0, orig=64)
+    qr = O.rope(O.rmsnorm_fwd(q, qn, eps) if qk else q, **rope)
+    kr = O.rope(O.rmsnorm_fwd(k, kn, eps) if qk else k, **rope)
+    assert_close(host(qo), qr, name="q")
+    got_k, got_v = host(ck), host(cv)
+    assert_close(got_k[:, :, pos:pos + T], kr.transpose(0, 2, 1, 3), name="k cache")
+    assert np.array_equal(got_v[:, :, pos:pos + T], v.transpose(0, 2, 1, 3))
+    keep = np.ones(S, bool)
+    keep[pos:pos + T] = False                       # other cache rows untouched
+    assert np.array_equal(got_k[:, :, keep], ck0[:, :, keep])
+    assert np.array_equal(got_v[:, :, keep], cv0[:, :, keep])
+
+
 # ------------------------------------------------------------------ argmax
 def test_device_argmax_equals_host_scan():
     nan, inf = np.nan, np.inf
@@ -153,10 +231,22 @@ def test_device_argmax_equals_host_scan():
     special = np.array([[1.0, 3.0, 3.0, 2.0], [nan, 5.0, 7.0, 1.0], [1.0, nan, 0.5, 0.0],
                         [-inf, -inf, -inf, -inf], [-inf, 2.0, inf, inf], [nan, nan, nan, nan]],
                        np.float32)
-    for x in (np.stack(rows), special):
+    rows[2][:] = -1.0
+    rows[2][[5, 100000]] = [-0.0, 0.0]                  # +0 and -0 tie: the first wins
+    nan_first = r.standard_normal(151936).astype(np.float32)
+    nan_first[0] = nan                                  # NaN at 0 wins by default
+    for x in (np.stack(rows + [nan_first]), special):
+        want = [OS.argmax(row) for row in x]
+        xd = dev(x)
         out = torch.zeros(x.shape[0], dtype=torch.int64, device="cuda")
-        call("ember_argmax_rows", p(dev(x)), x.shape[0], x.shape[1], p(out), None)
-        assert list(host(out)) == [OS.argmax(row) for row in x]
+        call("ember_argmax_rows", p(xd), x.shape[0], x.shape[1], p(out), None)
+        assert list(host(out)) == want
+        wsb = capi.lib().ember_argmax_rows_workspace_bytes(x.shape[0], x.shape[1])
+        ws = empty((max(1, wsb // 4),))
+        out.zero_()
+        call("ember_argmax_rows_ws", p(xd), x.shape[0], x.shape[1], p(out), p(ws), wsb, None)
+        assert list(host(out)) == want
+    assert want == [1, 0, 0, 0, 2, 0]
     # through ctd::sample: greedy on the device, the same tokens as the host path
     z = r.standard_normal((4, 5000)).astype(np.float32)
     assert np.array_equal(TR.sample(z, 0.0, on_device=True), TR.sample(z, 0.0))
@@ -341,3 +431,21 @@ def test_generate_stop_reasons_and_budget_forcing(gen_model):
         assert json.loads(lines[-1])["reason"] == why
     forced = [json.loads(l)["token"] for l in OG.generate(last_logits, cases[-1])[:-1]]
     assert forced[0] == t0 and forced[3:5] == [500, 501]   # two thinking tokens, then close
+
+
+def test_trainer_generate_greedy_matches_oracle():
+    """The shared generation loop (greedy: token kept on the device, next step
+    queued before the host reads it) through the C API."""
+    c = infer_cfg("qwen3")
+    tr, params = host_params(c, 11, std=0.3)
+    oc = oracle_cfg(c)
+    last_logits = lambda toks: O.model_logits(oc, params, np.array([toks]))[0, -1]  # noqa: E731
+    prompt = [5, 17, 300, 42, 7, 99]
+    ref = [json.loads(l)["token"] for l in
+           OG.generate(last_logits, {"input_ids": prompt, "max_new_tokens": 12,
+                                     "temperature": 0.0})[:-1]]
+    toks, pf, dc = tr.generate(prompt, 12, max_seq=40)
+    assert list(toks) == ref and pf > 0 and dc > 0
+    toks, _, _ = tr.generate(prompt, 12, max_seq=40)      # repeatable
+    assert list(toks) == ref
+    tr.close()
