@@ -182,13 +182,42 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_scalar(
   }
 }
 
-__global__ void column_sum(const float* __restrict__ part, float* __restrict__ out, int64_t nrows,
-                           int64_t H) {
-  const int64_t col = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (col >= H) return;
+// dw = column sums of the [nrows, H] partials.  A workgroup owns 64 columns;
+// its 16 waves take the rows r = j (mod 16), each lane one column (256 B
+// coalesced per wave load, kColUnroll loads in flight), and the 16 partial
+// sums meet in LDS in slice order: a fixed order, so dw is reproducible.
+constexpr int kColThreads = 1024;
+constexpr int kColSlices = kColThreads / kWave;
+constexpr int kColUnroll = 8;
+
+__global__ __launch_bounds__(kColThreads) void column_sum(const float* __restrict__ part,
+                                                          float* __restrict__ out,
+                                                          int64_t nrows, int64_t H) {
+  __shared__ float s_part[kColSlices][kWave];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int j = threadIdx.x / kWave;
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * kWave + lane;
   float t = 0.f;
-  for (int64_t r = 0; r < nrows; ++r) t += part[r * H + col];
-  out[col] = t;
+  if (col < H) {
+    for (int64_t r0 = j; r0 < nrows; r0 += kColSlices * kColUnroll) {
+      float v[kColUnroll];
+#pragma unroll
+      for (int u = 0; u < kColUnroll; ++u) {
+        const int64_t r = r0 + static_cast<int64_t>(u) * kColSlices;
+        v[u] = r < nrows ? part[r * H + col] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < kColUnroll; ++u) t += v[u];
+    }
+  }
+  s_part[j][lane] = t;
+  __syncthreads();
+  if (j == 0 && col < H) {
+    float sum = 0.f;
+#pragma unroll
+    for (int q = 0; q < kColSlices; ++q) sum += s_part[q][lane];
+    out[col] = sum;
+  }
 }
 
 bool vec_ok(int64_t H, const void* a, const void* b) {
@@ -294,6 +323,7 @@ extern "C" int ember_rmsnorm_bwd(const float* dy, const float* x, const float* w
     rc = launch_status();
   }
   if (rc || !dw) return rc;
-  column_sum<<<static_cast<unsigned>((H + 255) / 256), 256, 0, st>>>(part, dw, nb, H);
+  column_sum<<<static_cast<unsigned>((H + kWave - 1) / kWave), kColThreads, 0, st>>>(part, dw, nb,
+                                                                                  H);
   return launch_status();
 }

@@ -12,8 +12,14 @@
 #include "ctd/nn/linear.h"
 #include "ctd/nn/rms_norm.h"
 #include "ctd/ops/attention.h"
+#include "ctd/ops/elementwise.h"
 #include "ctd/ops/kv_cache.h"
+#include "ctd/ops/mask.h"
+#include "ctd/ops/matmul.h"
+#include "ctd/ops/permute.h"
+#include "ctd/ops/repeat_kv.h"
 #include "ctd/ops/rope.h"
+#include "ctd/ops/softmax.h"
 #include "ctd/tensor.h"
 
 namespace ctd::nn {
@@ -38,6 +44,24 @@ struct Attention {
   int group() const { return num_heads / num_kv_heads; }
   int hidden_size() const { return num_heads * head_dim; }
 
+  // The fused attention kernels take head_dim 64 or 128 (every preset);
+  // other head sizes run the reference's op chain below.
+  static bool fused_head_dim(int D) { return D == 64 || D == 128; }
+
+  // The reference's composition (attention.h:66-91, 123-141 of the
+  // reference): Q [B,T,H,D] against Kr, Vr [B,H,L,D], query t seeing keys
+  // j <= position_start + t.  Autograd-aware.  -> [B,T,H,D].
+  static Tensor attention_chain(const Tensor& Q, const Tensor& Kr, const Tensor& Vr,
+                                int position_start, float scale) {
+    const int64_t B = Q.shape()[0], T = Q.shape()[1], H = Q.shape()[2], D = Q.shape()[3];
+    const int64_t L = Kr.shape()[2];
+    Tensor q3 = ops::permute(Q, {0, 2, 1, 3}).reshape({B * H, T, D});
+    Tensor s = ops::bmm(q3, Kr.reshape({B * H, L, D}), /*transa=*/false, /*transb=*/true);
+    s = ops::apply_causal_mask(ops::mul_scalar(s, scale), position_start);
+    Tensor o = ops::bmm(ops::softmax(s), Vr.reshape({B * H, L, D}), false, false);
+    return ops::permute(o.reshape({B, H, T, D}), {0, 2, 1, 3});
+  }
+
   // Inference forward (no autograd).  Positions start at position_start.  With
   // kv, this call's K/V go to cache rows [position_start, position_start+T)
   // and the queries attend over rows [0, position_start+T).
@@ -61,7 +85,14 @@ struct Attention {
       ops::write_kv_inplace(kv->k, K, position_start);
       ops::write_kv_inplace(kv->v, V, position_start);
     }
-    if (position_start == 0) {
+    if (!fused_head_dim(D)) {
+      const int L = kv ? position_start + static_cast<int>(T) : static_cast<int>(T);
+      Tensor Kr = kv ? ops::read_kv_expanded(kv->k, L, group())
+                     : ops::permute(ops::repeat_kv_heads(K, group()), {0, 2, 1, 3});
+      Tensor Vr = kv ? ops::read_kv_expanded(kv->v, L, group())
+                     : ops::permute(ops::repeat_kv_heads(V, group()), {0, 2, 1, 3});
+      A = attention_chain(Q, Kr, Vr, position_start, scale);
+    } else if (position_start == 0) {
       // Prefill: every visible key is one of these T, so the training kernel
       // (MFMA tiles) runs on the fresh projections.
       A = ops::causal_attention_impl(Q, K, V, scale);
@@ -87,7 +118,15 @@ struct Attention {
     }
     Q = ops::rope(Q, /*position_start=*/0, rope_theta, rope_scaling);
     K = ops::rope(K, /*position_start=*/0, rope_theta, rope_scaling);
-    Tensor A = ops::causal_attention(Q, K, V, 1.0f / std::sqrt(static_cast<float>(D)));
+    const float scale = 1.0f / std::sqrt(static_cast<float>(D));
+    Tensor A;
+    if (fused_head_dim(D)) {
+      A = ops::causal_attention(Q, K, V, scale);
+    } else {
+      Tensor Kr = ops::permute(ops::repeat_kv_heads(K, group()), {0, 2, 1, 3});
+      Tensor Vr = ops::permute(ops::repeat_kv_heads(V, group()), {0, 2, 1, 3});
+      A = attention_chain(Q, Kr, Vr, 0, scale);
+    }
     return o_proj.forward(A.reshape({B, T, static_cast<int64_t>(H) * D}));
   }
 };

@@ -21,7 +21,8 @@ struct TransformerBlock {
   // six launches; otherwise the module ops run one by one.
   Tensor forward(const Tensor& x, KVLayer* kv = nullptr, int position_start = 0) const {
     autograd::NoGradGuard ng;
-    if (kv != nullptr && x.dim() == 3 && x.shape()[0] * x.shape()[1] <= ops::kDecodeMaxRows)
+    if (kv != nullptr && x.dim() == 3 && x.shape()[0] * x.shape()[1] <= ops::kDecodeMaxRows &&
+        Attention::fused_head_dim(self_attn.head_dim))
       return decode_step(x, *kv, position_start);
     Tensor h1 = input_layernorm.forward(x);
     Tensor a = self_attn.forward(h1, kv, position_start);

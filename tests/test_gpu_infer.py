@@ -262,6 +262,8 @@ def infer_cfg(variant):
         base.update(head_dim=128, qk_norm=1, rms_norm_eps=1e-6, rope_theta=1e6)
     elif variant == "llama3":
         base.update(num_heads=8, rope_theta=5e5, rope_factor=32.0, rope_original_max_pos=16)
+    elif variant == "d32":  # head size outside the fused kernels: the reference op chain
+        base.update(head_dim=32, qk_norm=1, rms_norm_eps=1e-6)
     return TR.make_config(**base)
 
 
@@ -285,7 +287,7 @@ def host_params(c, seed, std=0.2):
     return tr, params
 
 
-@pytest.mark.parametrize("variant", ["smollm2", "qwen3", "llama3"])
+@pytest.mark.parametrize("variant", ["smollm2", "qwen3", "llama3", "d32"])
 def test_prefill_with_cache_equals_no_cache(variant):
     c = infer_cfg(variant)
     tr, params = host_params(c, 1)
@@ -299,7 +301,7 @@ def test_prefill_with_cache_equals_no_cache(variant):
     tr.close()
 
 
-@pytest.mark.parametrize("variant", ["smollm2", "qwen3", "llama3"])
+@pytest.mark.parametrize("variant", ["smollm2", "qwen3", "llama3", "d32"])
 def test_prefill_then_decode_steps_equal_full_forward(variant):
     c = infer_cfg(variant)
     tr, params = host_params(c, 3)

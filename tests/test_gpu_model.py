@@ -131,7 +131,11 @@ def batch(c, B, T, seed):
 
 
 @pytest.mark.parametrize("qk_norm,llama3,D", [(False, False, 64), (True, False, 128),
-                                              (False, True, 64)])
+                                              (False, True, 64),
+                                              # head sizes outside the fused kernels' 64/128:
+                                              # the reference's bmm/mask/softmax chain
+                                              (True, False, 16), (False, True, 32),
+                                              (False, False, 8)])
 def test_tiny_model_loss_and_grads_vs_oracle(qk_norm, llama3, D):
     c = tiny_cfg(qk_norm, llama3, D)
     tr = TR.Trainer(c, seed=1, init_std=0.1, norm_value=None)
