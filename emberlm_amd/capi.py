@@ -75,6 +75,8 @@ SIGNATURES = {
     "ember_ce_masked_fwd_workspace_bytes": (sz, [i64]),
     "ember_ce_masked_fwd": (i32, [vp, vp, vp, i64, i64, vp, vp, vp, vp, sz, vp]),
     "ember_ce_masked_bwd": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, vp, vp]),
+    "ember_ce_masked_rows": (i32, [vp, vp, vp, i64, i64, vp, vp, vp]),
+    "ember_ce_masked_reduce": (i32, [vp, vp, i64, vp, vp, vp]),
     "ember_embedding_fwd": (i32, [vp, vp, vp, i64, i64, i64, vp]),
     "ember_embedding_bwd_workspace_bytes": (sz, [i64, i64]),
     "ember_embedding_bwd": (i32, [vp, vp, vp, i64, i64, i64, i32, vp, sz, vp]),

@@ -151,34 +151,48 @@ Tensor Model::forward_last_logits(const Tensor& input_ids, KVCache* cache,
   return lm_head.forward(norm.forward(last));
 }
 
-Tensor Model::forward_train_logits(const Tensor& input_ids) const {
-  Tensor h = embed_tokens.forward(input_ids);
-  for (const auto& layer : layers) {
-    if (gradient_checkpointing) {
+namespace {
+
+// embedding -> blocks (checkpointed when enabled) -> final RMSNorm: [B, T, H].
+Tensor train_hidden(const Model& m, const Tensor& input_ids) {
+  Tensor h = m.embed_tokens.forward(input_ids);
+  for (const auto& layer : m.layers) {
+    if (m.gradient_checkpointing) {
       h = autograd::checkpoint([&layer](const Tensor& x) { return layer.forward_train(x); }, h);
     } else {
       h = layer.forward_train(h);
     }
   }
-  h = norm.forward(h);
-  Linear lm_head{embed_tokens.weight};  // tied head
-  return lm_head.forward(h);
+  return m.norm.forward(h);
 }
 
+}  // namespace
+
+Tensor Model::forward_train_logits(const Tensor& input_ids) const {
+  Linear lm_head{embed_tokens.weight};  // tied head
+  return lm_head.forward(train_hidden(*this, input_ids));
+}
+
+// The losses run the tied LM head and the cross-entropy together a chunk of
+// rows at a time (ops::linear_cross_entropy_masked): the same loss as
+// cross_entropy(forward_train_logits(...)) without the [B*T, V] logits.
 Tensor Model::forward_train(const Tensor& input_ids, const Tensor& targets) const {
   const int64_t total = input_ids.numel();
-  Tensor logits = forward_train_logits(input_ids);
-  const int64_t V = logits.shape().back();
-  return ops::cross_entropy(logits.reshape({total, V}), targets.reshape({total}));
+  Tensor h = train_hidden(*this, input_ids);
+  Tensor ones = Tensor::empty({total}, DType::kFloat32, h.device());
+  CTD_CHECK(ember_fill(static_cast<float*>(ones.data_ptr()), total, 1.0f,
+                       runtime::compute_stream()));
+  return ops::linear_cross_entropy_masked(h.reshape({total, h.shape().back()}),
+                                          embed_tokens.weight, targets.reshape({total}), ones);
 }
 
 Tensor Model::forward_train_masked(const Tensor& input_ids, const Tensor& targets,
                                    const Tensor& loss_mask) const {
   const int64_t total = input_ids.numel();
-  Tensor logits = forward_train_logits(input_ids);
-  const int64_t V = logits.shape().back();
-  return ops::cross_entropy_masked(logits.reshape({total, V}), targets.reshape({total}),
-                                   loss_mask.reshape({total}));
+  Tensor h = train_hidden(*this, input_ids);
+  return ops::linear_cross_entropy_masked(h.reshape({total, h.shape().back()}),
+                                          embed_tokens.weight, targets.reshape({total}),
+                                          loss_mask.reshape({total}));
 }
 
 namespace {

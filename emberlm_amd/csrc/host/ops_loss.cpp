@@ -2,8 +2,12 @@
 // Reference: src/ops/loss.cu:104-429 and src/ops/embedding.cu.  The loss keeps
 // only lse[N] from the forward (no [N,V] probabilities) and, when its saved
 // logits are not shared with anyone else, writes dlogits over them.
+#include <algorithm>
+#include <atomic>
+
 #include "ctd/ops/embedding.h"
 #include "ctd/ops/loss.h"
+#include "ember_hip.h"
 #include "op_util.h"
 
 namespace ctd::ops {
@@ -92,6 +96,124 @@ Tensor cross_entropy_masked(const Tensor& logits, const Tensor& targets,
     autograd::set_history(o.loss, std::move(node));
   }
   return o.loss;
+}
+
+namespace {
+
+std::atomic<int64_t> g_head_chunk_rows{0};
+
+// Rows per chunk: at most ~2.5 GB of logits, a multiple of 256, at least 256.
+int64_t head_chunk_rows(int64_t N, int64_t V) {
+  if (const int64_t fixed = g_head_chunk_rows.load()) return std::min(N, fixed);
+  const int64_t budget = static_cast<int64_t>(2.5e9) / (V * static_cast<int64_t>(sizeof(float)));
+  int64_t r = std::max<int64_t>(256, budget / 256 * 256);
+  return std::min(N, r);
+}
+
+// C = op(A) op(B) (+ C when accumulate) through the C ABI with its split-K workspace.
+void head_gemm(bool ta, bool tb, int64_t M, int64_t N, int64_t K, const float* A, int64_t lda,
+               const float* B, int64_t ldb, float* C, int64_t ldc, bool accumulate) {
+  const size_t wsb = ember_gemm_f32_workspace_bytes(M, N, K, 1);
+  Tensor ws = wsb ? workspace(wsb) : Tensor{};
+  void* ev = runtime::gemm_profile_begin();
+  CTD_CHECK(ember_gemm_f32_ws(ta, tb, M, N, K, 1.0f, A, lda, 0, B, ldb, 0,
+                              accumulate ? 1.0f : 0.0f, C, ldc, 0, 1,
+                              wsb ? ws.data_ptr() : nullptr, wsb, S()));
+  runtime::gemm_profile_end(ev, 2.0 * M * N * K, 2 * ta + tb);
+}
+
+struct LinearCrossEntropyBackward : autograd::Node {
+  Tensor dh, dw, mask_sum;  // gradients for an upstream gradient of 1
+  bool want_h = false, want_w = false;
+  const char* name() const override { return "LinearCrossEntropyBackward"; }
+  std::vector<Tensor> backward(const std::vector<Tensor>& go) override {
+    autograd::NoGradGuard ng;
+    const Tensor& dy = go.at(0);
+    check_f32(dy, "linear_cross_entropy_masked backward", "grad");
+    float ms = 0.0f, g = 0.0f;
+    mask_sum.copy_to_host(&ms);
+    if (!(ms > 0.0f))
+      throw std::runtime_error("cross_entropy_masked: sum(loss_mask) == 0 in backward");
+    dy.copy_to_host(&g);
+    if (g != 1.0f) {
+      if (want_h) CTD_CHECK(ember_scale(cfp(dh), g, fp(dh), dh.numel(), S()));
+      if (want_w) CTD_CHECK(ember_scale(cfp(dw), g, fp(dw), dw.numel(), S()));
+    }
+    std::vector<Tensor> out = {want_h ? dh : Tensor{}, want_w ? dw : Tensor{}, Tensor{},
+                               Tensor{}};
+    dh = dw = mask_sum = Tensor{};
+    return out;
+  }
+};
+
+}  // namespace
+
+void set_linear_cross_entropy_chunk_rows(int64_t rows) {
+  require(rows >= 0, "set_linear_cross_entropy_chunk_rows: rows must be >= 0");
+  g_head_chunk_rows.store(rows);
+}
+
+Tensor linear_cross_entropy_masked(const Tensor& h, const Tensor& w, const Tensor& targets,
+                                   const Tensor& loss_mask) {
+  check_f32(h, "linear_cross_entropy_masked", "h");
+  check_f32(w, "linear_cross_entropy_masked", "weight");
+  check_f32(loss_mask, "linear_cross_entropy_masked", "loss_mask");
+  require(h.dim() == 2 && w.dim() == 2 && h.shape()[1] == w.shape()[1],
+          "linear_cross_entropy_masked: expected h [N, H] and weight [V, H]");
+  const int64_t N = h.shape()[0], H = h.shape()[1], V = w.shape()[0];
+  require(targets.dtype() == DType::kInt64 && targets.device().is_hip() &&
+              targets.is_contiguous() && targets.dim() == 1 && targets.shape()[0] == N,
+          "linear_cross_entropy_masked: targets must be contiguous int64 [N] on the HIP device");
+  require(loss_mask.dim() == 1 && loss_mask.shape()[0] == N,
+          "linear_cross_entropy_masked: loss_mask shape mismatch");
+  const bool want_h = autograd::any_requires_grad({h});
+  const bool want_w = autograd::any_requires_grad({w});
+  const bool grad = want_h || want_w;
+  const Device dev = h.device();
+  Tensor loss = Tensor::empty({1}, DType::kFloat32, dev);
+  Tensor mask_sum = Tensor::empty({1}, DType::kFloat32, dev);
+  Tensor lse = Tensor::empty({N}, DType::kFloat32, dev);
+  Tensor row_loss = Tensor::empty({N}, DType::kFloat32, dev);
+  const int64_t* tg = static_cast<const int64_t*>(targets.data_ptr());
+  Tensor dh, dw, one;
+  if (grad) {
+    // sum(mask) first: each chunk's dlogits needs it.
+    CTD_CHECK(ember_ce_masked_reduce(nullptr, cfp(loss_mask), N, fp(loss), fp(mask_sum), S()));
+    one = Tensor::empty({1}, DType::kFloat32, dev);
+    CTD_CHECK(ember_fill(fp(one), 1, 1.0f, S()));
+    if (want_h) dh = Tensor::empty({N, H}, DType::kFloat32, dev);
+    if (want_w) dw = Tensor::empty({V, H}, DType::kFloat32, dev);  // running dlogits^T h
+  }
+  if (N > 0) {
+    const int64_t rows = head_chunk_rows(N, V);
+    Tensor logits = Tensor::empty({rows, V}, DType::kFloat32, dev);
+    for (int64_t r0 = 0; r0 < N; r0 += rows) {
+      const int64_t n = std::min(rows, N - r0);
+      const float* hc = cfp(h) + r0 * H;
+      head_gemm(false, true, n, V, H, hc, H, cfp(w), H, fp(logits), V, false);
+      CTD_CHECK(ember_ce_masked_rows(cfp(logits), tg + r0, cfp(loss_mask) + r0, n, V,
+                                     fp(lse) + r0, fp(row_loss) + r0, S()));
+      if (!grad) continue;
+      CTD_CHECK(ember_ce_masked_bwd(cfp(logits), tg + r0, cfp(loss_mask) + r0, cfp(lse) + r0,
+                                    cfp(one), cfp(mask_sum), n, V, fp(logits), S()));
+      if (want_h) head_gemm(false, false, n, H, V, cfp(logits), V, cfp(w), H, fp(dh) + r0 * H, H,
+                            false);
+      if (want_w) head_gemm(true, false, V, H, n, cfp(logits), V, hc, H, fp(dw), H, r0 > 0);
+    }
+  }
+  CTD_CHECK(ember_ce_masked_reduce(cfp(row_loss), cfp(loss_mask), N, fp(loss), fp(mask_sum),
+                                   S()));
+  if (grad) {
+    auto node = std::make_shared<LinearCrossEntropyBackward>();
+    node->dh = dh;
+    node->dw = dw;
+    node->mask_sum = mask_sum;
+    node->want_h = want_h;
+    node->want_w = want_w;
+    node->next_edges = autograd::collect_next_edges({h, w, targets, loss_mask});
+    autograd::set_history(loss, std::move(node));
+  }
+  return loss;
 }
 
 // Plain mean cross-entropy = the masked loss with an all-ones mask

@@ -18,6 +18,7 @@
 #include "ctd/allocator.h"
 #include "ctd/generate.h"
 #include "ctd/nn/model.h"
+#include "ctd/ops/loss.h"
 #include "ctd/ops/repeat_kv.h"
 #include "ctd/optim.h"
 #include "ctd/runtime.h"
@@ -684,6 +685,10 @@ int ctd_trainer_generate(ctd_trainer_t t, const int64_t* prompt, int64_t P, int3
     if (prefill_ms) *prefill_ms = r.prefill_ms;
     if (decode_ms) *decode_ms = r.decode_ms;
   });
+}
+
+int ctd_set_head_chunk_rows(int64_t rows) {
+  return guarded([&] { ops::set_linear_cross_entropy_chunk_rows(rows); });
 }
 
 }  // extern "C"

@@ -80,7 +80,7 @@ __global__ __launch_bounds__(1024) void ce_reduce(const float* __restrict__ row_
   __shared__ double sm[1024];
   double a = 0.0, b = 0.0;
   for (int64_t i = threadIdx.x; i < N; i += 1024) {
-    a += row_loss[i];
+    if (row_loss) a += row_loss[i];
     b += mask[i];
   }
   sl[threadIdx.x] = a;
@@ -192,5 +192,26 @@ extern "C" int ember_ce_masked_bwd(const float* logits, const int64_t* tgt, cons
   else
     ce_bwd_rows<false><<<row_grid(N), kThreads, 0, st>>>(logits, tgt, mask, lse, dloss, mask_sum,
                                                          N, V, dlogits);
+  return launch_status();
+}
+
+extern "C" int ember_ce_masked_rows(const float* logits, const int64_t* tgt, const float* mask,
+                                    int64_t N, int64_t V, float* lse, float* row_loss,
+                                    ember_stream_t s) {
+  if (N < 0 || V <= 0) return EMBER_EINVAL;
+  if (N == 0) return EMBER_OK;
+  if (!logits || !tgt || !mask || !lse || !row_loss) return EMBER_EINVAL;
+  hipStream_t st = as_stream(s);
+  if (V % 4 == 0 && aligned16(logits))
+    ce_fwd_rows<true><<<row_grid(N), kThreads, 0, st>>>(logits, tgt, mask, N, V, lse, row_loss);
+  else
+    ce_fwd_rows<false><<<row_grid(N), kThreads, 0, st>>>(logits, tgt, mask, N, V, lse, row_loss);
+  return launch_status();
+}
+
+extern "C" int ember_ce_masked_reduce(const float* row_loss, const float* mask, int64_t N,
+                                      float* loss, float* mask_sum, ember_stream_t s) {
+  if (N < 0 || !loss || !mask_sum || (N > 0 && !mask)) return EMBER_EINVAL;
+  ce_reduce<<<1, 1024, 0, as_stream(s)>>>(row_loss, mask, N, loss, mask_sum);
   return launch_status();
 }

@@ -15,4 +15,16 @@ Tensor cross_entropy_masked(const Tensor& logits, const Tensor& targets,
 Tensor cross_entropy_masked_impl(const Tensor& logits, const Tensor& targets,
                                  const Tensor& loss_mask);
 
+// cross_entropy_masked(h W^T, targets, loss_mask) for h [N, H], W [V, H] (the
+// tied LM head and its loss) without materialising the [N, V] logits: rows go
+// through in chunks of at most a few GB of logits, and when h or W needs a
+// gradient the chunk's dlogits, dh and dW (for an upstream gradient of 1) are
+// formed right there; backward scales them by the upstream gradient.  The
+// loss equals cross_entropy_masked's bit for bit; same error on sum(mask) == 0.
+Tensor linear_cross_entropy_masked(const Tensor& h, const Tensor& w, const Tensor& targets,
+                                   const Tensor& loss_mask);
+// Rows per chunk of linear_cross_entropy_masked (process-wide); 0 restores the
+// automatic choice (about 2.5 GB of logits per chunk).
+void set_linear_cross_entropy_chunk_rows(int64_t rows);
+
 }  // namespace ctd::ops

@@ -180,6 +180,10 @@ int ctd_trainer_generate(ctd_trainer_t t, const int64_t* prompt, int64_t P, int3
                          int64_t max_seq, int64_t* tokens, double* prefill_ms,
                          double* decode_ms);
 
+/* Rows per chunk of the fused LM head + loss (ops::set_linear_cross_entropy_chunk_rows;
+ * 0 = automatic). */
+int ctd_set_head_chunk_rows(int64_t rows);
+
 #ifdef __cplusplus
 }
 #endif

@@ -293,6 +293,16 @@ int ember_ce_masked_bwd(const float* logits, const int64_t* tgt, const float* ma
                         const float* lse, const float* dloss, const float* mask_sum, int64_t N,
                         int64_t V, float* dlogits, ember_stream_t s);
 
+/* The two halves of ember_ce_masked_fwd, for callers that produce the logits
+ * a slice of rows at a time (the chunked LM head + loss): per-row lse[N] and
+ * row_loss[N] = mask * (lse - logit[tgt]); then loss[0] = sum(row_loss) /
+ * sum(mask) and mask_sum[0] in the same fixed order (row_loss NULL: mask_sum
+ * only, loss 0). */
+int ember_ce_masked_rows(const float* logits, const int64_t* tgt, const float* mask, int64_t N,
+                         int64_t V, float* lse, float* row_loss, ember_stream_t s);
+int ember_ce_masked_reduce(const float* row_loss, const float* mask, int64_t N, float* loss,
+                           float* mask_sum, ember_stream_t s);
+
 /* -------------------------------------------------------------- embedding
  * out[i,:] = w[ids[i],:] (src/ops/embedding.cu:15-24). */
 int ember_embedding_fwd(const int64_t* ids, const float* w, float* out, int64_t n, int64_t H,

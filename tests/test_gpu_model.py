@@ -170,6 +170,28 @@ def test_tiny_model_loss_and_grads_vs_oracle(qk_norm, llama3, D):
     tr.close()
 
 
+def test_chunked_lm_head_loss_equals_single_chunk():
+    """The LM head + loss run a chunk of rows at a time; the loss does not
+    depend on the chunking (bitwise), the gradients only through the order dW
+    is summed in, and both match the oracle."""
+    c = tiny_cfg(qk_norm=True, D=64)
+    ids, tg, mask = batch(c, 2, 96, seed=8)
+    runs = []
+    for rows in (0, 64, 40):   # automatic (one chunk), 3 chunks, 5 chunks (ragged)
+        TR.set_head_chunk_rows(rows)
+        tr = TR.Trainer(c, seed=4, init_std=0.1, norm_value=None)
+        tr.set_batch(ids, tg, mask)
+        loss = tr.forward_backward(True)
+        runs.append((loss, [tr.get_grad(i) for i in range(tr.num_params())], tr.names))
+        tr.close()
+    TR.set_head_chunk_rows(0)
+    base_loss, base_grads, names = runs[0]
+    for loss, grads, _ in runs[1:]:
+        assert loss == base_loss
+        for name, g, b in zip(names, grads, base_grads):
+            assert_close(g, b, rtol=1e-5, name=name)
+
+
 def test_offload_equals_on_device_over_steps():
     c = tiny_cfg(qk_norm=True, D=128)
     a = TR.Trainer(c, seed=3, init_std=0.05)
