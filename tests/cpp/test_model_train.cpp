@@ -1,0 +1,279 @@
+// C++-API tests on tiny random models, written as the reference's own tests
+// are (tests/test_train_forward.cpp:95-208, tests/test_integration_kvcache.cpp:
+// 57-123 of the reference), against include/ctd/ directly.  Run on a GPU by
+// tests/test_gpu_cpp.py; the CPU oracle (oracle/ember_oracle.h) pins the
+// logits.  Exit status = number of failed tests.
+#include <cmath>
+#include <cstdio>
+#include <functional>
+#include <random>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "ctd/autograd.h"
+#include "ctd/nn/kv_cache.h"
+#include "ctd/nn/model.h"
+#include "ctd/optim.h"
+#include "ctd/tensor.h"
+#include "ember_oracle.h"
+
+using namespace ctd;
+
+namespace {
+
+int g_failed = 0;
+std::string g_current;
+
+void check(bool ok, const std::string& what) {
+  if (!ok) {
+    ++g_failed;
+    std::printf("  FAILED: %s (in %s)\n", what.c_str(), g_current.c_str());
+  }
+}
+
+struct TinyCfg {
+  int V = 8;
+  int D = 8;   // hidden
+  int H = 2;   // query heads
+  int Hk = 1;  // kv heads
+  int Dh = 4;  // head_dim
+  int I = 16;
+  int L = 1;
+  float eps = 1e-5f;
+  float theta = 100.0f;
+};
+
+Tensor rand_tensor(const std::vector<int64_t>& shape, std::mt19937& rng, float scale,
+                   bool grad) {
+  std::normal_distribution<float> nd(0.0f, 1.0f);
+  int64_t n = 1;
+  for (auto d : shape) n *= d;
+  std::vector<float> h(static_cast<size_t>(n));
+  for (auto& v : h) v = nd(rng) * scale;
+  Tensor t = Tensor::from_host(h.data(), shape, DType::kFloat32, kHIP0);
+  if (grad) t.requires_grad_(true);
+  return t;
+}
+
+Tensor linear_w(int64_t out, int64_t in, std::mt19937& rng, bool grad) {
+  return rand_tensor({out, in}, rng, 1.0f / std::sqrt(static_cast<float>(in)), grad);
+}
+
+Tensor ones_vec(int64_t n, bool grad) {
+  std::vector<float> h(static_cast<size_t>(n), 1.0f);
+  Tensor t = Tensor::from_host(h.data(), {n}, DType::kFloat32, kHIP0);
+  if (grad) t.requires_grad_(true);
+  return t;
+}
+
+nn::Model build_tiny(const TinyCfg& c, std::mt19937& rng, bool grad) {
+  nn::Model m;
+  m.config = nn::LlamaConfig{
+      .vocab_size = c.V,
+      .hidden_size = c.D,
+      .intermediate_size = c.I,
+      .num_hidden_layers = c.L,
+      .num_attention_heads = c.H,
+      .num_key_value_heads = c.Hk,
+      .head_dim = c.Dh,
+      .max_position_embeddings = 64,
+      .rms_norm_eps = c.eps,
+      .rope_theta = c.theta,
+      .tie_word_embeddings = true,
+  };
+  m.embed_tokens = nn::Embedding{rand_tensor({c.V, c.D}, rng, 0.02f, grad)};
+  m.norm = nn::RMSNorm{ones_vec(c.D, grad), c.eps};
+  for (int i = 0; i < c.L; ++i) {
+    nn::TransformerBlock blk{
+        .input_layernorm = {ones_vec(c.D, grad), c.eps},
+        .post_attention_layernorm = {ones_vec(c.D, grad), c.eps},
+        .self_attn =
+            {
+                .q_proj = {linear_w(c.H * c.Dh, c.D, rng, grad)},
+                .k_proj = {linear_w(c.Hk * c.Dh, c.D, rng, grad)},
+                .v_proj = {linear_w(c.Hk * c.Dh, c.D, rng, grad)},
+                .o_proj = {linear_w(c.D, c.H * c.Dh, rng, grad)},
+                .num_heads = c.H,
+                .num_kv_heads = c.Hk,
+                .head_dim = c.Dh,
+                .rope_theta = c.theta,
+            },
+        .mlp =
+            {
+                .gate_proj = {linear_w(c.I, c.D, rng, grad)},
+                .up_proj = {linear_w(c.I, c.D, rng, grad)},
+                .down_proj = {linear_w(c.D, c.I, rng, grad)},
+            },
+    };
+    m.layers.push_back(std::move(blk));
+  }
+  return m;
+}
+
+std::vector<Tensor> params_of(nn::Model& m) {
+  std::vector<Tensor> ps;
+  for (auto& [name, t] : m.collect_parameters().all) ps.push_back(t);
+  return ps;
+}
+
+std::vector<float> host(const Tensor& t) {
+  std::vector<float> h(static_cast<size_t>(t.numel()));
+  t.copy_to_host(h.data());
+  return h;
+}
+
+double max_abs_diff(const std::vector<float>& a, const std::vector<float>& b) {
+  if (a.size() != b.size()) return INFINITY;
+  double m = 0.0;
+  for (size_t i = 0; i < a.size(); ++i)
+    m = std::max(m, std::abs(static_cast<double>(a[i]) - static_cast<double>(b[i])));
+  return m;
+}
+
+// Oracle logits [B*T*V] of the model (collect_parameters order).
+std::vector<double> oracle_logits(nn::Model& m, const std::vector<int64_t>& ids, int64_t B,
+                                  int64_t T) {
+  const nn::LlamaConfig& c = m.config;
+  orc_cfg oc{};
+  oc.vocab = c.vocab_size;
+  oc.hidden = c.hidden_size;
+  oc.inter = c.intermediate_size;
+  oc.layers = c.num_hidden_layers;
+  oc.heads = c.num_attention_heads;
+  oc.kv_heads = c.num_key_value_heads;
+  oc.head_dim = c.head_dim;
+  oc.eps = c.rms_norm_eps;
+  oc.theta = c.rope_theta;
+  oc.rope_factor = c.rope_scaling_factor;
+  oc.rope_low_freq = c.rope_scaling_low_freq_factor;
+  oc.rope_high_freq = c.rope_scaling_high_freq_factor;
+  oc.rope_orig_max_pos = c.rope_scaling_original_max_pos;
+  oc.qk_norm = c.qk_norm ? 1 : 0;
+  std::vector<std::vector<double>> store;
+  std::vector<const double*> ptrs;
+  for (const Tensor& p : params_of(m)) {
+    std::vector<float> h = host(p);
+    store.emplace_back(h.begin(), h.end());
+  }
+  for (auto& s : store) ptrs.push_back(s.data());
+  std::vector<double> out(static_cast<size_t>(B * T * c.vocab_size));
+  orc_model_logits(&oc, ptrs.data(), ids.data(), out.data(), B, T);
+  return out;
+}
+
+void run(const char* name, const std::function<void()>& fn) {
+  g_current = name;
+  std::printf("[ RUN      ] %s\n", name);
+  const int before = g_failed;
+  try {
+    fn();
+  } catch (const std::exception& e) {
+    ++g_failed;
+    std::printf("  FAILED: exception %s\n", e.what());
+  }
+  std::printf("[ %s ] %s\n", g_failed == before ? "      OK" : "  FAILED", name);
+  std::fflush(stdout);
+}
+
+// reference test_train_forward.cpp:138-171 (+ the oracle)
+void train_logits_match_inference_logits(TinyCfg c) {
+  std::mt19937 rng(42);
+  nn::Model m = build_tiny(c, rng, /*grad=*/false);
+  std::vector<int64_t> hids = {1, 4, 0, 6, 7, 2, 3, 5};
+  for (auto& v : hids) v %= c.V;
+  Tensor ids = Tensor::from_host(hids.data(), {2, 4}, DType::kInt64, kHIP0);
+  Tensor inf, train;
+  {
+    autograd::NoGradGuard ng;
+    inf = m.forward(ids);
+    train = m.forward_train_logits(ids);
+  }
+  check(inf.shape() == train.shape(), "logit shapes");
+  const std::vector<float> a = host(inf), b = host(train);
+  check(max_abs_diff(a, b) < 1e-4, "inference vs training logits < 1e-4");
+  const std::vector<double> ref = oracle_logits(m, hids, 2, 4);
+  double worst = 0.0, scale = 0.0;
+  for (size_t i = 0; i < ref.size(); ++i) {
+    worst = std::max(worst, std::abs(a[i] - ref[i]));
+    scale = std::max(scale, std::abs(ref[i]));
+  }
+  check(worst <= 1e-4 * scale + 1e-6, "logits vs oracle");
+}
+
+// reference test_train_forward.cpp:174-208, also with gradient checkpointing
+// and with the offloaded optimizer: the three runs give the same loss bits.
+void overfits_tiny_batch() {
+  const int B = 2, T = 4;
+  std::vector<int64_t> hx = {1, 4, 0, 6, 7, 2, 3, 5};
+  std::vector<int64_t> hy = {4, 0, 6, 3, 2, 3, 5, 1};
+  std::vector<float> finals;
+  for (int variant = 0; variant < 3; ++variant) {
+    std::mt19937 rng(123);
+    TinyCfg c;
+    nn::Model m = build_tiny(c, rng, /*grad=*/true);
+    m.gradient_checkpointing = variant >= 1;
+    Tensor x = Tensor::from_host(hx.data(), {B, T}, DType::kInt64, kHIP0);
+    Tensor y = Tensor::from_host(hy.data(), {B, T}, DType::kInt64, kHIP0);
+    optim::AdamW opt(params_of(m), /*lr=*/1e-2f, /*wd=*/0.0f, 0.9f, 0.95f, 1e-8f,
+                     /*offload=*/variant == 2);
+    constexpr int Steps = 300;
+    float first = 0.0f, last = 0.0f;
+    for (int step = 0; step < Steps; ++step) {
+      opt.zero_grad();
+      Tensor loss = m.forward_train(x, y);
+      loss.backward();
+      opt.step();
+      if (step == 0) loss.copy_to_host(&first);
+      if (step == Steps - 1) loss.copy_to_host(&last);
+    }
+    std::printf("  variant %d: first %.5f final %.6f\n", variant, first, last);
+    check(first > 1.5f && first < 4.0f, "initial loss near log(8)");
+    check(last < 0.05f, "final loss < 0.05");
+    finals.push_back(last);
+  }
+  check(finals[0] == finals[1], "checkpointing leaves the loss bits unchanged");
+  check(finals[0] == finals[2], "offloaded AdamW leaves the loss bits unchanged");
+}
+
+// reference test_integration_kvcache.cpp:57-123 on a tiny random model
+void kv_cache_equivalences(TinyCfg c) {
+  std::mt19937 rng(7);
+  nn::Model m = build_tiny(c, rng, /*grad=*/false);
+  const int64_t T = 12;
+  std::vector<int64_t> hids(T);
+  for (int64_t i = 0; i < T; ++i) hids[i] = (3 * i + 1) % c.V;
+  Tensor ids = Tensor::from_host(hids.data(), {1, T}, DType::kInt64, kHIP0);
+  const std::vector<float> full = host(m.forward(ids));
+  {
+    nn::KVCache cache = nn::KVCache::allocate(c.L, c.Hk, c.Dh, 1, T + 8, kHIP0);
+    const std::vector<float> with = host(m.forward(ids, &cache, 0));
+    check(max_abs_diff(full, with) < 5e-5, "prefill with cache == without");
+    check(cache.current_len == T, "current_len after prefill");
+  }
+  nn::KVCache cache = nn::KVCache::allocate(c.L, c.Hk, c.Dh, 1, T + 4, kHIP0);
+  Tensor prefix = Tensor::from_host(hids.data(), {1, T - 3}, DType::kInt64, kHIP0);
+  (void)m.forward(prefix, &cache, 0);
+  for (int64_t t = T - 3; t < T; ++t) {
+    Tensor one = Tensor::from_host(&hids[t], {1, 1}, DType::kInt64, kHIP0);
+    const std::vector<float> step = host(m.forward(one, &cache, static_cast<int>(t)));
+    std::vector<float> row(full.begin() + t * c.V, full.begin() + (t + 1) * c.V);
+    check(max_abs_diff(step, row) < 5e-4, "decode step == full-sequence row");
+    check(cache.current_len == t + 1, "current_len after decode");
+  }
+}
+
+}  // namespace
+
+int main() {
+  run("ModelTrain.TrainLogitsMatchInferenceLogits",
+      [] { train_logits_match_inference_logits(TinyCfg{}); });
+  run("ModelTrain.TrainLogitsMatchInferenceLogits_D64",
+      [] { train_logits_match_inference_logits(TinyCfg{32, 128, 2, 1, 64, 64, 2, 1e-5f, 1e4f}); });
+  run("ModelTrain.OverfitsTinyBatch", [] { overfits_tiny_batch(); });
+  run("Integration.KVCacheEquivalences", [] { kv_cache_equivalences(TinyCfg{}); });
+  run("Integration.KVCacheEquivalences_D64",
+      [] { kv_cache_equivalences(TinyCfg{32, 128, 2, 1, 64, 64, 2, 1e-5f, 1e4f}); });
+  std::printf("%d failure(s)\n", g_failed);
+  return g_failed;
+}
