@@ -266,6 +266,7 @@ def main():
              "NN": "gemm_f32_dma<A K-contig, B N-contig> (dX, NN)",
              "TN": "gemm_f32_dma<A M-contig, B N-contig> (dW, TN)",
              "TT": "gemm_f32_dma<A M-contig, B K-contig> (TT)"}
+    attn = {k: prof.pop(k) for k in ("attn_fwd", "attn_bwd")}
     dom = max(prof, key=lambda k: prof[k].total_ms)
     p = prof[dom]
     per_launch_flops = p.flops / max(p.launches, 1)
@@ -314,6 +315,16 @@ def main():
                          round(all_fl / (all_ms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)
                          if all_ms else None,
                      "ms_per_step": round(all_ms / args.steps, 2)},
+        "attention": {
+            k: {"launches": a.launches, "ms_per_step": round(a.total_ms / args.steps, 2),
+                "avg_launch_ms": round(a.total_ms / max(a.launches, 1), 4),
+                "tflops": round(a.flops / (a.total_ms / 1e3) / 1e12, 2) if a.total_ms else None,
+                "frac_of_fp32_mfma_peak":
+                    round(a.flops / (a.total_ms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)
+                    if a.total_ms else None,
+                "executed_tflops": round(a.flops * (1.0 if k == "attn_fwd" else 1.75)
+                                         / (a.total_ms / 1e3) / 1e12, 2) if a.total_ms else None}
+            for k, a in attn.items()},
         "roofline": {"kernel": kname[dom], "bound": "mfma", "achieved": round(achieved, 2),
                      "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),

@@ -467,6 +467,14 @@ AttnDims attn_dims(const Tensor& q, const Tensor& k, const Tensor& v) {
   return d;
 }
 
+// Algorithmic FLOPs of the causal forward: S = Q K^T and O = P V over the
+// T(T+1)/2 visible (query, key) pairs.  The backward's four products (dV,
+// dP, dQ, dK) are twice this; the kernels execute 3.5x (S and dP are
+// recomputed in both backward kernels).
+double attn_fwd_flops(const AttnDims& d) {
+  return 4.0 * static_cast<double>(d.B) * d.H * d.D * (static_cast<double>(d.T) * (d.T + 1) / 2);
+}
+
 struct CausalAttentionBackward : autograd::Node {
   Tensor q, k, v, o, lse;
   float scale = 1.0f;
@@ -479,8 +487,10 @@ struct CausalAttentionBackward : autograd::Node {
     Tensor dq = empty_like(q), dk = empty_like(k), dv = empty_like(v);
     const size_t wsb = ember_attn_bwd_workspace_bytes(d.B, d.T, d.H);
     Tensor ws = workspace(wsb);
+    void* ev = runtime::gemm_profile_begin();
     CTD_CHECK(ember_attn_bwd(cfp(q), cfp(k), cfp(v), cfp(o), cfp(lse), cfp(dout), fp(dq), fp(dk),
                              fp(dv), d.B, d.T, d.H, d.Hk, d.D, scale, ws.data_ptr(), wsb, S()));
+    runtime::gemm_profile_end(ev, 2.0 * attn_fwd_flops(d), runtime::kProfileAttnBwd);
     q = k = v = o = lse = Tensor{};
     return {dq, dk, dv};
   }
@@ -493,8 +503,10 @@ Tensor causal_attention_impl(const Tensor& q, const Tensor& k, const Tensor& v, 
   const AttnDims d = attn_dims(q, k, v);
   Tensor o = empty_like(q);
   Tensor lse = Tensor::empty({d.B, d.H, d.T}, DType::kFloat32, q.device());
+  void* ev = runtime::gemm_profile_begin();
   CTD_CHECK(ember_attn_fwd(cfp(q), cfp(k), cfp(v), fp(o), fp(lse), d.B, d.T, d.H, d.Hk, d.D,
                            scale, S()));
+  runtime::gemm_profile_end(ev, attn_fwd_flops(d), runtime::kProfileAttnFwd);
   if (lse_out) *lse_out = lse;
   return o;
 }

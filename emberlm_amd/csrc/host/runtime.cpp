@@ -158,14 +158,14 @@ void gemm_profile_end(void* begin, double flops, int variant) {
   check(ember_event_record(e, compute_stream()), "gemm profiler record");
   p.spans.emplace_back(begin, e);
   p.flops.push_back(flops);
-  p.variant.push_back(variant & 3);
+  p.variant.push_back(variant >= 0 && variant < kProfileVariants ? variant : 0);
 }
 
 void gemm_profile_collect(int64_t* launches, double* flops, double* total_ms) {
   auto& p = prof();
   std::lock_guard<std::mutex> lk(p.mu);
   synchronize();
-  for (int v = 0; v < 4; ++v) {
+  for (int v = 0; v < kProfileVariants; ++v) {
     launches[v] = 0;
     flops[v] = 0.0;
     total_ms[v] = 0.0;

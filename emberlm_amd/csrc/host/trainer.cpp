@@ -515,10 +515,10 @@ int ctd_gemm_profile_enable(int32_t on) {
 
 int ctd_gemm_profile_collect(ctd_gemm_profile* out) {
   return guarded([&] {
-    int64_t l[4];
-    double f[4], ms[4];
+    int64_t l[runtime::kProfileVariants];
+    double f[runtime::kProfileVariants], ms[runtime::kProfileVariants];
     runtime::gemm_profile_collect(l, f, ms);
-    for (int v = 0; v < 4; ++v) out[v] = ctd_gemm_profile{l[v], f[v], ms[v]};
+    for (int v = 0; v < runtime::kProfileVariants; ++v) out[v] = ctd_gemm_profile{l[v], f[v], ms[v]};
   });
 }
 

@@ -157,9 +157,9 @@ def gemm_profile(enable=None):
     if enable is not None:
         _ck(lib().ctd_gemm_profile_enable(int(enable)), "gemm_profile_enable")
         return None
-    g = (GemmProfile * 4)()
+    g = (GemmProfile * 6)()
     _ck(lib().ctd_gemm_profile_collect(g), "gemm_profile_collect")
-    return {name: g[i] for i, name in enumerate(("NN", "NT", "TN", "TT"))}
+    return {name: g[i] for i, name in enumerate(("NN", "NT", "TN", "TT", "attn_fwd", "attn_bwd"))}
 
 
 class Trainer:

@@ -46,10 +46,14 @@ bool device_available();
 void gemm_profile_enable(bool on);
 bool gemm_profiling();
 void* gemm_profile_begin();                     // null when disabled
-// variant = 2*transa + transb of the launch (which kernel instantiation ran).
+// variant of the launch: 2*transa + transb for a GEMM (which kernel
+// instantiation ran), kProfileAttnFwd / kProfileAttnBwd for fused attention.
 void gemm_profile_end(void* begin, double flops, int variant);
+constexpr int kProfileAttnFwd = 4;
+constexpr int kProfileAttnBwd = 5;
+constexpr int kProfileVariants = 6;
 // Resolves the recorded events (synchronises) and resets the record; the
-// arrays have 4 entries, one per variant.
+// arrays have kProfileVariants entries, one per variant.
 void gemm_profile_collect(int64_t* launches, double* flops, double* total_ms);
 
 }  // namespace ctd::runtime

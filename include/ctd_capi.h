@@ -115,10 +115,11 @@ int ctd_trainer_synchronize(ctd_trainer_t t);
 int ctd_memory_stats(ctd_memory* out);
 int ctd_reset_peak_memory(void);
 
-/* GEMM timing: while enabled, every ember_gemm_f32 launched by the ops layer
- * is bracketed by HIP events on the compute stream; collect resolves them
- * into out[4], indexed by 2*transa + transb (one entry per kernel
- * instantiation: NN, NT, TN, TT). */
+/* Kernel timing: while enabled, every ember_gemm_f32 and fused-attention call
+ * launched by the ops layer is bracketed by HIP events on the compute stream;
+ * collect resolves them into out[6]: [0..3] GEMMs indexed by 2*transa + transb
+ * (one entry per kernel instantiation: NN, NT, TN, TT), [4] attention forward,
+ * [5] attention backward (flops: the algorithmic count, no recompute). */
 int ctd_gemm_profile_enable(int32_t on);
 int ctd_gemm_profile_collect(ctd_gemm_profile* out);
 
