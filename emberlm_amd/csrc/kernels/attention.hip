@@ -1,4 +1,4 @@
-// Fused causal GQA attention, forward and backward, on fp32 MFMA (32x32x2).
+// Fused causal GQA attention, forward and backward, on fp32 MFMA.
 //
 // Replaces the reference's materialised chain (include/ctd/nn/attention.h:100-143):
 // repeat_kv_heads + permute (x3), bmm(Q,K^T), mul_scalar(1/sqrt(D)),
@@ -9,9 +9,11 @@
 //
 // Layout: q, o, dq [B,T,H,D]; k, v, dk, dv [B,T,Hk,D]; lse, delta [B,H,T].
 //
-// MFMA fragment conventions (v_mfma_f32_32x32x2_f32, wave64): A operand lane
-// (g = lane/32, r = lane%32) holds A[m=r][k=g]; B operand holds B[k=g][n=r];
-// accumulator register e holds C[m = 8*(e/4) + 4*g + (e%4)][n = r].
+// MFMA fragment conventions (wave64).  v_mfma_f32_32x32x2_f32 (forward): A
+// operand lane (g = lane/32, r = lane%32) holds A[m=r][k=g]; B operand holds
+// B[k=g][n=r]; accumulator register e holds C[m = 8*(e/4) + 4*g + (e%4)][n = r].
+// v_mfma_f32_16x16x4_f32 (backward): lane (g = lane/16, i = lane%16) holds
+// A[m=i][k=g] and B[k=g][n=i]; accumulator register e holds C[m = 4*g + e][n = i].
 //
 // Forward, per wave of 32 queries: S^T = K Q^T puts the query index in the
 // lane (n = r), so the online-softmax statistics of a query live in one lane
@@ -25,13 +27,15 @@
 //
 // Backward (no atomics, so dK/dV/dQ are bitwise reproducible):
 //   attn_delta:  delta = rowsum(dO * O);
-//   attn_bwd_dq: per 32 queries, S^T = K Q^T and dP^T = V dO^T, then
+//   attn_bwd_dq: per 16 queries, S^T = K Q^T and dP^T = V dO^T, then
 //                dQ^T += K^T dS^T (same orientation as the forward);
-//   attn_bwd_dkdv: per 32 keys, S = Q K^T and dP = dO V^T put the key in the
+//   attn_bwd_dkdv: per 16 keys, S = Q K^T and dP = dO V^T put the key in the
 //                lane, so dV^T += dO^T P and dK^T += Q^T dS accumulate in
 //                registers across every query tile and every query head of
 //                the KV head's group, in a fixed order.
-// Both backward kernels double-buffer their streamed tiles the same way.
+// Both backward kernels run on 16x16x4 MFMA tiles (64 rows per workgroup,
+// two waves per SIMD at D = 128; 32x32x2 tiles need more than 256 registers
+// per lane there) and double-buffer their streamed tiles the same way.
 #include "common.h"
 
 using namespace ember;
@@ -307,21 +311,34 @@ __global__ __launch_bounds__(kThreads) void attn_delta_kernel(const float* __res
   }
 }
 
+__device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// dQ on 16x16x4 MFMA tiles (lane l: A[l%16][l/16], B[l/16][l%16],
+// accumulator e = C[4*(l/16) + e][l%16]).  A wave owns 16 queries, a
+// workgroup 64.  Per 32-key tile (halves kt of 16 keys):
+//   S^T = K Q^T and dP^T = V dO^T (m = key, n = query): MFMA step 4t+j
+//   contracts over d = 16t + 4g + j, so each K / V fragment is one b128 LDS
+//   read and the Q / dO rows sit in registers in the matching order;
+//   dS^T comes out with the query in the lane and keys 16kt + 4g + e in the
+//   registers, which is the B operand of dQ^T += K^T dS^T (m = d, contraction
+//   over the 4 keys {16kt + 4g + e : g}); its A operand is one b32 LDS read.
+// The query's lse and delta are per-lane scalars.
 template <int D>
 struct DqCfg {
-  static constexpr int kBQ = 128, kBK = 32, kKS = D + 4, kVS = D + 4, kOS = D + 4;
-  static constexpr int kBuf = kBK * (kKS + kVS);
-  static constexpr int kOut = kBQ * kOS;
-  static constexpr int kSmem = 2 * kBuf > kOut ? 2 * kBuf : kOut;
+  static constexpr int kBQ = 64, kBK = 32, kKS = D + 4;
+  static constexpr int kBuf = 2 * kBK * kKS;  // one K+V stage
+  static constexpr int kSmem = 2 * kBuf;
 };
 
 template <int D>
-__global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
+__global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta,
     float* __restrict__ dq, int T, int H, int Hk, float scale_log2, float scale) {
   using C = DqCfg<D>;
-  constexpr int HALF = D / 2, NDT = D / 32;
+  constexpr int NT = D / 16;  // d tiles; float4 groups of a lane's Q/dO row
   __shared__ __attribute__((aligned(16))) float smem[C::kSmem];
 
   const int nqb = (T + C::kBQ - 1) / C::kBQ;
@@ -329,23 +346,33 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
   const int qb = nqb - 1 - wi.tile;  // longest rows first
   const int h = wi.row % H, b = wi.row / H;
   const int hk = h / (H / Hk);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 5, r = lane & 31;
-  const int q0 = qb * C::kBQ, qw0 = q0 + 32 * w, myq = qw0 + r;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, i = lane & 15;
+  const int q0 = qb * C::kBQ, qw0 = q0 + 16 * w, myq = qw0 + i;
   const int64_t qs = static_cast<int64_t>(H) * D, ks = static_cast<int64_t>(Hk) * D;
   const int64_t qoff = static_cast<int64_t>(b) * T * qs + static_cast<int64_t>(h) * D;
   const float* kbase = k + static_cast<int64_t>(b) * T * ks + static_cast<int64_t>(hk) * D;
   const float* vbase = v + static_cast<int64_t>(b) * T * ks + static_cast<int64_t>(hk) * D;
 
-  float qreg[HALF], doreg[HALF];
-  load_half<HALF>(qreg, q + qoff, qs, myq, T, HALF * g, scale_log2);
-  load_half<HALF>(doreg, dout + qoff, qs, myq, T, HALF * g, 1.0f);
+  f32x4 qreg[NT], doreg[NT];
+  if (myq < T) {
+    const f32x4* qr = reinterpret_cast<const f32x4*>(q + qoff + myq * qs);
+    const f32x4* dr = reinterpret_cast<const f32x4*>(dout + qoff + myq * qs);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      qreg[t] = qr[4 * t + g] * scale_log2;
+      doreg[t] = dr[4 * t + g];
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) qreg[t] = doreg[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
   const int64_t srow = (static_cast<int64_t>(b) * H + h) * T;
   const float lse2 = myq < T ? lse[srow + myq] * kLog2e : 0.f;
   const float dlt = myq < T ? delta[srow + myq] : 0.f;
 
-  f32x16 acc[NDT];
+  f32x4 acc[NT];
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) zero16(acc[dt]);
+  for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int kend = min(T, q0 + C::kBQ);
   const int nkb = (kend + C::kBK - 1) / C::kBK;
@@ -353,7 +380,7 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
   tk.load(kbase, ks, T);
   tv.load(vbase, ks, T);
   tk.store(smem, C::kKS);
-  tv.store(smem + C::kBK * C::kKS, C::kVS);
+  tv.store(smem + C::kBK * C::kKS, C::kKS);
   __syncthreads();
 
   for (int kb = 0; kb < nkb; ++kb) {
@@ -365,84 +392,113 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dq_kernel(
     }
     const float* Ks = smem + (kb & 1) * C::kBuf;
     const float* Vs = Ks + C::kBK * C::kKS;
-    if (k0 <= qw0 + 31) {
-      f32x16 s, dp;
-      zero16(s);
-      zero16(dp);
+    if (k0 <= qw0 + 15) {  // some key of the tile is seen by some query of this wave
+      f32x4 s[2], dp[2];
 #pragma unroll
-      for (int s4 = 0; s4 < HALF / 4; ++s4) {
-        const f32x4 kf = *reinterpret_cast<const f32x4*>(Ks + r * C::kKS + HALF * g + 4 * s4);
-        const f32x4 vf = *reinterpret_cast<const f32x4*>(Vs + r * C::kVS + HALF * g + 4 * s4);
+      for (int kt = 0; kt < 2; ++kt) s[kt] = dp[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          s = mfma32(kf[j], qreg[4 * s4 + j], s);
-          dp = mfma32(vf[j], doreg[4 * s4 + j], dp);
+      for (int t = 0; t < NT; ++t) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+          const f32x4 kf =
+              *reinterpret_cast<const f32x4*>(Ks + (16 * kt + i) * C::kKS + 16 * t + 4 * g);
+          const f32x4 vf =
+              *reinterpret_cast<const f32x4*>(Vs + (16 * kt + i) * C::kKS + 16 * t + 4 * g);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            s[kt] = mfma16(kf[j], qreg[t][j], s[kt]);
+            dp[kt] = mfma16(vf[j], doreg[t][j], dp[kt]);
+          }
         }
       }
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int key = k0 + acc_row(e, g);
-        const float p = (key > myq || key >= T) ? 0.f : fast_exp2(s[e] - lse2);
-        s[e] = p * (dp[e] - dlt);
-      }
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const auto kv = *reinterpret_cast<const typename DVec<NDT>::T*>(
-            Ks + acc_row(e, g) * C::kKS + NDT * r);
+        for (int e = 0; e < 4; ++e) {
+          const int key = k0 + 16 * kt + 4 * g + e;
+          const float p = (key > myq || key >= T) ? 0.f : fast_exp2(s[kt][e] - lse2);
+          s[kt][e] = p * (dp[kt][e] - dlt);
+        }
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) acc[dt] = mfma32(kv[dt], s[e], acc[dt]);
-      }
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = (16 * kt + 4 * g + e) * C::kKS;
+#pragma unroll
+          for (int t = 0; t < NT; ++t) acc[t] = mfma16(Ks[row + 16 * t + i], s[kt][e], acc[t]);
+        }
     }
     if (more) {
       float* nb = smem + ((kb + 1) & 1) * C::kBuf;
       tk.store(nb, C::kKS);
-      tv.store(nb + C::kBK * C::kKS, C::kVS);
+      tv.store(nb + C::kBK * C::kKS, C::kKS);
     }
     __syncthreads();
   }
 
-  acc_to_rows<NDT>(smem, C::kOS, acc, w, g, r, scale);
-  __syncthreads();
-  unstage_rows<D>(smem, C::kOS, dq + qoff + static_cast<int64_t>(q0) * qs, qs, C::kBQ, T - q0);
+  // Accumulator tile t, lane (g, i), register e holds d = 16t + 4g + e of query i.
+  if (myq < T) {
+    f32x4* dqr = reinterpret_cast<f32x4*>(dq + qoff + myq * qs);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) dqr[4 * t + g] = acc[t] * scale;
+  }
 }
 
+// dK/dV on 16x16x4 MFMA tiles.  A wave owns 16 keys, a workgroup 64, so a
+// wave holds half the accumulators and half the K/V registers that 32 keys
+// on 32x32x2 tiles would need (those spill past 256 VGPRs into AGPRs at
+// D = 128, one wave per SIMD): two waves fit on a SIMD, and one wave's
+// softmax section and barrier waits run under the other's MFMAs.  Per
+// 32-query tile:
+//   S = Q K^T and dP = dO V^T (m = query, n = key): MFMA step 4t+j contracts
+//   over d = 16t + 4g + j, so each Q / dO fragment is one b128 LDS read and
+//   the K / V rows sit in registers in the matching order;
+//   P and dS come out with the key in the lane (n = l%16) and queries
+//   16mt + 4g + e in the registers, which is exactly the B operand of
+//   dV^T += dO^T P and dK^T += Q^T dS (m = d, n = key, contraction over the
+//   4 queries {16mt + 4g + e : g}); their A operand is one b32 LDS read.
 template <int D>
 struct DkvCfg {
-  static constexpr int kBKeys = 128, kBQ = 32, kQS = D + 4, kOS = D + 4;
+  static constexpr int kBKeys = 64, kBQ = 32, kQS = D + 4;
   static constexpr int kBuf = 2 * kBQ * kQS + 2 * kBQ;  // Q, dO, lse, delta
-  static constexpr int kOut = kBKeys * kOS;
-  static constexpr int kSmem = 2 * kBuf > kOut ? 2 * kBuf : kOut;
+  static constexpr int kSmem = 2 * kBuf;
 };
 
 template <int D>
-__global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(
+__global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta,
     float* __restrict__ dk, float* __restrict__ dv, int T, int H, int Hk, float scale_log2,
     float scale) {
   using C = DkvCfg<D>;
-  constexpr int HALF = D / 2, NDT = D / 32;
+  constexpr int NT = D / 16;  // d tiles; float4 groups of a lane's K/V row
   __shared__ __attribute__((aligned(16))) float smem[C::kSmem];
 
   const WorkItem wi = work_item((T + C::kBKeys - 1) / C::kBKeys);
   const int kb = wi.tile;  // small key blocks see the most queries: launched first
   const int hk = wi.row % Hk, b = wi.row / Hk;
   const int group = H / Hk;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 5, r = lane & 31;
-  const int key0 = kb * C::kBKeys, kw0 = key0 + 32 * w, mykey = kw0 + r;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, i = lane & 15;
+  const int key0 = kb * C::kBKeys, kw0 = key0 + 16 * w, mykey = kw0 + i;
   const int64_t qs = static_cast<int64_t>(H) * D, ks = static_cast<int64_t>(Hk) * D;
   const int64_t koff = static_cast<int64_t>(b) * T * ks + static_cast<int64_t>(hk) * D;
 
-  float kreg[HALF], vreg[HALF];
-  load_half<HALF>(kreg, k + koff, ks, mykey, T, HALF * g, scale_log2);
-  load_half<HALF>(vreg, v + koff, ks, mykey, T, HALF * g, 1.0f);
-
-  f32x16 adk[NDT], adv[NDT];
+  f32x4 kreg[NT], vreg[NT];
+  if (mykey < T) {
+    const f32x4* kr = reinterpret_cast<const f32x4*>(k + koff + mykey * ks);
+    const f32x4* vr = reinterpret_cast<const f32x4*>(v + koff + mykey * ks);
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) {
-    zero16(adk[dt]);
-    zero16(adv[dt]);
+    for (int t = 0; t < NT; ++t) {
+      kreg[t] = kr[4 * t + g] * scale_log2;
+      vreg[t] = vr[4 * t + g];
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) kreg[t] = vreg[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  f32x4 adk[NT], adv[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) adk[t] = adv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // The streamed sequence: for each query head of the group, the query tiles
   // key0, key0 + 32, ... below T.
@@ -484,60 +540,69 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_dkdv_kernel(
     const float* Ds = Qs + C::kBQ * C::kQS;
     const float* Ls = Qs + 2 * C::kBQ * C::kQS;
     const float* Es = Ls + C::kBQ;
-    if (qt0 + C::kBQ - 1 >= kw0) {
-      f32x16 s, dp;
-      zero16(s);
-      zero16(dp);
+    if (qt0 + C::kBQ - 1 >= kw0) {  // some query of the tile sees some key of this wave
+      f32x4 s[2], dp[2];
 #pragma unroll
-      for (int s4 = 0; s4 < HALF / 4; ++s4) {
-        const f32x4 qf = *reinterpret_cast<const f32x4*>(Qs + r * C::kQS + HALF * g + 4 * s4);
-        const f32x4 of = *reinterpret_cast<const f32x4*>(Ds + r * C::kQS + HALF * g + 4 * s4);
+      for (int mt = 0; mt < 2; ++mt) s[mt] = dp[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          s = mfma32(qf[j], kreg[4 * s4 + j], s);
-          dp = mfma32(of[j], vreg[4 * s4 + j], dp);
+      for (int t = 0; t < NT; ++t) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          const f32x4 qf =
+              *reinterpret_cast<const f32x4*>(Qs + (16 * mt + i) * C::kQS + 16 * t + 4 * g);
+          const f32x4 of =
+              *reinterpret_cast<const f32x4*>(Ds + (16 * mt + i) * C::kQS + 16 * t + 4 * g);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            s[mt] = mfma16(qf[j], kreg[t][j], s[mt]);
+            dp[mt] = mfma16(of[j], vreg[t][j], dp[mt]);
+          }
         }
       }
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int ql = acc_row(e, g);
-        const int qq = qt0 + ql;
-        const float p = (qq < mykey || qq >= T) ? 0.f : fast_exp2(s[e] - Ls[ql]);
-        s[e] = p;
-        dp[e] = p * (dp[e] - Es[ql]);
-      }
+      for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int ql = acc_row(e, g);
-        const auto ov = *reinterpret_cast<const typename DVec<NDT>::T*>(Ds + ql * C::kQS + NDT * r);
-        const auto qv = *reinterpret_cast<const typename DVec<NDT>::T*>(Qs + ql * C::kQS + NDT * r);
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          adv[dt] = mfma32(ov[dt], s[e], adv[dt]);
-          adk[dt] = mfma32(qv[dt], dp[e], adk[dt]);
+        for (int e = 0; e < 4; ++e) {
+          const int ql = 16 * mt + 4 * g + e;
+          const int qq = qt0 + ql;
+          const float p = (qq < mykey || qq >= T) ? 0.f : fast_exp2(s[mt][e] - Ls[ql]);
+          s[mt][e] = p;
+          dp[mt][e] = p * (dp[mt][e] - Es[ql]);
         }
-      }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = (16 * mt + 4 * g + e) * C::kQS;
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            adv[t] = mfma16(Ds[row + 16 * t + i], s[mt][e], adv[t]);
+            adk[t] = mfma16(Qs[row + 16 * t + i], dp[mt][e], adk[t]);
+          }
+        }
     }
     if (more) commit(smem + ((step + 1) & 1) * C::kBuf);
     __syncthreads();
   }
 
-  acc_to_rows<NDT>(smem, C::kOS, adk, w, g, r, scale);
-  __syncthreads();
-  unstage_rows<D>(smem, C::kOS, dk + koff + static_cast<int64_t>(key0) * ks, ks, C::kBKeys,
-                  T - key0);
-  __syncthreads();
-  acc_to_rows<NDT>(smem, C::kOS, adv, w, g, r, 1.0f);
-  __syncthreads();
-  unstage_rows<D>(smem, C::kOS, dv + koff + static_cast<int64_t>(key0) * ks, ks, C::kBKeys,
-                  T - key0);
+  // Accumulator tile t, lane (g, i), register e holds d = 16t + 4g + e of key i.
+  if (mykey < T) {
+    f32x4* dkr = reinterpret_cast<f32x4*>(dk + koff + mykey * ks);
+    f32x4* dvr = reinterpret_cast<f32x4*>(dv + koff + mykey * ks);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      dkr[4 * t + g] = adk[t] * scale;
+      dvr[4 * t + g] = adv[t];
+    }
+  }
 }
 
 int check_shapes(int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D) {
   if (B < 0 || T < 0 || H <= 0 || Hk <= 0 || H % Hk != 0) return EMBER_EINVAL;
   if (D != 64 && D != 128) return EMBER_EINVAL;
   if (T > 0x7fffffff / 2 || H > 65535 || Hk > 65535 || B > 65535) return EMBER_EINVAL;
-  if ((T + 127) / 128 * H * B > 0x7fffffff) return EMBER_EINVAL;  // 1-D grid
+  // 1-D grids: 128-query forward tiles, 64-row backward tiles, Hk <= H.
+  if ((T + 63) / 64 * H * B > 0x7fffffff) return EMBER_EINVAL;
   return EMBER_OK;
 }
 
@@ -584,8 +649,10 @@ extern "C" int ember_attn_bwd(const float* q, const float* k, const float* v, co
   const int64_t rows = B * T * H;
   const int Ti = static_cast<int>(T), Hi = static_cast<int>(H), Hki = static_cast<int>(Hk);
   const float sl = scale * kLog2e;
-  const dim3 gq(static_cast<unsigned>((T + 127) / 128 * H * B));
-  const dim3 gk(static_cast<unsigned>((T + 127) / 128 * Hk * B));
+  static_assert(DqCfg<64>::kBQ == 64 && DqCfg<128>::kBQ == 64, "dQ grid assumes 64 queries");
+  static_assert(DkvCfg<64>::kBKeys == 64 && DkvCfg<128>::kBKeys == 64, "dK/dV grid assumes 64 keys");
+  const dim3 gq(static_cast<unsigned>((T + 63) / 64 * H * B));
+  const dim3 gk(static_cast<unsigned>((T + 63) / 64 * Hk * B));
   if (D == 64) {
     attn_delta_kernel<64><<<static_cast<unsigned>((rows + 15) / 16), kThreads, 0, st>>>(
         o, dout, delta, rows, Ti, Hi);
