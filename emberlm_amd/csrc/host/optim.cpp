@@ -38,10 +38,14 @@ namespace ctd::optim {
 using namespace ctd::ops::detail;
 
 namespace {
-// Workgroups of one chunk update: one per CU.  A chunk is 448 MB of HBM
-// traffic per 2.6 ms of link time, far below what 256 resident workgroups
-// stream, and they fit next to the forward's GEMM blocks.
-constexpr int kUpdateBlocks = 256;
+// Workgroups of one chunk update: four per CU, of the 22-register scalar
+// form, so they fit next to the forward's GEMM and attention blocks.  The
+// update runs on the d2h stream between a chunk's arrival and its copy out,
+// so its length adds to the link's idle time: one workgroup per CU (one load
+// in flight per lane) took 307 ms for the isolated offloaded step of a
+// 1.7B-parameter model, four per CU 297 ms, the same as four times the loads
+// in flight per lane (unrolled or float4) at one or two per CU.
+constexpr int kUpdateBlocks = 1024;
 }  // namespace
 
 AdamW::AdamW(std::vector<Tensor> params, float lr, float weight_decay, float beta1, float beta2,
