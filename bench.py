@@ -178,6 +178,9 @@ def main():
                     help="launch one ember_scale over 1 GiB (reads 1 GiB, writes 1 GiB) first: "
                          "the known-size copy that calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE")
     ap.add_argument("--max-norm", type=float, default=1.0)
+    ap.add_argument("--prefetch-chunks", type=int, default=None,
+                    help="cap of the optimizer state the backward stages for the offloaded "
+                         "step (library default when omitted; 0 turns it off)")
     ap.add_argument("--decode-tokens", type=int, default=64,
                     help="tokens generated per inference measurement (0: skip)")
     ap.add_argument("--decode-only", action="store_true",
@@ -226,6 +229,8 @@ def main():
     tr = TR.Trainer(cfg, seed=0, init_std=0.02, norm_value=1.0)
     tr.set_checkpointing(ckpt)
     tr.make_optimizer(lr=1e-4, weight_decay=0.1, beta1=0.9, beta2=0.95, eps=1e-8, offload=offload)
+    if args.prefetch_chunks is not None:
+        tr.set_prefetch_chunks(args.prefetch_chunks)
     tr.synthetic_batch(B, T, seed=0, masked=masked)
     log(f"[bench] setup {time.time() - t0:.1f}s")
 
@@ -250,6 +255,10 @@ def main():
     TR.gemm_profile(False)
     prof = TR.gemm_profile()
     mem = TR.memory()
+    # m/v of the leading chunks that the last timed step's backward had already
+    # staged on the device (AdamW::prefetch): they cross host->device before
+    # the step's transfer window, so that window's rate is the device->host one.
+    prefetched = tr.offload_stats()[2] if offload else 0.0
 
     ms_step = wall / args.steps * 1e3
     tokens = B * T
@@ -308,6 +317,7 @@ def main():
                     "optimizer_phase_gbps_per_direction":
                         round(bytes_dir / (opt_ms / 1e3) / 1e9, 2) if offload and opt_ms > 0 else None,
                     "overlapped_with_next_forward": bool(offload),
+                    "prefetched_bytes_per_direction": prefetched,
                     "pcie_gen5_x16_gbps": PCIE_GEN5_X16_GBPS},
         "gemm_all": {"launches": sum(v.launches for v in prof.values()),
                      "tflops": round(all_fl / (all_ms / 1e3) / 1e12, 2) if all_ms else None,
@@ -344,7 +354,7 @@ def main():
         tr.synchronize()
         tr.opt_step()
         tr.zero_grad()
-        iso_ms, iso_bytes = tr.offload_stats()
+        iso_ms, iso_bytes, _ = tr.offload_stats()
         gbps = iso_bytes / (iso_ms / 1e3) / 1e9 if iso_ms > 0 else 0.0
         result["offload"]["isolated_step_ms"] = round(iso_ms, 2)
         result["offload"]["isolated_gbps_per_direction"] = round(gbps, 2)

@@ -156,9 +156,18 @@ namespace {
 // embedding -> blocks (checkpointed when enabled) -> final RMSNorm: [B, T, H].
 Tensor train_hidden(const Model& m, const Tensor& input_ids) {
   Tensor h = m.embed_tokens.forward(input_ids);
-  for (const auto& layer : m.layers) {
+  for (size_t i = 0; i < m.layers.size(); ++i) {
+    const TransformerBlock& layer = m.layers[i];
     if (m.gradient_checkpointing) {
-      h = autograd::checkpoint([&layer](const Tensor& x) { return layer.forward_train(x); }, h);
+      // checkpoint() runs fn under no-grad in the forward pass and with grad
+      // enabled when the backward pass re-runs it.
+      const int li = static_cast<int>(i);
+      h = autograd::checkpoint(
+          [&m, &layer, li](const Tensor& x) {
+            if (m.recompute_hook && autograd::is_grad_enabled()) m.recompute_hook(li);
+            return layer.forward_train(x);
+          },
+          h);
     } else {
       h = layer.forward_train(h);
     }

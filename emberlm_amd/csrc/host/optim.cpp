@@ -25,6 +25,13 @@
 // parameters are updated and the remaining transfers hide behind it.  Each
 // gradient stays alive until its parameter's update has run (release_after),
 // since zero_grad() lets go of it while the update may still be reading it.
+//
+// The forward reads the first parameter in streaming order (the embedding)
+// first, and waits for its update.  prefetch(), called late in the backward
+// while the host link is idle, copies the chunks covering that parameter into
+// a device buffer from the caching allocator; step() then runs their updates
+// before any copy, so that parameter is final a few kernels after the
+// backward ends, and copies them out after the ring.
 #include <algorithm>
 #include <chrono>
 #include <cmath>
@@ -66,6 +73,11 @@ AdamW::AdamW(std::vector<ParamGroup> groups, float beta1, float beta2, float eps
 
 AdamW::~AdamW() {
   if (in_flight_ && ev_done_) ember_event_synchronize(ev_done_);
+  // A pending prefetch's copies must land before its buffer goes back to the
+  // allocator.
+  if (pf_elems_ > 0 && ev_pf_loaded_) ember_event_synchronize(ev_pf_loaded_);
+  pf_m_ = Tensor{};
+  pf_v_ = Tensor{};
   runtime::collect_released();
   // Our events die with us: no storage may keep pointing at them.
   for (size_t gi = 0; gi < ev_param_.size(); ++gi)
@@ -88,6 +100,9 @@ AdamW::~AdamW() {
   ember_event_destroy(ev_done_);
   ember_event_destroy(ev_begin_);
   ember_event_destroy(ev_start_);
+  ember_event_destroy(ev_pf_ready_);
+  ember_event_destroy(ev_pf_loaded_);
+  ember_event_destroy(ev_pf_drained_);
 }
 
 Tensor& AdamW::m_tensor(size_t gi, size_t pi) {
@@ -190,6 +205,9 @@ void AdamW::init_offload_state() {
     CTD_CHECK(ember_event_create(&ev_done_));
     CTD_CHECK(ember_event_create(&ev_begin_));
     CTD_CHECK(ember_event_create(&ev_start_));
+    CTD_CHECK(ember_event_create(&ev_pf_ready_));
+    CTD_CHECK(ember_event_create(&ev_pf_loaded_));
+    CTD_CHECK(ember_event_create(&ev_pf_drained_));
   }
   ev_param_.resize(groups_.size());
   for (size_t gi = 0; gi < groups_.size(); ++gi)
@@ -227,6 +245,32 @@ void AdamW::step_ondevice() {
   }
 }
 
+void AdamW::prefetch() {
+  if (!offload_ || max_prefetch_chunks_ <= 0 || pf_elems_ > 0) return;
+  init_offload_state();
+  if (layout_.empty() || flat_n_ <= 0) return;
+  const Segment& first = layout_.front();
+  const int64_t nch = std::min((first.off + first.n + chunk_elems_ - 1) / chunk_elems_,
+                               max_prefetch_chunks_);
+  const int64_t elems = std::min(nch * chunk_elems_, flat_n_);
+  ember_stream_t cs = S(), hs = runtime::h2d_stream();
+  // The buffer comes from the caching allocator, which orders reuse on the
+  // compute stream: the copies wait until that stream has reached this call.
+  // They also wait for the previous step's copies out, which write the host
+  // state read here.
+  pf_m_ = Tensor::empty({elems}, DType::kFloat32, kHIP0);
+  pf_v_ = Tensor::empty({elems}, DType::kFloat32, kHIP0);
+  CTD_CHECK(ember_event_record(ev_pf_ready_, cs));
+  CTD_CHECK(ember_stream_wait_event(hs, ev_pf_ready_));
+  if (in_flight_) CTD_CHECK(ember_stream_wait_event(hs, ev_done_));
+  const size_t nb = static_cast<size_t>(elems) * sizeof(float);
+  CTD_CHECK(ember_memcpy_async(pf_m_.data_ptr(), flat_m_.data_ptr(), nb, 0, hs));
+  CTD_CHECK(ember_memcpy_async(pf_v_.data_ptr(), flat_v_.data_ptr(), nb, 0, hs));
+  CTD_CHECK(ember_event_record(ev_pf_loaded_, hs));
+  pf_elems_ = elems;
+  pf_chunk_elems_ = chunk_elems_;
+}
+
 void AdamW::step_offloaded() {
   const auto t0 = std::chrono::steady_clock::now();
   const float bc1 = 1.0f - std::pow(beta1_, static_cast<float>(step_));
@@ -244,6 +288,18 @@ void AdamW::step_offloaded() {
   CTD_CHECK(ember_event_record(ev_start_, cs));
   CTD_CHECK(ember_stream_wait_event(ds, ev_start_));
   CTD_CHECK(ember_event_record(ev_begin_, hs));
+  // A prefetch cut with another chunk size does not line up with this
+  // step's chunks: let it land and drop it.
+  if (pf_elems_ > 0 && pf_chunk_elems_ != chunk_elems_) {
+    CTD_CHECK(ember_event_synchronize(ev_pf_loaded_));
+    pf_m_ = Tensor{};
+    pf_v_ = Tensor{};
+    pf_elems_ = 0;
+  }
+  const int64_t pf_elems = pf_elems_;
+  float* pf_m = pf_elems > 0 ? static_cast<float*>(pf_m_.data_ptr()) : nullptr;
+  float* pf_v = pf_elems > 0 ? static_cast<float*>(pf_v_.data_ptr()) : nullptr;
+  if (pf_elems > 0) CTD_CHECK(ember_stream_wait_event(ds, ev_pf_loaded_));
 
   // Device pointers of every parameter with a gradient, in layout order
   // (taken before any storage gets this step's ready event).
@@ -264,25 +320,16 @@ void AdamW::step_offloaded() {
   float* hm = static_cast<float*>(flat_m_.data_ptr());
   float* hv = static_cast<float*>(flat_v_.data_ptr());
   size_t k = 0;  // first segment not yet finished
-  int64_t chunk = 0;
-  double bytes = 0.0;
-  for (int64_t c0 = 0; c0 < flat_n_; c0 += chunk_elems_, ++chunk) {
-    const int64_t len = std::min(chunk_elems_, flat_n_ - c0);
-    const size_t nb = static_cast<size_t>(len) * sizeof(float);
-    const int s = static_cast<int>(chunk % kSlots);
-    if (chunk >= kSlots) CTD_CHECK(ember_stream_wait_event(hs, ev_drained_[s]));
-    CTD_CHECK(ember_memcpy_async(d_m_[s], hm + c0, nb, 0, hs));
-    CTD_CHECK(ember_memcpy_async(d_v_[s], hv + c0, nb, 0, hs));
-    CTD_CHECK(ember_event_record(ev_loaded_[s], hs));
-    CTD_CHECK(ember_stream_wait_event(ds, ev_loaded_[s]));
-    // Update every parameter piece inside [c0, c0 + len).
+  // Updates every parameter piece inside [c0, c0 + len), whose m/v sit at
+  // cm/cv on the device, and marks each parameter that ends there as done.
+  auto update_range = [&](int64_t c0, int64_t len, float* cm, float* cv) {
     while (k < layout_.size() && layout_[k].off < c0 + len) {
       const Segment& sg = layout_[k];
       const int64_t lo = std::max(sg.off, c0), hi = std::min(sg.off + sg.n, c0 + len);
       if (work[k].p && hi > lo) {
         const ParamGroup& group = groups_[sg.gi];
         CTD_CHECK(ember_adamw_bounded(work[k].p + (lo - sg.off), work[k].g + (lo - sg.off),
-                                      d_m_[s] + (lo - c0), d_v_[s] + (lo - c0), hi - lo, group.lr,
+                                      cm + (lo - c0), cv + (lo - c0), hi - lo, group.lr,
                                       beta1_, beta2_, eps_, group.weight_decay, bc1, bc2,
                                       kUpdateBlocks, ds));
       }
@@ -297,10 +344,42 @@ void AdamW::step_offloaded() {
       }
       ++k;
     }
+  };
+
+  double bytes_in = 0.0, bytes_out = 0.0;
+  // The prefetched state (a whole number of chunks, or the whole state) is
+  // updated before anything else and copied out after everything else: the
+  // d2h stream runs the updates in streaming order, which is the order the
+  // next forward waits for them, and no copy of it holds back a later one.
+  if (pf_elems > 0) update_range(0, pf_elems, pf_m, pf_v);
+  int64_t ring = 0;  // chunks streamed through the ring so far
+  for (int64_t c0 = pf_elems; c0 < flat_n_; c0 += chunk_elems_, ++ring) {
+    const int64_t len = std::min(chunk_elems_, flat_n_ - c0);
+    const size_t nb = static_cast<size_t>(len) * sizeof(float);
+    const int s = static_cast<int>(ring % kSlots);
+    if (ring >= kSlots) CTD_CHECK(ember_stream_wait_event(hs, ev_drained_[s]));
+    CTD_CHECK(ember_memcpy_async(d_m_[s], hm + c0, nb, 0, hs));
+    CTD_CHECK(ember_memcpy_async(d_v_[s], hv + c0, nb, 0, hs));
+    CTD_CHECK(ember_event_record(ev_loaded_[s], hs));
+    CTD_CHECK(ember_stream_wait_event(ds, ev_loaded_[s]));
+    update_range(c0, len, d_m_[s], d_v_[s]);
     CTD_CHECK(ember_memcpy_async(hm + c0, d_m_[s], nb, 1, ds));
     CTD_CHECK(ember_memcpy_async(hv + c0, d_v_[s], nb, 1, ds));
     CTD_CHECK(ember_event_record(ev_drained_[s], ds));
-    bytes += 2.0 * static_cast<double>(nb);
+    bytes_in += 2.0 * static_cast<double>(nb);
+    bytes_out += 2.0 * static_cast<double>(nb);
+  }
+  if (pf_elems > 0) {
+    // One copy out per buffer, after which it goes back to the allocator.
+    const size_t nb = static_cast<size_t>(pf_elems) * sizeof(float);
+    CTD_CHECK(ember_memcpy_async(hm, pf_m, nb, 1, ds));
+    CTD_CHECK(ember_memcpy_async(hv, pf_v, nb, 1, ds));
+    CTD_CHECK(ember_event_record(ev_pf_drained_, ds));
+    runtime::release_after(ev_pf_drained_, {pf_m_.storage(), pf_v_.storage()});
+    pf_m_ = Tensor{};
+    pf_v_ = Tensor{};
+    pf_elems_ = 0;
+    bytes_out += 2.0 * static_cast<double>(nb);
   }
   CTD_CHECK(ember_event_record(ev_done_, ds));
   // Only now, after the last data_ptr() above: later users of a parameter or
@@ -312,8 +391,9 @@ void AdamW::step_offloaded() {
     p.grad().storage()->set_ready_event(ev_param_[layout_[j].gi][layout_[j].pi]);
   }
   in_flight_ = true;
-  stats_.last_h2d_bytes = bytes;
-  stats_.last_d2h_bytes = bytes;
+  stats_.last_h2d_bytes = bytes_in;
+  stats_.last_d2h_bytes = bytes_out;
+  stats_.last_prefetch_bytes = bytes_out - bytes_in;
   stats_.last_step_ms =
       std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
 }

@@ -353,6 +353,19 @@ int run(const Config& cfg) {
     }
     opt.set_update_order(std::move(order));
   }
+  // The last micro-batch's backward stages the first parameters' optimizer
+  // state while the host link is idle; clearing the hook on the way out keeps
+  // the model from calling into the optimizer after it is gone.
+  bool prefetch_armed = false;
+  struct HookReset {
+    nn::Model& m;
+    ~HookReset() { m.recompute_hook = nullptr; }
+  } hook_reset{model};
+  if (cfg.offload_optimizer) {
+    model.recompute_hook = [&opt, &prefetch_armed](int layer) {
+      if (prefetch_armed && layer == kOptimizerPrefetchLayer) opt.prefetch();
+    };
+  }
 
   int64_t start_step = 0;
   if (resuming) {
@@ -394,7 +407,9 @@ int run(const Config& cfg) {
       if (b.sum_mask <= 0.0f) continue;
       Tensor loss = model.forward_train_masked(b.input_ids, b.targets, b.loss_mask);
       Tensor scaled = ops::mul_scalar(loss, inv_accum);
+      prefetch_armed = micro == cfg.grad_accum_steps - 1;
       scaled.backward();
+      prefetch_armed = false;
       float l = 0.0f;
       loss.copy_to_host(&l);
       accum_loss += static_cast<double>(l) * static_cast<double>(b.sum_mask);

@@ -101,7 +101,11 @@ struct Trainer {
   int64_t B = 0, T = 0;
   float mask_sum = 0.f;
   std::unique_ptr<optim::AdamW> opt;
+  // Set while train_step's backward runs: only then does the model's
+  // recompute hook start the offloaded optimizer's prefetch.
+  bool prefetch_armed = false;
 };
+
 
 // Decay group, then no-decay group: the order ctd_train hands the parameters
 // to clip_grad_norm_ (tools/ctd_train/main.cpp:296-299), which fixes the order
@@ -373,7 +377,13 @@ int ctd_trainer_make_optimizer(ctd_trainer_t t, float lr, float weight_decay, fl
     // Two groups like ctd_train (main.cpp:299-311): decay, then no_decay with wd 0.
     std::vector<optim::ParamGroup> groups{{tr->named.decay, lr, weight_decay},
                                           {tr->named.no_decay, lr, 0.0f}};
+    tr->model.recompute_hook = nullptr;
     tr->opt = std::make_unique<optim::AdamW>(std::move(groups), beta1, beta2, eps, offload != 0);
+    if (offload) {
+      tr->model.recompute_hook = [tr](int layer) {
+        if (tr->prefetch_armed && layer == train::kOptimizerPrefetchLayer) tr->opt->prefetch();
+      };
+    }
     if (chunk_elems > 0) tr->opt->set_offload_chunk(chunk_elems);
     // Stream parameters in model order (collect_parameters), the order in
     // which the forward reads them, so it can overlap the offloaded update.
@@ -420,17 +430,30 @@ int ctd_trainer_get_opt_state(ctd_trainer_t t, int64_t i, float* m, float* v, in
   });
 }
 
-int ctd_trainer_offload_stats(ctd_trainer_t t, double* stream_ms, double* bytes_per_direction) {
+int ctd_trainer_offload_stats(ctd_trainer_t t, double* stream_ms, double* bytes_per_direction,
+                              double* prefetched_bytes) {
   return guarded([&] {
     Trainer* tr = as_trainer(t);
-    double ms = 0.0, b = 0.0;
+    double ms = 0.0, b = 0.0, pf = 0.0;
     if (tr->opt && tr->opt->is_offloaded()) {
       tr->opt->wait_idle();
-      ms = tr->opt->offload_stats().last_stream_ms;
-      b = tr->opt->offload_stats().last_h2d_bytes;
+      const optim::OffloadStats& st = tr->opt->offload_stats();
+      ms = st.last_stream_ms;
+      b = st.last_d2h_bytes;
+      pf = st.last_prefetch_bytes;
     }
     if (stream_ms) *stream_ms = ms;
     if (bytes_per_direction) *bytes_per_direction = b;
+    if (prefetched_bytes) *prefetched_bytes = pf;
+  });
+}
+
+int ctd_trainer_set_prefetch_chunks(ctd_trainer_t t, int64_t chunks) {
+  return guarded([&] {
+    Trainer* tr = as_trainer(t);
+    if (!tr->opt) throw std::runtime_error("no optimizer");
+    if (chunks < 0) throw std::runtime_error("prefetch chunks must be >= 0");
+    tr->opt->set_prefetch_chunks(chunks);
   });
 }
 
@@ -452,7 +475,14 @@ int ctd_trainer_train_step(ctd_trainer_t t, float max_norm, ctd_step_times* time
     CTD_CHECK(ember_event_record(ev[0], cs));
     Tensor loss = tr->model.forward_train_masked(tr->ids, tr->targets, tr->mask);
     CTD_CHECK(ember_event_record(ev[1], cs));
-    loss.backward();
+    {
+      struct Arm {
+        bool& flag;
+        ~Arm() { flag = false; }
+      } arm{tr->prefetch_armed};
+      tr->prefetch_armed = true;
+      loss.backward();
+    }
     CTD_CHECK(ember_event_record(ev[2], cs));
     float gn = 0.f;
     if (max_norm > 0.f) {

@@ -70,7 +70,9 @@ _SIGS = {
     "ctd_trainer_zero_grad": (i32, [vp]),
     "ctd_trainer_get_opt_state": (i32, [vp, i64, fptr, fptr, i64]),
     "ctd_trainer_step_count": (i32, [vp, lptr]),
-    "ctd_trainer_offload_stats": (i32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    "ctd_trainer_offload_stats": (i32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_double),
+                                        C.POINTER(C.c_double)]),
+    "ctd_trainer_set_prefetch_chunks": (i32, [vp, i64]),
     "ctd_trainer_train_step": (i32, [vp, f32, C.POINTER(StepTimes)]),
     "ctd_trainer_synchronize": (i32, [vp]),
     "ctd_memory_stats": (i32, [C.POINTER(Memory)]),
@@ -282,10 +284,19 @@ class Trainer:
         return t
 
     def offload_stats(self):
-        """(stream_ms, bytes_per_direction) of the last offloaded step, after it finished."""
-        ms, b = C.c_double(), C.c_double()
-        _ck(lib().ctd_trainer_offload_stats(self.h, C.byref(ms), C.byref(b)), "offload_stats")
-        return ms.value, b.value
+        """(stream_ms, bytes_per_direction, prefetched_bytes) of the last offloaded
+        step, after it finished: its device time from first copy in to last copy
+        out, the m/v bytes it moved per direction, and how many of those a
+        prefetch during train_step's backward had copied in before the step."""
+        ms, b, pf = C.c_double(), C.c_double(), C.c_double()
+        _ck(lib().ctd_trainer_offload_stats(self.h, C.byref(ms), C.byref(b), C.byref(pf)),
+            "offload_stats")
+        return ms.value, b.value, pf.value
+
+    def set_prefetch_chunks(self, chunks):
+        """Cap (in optimizer-state chunks) of the m/v that train_step's backward
+        stages on the device for the offloaded step; 0 turns it off."""
+        _ck(lib().ctd_trainer_set_prefetch_chunks(self.h, int(chunks)), "set_prefetch_chunks")
 
     def synchronize(self):
         _ck(lib().ctd_trainer_synchronize(self.h), "synchronize")

@@ -1,5 +1,6 @@
 #pragma once
 // LlamaConfig presets, Model and weight loading (mirrors nn/model.h of the reference).
+#include <functional>
 #include <string>
 #include <vector>
 
@@ -50,6 +51,12 @@ struct Model {
   std::vector<TransformerBlock> layers;
   RMSNorm norm;
   bool gradient_checkpointing = false;
+  // Called with the layer index when the backward pass re-runs a checkpointed
+  // layer's forward, before the re-run (never during the forward pass itself).
+  // A trainer uses it to start work that should overlap the end of the
+  // backward, such as staging the offloaded optimizer state
+  // (optim::AdamW::prefetch).  Empty: nothing is called.
+  std::function<void(int)> recompute_hook;
 
   // Inference: input_ids int64 [B, T] -> logits fp32 [B, T, vocab], positions
   // from position_start.  With a cache, each layer's K/V are written at rows

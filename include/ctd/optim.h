@@ -8,7 +8,8 @@
 // With offload = true, m and v live in page-locked host memory, one flat
 // buffer each with the parameters laid out in streaming order, and step()
 // streams them through a ring of device buffers in fixed-size chunks that may
-// span several (small) parameters: the
+// span several (small) parameters (the first chunks optionally staged ahead of
+// step() by prefetch()): the
 // host->device copies, the fused update and the device->host copies of
 // neighbouring chunks overlap on two copy streams and an optimizer stream.
 // step() returns once the work is enqueued; the compute stream is not held
@@ -38,6 +39,9 @@ struct OffloadStats {
   // Device time from the first copy in to the last copy out of the most
   // recent offloaded step that has finished (0 until one has).
   double last_stream_ms = 0.0;
+  // Bytes per direction (m and v) of the last step's state that prefetch()
+  // had copied in before step(); last_h2d_bytes excludes them.
+  double last_prefetch_bytes = 0.0;
 };
 
 class AdamW {
@@ -79,6 +83,18 @@ class AdamW {
   // of m and v, so it must come before the state exists (first step(),
   // ensure_state_initialized()).
   void set_update_order(std::vector<std::pair<size_t, size_t>> order);
+  // Stages on the device the optimizer state of the first parameters in
+  // streaming order -- the chunks that cover the first parameter, at most
+  // set_prefetch_chunks() of them -- copying it in on the h2d stream once the
+  // compute stream has reached this call.  The next step() updates those
+  // chunks as soon as the gradients are final instead of after their
+  // transfer, so the next forward, which reads that parameter first, waits
+  // for less; it hands the buffer back once they are copied out.  Meant for
+  // late in the backward pass, when the host link is idle and most
+  // activations are freed.  Does nothing without offload, with a prefetch
+  // already pending, or with set_prefetch_chunks(0).
+  void prefetch();
+  void set_prefetch_chunks(int64_t n) { max_prefetch_chunks_ = n < 0 ? 0 : n; }
   // Blocks until the last offloaded step() has finished on every stream.
   void wait_idle();
   const OffloadStats& offload_stats();
@@ -125,6 +141,14 @@ class AdamW {
   Tensor flat_m_, flat_v_;       // pinned host buffers the per-parameter m/v view
   int64_t flat_n_ = 0;
   OffloadStats stats_;
+  // prefetch(): device copies of the state's first pf_elems_ floats, made with
+  // chunks of pf_chunk_elems_ (0 elements: nothing pending).
+  int64_t max_prefetch_chunks_ = 32;
+  Tensor pf_m_, pf_v_;
+  int64_t pf_elems_ = 0, pf_chunk_elems_ = 0;
+  void* ev_pf_ready_ = nullptr;    // compute stream: the buffer's memory is free
+  void* ev_pf_loaded_ = nullptr;   // h2d stream: the prefetch copies are done
+  void* ev_pf_drained_ = nullptr;  // d2h stream: its chunks are copied out
 };
 
 // Global L2 norm clipping; returns the pre-clip total norm.

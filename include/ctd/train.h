@@ -89,6 +89,14 @@ Batch make_batch(const DataSplit& split, const std::vector<int64_t>& doc_indices
 // total_steps (main.cpp:176-188), in float as there.
 float lr_at_step(int step, const Config& c);
 
+// Layer whose re-run in the backward pass starts the offloaded optimizer's
+// prefetch (nn::Model::recompute_hook -> optim::AdamW::prefetch): layer 0,
+// the last one the backward re-runs.  Its re-run and backward (about 96 ms
+// at Qwen3-1.7B, B=8, T=4096) cover the transfer of the embedding's m/v
+// (2.55 GB, about 51 ms), and the staging buffer is held for the shortest
+// time (layer 1 measured the same step time and a 0.07 GB higher peak).
+constexpr int kOptimizerPrefetchLayer = 0;
+
 // Mask-weighted mean masked CE over the whole split, one document per forward
 // (main.cpp:191-206).
 float run_val(const nn::Model& model, const DataSplit& val, int seq_len, Device device);

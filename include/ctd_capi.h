@@ -103,9 +103,18 @@ int ctd_trainer_zero_grad(ctd_trainer_t t);
 int ctd_trainer_get_opt_state(ctd_trainer_t t, int64_t i, float* m, float* v, int64_t numel);
 int ctd_trainer_step_count(ctd_trainer_t t, int64_t* steps);
 /* Offloaded AdamW: waits for the last step() to finish, then reports its
- * device time from first copy in to last copy out and the bytes it moved per
- * direction (zeros without offload). */
-int ctd_trainer_offload_stats(ctd_trainer_t t, double* stream_ms, double* bytes_per_direction);
+ * device time from its first copy in to its last copy out, the optimizer
+ * state it moved per direction (m and v, all of it copied out inside that
+ * time), and how much of that state a prefetch during the backward pass had
+ * already copied in before step() (zeros without offload).  Any output may
+ * be NULL. */
+int ctd_trainer_offload_stats(ctd_trainer_t t, double* stream_ms, double* bytes_per_direction,
+                              double* prefetched_bytes);
+/* Upper bound, in optimizer-state chunks, of what train_step's backward
+ * prefetches for the offloaded step (default 32; 0 turns the prefetch off).
+ * The staged m/v of the first parameter are device memory held from late in
+ * the backward until their copy out. */
+int ctd_trainer_set_prefetch_chunks(ctd_trainer_t t, int64_t chunks);
 
 /* One full training step (forward, backward, clip to max_norm when > 0,
  * optimizer step, zero_grad) with HIP-event phase times. */

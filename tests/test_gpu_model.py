@@ -234,8 +234,47 @@ def test_overlapped_offload_train_steps_equal_on_device():
         ma, va = a.opt_state(i)
         mb, vb = b.opt_state(i)
         assert np.array_equal(ma, mb) and np.array_equal(va, vb), a.names[i]
-    ms, nbytes = a.offload_stats()
-    assert ms > 0 and nbytes >= 8 * sum(a.numels)
+    ms, nbytes, prefetched = a.offload_stats()
+    assert ms > 0 and nbytes >= 8 * sum(a.numels) and prefetched == 0  # no checkpointing
+    a.close()
+    b.close()
+
+
+@pytest.mark.parametrize("chunk", [3000, 1 << 20, 50000])
+def test_prefetched_offload_with_checkpointing_equals_on_device(chunk):
+    # With checkpointing on, train_step's backward stages the m/v of the first
+    # parameter in streaming order (the embedding) on the device when it re-runs
+    # layer 0 (AdamW::prefetch), and step() updates those chunks from there.
+    # chunk 3000: the embedding spans 43 chunks, more than the 32 prefetched;
+    # 1 << 20: the whole state is one chunk, so step() copies nothing in;
+    # 50000: the third prefetched chunk runs past the embedding into layer 0.
+    c = tiny_cfg(qk_norm=True, D=64)
+    a = TR.Trainer(c, seed=6, init_std=0.05)
+    b = TR.Trainer(c, seed=6, init_std=0.05)
+    for t in (a, b):
+        t.set_checkpointing(True)
+    a.make_optimizer(lr=1e-3, weight_decay=0.1, offload=True, chunk_elems=chunk)
+    b.make_optimizer(lr=1e-3, weight_decay=0.1, offload=False)
+    losses = {id(a): [], id(b): []}
+    for step in range(4):
+        for t in (a, b):
+            t.synthetic_batch(2, 96, seed=20 + step, masked=True)
+            losses[id(t)].append(t.train_step(1.0).loss)
+    assert losses[id(a)] == losses[id(b)]
+    for i in range(a.num_params()):
+        assert np.array_equal(a.get_param(i), b.get_param(i)), a.names[i]
+        ma, va = a.opt_state(i)
+        mb, vb = b.opt_state(i)
+        assert np.array_equal(ma, mb) and np.array_equal(va, vb), a.names[i]
+    # Expected prefetch: whole chunks covering the first parameter, at most 32,
+    # within the flat state (each parameter padded to 64 floats).
+    assert a.names[0] == "model.embed_tokens.weight"
+    chunk_r = (chunk + 63) // 64 * 64
+    flat_n = sum((n + 63) // 64 * 64 for n in a.numels)
+    nch = min(-(-a.numels[0] // chunk_r), 32)
+    ms, nbytes, prefetched = a.offload_stats()
+    assert ms > 0 and nbytes == 8 * flat_n
+    assert prefetched == 8 * min(nch * chunk_r, flat_n)
     a.close()
     b.close()
 
