@@ -128,6 +128,71 @@ def profiled_traffic(workload, variant):
     return None, None
 
 
+def pinned_copy_rates(nbytes=1 << 30):
+    """The box's own pinned-memory copy rates in GB/s, over `nbytes` each:
+    host->device alone, device->host alone, and both at once on two streams
+    (per direction) -- the link ceiling the offloaded step is held to."""
+    from emberlm_amd import capi
+    lib, ck = capi.lib(), capi.check
+    hin, hout, din, dout = (C.c_void_p() for _ in range(4))
+    streams = [C.c_void_p(), C.c_void_p()]
+    evs = [C.c_void_p() for _ in range(3)]
+    ck(lib.ember_host_malloc_pinned(C.byref(hin), nbytes), "pinned alloc")
+    ck(lib.ember_host_malloc_pinned(C.byref(hout), nbytes), "pinned alloc")
+    ck(lib.ember_device_malloc(C.byref(din), nbytes), "device alloc")
+    ck(lib.ember_device_malloc(C.byref(dout), nbytes), "device alloc")
+    for s in streams:
+        ck(lib.ember_stream_create(C.byref(s)), "stream")
+    for e in evs:
+        ck(lib.ember_event_create(C.byref(e)), "event")
+    h2d = (din, hin, 0)
+    d2h = (hout, dout, 1)
+
+    def span(jobs):
+        # jobs[i] runs on streams[i], all released by one event on streams[0]
+        ck(lib.ember_event_record(evs[0], streams[0]), "record")
+        for i, (dst, src, kind) in enumerate(jobs):
+            ck(lib.ember_stream_wait_event(streams[i], evs[0]), "wait")
+            ck(lib.ember_memcpy_async(dst, src, nbytes, kind, streams[i]), "copy")
+            ck(lib.ember_event_record(evs[1 + i], streams[i]), "record")
+        ms = 0.0
+        for i in range(len(jobs)):
+            ck(lib.ember_event_synchronize(evs[1 + i]), "sync")
+            t = C.c_float()
+            ck(lib.ember_event_elapsed_ms(C.byref(t), evs[0], evs[1 + i]), "elapsed")
+            ms = max(ms, t.value)
+        return nbytes / (ms / 1e3) / 1e9
+
+    try:
+        span([h2d, d2h])  # first touch of the pinned pages, not timed
+        return {"bytes": nbytes, "h2d": round(span([h2d]), 2), "d2h": round(span([d2h]), 2),
+                "duplex_per_direction": round(span([h2d, d2h]), 2)}
+    finally:
+        for e in evs:
+            lib.ember_event_destroy(e)
+        for s in streams:
+            lib.ember_stream_destroy(s)
+        lib.ember_device_free(din)
+        lib.ember_device_free(dout)
+        lib.ember_host_free_pinned(hin)
+        lib.ember_host_free_pinned(hout)
+
+
+def link_probe():
+    """pinned_copy_rates() in a child process: there its two streams are the
+    only ones and get hardware queues of their own, whereas in this process
+    they would share queues with the trainer's compute and copy streams and
+    the two directions would run one after the other."""
+    import subprocess
+    try:
+        out = subprocess.run([sys.executable, os.path.abspath(__file__), "--link-probe"],
+                             capture_output=True, text=True, timeout=180, check=True).stdout
+        return json.loads(out.strip().splitlines()[-1])
+    except (subprocess.SubprocessError, ValueError, IndexError) as e:
+        log(f"[bench] link probe failed: {e}")
+        return None
+
+
 def decode_point(tr, cfg, n_params, prompt_len, new_tokens):
     """ctd_generate's loop (greedy, batch 1) on the benchmark's model: a prompt
     of prompt_len seeded ids, then new_tokens tokens through the KV cache.
@@ -186,7 +251,13 @@ def main():
     ap.add_argument("--decode-only", action="store_true",
                     help="only the inference measurement (greedy ctd_generate loop on the "
                          "workload's model): prints one JSON line with the decode points")
+    ap.add_argument("--link-probe", action="store_true",
+                    help="only the pinned host<->device copy rates of this box (one JSON line)")
     args = ap.parse_args()
+
+    if args.link_probe:
+        print(json.dumps(pinned_copy_rates()))
+        return
 
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported "
@@ -359,6 +430,13 @@ def main():
         result["offload"]["isolated_step_ms"] = round(iso_ms, 2)
         result["offload"]["isolated_gbps_per_direction"] = round(gbps, 2)
         result["offload"]["isolated_frac_of_pcie"] = round(gbps / PCIE_GEN5_X16_GBPS, 4)
+        result["offload"]["isolated_aggregate_gbps"] = round(2 * gbps, 2)
+        link = link_probe()
+        if link is not None:
+            result["offload"]["box_pinned_copy_gbps"] = link
+            result["offload"]["isolated_frac_of_box_duplex"] = round(
+                gbps / link["duplex_per_direction"], 4)
+        log(f"[bench] pinned copies on this box: {link}")
         log(f"[bench] isolated offloaded step: {iso_ms:.0f} ms, {gbps:.1f} GB/s per direction")
 
     if args.nockpt_steps > 0 and ckpt:

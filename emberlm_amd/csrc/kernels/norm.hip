@@ -63,6 +63,54 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_vec(const float* __restr
   }
 }
 
+// The same with the row held in registers: MAXC float4 chunks per lane, all
+// loaded before the sum of squares and written from there, so x is read
+// once and its loads are in flight together.  Same arithmetic, same order.
+template <int LPR, int MAXC>
+__global__ __launch_bounds__(kThreads) void rmsnorm_fwd_reg(const float* __restrict__ x,
+                                                            const float* __restrict__ w,
+                                                            float* __restrict__ y,
+                                                            float* __restrict__ rstd,
+                                                            int64_t rows, int64_t H, float eps) {
+  constexpr int RPB = kThreads / LPR;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / LPR;
+  const int sub = threadIdx.x % LPR;
+  const int64_t nc = H / 4;
+  const bool live = row < rows;
+  const f32x4* xr = reinterpret_cast<const f32x4*>(x + (live ? row : 0) * H);
+  f32x4 v[MAXC];
+  float ss = 0.f;
+  if (live) {
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j) {
+      const int64_t ci = sub + static_cast<int64_t>(j) * LPR;
+      v[j] = ci < nc ? xr[ci] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j)
+      if (sub + static_cast<int64_t>(j) * LPR < nc)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ss = fmaf(v[j][e], v[j][e], ss);
+  }
+  ss = group_sum(ss, LPR);
+  if (!live) return;
+  const float s = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
+  if (rstd && sub == 0) rstd[row] = s;
+  f32x4* yr = reinterpret_cast<f32x4*>(y + row * H);
+  const f32x4* wv = reinterpret_cast<const f32x4*>(w);
+#pragma unroll
+  for (int j = 0; j < MAXC; ++j) {
+    const int64_t ci = sub + static_cast<int64_t>(j) * LPR;
+    if (ci < nc) {
+      const f32x4 ww = wv[ci];
+      f32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = v[j][e] * s * ww[e];
+      yr[ci] = o;
+    }
+  }
+}
+
 // Any H: one block per row, scalar accesses.
 __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_scalar(const float* __restrict__ x,
                                                                const float* __restrict__ w,
@@ -104,13 +152,21 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
     const bool live = row < rows;
     const f32x4* xr = reinterpret_cast<const f32x4*>(x + (live ? row : 0) * H);
     const f32x4* gr = reinterpret_cast<const f32x4*>(dy + (live ? row : 0) * H);
+    // The row's x and dy chunks stay in registers for the dx pass below.
+    f32x4 xv[MAXC], gv[MAXC];
     float ss = 0.f, c = 0.f;
-    if (live)
+    if (live) {
+#pragma unroll
+      for (int j = 0; j < MAXC; ++j) {
+        const int64_t ci = sub + static_cast<int64_t>(j) * LPR;
+        xv[j] = ci < nc ? xr[ci] : f32x4{0.f, 0.f, 0.f, 0.f};
+        gv[j] = ci < nc ? gr[ci] : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
 #pragma unroll
       for (int j = 0; j < MAXC; ++j) {
         const int64_t ci = sub + static_cast<int64_t>(j) * LPR;
         if (ci < nc) {
-          const f32x4 v = xr[ci], g = gr[ci], ww = wv[ci];
+          const f32x4 v = xv[j], g = gv[j], ww = wv[ci];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             ss = fmaf(v[e], v[e], ss);
@@ -118,6 +174,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
           }
         }
       }
+    }
     ss = group_sum(ss, LPR);
     c = group_sum(c, LPR);
     if (!live) continue;
@@ -127,7 +184,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
     for (int j = 0; j < MAXC; ++j) {
       const int64_t ci = sub + static_cast<int64_t>(j) * LPR;
       if (ci < nc) {
-        const f32x4 v = xr[ci], g = gr[ci], ww = wv[ci];
+        const f32x4 v = xv[j], g = gv[j], ww = wv[ci];
         f32x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -263,7 +320,27 @@ extern "C" int ember_rmsnorm_fwd(const float* x, const float* w, float* y, float
   if (vec_ok(H, x, y) && aligned16(w)) {
     const int lpr = lanes_per_row(H);
     const unsigned nb = static_cast<unsigned>((rows + kThreads / lpr - 1) / (kThreads / lpr));
-    switch (lpr) {
+    const int64_t chunks = (H / 4 + lpr - 1) / lpr;  // > 1 only at lpr = 64
+#define EMBER_FWD_REG(L, MC)                                                               \
+  rmsnorm_fwd_reg<L, MC><<<nb, kThreads, 0, st>>>(x, w, y, rstd, rows, H, eps);            \
+  return launch_status();
+    if (chunks == 1) {
+      switch (lpr) {
+        case 1: EMBER_FWD_REG(1, 1)
+        case 2: EMBER_FWD_REG(2, 1)
+        case 4: EMBER_FWD_REG(4, 1)
+        case 8: EMBER_FWD_REG(8, 1)
+        case 16: EMBER_FWD_REG(16, 1)
+        case 32: EMBER_FWD_REG(32, 1)
+        default: EMBER_FWD_REG(64, 1)
+      }
+    }
+    if (chunks <= 2) { EMBER_FWD_REG(64, 2) }
+    if (chunks <= 4) { EMBER_FWD_REG(64, 4) }
+    if (chunks <= 8) { EMBER_FWD_REG(64, 8) }
+    if (chunks <= 16) { EMBER_FWD_REG(64, 16) }
+#undef EMBER_FWD_REG
+    switch (lpr) {  // wider rows: the chunk loop
       case 1: rmsnorm_fwd_vec<1><<<nb, kThreads, 0, st>>>(x, w, y, rstd, rows, H, eps); break;
       case 2: rmsnorm_fwd_vec<2><<<nb, kThreads, 0, st>>>(x, w, y, rstd, rows, H, eps); break;
       case 4: rmsnorm_fwd_vec<4><<<nb, kThreads, 0, st>>>(x, w, y, rstd, rows, H, eps); break;

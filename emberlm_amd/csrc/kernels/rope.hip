@@ -39,11 +39,23 @@ __global__ __launch_bounds__(256) void rope_kernel(const float* x,
   sn *= sign;
   const float* xb = x + tok * H * D;
   float* yb = y + tok * H * D;
-  for (int h = 0; h < H; ++h) {
-    const float a = xb[h * D + i];
-    const float b = xb[h * D + i + half];
-    yb[h * D + i] = a * cs - b * sn;
-    yb[h * D + i + half] = a * sn + b * cs;
+  // Up to kHeads heads' pairs are loaded before any is stored (y may be x,
+  // which otherwise keeps each head's loads behind the previous head's stores).
+  constexpr int kHeads = 8;
+  for (int h0 = 0; h0 < H; h0 += kHeads) {
+    float a[kHeads], b[kHeads];
+#pragma unroll
+    for (int j = 0; j < kHeads; ++j)
+      if (h0 + j < H) {
+        a[j] = xb[(h0 + j) * D + i];
+        b[j] = xb[(h0 + j) * D + i + half];
+      }
+#pragma unroll
+    for (int j = 0; j < kHeads; ++j)
+      if (h0 + j < H) {
+        yb[(h0 + j) * D + i] = a[j] * cs - b[j] * sn;
+        yb[(h0 + j) * D + i + half] = a[j] * sn + b[j] * cs;
+      }
   }
 }
 

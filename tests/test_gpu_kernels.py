@@ -412,6 +412,22 @@ def test_sumsq_multi():
     sizes = (C.c_int64 * 3)(4, 9, 16)
     call("ember_sumsq_multi", ptrs, sizes, 3, p(out), p(ws), wsb, None)
     assert abs(math.sqrt(host(out)[0]) - math.sqrt(29)) < 1e-5
+    # The float4 path over the most workgroups a tensor gets (50M + 1 elements:
+    # a ragged tail), and a view one float off a 16-byte boundary (the scalar
+    # path); a second call must give the same bits.
+    big = r.standard_normal(50_000_001).astype(np.float32)
+    base = r.standard_normal(1001).astype(np.float32)
+    tb, tbase = dev(big), dev(base)
+    ptrs = (C.c_void_p * 2)(tb.data_ptr(), tbase.data_ptr() + 4)
+    sizes = (C.c_int64 * 2)(big.size, 1000)
+    wsb = lib.ember_sumsq_workspace_bytes(2)
+    ws = empty((wsb // 4,))
+    call("ember_sumsq_multi", ptrs, sizes, 2, p(out), p(ws), wsb, None)
+    first = host(out)[0]
+    ref = float((big.astype(np.float64) ** 2).sum() + (base[1:].astype(np.float64) ** 2).sum())
+    assert abs(first - ref) <= 1e-5 * ref
+    call("ember_sumsq_multi", ptrs, sizes, 2, p(out), p(ws), wsb, None)
+    assert host(out)[0] == first
 
 
 # ------------------------------------------------------------ attention
