@@ -9,21 +9,20 @@
 //
 // Layout: q, o, dq [B,T,H,D]; k, v, dk, dv [B,T,Hk,D]; lse, delta [B,H,T].
 //
-// MFMA fragment conventions (wave64).  v_mfma_f32_32x32x2_f32 (forward): A
-// operand lane (g = lane/32, r = lane%32) holds A[m=r][k=g]; B operand holds
-// B[k=g][n=r]; accumulator register e holds C[m = 8*(e/4) + 4*g + (e%4)][n = r].
-// v_mfma_f32_16x16x4_f32 (backward): lane (g = lane/16, i = lane%16) holds
-// A[m=i][k=g] and B[k=g][n=i]; accumulator register e holds C[m = 4*g + e][n = i].
+// Every kernel runs on v_mfma_f32_16x16x4_f32 tiles (wave64): lane
+// (g = lane/16, i = lane%16) holds A[m=i][k=g] and B[k=g][n=i]; accumulator
+// register e holds C[m = 4*g + e][n = i].  A wave owns 16 rows (queries or
+// keys), so its register-resident rows and accumulators take half of what 32
+// rows on 32x32x2 tiles would, and at D = 128 two to four waves share a SIMD:
+// one wave's softmax section and barrier waits run under another's MFMAs.
 //
-// Forward, per wave of 32 queries: S^T = K Q^T puts the query index in the
-// lane (n = r), so the online-softmax statistics of a query live in one lane
-// pair (g = 0/1) and the probabilities come out exactly in the B-operand
-// layout of O^T += V^T P^T: accumulator register e of S^T is the B value of
-// the MFMA step that contracts over keys {8*(e/4)+(e%4), 8*(e/4)+4+(e%4)}.
-// Q stays in registers (pre-multiplied by scale*log2(e)).  K/V tiles of 32
-// keys are double-buffered in LDS: the global loads of tile i+1 are issued
-// into registers before the MFMAs of tile i and written to the other buffer
-// after them, so one barrier per tile remains and load latency is hidden.
+// Forward, per wave of 16 queries: S^T = K Q^T puts the query index in the
+// lane (n = i), and the probabilities come out exactly in the B-operand layout
+// of O^T += V^T P^T.  Q stays in registers (pre-multiplied by scale*log2(e)).
+// K/V tiles of 32 keys are double-buffered in LDS: the global loads of tile
+// i+1 are issued into registers before the MFMAs of tile i and written to the
+// other buffer after them, so one barrier per tile remains and load latency
+// is hidden.
 //
 // Backward (no atomics, so dK/dV/dQ are bitwise reproducible):
 //   attn_delta:  delta = rowsum(dO * O);
@@ -33,8 +32,8 @@
 //                lane, so dV^T += dO^T P and dK^T += Q^T dS accumulate in
 //                registers across every query tile and every query head of
 //                the KV head's group, in a fixed order.
-// Both backward kernels run on 16x16x4 MFMA tiles (64 rows per workgroup,
-// two waves per SIMD at D = 128; 32x32x2 tiles need more than 256 registers
+// Both backward kernels take 64 rows per workgroup (two waves per SIMD at
+// D = 128; 32 rows per wave on 32x32x2 tiles needed more than 256 registers
 // per lane there) and double-buffer their streamed tiles the same way.
 #include "common.h"
 
@@ -46,19 +45,12 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ f32x16 mfma32(float a, float b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+__device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
 // 2^x on the transcendental unit (inputs here are <= 0 or -inf).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-__device__ __forceinline__ int acc_row(int e, int g) { return 8 * (e >> 2) + 4 * g + (e & 3); }
-
-__device__ __forceinline__ void zero16(f32x16& a) {
-#pragma unroll
-  for (int e = 0; e < 16; ++e) a[e] = 0.f;
-}
 
 // Block order.  Every attention kernel runs a 1-D grid of (tile, row) work
 // items, row = (b, head).  Blocks are dispatched in index order and dealt
@@ -78,19 +70,20 @@ __device__ __forceinline__ WorkItem work_item(int ntiles) {
   return {L / rows, rr};
 }
 
-// ROWS rows of D floats staged global -> registers -> LDS.  All loads of a
-// tile are issued before the first wait; rows at or beyond `valid` are zero.
-template <int D, int ROWS>
+// ROWS rows of D floats staged global -> registers -> LDS by a block of
+// THREADS.  All loads of a tile are issued before the first wait; rows at or
+// beyond `valid` are zero.
+template <int D, int ROWS, int THREADS = kThreads>
 struct RowTile {
   static constexpr int kChunks = ROWS * D / 4;
-  static constexpr int kPer = kChunks / kThreads;
-  static_assert(kChunks % kThreads == 0, "tile does not split evenly over the block");
+  static constexpr int kPer = kChunks / THREADS;
+  static_assert(kChunks % THREADS == 0, "tile does not split evenly over the block");
   f32x4 r[kPer];
 
   __device__ __forceinline__ void load(const float* __restrict__ src, int64_t gstride, int valid) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const int c = threadIdx.x + i * kThreads;
+      const int c = threadIdx.x + i * THREADS;
       const int row = c / (D / 4), c4 = c % (D / 4);
       r[i] = row < valid ? reinterpret_cast<const f32x4*>(src + row * gstride)[c4]
                          : f32x4{0.f, 0.f, 0.f, 0.f};
@@ -99,91 +92,40 @@ struct RowTile {
   __device__ __forceinline__ void store(float* __restrict__ lds, int ls) const {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const int c = threadIdx.x + i * kThreads;
+      const int c = threadIdx.x + i * THREADS;
       const int row = c / (D / 4), c4 = c % (D / 4);
       *reinterpret_cast<f32x4*>(lds + row * ls + 4 * c4) = r[i];
     }
   }
 };
 
-// Write LDS rows [rows][D] (stride ls) to global rows, skipping rows >= valid.
-template <int D>
-__device__ __forceinline__ void unstage_rows(const float* __restrict__ lds, int ls,
-                                             float* __restrict__ dst, int64_t gstride, int rows,
-                                             int valid) {
-  for (int c = threadIdx.x; c < rows * (D / 4); c += kThreads) {
-    const int row = c / (D / 4), c4 = c % (D / 4);
-    if (row < valid)
-      reinterpret_cast<f32x4*>(dst + row * gstride)[c4] =
-          *reinterpret_cast<const f32x4*>(lds + row * ls + 4 * c4);
-  }
-}
-
-// Load the D/2 values of row `row` starting at column `col0` into registers,
-// times `mul`; zeros when row >= T.
-template <int HALF>
-__device__ __forceinline__ void load_half(float (&reg)[HALF], const float* __restrict__ base,
-                                          int64_t stride, int row, int T, int col0, float mul) {
-  if (row < T) {
-    const f32x4* src = reinterpret_cast<const f32x4*>(base + row * stride + col0);
-#pragma unroll
-    for (int c = 0; c < HALF / 4; ++c) {
-      const f32x4 t = src[c];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) reg[4 * c + j] = t[j] * mul;
-    }
-  } else {
-#pragma unroll
-    for (int c = 0; c < HALF; ++c) reg[c] = 0.f;
-  }
-}
-
-// Transposes a wave's 32-column accumulator block through LDS into rows
-// [32*w + r][D] of `lds` (stride ls), scaled by `mul`.  The D index is
-// interleaved over the NDT accumulator tiles: row m of tile dt is d = NDT*m + dt,
-// so the A operand of every D-tiled MFMA is one b128 LDS read of NDT
-// consecutive d values (NDT = 4 at D = 128, 2 at D = 64).
-template <int NDT>
-__device__ __forceinline__ void acc_to_rows(float* __restrict__ lds, int ls,
-                                            const f32x16 (&acc)[NDT], int w, int g, int r,
-                                            float mul) {
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int e = 0; e < 16; ++e)
-      lds[(32 * w + r) * ls + NDT * acc_row(e, g) + dt] = acc[dt][e] * mul;
-}
-
-// NDT consecutive floats of an LDS row (the interleaved A operand above).
-template <int NDT>
-struct DVec;
-template <>
-struct DVec<4> {
-  using T = f32x4;
-};
-template <>
-struct DVec<2> {
-  typedef float T __attribute__((ext_vector_type(2)));
-};
-
 // ------------------------------------------------------------------ forward
+// Forward.  A wave owns 16 queries and a workgroup of eight waves 128, so
+// every K/V tile in LDS serves 128 queries, and at 124 registers per lane
+// (D = 128) four waves fit on a SIMD (32 queries per wave on 32x32x2 tiles
+// took 239 and two waves: 1.14x slower at B=8, T=4096, H=16, Hk=8).  Per
+// 32-key tile (halves kt of 16 keys):
+//   S^T = K Q^T (m = key, n = query): MFMA step 4t+j contracts over
+//   d = 16t + 4g + j, each K fragment one b128 LDS read, Q in registers;
+//   register e of s[kt] in lane (g, i) is the score of key 16kt + 4g + e for
+//   query i: a query's running max is reduced over its four lanes (g), and
+//   its running sum is kept per lane and added up at the end;
+//   O^T += V^T P^T (m = d, n = query, contraction over the 4 keys
+//   {16kt + 4g + e : g}): P is the B operand straight from s[kt], the A
+//   operand one b32 LDS read of V.
 template <int D>
 struct FwdCfg {
-  static constexpr int kBQ = 128, kBK = 32, kKS = D + 4, kVS = D + 8, kOS = D + 4;
-  static constexpr int kBuf = kBK * (kKS + kVS);  // one K+V stage
-  static constexpr int kOut = kBQ * kOS;
-  static constexpr int kSmem = 2 * kBuf > kOut ? 2 * kBuf : kOut;
+  static constexpr int kThreads = 512, kBQ = 128, kBK = 32, kKS = D + 4;
+  static constexpr int kBuf = 2 * kBK * kKS;  // one K+V stage
+  static constexpr int kSmem = 2 * kBuf;
 };
 
 template <int D>
-__global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const float* __restrict__ q,
-                                                               const float* __restrict__ k,
-                                                               const float* __restrict__ v,
-                                                               float* __restrict__ o,
-                                                               float* __restrict__ lse, int T,
-                                                               int H, int Hk, float scale_log2) {
+__global__ __launch_bounds__(FwdCfg<D>::kThreads, 2) void attn_fwd_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    float* __restrict__ o, float* __restrict__ lse, int T, int H, int Hk, float scale_log2) {
   using C = FwdCfg<D>;
-  constexpr int HALF = D / 2, NDT = D / 32;
+  constexpr int NT = D / 16;
   __shared__ __attribute__((aligned(16))) float smem[C::kSmem];
 
   const int nqb = (T + C::kBQ - 1) / C::kBQ;
@@ -191,28 +133,34 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const float* __re
   const int qb = nqb - 1 - wi.tile;  // longest rows first
   const int h = wi.row % H, b = wi.row / H;
   const int hk = h / (H / Hk);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 5, r = lane & 31;
-  const int q0 = qb * C::kBQ, qw0 = q0 + 32 * w, myq = qw0 + r;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, i = lane & 15;
+  const int q0 = qb * C::kBQ, qw0 = q0 + 16 * w, myq = qw0 + i;
   const int64_t qs = static_cast<int64_t>(H) * D, ks = static_cast<int64_t>(Hk) * D;
-  const float* qbase = q + static_cast<int64_t>(b) * T * qs + static_cast<int64_t>(h) * D;
+  const int64_t qoff = static_cast<int64_t>(b) * T * qs + static_cast<int64_t>(h) * D;
   const float* kbase = k + static_cast<int64_t>(b) * T * ks + static_cast<int64_t>(hk) * D;
   const float* vbase = v + static_cast<int64_t>(b) * T * ks + static_cast<int64_t>(hk) * D;
 
-  float qreg[HALF];
-  load_half<HALF>(qreg, qbase, qs, myq, T, HALF * g, scale_log2);
-
-  f32x16 acc[NDT];
+  f32x4 qreg[NT];
+  if (myq < T) {
+    const f32x4* qr = reinterpret_cast<const f32x4*>(q + qoff + myq * qs);
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) zero16(acc[dt]);
+    for (int t = 0; t < NT; ++t) qreg[t] = qr[4 * t + g] * scale_log2;
+  } else {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) qreg[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  f32x4 acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
   const int kend = min(T, q0 + C::kBQ);
   const int nkb = (kend + C::kBK - 1) / C::kBK;
-  RowTile<D, C::kBK> tk, tv;
+  RowTile<D, C::kBK, C::kThreads> tk, tv;
   tk.load(kbase, ks, T);
   tv.load(vbase, ks, T);
   tk.store(smem, C::kKS);
-  tv.store(smem + C::kBK * C::kKS, C::kVS);
+  tv.store(smem + C::kBK * C::kKS, C::kKS);
   __syncthreads();
 
   for (int kb = 0; kb < nkb; ++kb) {
@@ -224,66 +172,75 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const float* __re
     }
     const float* Ks = smem + (kb & 1) * C::kBuf;
     const float* Vs = Ks + C::kBK * C::kKS;
-    if (k0 <= qw0 + 31) {
-      f32x16 s;
-      zero16(s);
+    if (k0 <= qw0 + 15) {  // some key of the tile is seen by some query of this wave
+      f32x4 s[2];
 #pragma unroll
-      for (int s4 = 0; s4 < HALF / 4; ++s4) {
-        const f32x4 kf = *reinterpret_cast<const f32x4*>(Ks + r * C::kKS + HALF * g + 4 * s4);
+      for (int kt = 0; kt < 2; ++kt) s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) s = mfma32(kf[j], qreg[4 * s4 + j], s);
-      }
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+          const f32x4 kf =
+              *reinterpret_cast<const f32x4*>(Ks + (16 * kt + i) * C::kKS + 16 * t + 4 * g);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) s[kt] = mfma16(kf[j], qreg[t][j], s[kt]);
+        }
       const bool need_mask = (k0 + C::kBK - 1 > qw0) || (k0 + C::kBK > T);
       float tmax = -INFINITY;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int key = k0 + acc_row(e, g);
-        if (need_mask && (key > myq || key >= T)) s[e] = -INFINITY;
-        tmax = fmaxf(tmax, s[e]);
-      }
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int key = k0 + 16 * kt + 4 * g + e;
+          if (need_mask && (key > myq || key >= T)) s[kt][e] = -INFINITY;
+          tmax = fmaxf(tmax, s[kt][e]);
+        }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
       tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
       const float m_new = fmaxf(m_run, tmax);
       const float alpha = fast_exp2(m_run - m_new);
       float psum = 0.f;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float pv = fast_exp2(s[e] - m_new);
-        s[e] = pv;
-        psum += pv;
-      }
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float pv = fast_exp2(s[kt][e] - m_new);
+          s[kt][e] = pv;
+          psum += pv;
+        }
       l_run = l_run * alpha + psum;
       m_run = m_new;
       if (__any(alpha != 1.0f)) {  // the running max moved for some query of the wave
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) acc[dt][e] *= alpha;
+        for (int t = 0; t < NT; ++t) acc[t] *= alpha;
       }
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const auto vv = *reinterpret_cast<const typename DVec<NDT>::T*>(
-            Vs + acc_row(e, g) * C::kVS + NDT * r);
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) acc[dt] = mfma32(vv[dt], s[e], acc[dt]);
-      }
+        for (int e = 0; e < 4; ++e) {
+          const int row = (16 * kt + 4 * g + e) * C::kKS;
+#pragma unroll
+          for (int t = 0; t < NT; ++t) acc[t] = mfma16(Vs[row + 16 * t + i], s[kt][e], acc[t]);
+        }
     }
     if (more) {
       float* nb = smem + ((kb + 1) & 1) * C::kBuf;
       tk.store(nb, C::kKS);
-      tv.store(nb + C::kBK * C::kKS, C::kVS);
+      tv.store(nb + C::kBK * C::kKS, C::kKS);
     }
     __syncthreads();
   }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
-  if (g == 0 && myq < T)
-    lse[(static_cast<int64_t>(b) * H + h) * T + myq] = (m_run + log2f(l_tot)) * kLn2;
-  acc_to_rows<NDT>(smem, C::kOS, acc, w, g, r, 1.0f / l_tot);
-  __syncthreads();
-  unstage_rows<D>(smem, C::kOS,
-                  o + static_cast<int64_t>(b) * T * qs + static_cast<int64_t>(q0) * qs +
-                      static_cast<int64_t>(h) * D,
-                  qs, C::kBQ, T - q0);
+  float l_tot = l_run + __shfl_xor(l_run, 16, kWave);
+  l_tot += __shfl_xor(l_tot, 32, kWave);
+  if (myq < T) {
+    if (g == 0) lse[(static_cast<int64_t>(b) * H + h) * T + myq] = (m_run + log2f(l_tot)) * kLn2;
+    // Accumulator tile t, lane (g, i), register e holds d = 16t + 4g + e of query i.
+    f32x4* orow = reinterpret_cast<f32x4*>(o + qoff + myq * qs);
+    const float inv = 1.0f / l_tot;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) orow[4 * t + g] = acc[t] * inv;
+  }
 }
 
 // --------------------------------------------------------------- backward
@@ -309,10 +266,6 @@ __global__ __launch_bounds__(kThreads) void attn_delta_kernel(const float* __res
     const int64_t t = bt % T, b = bt / T;
     delta[(b * H + h) * T + t] = a;
   }
-}
-
-__device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
 // dQ on 16x16x4 MFMA tiles (lane l: A[l%16][l/16], B[l/16][l%16],
@@ -616,13 +569,16 @@ extern "C" int ember_attn_fwd(const float* q, const float* k, const float* v, fl
   if (B == 0 || T == 0) return EMBER_OK;
   if (!q || !k || !v || !o || !lse) return EMBER_EINVAL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return EMBER_EALIGN;
+  static_assert(FwdCfg<64>::kBQ == 128 && FwdCfg<128>::kBQ == 128, "grid assumes 128 queries");
   const dim3 grid(static_cast<unsigned>((T + 127) / 128 * H * B));
   const float sl = scale * kLog2e;
   const int Ti = static_cast<int>(T), Hi = static_cast<int>(H), Hki = static_cast<int>(Hk);
   if (D == 64)
-    attn_fwd_kernel<64><<<grid, kThreads, 0, as_stream(s)>>>(q, k, v, o, lse, Ti, Hi, Hki, sl);
+    attn_fwd_kernel<64><<<grid, FwdCfg<64>::kThreads, 0, as_stream(s)>>>(q, k, v, o, lse, Ti, Hi,
+                                                                         Hki, sl);
   else
-    attn_fwd_kernel<128><<<grid, kThreads, 0, as_stream(s)>>>(q, k, v, o, lse, Ti, Hi, Hki, sl);
+    attn_fwd_kernel<128><<<grid, FwdCfg<128>::kThreads, 0, as_stream(s)>>>(q, k, v, o, lse, Ti,
+                                                                           Hi, Hki, sl);
   return launch_status();
 }
 
