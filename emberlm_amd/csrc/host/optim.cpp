@@ -74,7 +74,7 @@ AdamW::AdamW(std::vector<ParamGroup> groups, float beta1, float beta2, float eps
 AdamW::~AdamW() {
   if (in_flight_ && ev_done_) ember_event_synchronize(ev_done_);
   // A pending prefetch's copies must land before its buffer goes back to the
-  // allocator.
+  // allocator (no throwing from a destructor: the status is not checked).
   if (pf_elems_ > 0 && ev_pf_loaded_) ember_event_synchronize(ev_pf_loaded_);
   pf_m_ = Tensor{};
   pf_v_ = Tensor{};
@@ -107,12 +107,22 @@ AdamW::~AdamW() {
 
 Tensor& AdamW::m_tensor(size_t gi, size_t pi) {
   wait_idle();
+  drop_prefetch();  // the caller may write the host state the prefetch copied
   return state_.at(gi).at(pi).m;
 }
 
 Tensor& AdamW::v_tensor(size_t gi, size_t pi) {
   wait_idle();
+  drop_prefetch();
   return state_.at(gi).at(pi).v;
+}
+
+void AdamW::drop_prefetch() {
+  if (pf_elems_ <= 0) return;
+  CTD_CHECK(ember_event_synchronize(ev_pf_loaded_));
+  pf_m_ = Tensor{};
+  pf_v_ = Tensor{};
+  pf_elems_ = 0;
 }
 
 void AdamW::set_update_order(std::vector<std::pair<size_t, size_t>> order) {
@@ -290,12 +300,7 @@ void AdamW::step_offloaded() {
   CTD_CHECK(ember_event_record(ev_begin_, hs));
   // A prefetch cut with another chunk size does not line up with this
   // step's chunks: let it land and drop it.
-  if (pf_elems_ > 0 && pf_chunk_elems_ != chunk_elems_) {
-    CTD_CHECK(ember_event_synchronize(ev_pf_loaded_));
-    pf_m_ = Tensor{};
-    pf_v_ = Tensor{};
-    pf_elems_ = 0;
-  }
+  if (pf_chunk_elems_ != chunk_elems_) drop_prefetch();
   const int64_t pf_elems = pf_elems_;
   float* pf_m = pf_elems > 0 ? static_cast<float*>(pf_m_.data_ptr()) : nullptr;
   float* pf_v = pf_elems > 0 ? static_cast<float*>(pf_v_.data_ptr()) : nullptr;

@@ -69,7 +69,8 @@ class AdamW {
   size_t num_groups() const { return groups_.size(); }
   size_t num_params(size_t gi) const { return groups_.at(gi).params.size(); }
   // Optimizer state; with offload these are host tensors that an in-flight
-  // step() still writes, so both accessors first wait for it to finish.
+  // step() still writes, so both accessors first wait for it to finish, and
+  // they drop a pending prefetch() (the caller may change the state it copied).
   Tensor& m_tensor(size_t gi, size_t pi);
   Tensor& v_tensor(size_t gi, size_t pi);
 
@@ -115,6 +116,7 @@ class AdamW {
   void init_offload_state();
   void step_ondevice();
   void step_offloaded();
+  void drop_prefetch();  // wait for a pending prefetch's copies and discard them
 
   std::vector<ParamGroup> groups_;
   std::vector<std::vector<State>> state_;

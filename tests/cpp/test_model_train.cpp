@@ -236,6 +236,54 @@ void overfits_tiny_batch() {
   check(finals[0] == finals[2], "offloaded AdamW leaves the loss bits unchanged");
 }
 
+// The offloaded optimizer's prefetch (started from Model::recompute_hook when
+// the backward re-runs layer 0) gives the same weights as no prefetch, also
+// when the host state is rewritten through m_tensor() between the backward and
+// step() -- as a checkpoint load does -- which must drop the staged copy.
+void prefetch_then_host_state_change() {
+  const int B = 2, T = 4;
+  std::vector<int64_t> hx = {1, 4, 0, 6, 7, 2, 3, 5};
+  std::vector<int64_t> hy = {4, 0, 6, 3, 2, 3, 5, 1};
+  std::vector<std::vector<float>> finals;
+  for (int variant = 0; variant < 2; ++variant) {  // 0: no prefetch, 1: prefetch
+    std::mt19937 rng(99);
+    TinyCfg c;
+    nn::Model m = build_tiny(c, rng, /*grad=*/true);
+    m.gradient_checkpointing = true;
+    Tensor x = Tensor::from_host(hx.data(), {B, T}, DType::kInt64, kHIP0);
+    Tensor y = Tensor::from_host(hy.data(), {B, T}, DType::kInt64, kHIP0);
+    optim::AdamW opt(params_of(m), /*lr=*/1e-2f, /*wd=*/0.0f, 0.9f, 0.95f, 1e-8f,
+                     /*offload=*/true);
+    opt.set_offload_chunk(64);  // the embedding (64 floats) is one chunk of many
+    opt.set_prefetch_chunks(variant == 0 ? 0 : 32);
+    bool armed = false;
+    m.recompute_hook = [&opt, &armed](int layer) {
+      if (armed && layer == 0) opt.prefetch();
+    };
+    for (int step = 0; step < 3; ++step) {
+      opt.zero_grad();
+      Tensor loss = m.forward_train(x, y);
+      armed = true;
+      loss.backward();
+      armed = false;
+      if (step == 1) {  // rewrite the embedding's first moment on the host
+        Tensor& mt = opt.m_tensor(0, 0);
+        float* hm = static_cast<float*>(mt.data_ptr());
+        for (int64_t i = 0; i < mt.numel(); ++i) hm[i] = 0.25f;
+      }
+      opt.step();
+      opt.wait_idle();
+      const double pf = opt.offload_stats().last_prefetch_bytes;
+      if (variant == 1 && step == 1) check(pf == 0.0, "a rewritten state drops the prefetch");
+      if (variant == 1 && step == 2) check(pf > 0.0, "the backward prefetched the embedding's state");
+      if (variant == 0) check(pf == 0.0, "no prefetch when switched off");
+    }
+    m.recompute_hook = nullptr;
+    finals.push_back(host(params_of(m)[0]));
+  }
+  check(finals[0] == finals[1], "prefetch leaves the weights bits unchanged");
+}
+
 // reference test_integration_kvcache.cpp:57-123 on a tiny random model
 void kv_cache_equivalences(TinyCfg c) {
   std::mt19937 rng(7);
@@ -271,6 +319,7 @@ int main() {
   run("ModelTrain.TrainLogitsMatchInferenceLogits_D64",
       [] { train_logits_match_inference_logits(TinyCfg{32, 128, 2, 1, 64, 64, 2, 1e-5f, 1e4f}); });
   run("ModelTrain.OverfitsTinyBatch", [] { overfits_tiny_batch(); });
+  run("Optim.PrefetchThenHostStateChange", [] { prefetch_then_host_state_change(); });
   run("Integration.KVCacheEquivalences", [] { kv_cache_equivalences(TinyCfg{}); });
   run("Integration.KVCacheEquivalences_D64",
       [] { kv_cache_equivalences(TinyCfg{32, 128, 2, 1, 64, 64, 2, 1e-5f, 1e4f}); });
