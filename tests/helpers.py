@@ -1,5 +1,6 @@
 """Shared helpers for the parity tests (device buffers via torch, tolerances)."""
 import ctypes as C
+import math
 
 import numpy as np
 
@@ -63,3 +64,30 @@ def call(name, *args):
 def f32ptr(arr):
     arr = np.ascontiguousarray(arr, dtype=np.float32)
     return arr, arr.ctypes.data_as(C.POINTER(C.c_float))
+
+
+def assert_matches_golden(golden, prefix, got, rtol=1e-4, rows=False):
+    """Checks `got` against the summaries tests/golden/make_golden.py stored for
+    it: every sampled value within rtol*|b| + rtol*max|b|, the L2 norm (from the
+    sum of squares) and the maximum magnitude within rtol, the total sum within
+    rtol of the norm times sqrt(n), and (rows=True) every row's sum and L2 norm."""
+    got = np.asarray(got, dtype=np.float64)
+    flat = got.reshape(-1)
+    maxabs = float(golden[prefix + ".maxabs"])
+    idx = golden[prefix + ".idx"]
+    ref = golden[prefix + ".val"]
+    err = np.abs(flat[idx] - ref)
+    bound = rtol * np.abs(ref) + rtol * maxabs
+    assert (err <= bound).all(), (prefix, "samples", float(err.max()), float(bound[err.argmax()]))
+    norm_ref = math.sqrt(float(golden[prefix + ".sumsq"]))
+    norm = math.sqrt(float((flat * flat).sum()))
+    assert abs(norm - norm_ref) <= rtol * norm_ref, (prefix, "L2", norm, norm_ref)
+    assert abs(float(np.abs(flat).max()) - maxabs) <= rtol * maxabs, (prefix, "max")
+    assert abs(float(flat.sum()) - float(golden[prefix + ".sum"])) <= rtol * norm_ref * math.sqrt(
+        flat.size), (prefix, "sum")
+    if rows:
+        r2 = got.reshape(-1, got.shape[-1])
+        rs, rq = golden[prefix + ".row_sum"], golden[prefix + ".row_sumsq"]
+        rn = np.sqrt(rq)
+        assert (np.abs(r2.sum(1) - rs) <= rtol * rn * math.sqrt(r2.shape[1])).all(), (prefix, "row sums")
+        assert (np.abs(np.sqrt((r2 * r2).sum(1)) - rn) <= rtol * rn).all(), (prefix, "row norms")

@@ -9,18 +9,22 @@ against the CPU oracle, plus the checkpointing and offload invariants.
   loss and every gradient, with QK-Norm and with llama3 RoPE scaling.
 - c2 full SmolLM2-135M step at B4 T512 and c5 full Qwen3-1.7B step at B8 T4096:
   checkpoint on/off bitwise identical (c5: every gradient, by digest).
+- c1 block and c2 full step against the golden fixtures (tests/golden), an
+  independent float64 torch composition frozen in files.
 Tolerance: |a-b| <= 1e-4|b| + 1e-4 max|b| and relative L2 <= 1e-4; AdamW 1e-5.
 """
 import hashlib
 import json
 import math
+import os
 import struct
 
 import numpy as np
 import pytest
 
 import oracle as O
-from tests.helpers import assert_close
+from tests.golden import make_golden as MG
+from tests.helpers import assert_close, assert_matches_golden
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -112,6 +116,61 @@ def test_c1_block_fwd_bwd_checkpoint_and_offloaded_adamw():
             err = np.abs(got - ref)
             bound = 1e-5 * np.abs(ref) + 1e-6 * np.abs(ref).max()
             assert (err <= bound).all(), (k, nm, float(err.max()))
+    tr.close()
+
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def test_c1_block_vs_golden():
+    # The HIP block against the independent float64 torch fixture for
+    # BASELINE config 0 (tests/golden/make_golden.py), checkpointing off and on.
+    g = np.load(os.path.join(GOLDEN, "c1_block.npz"), allow_pickle=False)
+    w, x, dy = MG.c1_inputs()
+    c = TR.make_config(**C1)
+    tr = TR.Trainer(c, seed=0, init_std=0.02, norm_value=None)
+    lp = layer_params(tr, c, 0)
+    assert sorted(lp) == sorted(MG.BLOCK_KEYS)
+    for k, (i, _) in lp.items():
+        tr.set_param(i, w[k])
+    for ckpt in (False, True):
+        tr.zero_grad()
+        y, dx = tr.block_step(0, x, dy, checkpoint=ckpt)
+        assert_matches_golden(g, "y", y, rows=True)
+        assert_matches_golden(g, "dx", dx, rows=True)
+        for k, (i, _) in lp.items():
+            assert_matches_golden(g, "d_" + k, tr.get_grad(i))
+    tr.close()
+
+
+def test_c2_smollm2_step_vs_golden():
+    # BASELINE config 1 at full size (SmolLM2-135M, B=4, T=512, masked loss)
+    # against the independent float64 torch fixture: the loss and the
+    # gradients of the embedding (tied head), all of layer 0, the last layer's
+    # down projection and the final norm.
+    g = np.load(os.path.join(GOLDEN, "c2_model.npz"), allow_pickle=False)
+    params, ids, tg, mask = MG.c2_inputs()
+    c = TR.preset("smollm2-135m")
+    tr = TR.Trainer(c, seed=0, init_std=0.02)
+    names = ["embed"] + [f"l{i}.{k}" for i in range(c.num_layers) for k in MG.BLOCK_KEYS] + ["norm"]
+    assert tr.num_params() == len(params) == len(names)
+    for i, (name, prm) in enumerate(zip(tr.names, params)):
+        want = names[i]
+        if want == "embed":
+            assert name == "model.embed_tokens.weight"
+        elif want == "norm":
+            assert name == "model.norm.weight"
+        else:
+            layer, key = want[1:].split(".")
+            assert name.startswith(f"model.layers.{layer}.") and name.split(".")[-2] == key, name
+        assert tr.numels[i] == prm.size, name
+        tr.set_param(i, prm)
+    tr.set_batch(ids, tg, mask)
+    tr.set_checkpointing(True)
+    loss = tr.forward_backward(True)
+    assert abs(loss - float(g["loss"])) <= 1e-4 * abs(float(g["loss"])), (loss, float(g["loss"]))
+    for i in [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, len(names) - 2, len(names) - 1]:
+        assert_matches_golden(g, "g." + names[i], tr.get_grad(i))
     tr.close()
 
 
