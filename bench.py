@@ -372,7 +372,7 @@ def main():
         "config": {"workload": f"{args.workload} B{B} T{T} "
                                f"{'recompute' if ckpt else 'no-recompute'}"
                                f"{'+offload' if offload else ''}",
-                   "model": preset, "global_batch": B, "seq_len": T, "parallelism": "none (1 GPU)",
+                   "batch": B, "seq_len": T, "parallelism": "none (1 GPU)",
                    "gradient_checkpointing": ckpt, "offload_optimizer": offload,
                    "params": n_params},
         "peak_hbm_gb": round(mem.peak_allocated / 1e9, 3),
