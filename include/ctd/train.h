@@ -90,12 +90,12 @@ Batch make_batch(const DataSplit& split, const std::vector<int64_t>& doc_indices
 float lr_at_step(int step, const Config& c);
 
 // Layer whose re-run in the backward pass starts the offloaded optimizer's
-// prefetch (nn::Model::recompute_hook -> optim::AdamW::prefetch): layer 0,
-// the last one the backward re-runs.  Its re-run and backward (about 96 ms
-// at Qwen3-1.7B, B=8, T=4096) cover the transfer of the embedding's m/v
-// (2.55 GB, about 51 ms), and the staging buffer is held for the shortest
-// time (layer 1 measured the same step time and a 0.07 GB higher peak).
-constexpr int kOptimizerPrefetchLayer = 0;
+// prefetch (nn::Model::recompute_hook -> optim::AdamW::prefetch): layer 1,
+// the second-to-last one the backward re-runs, so that two layers of
+// backward cover the transfer of the embedding's m/v (2.55 GB, about 45 ms,
+// at Qwen3-1.7B; 2.15 GB against 2 x 26 ms of backward at LLaMA-3.2-1B,
+// B=4, T=2048).  Models of one layer get no prefetch.
+constexpr int kOptimizerPrefetchLayer = 1;
 
 // Mask-weighted mean masked CE over the whole split, one document per forward
 // (main.cpp:191-206).

@@ -305,7 +305,7 @@ def test_overlapped_offload_train_steps_equal_on_device():
 def test_prefetched_offload_with_checkpointing_equals_on_device(chunk):
     # With checkpointing on, train_step's backward stages the m/v of the first
     # parameter in streaming order (the embedding) on the device when it re-runs
-    # layer 0 (AdamW::prefetch), and step() updates those chunks from there.
+    # layer 1 (AdamW::prefetch), and step() updates those chunks from there.
     # chunk 3000: the embedding spans 43 chunks, more than the 32 prefetched;
     # 1 << 20: the whole state is one chunk, so step() copies nothing in;
     # 50000: the third prefetched chunk runs past the embedding into layer 0.
