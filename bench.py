@@ -251,6 +251,9 @@ def main():
     ap.add_argument("--decode-only", action="store_true",
                     help="only the inference measurement (greedy ctd_generate loop on the "
                          "workload's model): prints one JSON line with the decode points")
+    ap.add_argument("--prefetch-layer", type=int, default=None,
+                    help="layer whose re-run in the backward starts that prefetch (-1: none; "
+                         "default: the library's estimate for the model and batch)")
     ap.add_argument("--link-probe", action="store_true",
                     help="only the pinned host<->device copy rates of this box (one JSON line)")
     args = ap.parse_args()
@@ -302,6 +305,8 @@ def main():
     tr.make_optimizer(lr=1e-4, weight_decay=0.1, beta1=0.9, beta2=0.95, eps=1e-8, offload=offload)
     if args.prefetch_chunks is not None:
         tr.set_prefetch_chunks(args.prefetch_chunks)
+    if args.prefetch_layer is not None:
+        tr.set_prefetch_layer(args.prefetch_layer)
     tr.synthetic_batch(B, T, seed=0, masked=masked)
     log(f"[bench] setup {time.time() - t0:.1f}s")
 

@@ -362,8 +362,10 @@ int run(const Config& cfg) {
     ~HookReset() { m.recompute_hook = nullptr; }
   } hook_reset{model};
   if (cfg.offload_optimizer) {
-    model.recompute_hook = [&opt, &prefetch_armed](int layer) {
-      if (prefetch_armed && layer == kOptimizerPrefetchLayer) opt.prefetch();
+    const int at = optimizer_prefetch_layer(
+        model.config, static_cast<int64_t>(cfg.batch_size) * cfg.seq_len);
+    model.recompute_hook = [&opt, &prefetch_armed, at](int layer) {
+      if (prefetch_armed && layer == at) opt.prefetch();
     };
   }
 

@@ -104,6 +104,9 @@ struct Trainer {
   // Set while train_step's backward runs: only then does the model's
   // recompute hook start the offloaded optimizer's prefetch.
   bool prefetch_armed = false;
+  // Layer whose re-run starts it: >= 0 that layer, -1 never, -2 the estimate
+  // of train::optimizer_prefetch_layer for the batch.
+  int prefetch_layer = -2;
 };
 
 
@@ -381,7 +384,11 @@ int ctd_trainer_make_optimizer(ctd_trainer_t t, float lr, float weight_decay, fl
     tr->opt = std::make_unique<optim::AdamW>(std::move(groups), beta1, beta2, eps, offload != 0);
     if (offload) {
       tr->model.recompute_hook = [tr](int layer) {
-        if (tr->prefetch_armed && layer == train::kOptimizerPrefetchLayer) tr->opt->prefetch();
+        if (!tr->prefetch_armed) return;
+        const int at = tr->prefetch_layer >= -1
+                           ? tr->prefetch_layer
+                           : train::optimizer_prefetch_layer(tr->model.config, tr->B * tr->T);
+        if (layer == at) tr->opt->prefetch();
       };
     }
     if (chunk_elems > 0) tr->opt->set_offload_chunk(chunk_elems);
@@ -454,6 +461,13 @@ int ctd_trainer_set_prefetch_chunks(ctd_trainer_t t, int64_t chunks) {
     if (!tr->opt) throw std::runtime_error("no optimizer");
     if (chunks < 0) throw std::runtime_error("prefetch chunks must be >= 0");
     tr->opt->set_prefetch_chunks(chunks);
+  });
+}
+
+int ctd_trainer_set_prefetch_layer(ctd_trainer_t t, int32_t layer) {
+  return guarded([&] {
+    if (layer < -2) throw std::runtime_error("prefetch layer must be >= -2");
+    as_trainer(t)->prefetch_layer = layer;
   });
 }
 

@@ -73,6 +73,7 @@ _SIGS = {
     "ctd_trainer_offload_stats": (i32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_double),
                                         C.POINTER(C.c_double)]),
     "ctd_trainer_set_prefetch_chunks": (i32, [vp, i64]),
+    "ctd_trainer_set_prefetch_layer": (i32, [vp, i32]),
     "ctd_trainer_train_step": (i32, [vp, f32, C.POINTER(StepTimes)]),
     "ctd_trainer_synchronize": (i32, [vp]),
     "ctd_memory_stats": (i32, [C.POINTER(Memory)]),
@@ -297,6 +298,12 @@ class Trainer:
         """Cap (in optimizer-state chunks) of the m/v that train_step's backward
         stages on the device for the offloaded step; 0 turns it off."""
         _ck(lib().ctd_trainer_set_prefetch_chunks(self.h, int(chunks)), "set_prefetch_chunks")
+
+    def set_prefetch_layer(self, layer):
+        """Layer whose re-run in train_step's backward starts the prefetch:
+        an index, -1 for none, -2 (default) for the estimate from the model
+        and batch."""
+        _ck(lib().ctd_trainer_set_prefetch_layer(self.h, int(layer)), "set_prefetch_layer")
 
     def synchronize(self):
         _ck(lib().ctd_trainer_synchronize(self.h), "synchronize")

@@ -5,6 +5,7 @@
 // clipping, loss.jsonl logging, validation, and checkpoint save / resume with
 // the optimizer state.  `emberlm_amd/lib/ctd_train --config <path>` runs it.
 
+#include <cmath>
 #include <cstdint>
 #include <filesystem>
 #include <string>
@@ -90,12 +91,29 @@ Batch make_batch(const DataSplit& split, const std::vector<int64_t>& doc_indices
 float lr_at_step(int step, const Config& c);
 
 // Layer whose re-run in the backward pass starts the offloaded optimizer's
-// prefetch (nn::Model::recompute_hook -> optim::AdamW::prefetch): layer 1,
-// the second-to-last one the backward re-runs, so that two layers of
-// backward cover the transfer of the embedding's m/v (2.55 GB, about 45 ms,
-// at Qwen3-1.7B; 2.15 GB against 2 x 26 ms of backward at LLaMA-3.2-1B,
-// B=4, T=2048).  Models of one layer get no prefetch.
-constexpr int kOptimizerPrefetchLayer = 1;
+// prefetch (nn::Model::recompute_hook -> optim::AdamW::prefetch) for a batch
+// of `tokens`, or -1 for no prefetch.  The backward of that layer and of the
+// ones below it should cover the prefetch's copies, the embedding's m and v
+// (8 V d bytes) at about 50 GB/s, so that step() need not wait for them.  A
+// layer's backward re-runs its forward and runs its own, about 6 x tokens x
+// (its parameters) flops, estimated at 130 TFLOP/s.  Only a lead of one or
+// two layers is used, where the prefetch pays for its staging buffer
+// (Qwen3-1.7B at B=8, T=4096: layer 1, step 4045 -> 4006 ms for +0.8 GB of
+// peak HBM; LLaMA-3.2-1B at B=4, T=2048: layer 2, 828 -> 771 ms).  Models
+// that would need more lead have short forwards that wait little for the
+// update (Qwen3-0.6B at B=4, T=1024, layer 9: 278 -> 276 ms for a peak of
+// 6.12 -> 6.75 GB; SmolLM2-135M, layer 14: 105.5 -> 105.1 ms).
+inline int optimizer_prefetch_layer(const nn::LlamaConfig& c, int64_t tokens) {
+  constexpr double kMaxLead = 2.0;
+  const double d = c.hidden_size, D = c.head_dim;
+  const double layer_params = d * D * (2.0 * c.num_attention_heads + 2.0 * c.num_key_value_heads) +
+                              3.0 * d * c.intermediate_size;
+  const double layer_s = 6.0 * static_cast<double>(tokens) * layer_params / 130e12;
+  const double copy_s = 8.0 * c.vocab_size * d / 50e9;
+  const double k = layer_s > 0.0 ? std::ceil(copy_s / layer_s) : kMaxLead + 1.0;
+  if (k > kMaxLead || static_cast<int>(k) > c.num_hidden_layers - 1) return -1;
+  return k < 1.0 ? 1 : static_cast<int>(k);
+}
 
 // Mask-weighted mean masked CE over the whole split, one document per forward
 // (main.cpp:191-206).

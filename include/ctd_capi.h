@@ -115,6 +115,10 @@ int ctd_trainer_offload_stats(ctd_trainer_t t, double* stream_ms, double* bytes_
  * The staged m/v of the first parameter are device memory held from late in
  * the backward until their copy out. */
 int ctd_trainer_set_prefetch_chunks(ctd_trainer_t t, int64_t chunks);
+/* Layer whose re-run in train_step's backward starts that prefetch: a layer
+ * index, -1 for none, or -2 (the default) for ctd::train's estimate from the
+ * model and batch (include/ctd/train.h, optimizer_prefetch_layer). */
+int ctd_trainer_set_prefetch_layer(ctd_trainer_t t, int32_t layer);
 
 /* One full training step (forward, backward, clip to max_norm when > 0,
  * optimizer step, zero_grad) with HIP-event phase times. */

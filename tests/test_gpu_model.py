@@ -315,6 +315,7 @@ def test_prefetched_offload_with_checkpointing_equals_on_device(chunk):
     for t in (a, b):
         t.set_checkpointing(True)
     a.make_optimizer(lr=1e-3, weight_decay=0.1, offload=True, chunk_elems=chunk)
+    a.set_prefetch_layer(1)  # the estimate skips the prefetch for a model this small
     b.make_optimizer(lr=1e-3, weight_decay=0.1, offload=False)
     losses = {id(a): [], id(b): []}
     for step in range(4):
