@@ -97,6 +97,8 @@ SIGNATURES = {
     "ember_decode_gateup": (i32, [vp, i64, i64, vp, f32, vp, vp, i64, vp, vp]),
     "ember_decode_qkv_post": (i32, [vp, vp, vp, i64, i64, i64, i64, i64, vp, vp, f32,
                                     C.POINTER(f32), i64, vp, vp, vp, i64, vp]),
+    "ember_attn_decode_qkv": (i32, [vp, vp, vp, i64, i64, i64, i64, i64, vp, vp, f32,
+                                    C.POINTER(f32), i64, vp, vp, i64, f32, vp, vp, sz, vp]),
 }
 
 _lib = None

@@ -163,43 +163,86 @@ Tensor decode_gate_up(const Tensor& x, const Tensor& norm_w, float eps, const Te
   return out;
 }
 
-Tensor decode_qkv_post(const Tensor& q, const Tensor& k, const Tensor& v, int num_heads,
-                       int num_kv_heads, int head_dim, const Tensor& q_norm_w,
-                       const Tensor& k_norm_w, float eps, float theta, const RopeScaling& scaling,
-                       int position_start, Tensor& k_cache, Tensor& v_cache) {
-  check_f32(q, "decode_qkv_post", "q");
-  check_f32(k, "decode_qkv_post", "k");
-  check_f32(v, "decode_qkv_post", "v");
-  check_f32(k_cache, "decode_qkv_post", "k cache");
-  check_f32(v_cache, "decode_qkv_post", "v cache");
+namespace {
+
+// Checks shared by decode_qkv_post and decode_qkv_attention; returns the
+// RoPE frequencies of head_dim under theta / scaling.
+std::vector<float> check_qkv_post(const char* op, const Tensor& q, const Tensor& k,
+                                  const Tensor& v, int64_t H, int64_t Hk, int64_t D,
+                                  const Tensor& q_norm_w, const Tensor& k_norm_w, float theta,
+                                  const RopeScaling& scaling, int position_start,
+                                  const Tensor& k_cache, const Tensor& v_cache) {
+  const std::string o(op);
+  check_f32(q, op, "q");
+  check_f32(k, op, "k");
+  check_f32(v, op, "v");
+  check_f32(k_cache, op, "k cache");
+  check_f32(v_cache, op, "v cache");
   require(q.dim() == 3 && k.dim() == 3 && k.shape() == v.shape(),
-          "decode_qkv_post: expected q [B,T,H*D], k/v [B,T,Hk*D]");
+          o + ": expected q [B,T,H*D], k/v [B,T,Hk*D]");
   const int64_t B = q.shape()[0], T = q.shape()[1];
-  const int64_t H = num_heads, Hk = num_kv_heads, D = head_dim;
   require(q.shape()[2] == H * D && k.shape()[0] == B && k.shape()[1] == T &&
               k.shape()[2] == Hk * D,
-          "decode_qkv_post: q/k/v widths != heads * head_dim");
+          o + ": q/k/v widths != heads * head_dim");
   require(k_cache.dim() == 4 && k_cache.shape() == v_cache.shape() && k_cache.shape()[0] == B &&
               k_cache.shape()[1] == Hk && k_cache.shape()[3] == D,
-          "decode_qkv_post: cache / src dim mismatch");
-  const int64_t max_seq = k_cache.shape()[2];
-  require(position_start >= 0 && position_start + T <= max_seq,
+          o + ": cache / src dim mismatch");
+  require(position_start >= 0 && position_start + T <= k_cache.shape()[2],
           "write_kv: write range out of cache bounds");
   for (const Tensor* w : {&q_norm_w, &k_norm_w})
     if (w->defined()) {
-      check_f32(*w, "decode_qkv_post", "norm weight");
-      require(w->numel() == D, "decode_qkv_post: QK-Norm weight size != head_dim");
+      check_f32(*w, op, "norm weight");
+      require(w->numel() == D, o + ": QK-Norm weight size != head_dim");
     }
   std::vector<float> freqs(static_cast<size_t>(D / 2));
   CTD_CHECK(ember_rope_freqs_host(freqs.data(), static_cast<int>(D), theta, scaling.factor,
                                   scaling.low_freq_factor, scaling.high_freq_factor,
                                   scaling.original_max_pos));
+  return freqs;
+}
+
+}  // namespace
+
+Tensor decode_qkv_post(const Tensor& q, const Tensor& k, const Tensor& v, int num_heads,
+                       int num_kv_heads, int head_dim, const Tensor& q_norm_w,
+                       const Tensor& k_norm_w, float eps, float theta, const RopeScaling& scaling,
+                       int position_start, Tensor& k_cache, Tensor& v_cache) {
+  const int64_t H = num_heads, Hk = num_kv_heads, D = head_dim;
+  const std::vector<float> freqs =
+      check_qkv_post("decode_qkv_post", q, k, v, H, Hk, D, q_norm_w, k_norm_w, theta, scaling,
+                     position_start, k_cache, v_cache);
+  const int64_t B = q.shape()[0], T = q.shape()[1], max_seq = k_cache.shape()[2];
   Tensor qo = Tensor::empty({B, T, H, D}, DType::kFloat32, q.device());
   CTD_CHECK(ember_decode_qkv_post(cfp(q), cfp(k), cfp(v), B, T, H, Hk, D,
                                   q_norm_w.defined() ? cfp(q_norm_w) : nullptr,
                                   k_norm_w.defined() ? cfp(k_norm_w) : nullptr, eps, freqs.data(),
                                   position_start, fp(qo), fp(k_cache), fp(v_cache), max_seq, S()));
   return qo;
+}
+
+Tensor decode_qkv_attention(const Tensor& q, const Tensor& k, const Tensor& v, int num_heads,
+                            int num_kv_heads, int head_dim, const Tensor& q_norm_w,
+                            const Tensor& k_norm_w, float eps, float theta,
+                            const RopeScaling& scaling, int position_start, Tensor& k_cache,
+                            Tensor& v_cache, float scale) {
+  const int64_t H = num_heads, Hk = num_kv_heads, D = head_dim;
+  const std::vector<float> freqs =
+      check_qkv_post("decode_qkv_attention", q, k, v, H, Hk, D, q_norm_w, k_norm_w, theta,
+                     scaling, position_start, k_cache, v_cache);
+  require(Hk > 0 && H % Hk == 0, "decode_qkv_attention: num_heads % num_kv_heads != 0");
+  require(D == 64 || D == 128, "decode_qkv_attention: head_dim must be 64 or 128");
+  const int64_t B = q.shape()[0], T = q.shape()[1], max_seq = k_cache.shape()[2];
+  require(T <= kDecodeMaxRows, "decode_qkv_attention: more than 8 new rows per call");
+  Tensor o = Tensor::empty({B, T, H, D}, DType::kFloat32, q.device());
+  if (B == 0 || T == 0) return o;
+  const size_t wsb = ember_attn_decode_workspace_bytes(B, T, H, Hk, D, position_start + T);
+  Tensor ws = wsb ? workspace(wsb) : Tensor{};
+  CTD_CHECK(ember_attn_decode_qkv(cfp(q), cfp(k), cfp(v), B, T, H, Hk, D,
+                                  q_norm_w.defined() ? cfp(q_norm_w) : nullptr,
+                                  k_norm_w.defined() ? cfp(k_norm_w) : nullptr, eps, freqs.data(),
+                                  position_start, fp(k_cache), fp(v_cache), max_seq, scale, fp(o),
+                                  wsb ? ws.data_ptr() : nullptr, wsb, S()));
+  return o;
 }
 
 }  // namespace ctd::ops

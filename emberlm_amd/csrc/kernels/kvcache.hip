@@ -108,13 +108,60 @@ __device__ __forceinline__ float dot4(f32x4 a, f32x4 b) {
   return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
 }
 
-template <int D>
-__global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
+// The QK-Norm + RoPE + cache write of a decode step, folded into the
+// attention launch (ember_attn_decode_qkv): q is then the raw query
+// projection and the new key/value rows [pos, pos + T) come from kn / vn.
+constexpr int kMaxRopePairs = 64;  // D <= 128
+constexpr int kFoldRows = 8;       // new rows per call (T): a decode step's
+struct QkvFold {
+  const float* kn;    // [B, T, Hk, D] key projection
+  const float* vn;    // [B, T, Hk, D] value projection
+  const float* qn_w;  // [D] QK-Norm weights, or null (no norm)
+  const float* kn_w;
+  float* ck;          // the caches that DecodeArgs::k / v read
+  float* cv;
+  float eps;
+  float freqs[kMaxRopePairs];
+};
+
+// One D-float row spread over the LPK lanes of a key group, a float4 each:
+// RMSNorm with weight w (skipped when w is null), then the rotation of each
+// pair (i, i + D/2) by the angle whose cosine and sine are cs[i] and sn[i],
+// lanes d4 < LPK/2 holding the first halves and lane d4 + LPK/2 the partners.
+// With cs, sn the sincosf of float(position) * freq[i], the products are those
+// of the standalone QK-Norm and RoPE kernels; only the order of the norm's sum
+// of squares differs.
+template <int LPK>
+__device__ __forceinline__ f32x4 norm_rope(f32x4 x, int d4, const float* w, float eps,
+                                           const float* cs, const float* sn) {
+  if (w) {
+    const float rs =
+        1.0f / sqrtf(group_sum<LPK>(dot4(x, x)) / static_cast<float>(4 * LPK) + eps);
+    const f32x4 wv = *reinterpret_cast<const f32x4*>(w + 4 * d4);
+    x = f32x4{x.x * rs * wv.x, x.y * rs * wv.y, x.z * rs * wv.z, x.w * rs * wv.w};
+  }
+  const f32x4 y = {__shfl_xor(x.x, LPK / 2, kWave), __shfl_xor(x.y, LPK / 2, kWave),
+                   __shfl_xor(x.z, LPK / 2, kWave), __shfl_xor(x.w, LPK / 2, kWave)};
+  const bool first = d4 < LPK / 2;
+  const int f0 = 4 * (d4 % (LPK / 2));
+  f32x4 out;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const float cv = cs[f0 + c], sv = sn[f0 + c];
+    out[c] = first ? x[c] * cv - y[c] * sv : y[c] * sv + x[c] * cv;
+  }
+  return out;
+}
+
+template <int D, bool FOLD>
+__device__ __forceinline__ void attn_decode_body(const DecodeArgs& a, const QkvFold& f) {
   constexpr int LPK = D / 4;          // lanes per key row
   constexpr int KPW = kWave / LPK;    // keys per wave load
   constexpr int NG = kWaves * KPW;    // independent softmax groups per workgroup
+  constexpr int HALF = D / 2;
   __shared__ float s_ml[NG][kRowTile][2];
   __shared__ f32x4 s_o[NG][kRowTile][LPK];
+  __shared__ float s_rot[FOLD ? kFoldRows : 1][2][HALF];  // fold: cos, sin per (new row, pair)
 
   const int lane = threadIdx.x & (kWave - 1);
   const int w = threadIdx.x / kWave;
@@ -133,8 +180,62 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
   const float* vbase = a.v + b * a.kv_sb + hk * a.kv_sh + 4 * d4;
   const int64_t R = G * a.T;  // query rows of this KV head: r -> (t = r / G, h = hk*G + r % G)
 
+  // Raw q of a row tile; the first tile's is loaded before the fold's
+  // barriers, so its latency overlaps them.
+  f32x4 qraw[kRowTile];
+  auto load_q = [&](int64_t r0) {
+#pragma unroll
+    for (int r = 0; r < kRowTile; ++r) {
+      qraw[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (r0 + r < R) {
+        const int64_t t = (r0 + r) / G;
+        const int64_t h = hk * G + (r0 + r) % G;
+        qraw[r] = *reinterpret_cast<const f32x4*>(a.q + ((b * a.T + t) * a.H + h) * D + 4 * d4);
+      }
+    }
+  };
+  load_q(0);
+
+  if constexpr (FOLD) {
+    // This split's share of the new rows [pos, pos + T) (ke <= L = pos + T):
+    // normalised, rotated keys and the values into the cache, one row per
+    // lane group.  No other workgroup reads these rows in this launch; this
+    // one reads them after the second barrier.  The rotations' cosines and
+    // sines are tabulated once per workgroup, T * D/2 sincosf in parallel,
+    // while the raw rows load.
+    const int64_t p0 = (ks > a.pos ? ks : a.pos) + g_id;
+    f32x4 kraw = {0.f, 0.f, 0.f, 0.f}, vraw = {0.f, 0.f, 0.f, 0.f};
+    const int64_t row0 = ((b * a.T + (p0 - a.pos)) * a.Hk + hk) * D + 4 * d4;
+    if (p0 < ke) {
+      kraw = *reinterpret_cast<const f32x4*>(f.kn + row0);
+      vraw = *reinterpret_cast<const f32x4*>(f.vn + row0);
+    }
+    for (int e = threadIdx.x; e < a.T * HALF; e += kThreads) {
+      const int t = e / HALF, i = e % HALF;
+      float sn, cs;
+      sincosf(static_cast<float>(a.pos + t) * f.freqs[i], &sn, &cs);
+      s_rot[t][0][i] = cs;
+      s_rot[t][1][i] = sn;
+    }
+    __syncthreads();
+    for (int64_t p = p0; p < ke; p += NG) {
+      const int64_t t = p - a.pos;
+      if (p != p0) {
+        const int64_t src = ((b * a.T + t) * a.Hk + hk) * D + 4 * d4;
+        kraw = *reinterpret_cast<const f32x4*>(f.kn + src);
+        vraw = *reinterpret_cast<const f32x4*>(f.vn + src);
+      }
+      const int64_t dst = b * a.kv_sb + hk * a.kv_sh + p * a.kv_st + 4 * d4;
+      *reinterpret_cast<f32x4*>(f.ck + dst) =
+          norm_rope<LPK>(kraw, d4, f.kn_w, f.eps, s_rot[t][0], s_rot[t][1]);
+      *reinterpret_cast<f32x4*>(f.cv + dst) = vraw;
+    }
+    __syncthreads();
+  }
+
   for (int64_t r0 = 0; r0 < R; r0 += kRowTile) {
     const int nr = static_cast<int>(R - r0 < kRowTile ? R - r0 : kRowTile);
+    if (r0 > 0) load_q(r0);
     f32x4 q[kRowTile], acc[kRowTile];
     float m[kRowTile], l[kRowTile];
     int lim[kRowTile];  // keys j < lim[r] are visible to row r
@@ -147,11 +248,11 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
       q[r] = f32x4{0.f, 0.f, 0.f, 0.f};
       lim[r] = static_cast<int>(ks);
       if (r < nr) {
-        const int64_t row = r0 + r;
-        const int64_t t = row / G;
-        const int64_t h = hk * G + row % G;
-        q[r] = *reinterpret_cast<const f32x4*>(a.q + ((b * a.T + t) * a.H + h) * D + 4 * d4) *
-               a.qscale;
+        const int64_t t = (r0 + r) / G;
+        q[r] = qraw[r];
+        if constexpr (FOLD)
+          q[r] = norm_rope<LPK>(q[r], d4, f.qn_w, f.eps, s_rot[t][0], s_rot[t][1]);
+        q[r] *= a.qscale;
         const int64_t c = a.pos + t + 1;  // causal: key j <= pos + t
         lim[r] = static_cast<int>(c < ke ? c : ke);
         jend = lim[r] > jend ? lim[r] : jend;
@@ -245,6 +346,16 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
       }
     }
   }
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
+  attn_decode_body<D, false>(a, QkvFold{});
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void attn_decode_qkv_kernel(DecodeArgs a, QkvFold f) {
+  attn_decode_body<D, true>(a, f);
 }
 
 // One wave per output row: merge the splits in split order.  The split
@@ -362,18 +473,15 @@ extern "C" size_t ember_attn_decode_workspace_bytes(int64_t B, int64_t T, int64_
   return static_cast<size_t>(B * T * H) * p.nsplit * (D + 2) * sizeof(float);
 }
 
-extern "C" int ember_attn_decode(const float* q, const float* k, const float* v, float* o,
-                                 int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D,
-                                 int64_t L, int64_t pos, int64_t kv_sb, int64_t kv_sh,
-                                 int64_t kv_st, float scale, void* workspace,
-                                 size_t workspace_bytes, ember_stream_t s) {
-  if (B < 0 || T < 0 || H <= 0 || Hk <= 0 || H % Hk != 0 || pos < 0) return EMBER_EINVAL;
-  if (D != 64 && D != 128) return EMBER_EINVAL;
-  if (B == 0 || T == 0) return EMBER_OK;
-  if (L < 1 || !q || !k || !v || !o) return EMBER_EINVAL;
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || kv_sb % 4 ||
-      kv_sh % 4 || kv_st % 4)
-    return EMBER_EINVAL;
+namespace {
+
+// Shared by ember_attn_decode and ember_attn_decode_qkv (fold != null): checks
+// the split plan against the grid and the workspace, launches the split
+// kernel, then the merge when there is more than one split.
+int run_decode(const float* q, const float* k, const float* v, float* o, int64_t B, int64_t T,
+               int64_t H, int64_t Hk, int64_t D, int64_t L, int64_t pos, int64_t kv_sb,
+               int64_t kv_sh, int64_t kv_st, float scale, void* workspace,
+               size_t workspace_bytes, const QkvFold* fold, hipStream_t st) {
   const DecodePlan p = decode_plan(B, Hk, L);
   const int64_t blocks = B * Hk * p.nsplit;
   if (blocks > 0x7fffffff) return EMBER_EINVAL;
@@ -398,9 +506,12 @@ extern "C" int ember_attn_decode(const float* q, const float* k, const float* v,
   a.kps = p.kps;
   a.nsplit = p.nsplit;
   a.qscale = scale * 1.4426950408889634f;
-  hipStream_t st = as_stream(s);
   const unsigned grid = static_cast<unsigned>(blocks);
-  if (D == 128)
+  if (fold && D == 128)
+    attn_decode_qkv_kernel<128><<<grid, kThreads, 0, st>>>(a, *fold);
+  else if (fold)
+    attn_decode_qkv_kernel<64><<<grid, kThreads, 0, st>>>(a, *fold);
+  else if (D == 128)
     attn_decode_kernel<128><<<grid, kThreads, 0, st>>>(a);
   else
     attn_decode_kernel<64><<<grid, kThreads, 0, st>>>(a);
@@ -412,4 +523,52 @@ extern "C" int ember_attn_decode(const float* q, const float* k, const float* v,
   else
     attn_decode_combine<64><<<cgrid, kThreads, 0, st>>>(a.part_o, a.part_ml, o, rows, p.nsplit);
   return launch_status();
+}
+
+}  // namespace
+
+extern "C" int ember_attn_decode(const float* q, const float* k, const float* v, float* o,
+                                 int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D,
+                                 int64_t L, int64_t pos, int64_t kv_sb, int64_t kv_sh,
+                                 int64_t kv_st, float scale, void* workspace,
+                                 size_t workspace_bytes, ember_stream_t s) {
+  if (B < 0 || T < 0 || H <= 0 || Hk <= 0 || H % Hk != 0 || pos < 0) return EMBER_EINVAL;
+  if (D != 64 && D != 128) return EMBER_EINVAL;
+  if (B == 0 || T == 0) return EMBER_OK;
+  if (L < 1 || !q || !k || !v || !o) return EMBER_EINVAL;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || kv_sb % 4 ||
+      kv_sh % 4 || kv_st % 4)
+    return EMBER_EINVAL;
+  return run_decode(q, k, v, o, B, T, H, Hk, D, L, pos, kv_sb, kv_sh, kv_st, scale, workspace,
+                    workspace_bytes, nullptr, as_stream(s));
+}
+
+extern "C" int ember_attn_decode_qkv(const float* q, const float* k, const float* v, int64_t B,
+                                     int64_t T, int64_t H, int64_t Hk, int64_t D,
+                                     const float* q_norm_w, const float* k_norm_w, float eps,
+                                     const float* freqs_host, int64_t pos, float* cache_k,
+                                     float* cache_v, int64_t S, float scale, float* o,
+                                     void* workspace, size_t workspace_bytes, ember_stream_t s) {
+  if (B < 0 || T < 0 || H <= 0 || Hk <= 0 || H % Hk != 0 || pos < 0 || pos + T > S ||
+      !freqs_host)
+    return EMBER_EINVAL;
+  if ((D != 64 && D != 128) || T > kFoldRows) return EMBER_EINVAL;
+  if (B == 0 || T == 0) return EMBER_OK;
+  if (!q || !k || !v || !o || !cache_k || !cache_v) return EMBER_EINVAL;
+  for (const float* ptr : {q, k, v, static_cast<const float*>(o),
+                           static_cast<const float*>(cache_k), static_cast<const float*>(cache_v)})
+    if (!aligned16(ptr)) return EMBER_EINVAL;
+  if ((q_norm_w && !aligned16(q_norm_w)) || (k_norm_w && !aligned16(k_norm_w)))
+    return EMBER_EINVAL;
+  QkvFold f{};
+  f.kn = k;
+  f.vn = v;
+  f.qn_w = q_norm_w;
+  f.kn_w = k_norm_w;
+  f.ck = cache_k;
+  f.cv = cache_v;
+  f.eps = eps;
+  for (int64_t i = 0; i < D / 2; ++i) f.freqs[i] = freqs_host[i];
+  return run_decode(q, cache_k, cache_v, o, B, T, H, Hk, D, pos + T, pos, Hk * S * D, S * D, D,
+                    scale, workspace, workspace_bytes, &f, as_stream(s));
 }

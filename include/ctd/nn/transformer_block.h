@@ -18,7 +18,8 @@ struct TransformerBlock {
 
   // Inference forward.  With a KV cache and at most ops::kDecodeMaxRows token
   // rows (a decode step), the fused decode kernels run the same functions in
-  // six launches; otherwise the module ops run one by one.
+  // five launches (six when long contexts split the keys); otherwise the
+  // module ops run one by one.
   Tensor forward(const Tensor& x, KVLayer* kv = nullptr, int position_start = 0) const {
     autograd::NoGradGuard ng;
     if (kv != nullptr && x.dim() == 3 && x.shape()[0] * x.shape()[1] <= ops::kDecodeMaxRows &&
@@ -38,11 +39,10 @@ struct TransformerBlock {
     const int H = at.num_heads, Hk = at.num_kv_heads, D = at.head_dim;
     auto qkv = ops::decode_linear(x, input_layernorm.weight, input_layernorm.eps,
                                   {at.q_proj.weight, at.k_proj.weight, at.v_proj.weight});
-    Tensor q = ops::decode_qkv_post(qkv[0], qkv[1], qkv[2], H, Hk, D, at.q_norm.weight,
-                                    at.k_norm.weight, at.q_norm.eps, at.rope_theta,
-                                    at.rope_scaling, position_start, kv.k, kv.v);
-    Tensor a = ops::cached_attention(q, kv.k, kv.v, position_start + T, position_start,
-                                     1.0f / std::sqrt(static_cast<float>(D)));
+    Tensor a = ops::decode_qkv_attention(qkv[0], qkv[1], qkv[2], H, Hk, D, at.q_norm.weight,
+                                         at.k_norm.weight, at.q_norm.eps, at.rope_theta,
+                                         at.rope_scaling, position_start, kv.k, kv.v,
+                                         1.0f / std::sqrt(static_cast<float>(D)));
     Tensor h = ops::decode_linear(a.reshape({B, T, static_cast<int64_t>(H) * D}), Tensor{}, 0.0f,
                                   {at.o_proj.weight}, {x})[0];
     Tensor m = ops::decode_gate_up(h, post_attention_layernorm.weight,

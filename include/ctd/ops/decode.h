@@ -33,4 +33,13 @@ Tensor decode_qkv_post(const Tensor& q, const Tensor& k, const Tensor& v, int nu
                        const Tensor& k_norm_w, float eps, float theta, const RopeScaling& scaling,
                        int position_start, Tensor& k_cache, Tensor& v_cache);
 
+// decode_qkv_post followed by cached_attention(q, k_cache, v_cache,
+// position_start + T, position_start, scale), in one launch (plus the split
+// merge).  Returns the attention output [B,T,H,D].
+Tensor decode_qkv_attention(const Tensor& q, const Tensor& k, const Tensor& v, int num_heads,
+                            int num_kv_heads, int head_dim, const Tensor& q_norm_w,
+                            const Tensor& k_norm_w, float eps, float theta,
+                            const RopeScaling& scaling, int position_start, Tensor& k_cache,
+                            Tensor& v_cache, float scale);
+
 }  // namespace ctd::ops

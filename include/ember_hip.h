@@ -260,6 +260,22 @@ int ember_decode_qkv_post(const float* q, const float* k, const float* v, int64_
                           const float* k_norm_w, float eps, const float* freqs_host, int64_t pos,
                           float* q_out, float* cache_k, float* cache_v, int64_t S,
                           ember_stream_t s);
+/* ember_decode_qkv_post then ember_attn_decode over the cache, in the
+ * attention's launch: q [B,T,H,D] and k, v [B,T,Hk,D] are the raw
+ * projections; the normalised, rotated k and v go to cache rows
+ * [pos, pos + T) of cache_k / cache_v [B,Hk,S,D], and o [B,T,H,D] is the
+ * attention of the normalised, rotated q over cache rows [0, pos + T), query t
+ * seeing rows j <= pos + t.  Each workgroup writes, then reads, only the new
+ * rows inside its own key split.  T <= 8, D in {64,128}; pointers 16-byte aligned;
+ * `workspace` >= ember_attn_decode_workspace_bytes(B, T, H, Hk, D, pos + T).
+ * Replaces Attention::forward's q_norm/k_norm, apply_rope_inplace,
+ * write_kv_inplace and the attention over the cache (attention.h:55-91);
+ * EMBER_EINVAL unless pos + T <= S. */
+int ember_attn_decode_qkv(const float* q, const float* k, const float* v, int64_t B, int64_t T,
+                          int64_t H, int64_t Hk, int64_t D, const float* q_norm_w,
+                          const float* k_norm_w, float eps, const float* freqs_host, int64_t pos,
+                          float* cache_k, float* cache_v, int64_t S, float scale, float* o,
+                          void* workspace, size_t workspace_bytes, ember_stream_t s);
 
 /* ------------------------------------------------------------- sampling
  * out[r] = index of the largest value of row r of x [rows, n], the first such

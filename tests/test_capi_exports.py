@@ -76,6 +76,17 @@ def test_inference_entry_validation_without_gpu():
     assert lib.ember_attn_decode(None, None, None, None, *args) == -1
     args = (1, 1, 4, 2, 64, 0, 0, 0, 0, 0, 1.0, None, 0, None)
     assert lib.ember_attn_decode(None, None, None, None, *args) == -1
+    # folded QK-Norm/RoPE/cache write: pos + T <= S, D in {64,128}, H % Hk == 0
+    f = (C.c_float * 64)()
+    qkv = lambda B, T, H, Hk, D, pos, S: lib.ember_attn_decode_qkv(
+        None, None, None, B, T, H, Hk, D, None, None, 1e-6, f, pos, None, None, S, 1.0, None,
+        None, 0, None)
+    assert qkv(1, 2, 4, 2, 64, 7, 8) == -1
+    assert qkv(1, 1, 4, 2, 96, 0, 8) == -1
+    assert qkv(1, 1, 3, 2, 64, 0, 8) == -1
+    assert qkv(1, 9, 4, 2, 64, 0, 16) == -1                              # T <= 8
+    assert qkv(1, 1, 4, 2, 64, 0, 8) == -1                               # null pointers
+    assert qkv(0, 1, 4, 2, 64, 0, 8) == 0                                # nothing to do
     # short key ranges need no workspace; long ones split into >= 64-key chunks
     assert lib.ember_attn_decode_workspace_bytes(1, 1, 16, 8, 128, 10) == 0
     ws = lib.ember_attn_decode_workspace_bytes(1, 1, 16, 8, 128, 4096)

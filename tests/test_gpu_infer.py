@@ -8,6 +8,10 @@ tools/ctd_generate/main.cpp) against the CPU oracle.
   cache layout and the projection layout, one to five query heads per KV head,
   D 64/128, short and split key ranges (up to 8192 keys), T > 1 with an offset;
   bitwise run-to-run.
+- QK-Norm + RoPE + cache write folded into the decode attention
+  (ember_attn_decode_qkv) against the oracle and against the two launches it
+  replaces, new rows inside one split and across a split boundary; the value
+  rows and the untouched cache rows bitwise.
 - Skinny GEMM (M <= 8 rows, the decode Linear) against the oracle.
 - Device argmax against the host scan (ties, NaN, -inf), bitwise.
 - Model::forward with a cache, as the reference's KVCachePrefillEquivalence
@@ -220,6 +224,60 @@ def test_decode_qkv_post_vs_oracle(B, T, H, Hk, D, pos, qk, factor):
     keep[pos:pos + T] = False                       # other cache rows untouched
     assert np.array_equal(got_k[:, :, keep], ck0[:, :, keep])
     assert np.array_equal(got_v[:, :, keep], cv0[:, :, keep])
+
+
+@pytest.mark.parametrize("B,T,H,Hk,D,pos,S,qk,factor", [
+    (1, 1, 16, 8, 128, 4095, 4096, True, 0.0),   # qwen3-1.7b heads, full context, 64 splits
+    (1, 1, 16, 8, 128, 300, 512, True, 0.0),     # 5 splits
+    (2, 3, 8, 2, 64, 17, 24, False, 32.0),       # llama3 frequencies, one split
+    (1, 2, 9, 3, 64, 0, 4, False, 0.0),          # the cache's first rows
+    (1, 7, 4, 2, 128, 1018, 1030, True, 0.0),    # new rows 1018..1024 across splits 31 | 32
+])
+def test_decode_attention_qkv_fold(B, T, H, Hk, D, pos, S, qk, factor):
+    r = rng(H * D + pos + T)
+    theta, eps, scale, L = 5e5, 1e-6, 1.0 / np.sqrt(D), pos + T
+    q = r.standard_normal((B, T, H, D)).astype(np.float32)
+    k = r.standard_normal((B, T, Hk, D)).astype(np.float32)
+    v = r.standard_normal((B, T, Hk, D)).astype(np.float32)
+    qn, kn = ((1 + 0.1 * r.standard_normal(D)).astype(np.float32) for _ in range(2))
+    ck0 = r.standard_normal((B, Hk, S, D)).astype(np.float32)
+    cv0 = r.standard_normal((B, Hk, S, D)).astype(np.float32)
+    freqs = (C.c_float * (D // 2))()
+    capi.check(capi.lib().ember_rope_freqs_host(freqs, D, theta, factor, 1.0, 4.0, 64))
+    qd, kd, vd, qnd, knd = dev(q), dev(k), dev(v), dev(qn), dev(kn)
+    wsb = capi.lib().ember_attn_decode_workspace_bytes(B, T, H, Hk, D, L)
+    ws = empty((max(1, wsb // 4),))
+
+    def fused():
+        ck, cv, o = dev(ck0), dev(cv0), empty((B, T, H, D))
+        call("ember_attn_decode_qkv", p(qd), p(kd), p(vd), B, T, H, Hk, D,
+             p(qnd) if qk else None, p(knd) if qk else None, eps, freqs, pos, p(ck), p(cv), S,
+             scale, p(o), p(ws) if wsb else None, wsb, None)
+        return host(o), host(ck), host(cv)
+
+    o, got_k, got_v = fused()
+    rope = dict(theta=theta, pos0=pos, factor=factor, low=1.0, high=4.0, orig=64)
+    qr = O.rope(O.rmsnorm_fwd(q, qn, eps) if qk else q, **rope)
+    kr = O.rope(O.rmsnorm_fwd(k, kn, eps) if qk else k, **rope)
+    assert_close(got_k[:, :, pos:L], kr.transpose(0, 2, 1, 3), name="k cache")
+    assert np.array_equal(got_v[:, :, pos:L], v.transpose(0, 2, 1, 3))
+    keep = np.ones(S, bool)
+    keep[pos:L] = False                             # other cache rows untouched
+    assert np.array_equal(got_k[:, :, keep], ck0[:, :, keep])
+    assert np.array_equal(got_v[:, :, keep], cv0[:, :, keep])
+    kf, vf = ck0[:, :, :L].astype(np.float64), cv0[:, :, :L].astype(np.float64)
+    kf[:, :, pos:L] = kr.transpose(0, 2, 1, 3)
+    vf[:, :, pos:L] = v.transpose(0, 2, 1, 3)
+    ref = O.attention_offset(qr, kf.transpose(0, 2, 1, 3), vf.transpose(0, 2, 1, 3), pos, scale)
+    assert_close(o, ref, name="o")
+    # the two launches it replaces, on the same inputs
+    ck, cv, qo = dev(ck0), dev(cv0), empty((B, T, H, D))
+    call("ember_decode_qkv_post", p(qd), p(kd), p(vd), B, T, H, Hk, D, p(qnd) if qk else None,
+         p(knd) if qk else None, eps, freqs, pos, p(qo), p(ck), p(cv), S, None)
+    assert_close(o, decode(host(qo), host(ck), host(cv), L, pos, "cache", scale), rtol=1e-5,
+                 name="o vs qkv_post + attn_decode")
+    again = fused()
+    assert all(np.array_equal(a, b) for a, b in zip(again, (o, got_k, got_v)))  # reproducible
 
 
 # ------------------------------------------------------------------ argmax
