@@ -653,9 +653,14 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch) {
   }
   const int64_t tiles = cdiv(M, 128) * cdiv(N, 128) * batch;
   const int64_t target = 6 * kCUs;  // two waves of 3 blocks per CU
-  if (batch == 1 && tiles < target && K >= 4096) {
+  // K chunks of at least 1024 from K = 4096 up.  A grid that would fill at
+  // most half the CUs (e.g. the projections of a short prefill, M = 128) is
+  // latency-bound on its one pass over K: chunks of at least 256 from K = 512.
+  const bool few = 2 * tiles <= kCUs;
+  const int64_t min_chunk = few ? 256 : 1024;
+  if (batch == 1 && tiles < target && K >= (few ? 2 * min_chunk : 4096)) {
     int64_t s = std::min<int64_t>(16, cdiv(target, tiles));
-    s = std::min<int64_t>(s, K / 1024);
+    s = std::min<int64_t>(s, K / min_chunk);
     if (s >= 2) {
       p.kchunk = cdiv(cdiv(K, s), kBK) * kBK;
       p.splits = cdiv(K, p.kchunk);

@@ -61,6 +61,17 @@ def test_argument_validation_without_gpu():
     assert lib.ember_ce_masked_fwd_workspace_bytes(32768) == 32768 * 4
 
 
+def test_gemm_split_plan_without_gpu():
+    lib = capi.lib()
+    # a short prefill's projection (M = 128, 16 tiles): 8 K chunks of 256
+    assert lib.ember_gemm_f32_workspace_bytes(128, 2048, 2048, 1) == 8 * 128 * 2048 * 4
+    # the c5 k/v weight gradient (128 tiles, K = 32768 tokens): 12 chunks
+    assert lib.ember_gemm_f32_workspace_bytes(1024, 2048, 32768, 1) == 12 * 1024 * 2048 * 4
+    # enough tiles, or K too short to split: one pass over K
+    assert lib.ember_gemm_f32_workspace_bytes(4096, 2048, 2048, 1) == 0
+    assert lib.ember_gemm_f32_workspace_bytes(128, 2048, 511, 1) == 0
+
+
 def test_inference_entry_validation_without_gpu():
     lib = capi.lib()
     # cache rows [pos, pos+T) must fit in S

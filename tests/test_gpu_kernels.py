@@ -121,10 +121,11 @@ def gemm_ws(a, b, ta, tb, alpha=1.0, beta=0.0, c=None, ws_bytes=None):
 
 
 @pytest.mark.parametrize("ta,tb,K", [(1, 0, 5003), (0, 0, 5003), (0, 1, 5003), (1, 1, 5003),
-                                     (1, 0, 5008), (0, 1, 5008)])
+                                     (1, 0, 5008), (0, 1, 5008), (0, 1, 1000), (0, 1, 2048)])
 def test_gemm_split_k_vs_oracle(ta, tb, K):
-    # Few output tiles and a long K: the K-split path with partials (K % 16 == 0
-    # takes the LDS-DMA kernel, a ragged K the register-staged one).
+    # Few output tiles: the K-split path with partials (K % 16 == 0 takes the
+    # LDS-DMA kernel, a ragged K the register-staged one), 16 splits of a long K
+    # and 3 or 8 of a short one.
     M, N = 132, 200
     r = rng(11 + 2 * ta + tb)
     a = r.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
