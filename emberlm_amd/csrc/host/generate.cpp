@@ -241,14 +241,14 @@ int run(const std::string& model_path, const std::string& request, std::ostream&
   try {
     const Request req = parse_request(request);
     const auto t0 = std::chrono::steady_clock::now();
-    log << "[ctd_generate] loading " << model_path << "\n";
+    log << "ctd_generate: weights " << model_path << "\n";
     const TensorDict weights = load_safetensors(model_path, kHIP0);
     const nn::LlamaConfig cfg = model_config.empty() ? nn::autodetect_config(weights)
                                                      : train::load_model_config(model_config);
-    log << "[ctd_generate] arch: hidden=" << cfg.hidden_size
-        << " layers=" << cfg.num_hidden_layers << "\n";
+    log << "ctd_generate: " << cfg.num_hidden_layers << " layers of width " << cfg.hidden_size
+        << ", vocabulary " << cfg.vocab_size << "\n";
     const nn::Model model = nn::build_model(weights, cfg);
-    log << "[ctd_generate] model ready in " << seconds_since(t0) << " s\n";
+    log << "ctd_generate: loaded in " << seconds_since(t0) << " s\n";
 
     const int prompt_len = static_cast<int>(req.input_ids.size());
     if (prompt_len == 0) {
@@ -264,11 +264,10 @@ int run(const std::string& model_path, const std::string& request, std::ostream&
     const LoopResult r = generate_loop(model, req, [&](int64_t tok) {
       out << line(json::ObjectWriter().field("token", tok)) << std::flush;
     });
-    log << "[ctd_generate] prefill (" << prompt_len << " tok) in " << r.prefill_ms / 1e3
-        << " s\n";
     const double dt = r.decode_ms / 1e3;
-    log << "[ctd_generate] generated " << r.generated << " tok in " << dt << " s  ("
-        << r.generated / std::max(dt, 1e-9) << " tok/s)\n";
+    log << "ctd_generate: prompt of " << prompt_len << " tokens in " << r.prefill_ms << " ms, "
+        << r.generated << " new tokens in " << dt << " s (" << r.generated / std::max(dt, 1e-9)
+        << " tokens/s)\n";
     out << line(json::ObjectWriter()
                     .field("done", true)
                     .field("generated_tokens", r.generated)
@@ -276,7 +275,7 @@ int run(const std::string& model_path, const std::string& request, std::ostream&
         << std::flush;
     return 0;
   } catch (const std::exception& e) {
-    log << "[ctd_generate] error: " << e.what() << "\n";
+    log << "ctd_generate: error: " << e.what() << "\n";
     out << line(json::ObjectWriter()
                     .field("done", true)
                     .field("error", e.what())

@@ -190,32 +190,38 @@ inline std::string number_text(double v) {
   return s;
 }
 
+// Appends s as a JSON string literal: quotes, backslashes and the short
+// control escapes, other control bytes as \u00XX, everything else verbatim.
+inline void append_quoted(std::string& out, const std::string& s) {
+  out += '"';
+  for (char c : s) {
+    switch (c) {
+      case '"': out += "\\\""; break;
+      case '\\': out += "\\\\"; break;
+      case '\b': out += "\\b"; break;
+      case '\f': out += "\\f"; break;
+      case '\n': out += "\\n"; break;
+      case '\r': out += "\\r"; break;
+      case '\t': out += "\\t"; break;
+      default:
+        if (static_cast<unsigned char>(c) < 0x20) {
+          char buf[8];
+          std::snprintf(buf, sizeof(buf), "\\u%04x", static_cast<unsigned>(c));
+          out += buf;
+        } else {
+          out += c;
+        }
+    }
+  }
+  out += '"';
+}
+
 // Compact one-line object writer, keys in the order given.
 class ObjectWriter {
  public:
   ObjectWriter& field(const std::string& k, const std::string& v) {
     key(k);
-    out_ += '"';
-    for (char c : v) {
-      switch (c) {
-        case '"': out_ += "\\\""; break;
-        case '\\': out_ += "\\\\"; break;
-        case '\b': out_ += "\\b"; break;
-        case '\f': out_ += "\\f"; break;
-        case '\n': out_ += "\\n"; break;
-        case '\r': out_ += "\\r"; break;
-        case '\t': out_ += "\\t"; break;
-        default:
-          if (static_cast<unsigned char>(c) < 0x20) {
-            char buf[8];
-            std::snprintf(buf, sizeof(buf), "\\u%04x", static_cast<unsigned>(c));
-            out_ += buf;
-          } else {
-            out_ += c;
-          }
-      }
-    }
-    out_ += '"';
+    append_quoted(out_, v);
     return *this;
   }
   ObjectWriter& field(const std::string& k, bool v) {

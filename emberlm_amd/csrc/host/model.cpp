@@ -205,89 +205,107 @@ Tensor Model::forward_train_masked(const Tensor& input_ids, const Tensor& target
 }
 
 namespace {
-const Tensor& must(const TensorDict& w, const std::string& key) {
+
+// The weights of one decoder layer as data: the HF key under
+// "model.layers.<i>.", whether AdamW decays it (the projections) or not (the
+// norms), whether it exists only in QK-Norm models, and the block member that
+// holds it.  The row order is collect_parameters' order within a layer, which
+// fixes the checkpoint's tensor order and the optimizer-state layout
+// (src/nn/model.cpp:63-100 of the reference lists the same keys in the same
+// order).
+struct LayerWeight {
+  const char* key;
+  bool decay;
+  bool qk_norm_only;
+  Tensor& (*slot)(TransformerBlock&);
+};
+
+constexpr LayerWeight kLayerWeights[] = {
+    {"input_layernorm.weight", false, false,
+     [](TransformerBlock& b) -> Tensor& { return b.input_layernorm.weight; }},
+    {"self_attn.q_proj.weight", true, false,
+     [](TransformerBlock& b) -> Tensor& { return b.self_attn.q_proj.weight; }},
+    {"self_attn.k_proj.weight", true, false,
+     [](TransformerBlock& b) -> Tensor& { return b.self_attn.k_proj.weight; }},
+    {"self_attn.v_proj.weight", true, false,
+     [](TransformerBlock& b) -> Tensor& { return b.self_attn.v_proj.weight; }},
+    {"self_attn.o_proj.weight", true, false,
+     [](TransformerBlock& b) -> Tensor& { return b.self_attn.o_proj.weight; }},
+    {"self_attn.q_norm.weight", false, true,
+     [](TransformerBlock& b) -> Tensor& { return b.self_attn.q_norm.weight; }},
+    {"self_attn.k_norm.weight", false, true,
+     [](TransformerBlock& b) -> Tensor& { return b.self_attn.k_norm.weight; }},
+    {"post_attention_layernorm.weight", false, false,
+     [](TransformerBlock& b) -> Tensor& { return b.post_attention_layernorm.weight; }},
+    {"mlp.gate_proj.weight", true, false,
+     [](TransformerBlock& b) -> Tensor& { return b.mlp.gate_proj.weight; }},
+    {"mlp.up_proj.weight", true, false,
+     [](TransformerBlock& b) -> Tensor& { return b.mlp.up_proj.weight; }},
+    {"mlp.down_proj.weight", true, false,
+     [](TransformerBlock& b) -> Tensor& { return b.mlp.down_proj.weight; }},
+};
+
+constexpr const char* kEmbedKey = "model.embed_tokens.weight";  // also the tied LM head
+constexpr const char* kFinalNormKey = "model.norm.weight";
+
+std::string layer_prefix(size_t i) { return "model.layers." + std::to_string(i) + "."; }
+
+const Tensor& required(const TensorDict& w, const std::string& key) {
   auto it = w.find(key);
-  if (it == w.end()) throw std::runtime_error("build_model: missing weight '" + key + "'");
+  if (it == w.end()) throw std::runtime_error("build_model: the weights have no tensor " + key);
   return it->second;
 }
-Tensor maybe(const TensorDict& w, const std::string& key) {
-  auto it = w.find(key);
-  return it != w.end() ? it->second : Tensor{};
-}
+
 }  // namespace
 
 Model build_model(const TensorDict& w, const LlamaConfig& cfg) {
   Model m;
   m.config = cfg;
-  m.embed_tokens = Embedding{must(w, "model.embed_tokens.weight")};
-  m.norm = RMSNorm{must(w, "model.norm.weight"), cfg.rms_norm_eps};
-  m.layers.reserve(static_cast<size_t>(cfg.num_hidden_layers));
-  for (int i = 0; i < cfg.num_hidden_layers; ++i) {
-    const std::string p = "model.layers." + std::to_string(i) + ".";
-    TransformerBlock blk{
-        .input_layernorm = {must(w, p + "input_layernorm.weight"), cfg.rms_norm_eps},
-        .post_attention_layernorm = {must(w, p + "post_attention_layernorm.weight"),
-                                     cfg.rms_norm_eps},
-        .self_attn =
-            {
-                .q_proj = {must(w, p + "self_attn.q_proj.weight")},
-                .k_proj = {must(w, p + "self_attn.k_proj.weight")},
-                .v_proj = {must(w, p + "self_attn.v_proj.weight")},
-                .o_proj = {must(w, p + "self_attn.o_proj.weight")},
-                .num_heads = cfg.num_attention_heads,
-                .num_kv_heads = cfg.num_key_value_heads,
-                .head_dim = cfg.head_dim,
-                .rope_theta = cfg.rope_theta,
-                .rope_scaling = {cfg.rope_scaling_factor, cfg.rope_scaling_low_freq_factor,
-                                 cfg.rope_scaling_high_freq_factor,
-                                 cfg.rope_scaling_original_max_pos},
-                .q_norm = {maybe(w, p + "self_attn.q_norm.weight"), cfg.rms_norm_eps},
-                .k_norm = {maybe(w, p + "self_attn.k_norm.weight"), cfg.rms_norm_eps},
-            },
-        .mlp =
-            {
-                .gate_proj = {must(w, p + "mlp.gate_proj.weight")},
-                .up_proj = {must(w, p + "mlp.up_proj.weight")},
-                .down_proj = {must(w, p + "mlp.down_proj.weight")},
-            },
-    };
-    m.layers.push_back(std::move(blk));
+  m.embed_tokens.weight = required(w, kEmbedKey);
+  m.norm = RMSNorm{required(w, kFinalNormKey), cfg.rms_norm_eps};
+  const ops::RopeScaling scaling{cfg.rope_scaling_factor, cfg.rope_scaling_low_freq_factor,
+                            cfg.rope_scaling_high_freq_factor, cfg.rope_scaling_original_max_pos};
+  m.layers.resize(static_cast<size_t>(cfg.num_hidden_layers));
+  for (size_t i = 0; i < m.layers.size(); ++i) {
+    TransformerBlock& blk = m.layers[i];
+    Attention& a = blk.self_attn;
+    a.num_heads = cfg.num_attention_heads;
+    a.num_kv_heads = cfg.num_key_value_heads;
+    a.head_dim = cfg.head_dim;
+    a.rope_theta = cfg.rope_theta;
+    a.rope_scaling = scaling;
+    for (RMSNorm* n : {&blk.input_layernorm, &blk.post_attention_layernorm, &a.q_norm, &a.k_norm})
+      n->eps = cfg.rms_norm_eps;
+    const std::string pre = layer_prefix(i);
+    for (const LayerWeight& lw : kLayerWeights) {
+      auto it = w.find(pre + lw.key);
+      if (it != w.end())
+        lw.slot(blk) = it->second;
+      else if (!lw.qk_norm_only)
+        required(w, pre + lw.key);  // throws
+    }
   }
   return m;
 }
 
 Model::NamedParameters Model::collect_parameters() {
   NamedParameters out;
-  auto add = [&](const std::string& name, Tensor& t, bool decay) {
+  auto take = [&out](std::string name, Tensor& t, bool decay) {
     t.requires_grad_(true);
-    out.all.emplace_back(name, t);
-    if (decay) {
-      out.decay.push_back(t);
-      out.decay_names.push_back(name);
-    } else {
-      out.no_decay.push_back(t);
-      out.no_decay_names.push_back(name);
-    }
+    (decay ? out.decay : out.no_decay).push_back(t);
+    (decay ? out.decay_names : out.no_decay_names).push_back(name);
+    out.all.emplace_back(std::move(name), t);
   };
-  add("model.embed_tokens.weight", embed_tokens.weight, true);  // tied with the LM head
+  take(kEmbedKey, embed_tokens.weight, true);
   for (size_t i = 0; i < layers.size(); ++i) {
-    const std::string p = "model.layers." + std::to_string(i) + ".";
-    auto& L = layers[i];
-    add(p + "input_layernorm.weight", L.input_layernorm.weight, false);
-    add(p + "self_attn.q_proj.weight", L.self_attn.q_proj.weight, true);
-    add(p + "self_attn.k_proj.weight", L.self_attn.k_proj.weight, true);
-    add(p + "self_attn.v_proj.weight", L.self_attn.v_proj.weight, true);
-    add(p + "self_attn.o_proj.weight", L.self_attn.o_proj.weight, true);
-    if (L.self_attn.has_qk_norm()) {
-      add(p + "self_attn.q_norm.weight", L.self_attn.q_norm.weight, false);
-      add(p + "self_attn.k_norm.weight", L.self_attn.k_norm.weight, false);
+    const std::string pre = layer_prefix(i);
+    for (const LayerWeight& lw : kLayerWeights) {
+      Tensor& t = lw.slot(layers[i]);
+      if (lw.qk_norm_only && !t.defined()) continue;
+      take(pre + lw.key, t, lw.decay);
     }
-    add(p + "post_attention_layernorm.weight", L.post_attention_layernorm.weight, false);
-    add(p + "mlp.gate_proj.weight", L.mlp.gate_proj.weight, true);
-    add(p + "mlp.up_proj.weight", L.mlp.up_proj.weight, true);
-    add(p + "mlp.down_proj.weight", L.mlp.down_proj.weight, true);
   }
-  add("model.norm.weight", norm.weight, false);
+  take(kFinalNormKey, norm.weight, false);
   return out;
 }
 

@@ -42,16 +42,22 @@ std::string read_text(const fs::path& p) {
   return ss.str();
 }
 
-std::vector<uint8_t> read_file(const fs::path& p) {
+// Reads a whole data file into `out`, whose element size the file's length
+// must be a multiple of.
+template <typename T>
+void read_array(const fs::path& p, std::vector<T>& out) {
+  std::error_code ec;
+  const uintmax_t bytes = fs::file_size(p, ec);
+  if (ec) throw std::runtime_error("data: cannot stat " + p.string() + " (" + ec.message() + ")");
+  if (bytes % sizeof(T) != 0)
+    throw std::runtime_error("data: " + p.string() + " is " + std::to_string(bytes) +
+                             " bytes, not a whole number of " + std::to_string(sizeof(T)) +
+                             "-byte values");
+  out.resize(static_cast<size_t>(bytes / sizeof(T)));
   std::ifstream f(p, std::ios::binary);
-  if (!f) throw std::runtime_error("cannot open " + p.string());
-  f.seekg(0, std::ios::end);
-  const auto sz = static_cast<size_t>(f.tellg());
-  f.seekg(0, std::ios::beg);
-  std::vector<uint8_t> buf(sz);
-  if (sz > 0 && !f.read(reinterpret_cast<char*>(buf.data()), static_cast<std::streamsize>(sz)))
-    throw std::runtime_error("short read " + p.string());
-  return buf;
+  if (!f || (bytes > 0 && !f.read(reinterpret_cast<char*>(out.data()),
+                                  static_cast<std::streamsize>(bytes))))
+    throw std::runtime_error("data: cannot read " + p.string());
 }
 
 const json::JVal* key(const json::JVal& j, const char* k) { return j.find(k); }
@@ -157,19 +163,19 @@ Config load_config(const fs::path& cfg_path) {
 
 DataSplit load_split(const fs::path& tok_path, const fs::path& mask_path, int seq_len) {
   if (seq_len < 2) throw std::runtime_error("load_split: seq_len must be >= 2");
-  const auto tok_bytes = read_file(tok_path);
-  const auto mask_bytes = read_file(mask_path);
-  const size_t row_bytes = static_cast<size_t>(seq_len) * 4;
-  if (tok_bytes.size() % row_bytes != 0)
-    throw std::runtime_error("token bin size not multiple of seq_len*4: " + tok_path.string());
   DataSplit s;
-  s.num_docs = static_cast<int64_t>(tok_bytes.size() / row_bytes);
-  if (static_cast<int64_t>(mask_bytes.size()) != s.num_docs * seq_len)
-    throw std::runtime_error("mask size mismatch for " + mask_path.string());
-  s.tokens.resize(static_cast<size_t>(s.num_docs) * static_cast<size_t>(seq_len));
-  if (!tok_bytes.empty()) std::memcpy(s.tokens.data(), tok_bytes.data(), tok_bytes.size());
-  s.masks.resize(mask_bytes.size());
-  if (!mask_bytes.empty()) std::memcpy(s.masks.data(), mask_bytes.data(), mask_bytes.size());
+  read_array(tok_path, s.tokens);
+  read_array(mask_path, s.masks);
+  const size_t per_doc = static_cast<size_t>(seq_len);
+  if (s.tokens.size() % per_doc != 0)
+    throw std::runtime_error("data: " + tok_path.string() + " holds " +
+                             std::to_string(s.tokens.size()) + " tokens, not whole documents of " +
+                             std::to_string(seq_len));
+  s.num_docs = static_cast<int64_t>(s.tokens.size() / per_doc);
+  if (s.masks.size() != s.tokens.size())
+    throw std::runtime_error("data: " + mask_path.string() + " has " +
+                             std::to_string(s.masks.size()) + " mask values for " +
+                             std::to_string(s.tokens.size()) + " tokens");
   return s;
 }
 
@@ -225,19 +231,42 @@ float lr_at_step(int step, const Config& c) {
 }
 
 float run_val(const nn::Model& model, const DataSplit& val, int seq_len, Device device) {
+  // The whole split goes to the device in one batch of copies; each document
+  // is then one forward over row views of it, its loss left on the device
+  // until every forward is queued, so the pass has no per-document round
+  // trip.  Weighting and skipping follow main.cpp:195-207: each document's
+  // masked-mean loss weighs by its own mask sum (summed in float, in token
+  // order, like make_host_batch), documents without targets are skipped, and
+  // the weighted sum is formed in double in document order.
+  if (val.num_docs == 0) return 0.0f;
+  std::vector<int64_t> all(static_cast<size_t>(val.num_docs));
+  for (int64_t i = 0; i < val.num_docs; ++i) all[static_cast<size_t>(i)] = i;
+  const HostBatch h = make_host_batch(val, all, seq_len);
+  const int64_t T = h.T;
+  const Tensor ids = Tensor::from_host(h.input_ids.data(), {h.B, T}, DType::kInt64, device);
+  const Tensor tgt = Tensor::from_host(h.targets.data(), {h.B, T}, DType::kInt64, device);
+  const Tensor msk = Tensor::from_host(h.loss_mask.data(), {h.B, T}, DType::kFloat32, device);
+
   autograd::NoGradGuard no_grad;
-  double sum_loss = 0.0, total_mask = 0.0;
-  for (int64_t i = 0; i < val.num_docs; ++i) {
-    Batch b = make_batch(val, {i}, seq_len, device);
-    if (b.sum_mask <= 0.0f) continue;
-    Tensor loss = model.forward_train_masked(b.input_ids, b.targets, b.loss_mask);
-    float l = 0.0f;
-    loss.copy_to_host(&l);
-    sum_loss += static_cast<double>(l) * static_cast<double>(b.sum_mask);
-    total_mask += static_cast<double>(b.sum_mask);
+  std::vector<float> weight;
+  std::vector<Tensor> losses;
+  for (int64_t d = 0; d < h.B; ++d) {
+    float w = 0.0f;
+    for (int64_t t = 0; t < T; ++t) w += h.loss_mask[static_cast<size_t>(d * T + t)];
+    if (w <= 0.0f) continue;
+    losses.push_back(model.forward_train_masked(ids.view_at(d * T, {1, T}),
+                                                tgt.view_at(d * T, {1, T}),
+                                                msk.view_at(d * T, {1, T})));
+    weight.push_back(w);
   }
-  if (total_mask <= 0.0) return 0.0f;
-  return static_cast<float>(sum_loss / total_mask);
+  double num = 0.0, den = 0.0;
+  for (size_t i = 0; i < losses.size(); ++i) {
+    float l = 0.0f;
+    losses[i].copy_to_host(&l);
+    num += static_cast<double>(l) * static_cast<double>(weight[i]);
+    den += static_cast<double>(weight[i]);
+  }
+  return den > 0.0 ? static_cast<float>(num / den) : 0.0f;
 }
 
 fs::path opt_path_for(const fs::path& weights_path) {
@@ -264,34 +293,26 @@ void save_optimizer_state(optim::AdamW& opt, const nn::Model::NamedParameters& n
 
 void load_optimizer_state(optim::AdamW& opt, const nn::Model::NamedParameters& named,
                           const fs::path& path) {
-  TensorDict o = load_safetensors(path, kCPU);
+  // Each m/v entry is read straight into the optimizer's own buffer: pinned
+  // host memory when offloaded, device memory otherwise.
+  const SafetensorsReader file(path);
   opt.ensure_state_initialized();
-  auto load_into = [&](Tensor& dst, const std::string& k) {
-    auto it = o.find(k);
-    if (it == o.end()) throw std::runtime_error("resume: missing " + k);
-    if (it->second.shape() != dst.shape()) throw std::runtime_error("resume: shape mismatch for " + k);
-    if (it->second.dtype() != DType::kFloat32) throw std::runtime_error("resume: expected fp32 for " + k);
-    if (dst.device().is_hip()) {
-      CTD_CHECK(ember_memcpy_async(dst.data_ptr(), it->second.data_ptr(), dst.nbytes(), 0,
-                                   runtime::compute_stream()));
-      runtime::synchronize();
-    } else {
-      std::memcpy(dst.data_ptr(), it->second.data_ptr(), dst.nbytes());
+  const std::vector<std::string>* names[2] = {&named.decay_names, &named.no_decay_names};
+  for (int g = 0; g < 2; ++g)
+    for (size_t i = 0; i < names[g]->size(); ++i) {
+      const std::string& n = (*names[g])[i];
+      for (const char* which : {"m", "v"}) {
+        const std::string k = std::string("optimizer.") + which + "." + n;
+        if (!file.find(k)) throw std::runtime_error("resume: " + path.string() + " lacks " + k);
+        Tensor dst = which[0] == 'm' ? opt.m_tensor(g, i) : opt.v_tensor(g, i);
+        file.read(k, dst);
+      }
     }
-  };
-  for (size_t i = 0; i < named.decay_names.size(); ++i) {
-    load_into(opt.m_tensor(0, i), "optimizer.m." + named.decay_names[i]);
-    load_into(opt.v_tensor(0, i), "optimizer.v." + named.decay_names[i]);
-  }
-  for (size_t i = 0; i < named.no_decay_names.size(); ++i) {
-    load_into(opt.m_tensor(1, i), "optimizer.m." + named.no_decay_names[i]);
-    load_into(opt.v_tensor(1, i), "optimizer.v." + named.no_decay_names[i]);
-  }
-  auto it = o.find("optimizer.step");
-  if (it == o.end()) throw std::runtime_error("resume: missing optimizer.step");
-  float step_f = 0.0f;
-  std::memcpy(&step_f, it->second.data_ptr(), sizeof(float));
-  opt.set_step_count(static_cast<int64_t>(step_f));
+  Tensor step = Tensor::empty({1}, DType::kFloat32, kCPU);
+  if (!file.find("optimizer.step"))
+    throw std::runtime_error("resume: " + path.string() + " lacks optimizer.step");
+  file.read("optimizer.step", step);
+  opt.set_step_count(static_cast<int64_t>(*static_cast<const float*>(step.data_ptr())));
 }
 
 std::string train_event(int step, float loss, float lr, float grad_norm, double tokens_per_sec,
@@ -319,10 +340,10 @@ std::string val_event(int step, float loss, double wall_s) {
 int run(const Config& cfg) {
   using clock = std::chrono::steady_clock;
   fs::create_directories(cfg.run_dir);
-  std::cerr << "[ctd_train] run=" << cfg.run_name << " dir=" << cfg.run_dir << "\n";
+  std::cerr << "ctd_train: run " << cfg.run_name << " in " << cfg.run_dir << "\n";
   const bool resuming = !cfg.resume_from.empty();
   const fs::path weights_path = resuming ? cfg.resume_from : cfg.init_weights;
-  std::cerr << "[ctd_train] " << (resuming ? "resuming from " : "loading init weights ")
+  std::cerr << "ctd_train: " << (resuming ? "resume weights " : "initial weights ")
             << weights_path << "\n";
   TensorDict weights = load_safetensors(weights_path, kHIP0);
   const nn::LlamaConfig arch = cfg.has_model ? cfg.model : nn::autodetect_config(weights);
@@ -330,8 +351,8 @@ int run(const Config& cfg) {
   weights.clear();
   model.gradient_checkpointing = cfg.gradient_checkpointing;
   auto named = model.collect_parameters();
-  std::cerr << "[ctd_train] parameters: " << named.decay.size() << " decay + "
-            << named.no_decay.size() << " no_decay\n";
+  std::cerr << "ctd_train: " << named.all.size() << " parameter tensors (" << named.decay.size()
+            << " with weight decay)\n";
 
   std::vector<Tensor> all_params;
   all_params.insert(all_params.end(), named.decay.begin(), named.decay.end());
@@ -375,10 +396,11 @@ int run(const Config& cfg) {
     if (fs::exists(op)) {
       load_optimizer_state(opt, named, op);
       start_step = opt.step_count();
-      std::cerr << "[ctd_train] resumed at step " << start_step << "\n";
+      std::cerr << "ctd_train: optimizer state from " << op << ", next step " << start_step + 1
+                << "\n";
     } else {
-      std::cerr << "[ctd_train] no optimizer state at " << op
-                << " - continuing with fresh m/v (warmup will restart)\n";
+      std::cerr << "ctd_train: " << op << " not found: m and v start from zero and the "
+                << "schedule from step 1\n";
     }
   }
 
@@ -387,7 +409,8 @@ int run(const Config& cfg) {
   const DataSplit val = load_split(cfg.data_dir / "val.bin", cfg.data_dir / "val_mask.bin",
                                    cfg.seq_len);
   if (train.num_docs < 1) throw std::runtime_error("train split is empty");
-  std::cerr << "[ctd_train] train=" << train.num_docs << " val=" << val.num_docs << "\n";
+  std::cerr << "ctd_train: " << train.num_docs << " training and " << val.num_docs
+            << " validation documents\n";
 
   std::mt19937_64 rng(cfg.seed + static_cast<uint64_t>(start_step));
   std::uniform_int_distribution<int64_t> pick(0, train.num_docs - 1);
@@ -432,30 +455,30 @@ int run(const Config& cfg) {
     if (cfg.log_every > 0 && step % cfg.log_every == 0) {
       log << train_event(step, train_loss, lr, grad_norm, tps, wall_s) << "\n";
       log.flush();
-      std::cerr << "[step " << step << "/" << cfg.total_steps << "] loss=" << train_loss
-                << " lr=" << lr << " |g|=" << grad_norm << " tok/s=" << static_cast<int>(tps)
-                << "\n";
+      std::cerr << "ctd_train: step " << step << " of " << cfg.total_steps << "  loss "
+                << train_loss << "  lr " << lr << "  grad norm " << grad_norm << "  "
+                << static_cast<int64_t>(tps) << " tokens/s\n";
     }
     if (cfg.val_every > 0 && step % cfg.val_every == 0) {
       const float vl = run_val(model, val, cfg.seq_len, kHIP0);
       const double w = std::chrono::duration<double>(clock::now() - t_run_start).count();
       log << val_event(step, vl, w) << "\n";
       log.flush();
-      std::cerr << "[step " << step << "] val_loss=" << vl << "\n";
+      std::cerr << "ctd_train: step " << step << "  validation loss " << vl << "\n";
     }
     if (cfg.save_every > 0 && step % cfg.save_every == 0) {
       const fs::path ckpt = cfg.run_dir / ("ckpt_step_" + std::to_string(step) + ".safetensors");
       runtime::synchronize();
       save_safetensors(named.all, ckpt);
       save_optimizer_state(opt, named, opt_path_for(ckpt));
-      std::cerr << "[step " << step << "] saved " << ckpt << " (+ optimizer)\n";
+      std::cerr << "ctd_train: step " << step << "  wrote " << ckpt << " and its optimizer state\n";
     }
   }
   const fs::path final_ckpt = cfg.run_dir / "final.safetensors";
   runtime::synchronize();
   save_safetensors(named.all, final_ckpt);
   save_optimizer_state(opt, named, opt_path_for(final_ckpt));
-  std::cerr << "[ctd_train] done. final -> " << final_ckpt << " (+ optimizer)\n";
+  std::cerr << "ctd_train: finished; wrote " << final_ckpt << " and its optimizer state\n";
   return 0;
 }
 

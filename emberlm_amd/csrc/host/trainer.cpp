@@ -578,15 +578,11 @@ int ctd_trainer_save(ctd_trainer_t t, const char* path) {
 int ctd_trainer_load(ctd_trainer_t t, const char* path) {
   return guarded([&] {
     Trainer* tr = as_trainer(t);
-    TensorDict w = load_safetensors(path, kCPU);
+    const SafetensorsReader file(path);  // each parameter is read straight into place
     for (auto& [name, p] : tr->named.all) {
-      auto it = w.find(name);
-      if (it == w.end()) throw std::runtime_error("load: missing " + name);
-      if (it->second.shape() != p.shape()) throw std::runtime_error("load: shape mismatch " + name);
-      CTD_CHECK(ember_memcpy_async(p.data_ptr(), it->second.data_ptr(), p.nbytes(), 0,
-                                   runtime::compute_stream()));
+      if (!file.find(name)) throw std::runtime_error(std::string("load: ") + path + " lacks " + name);
+      file.read(name, p);
     }
-    runtime::synchronize();
     if (tr->opt) train::load_optimizer_state(*tr->opt, tr->named, train::opt_path_for(path));
   });
 }

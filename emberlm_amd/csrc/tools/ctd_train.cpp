@@ -19,7 +19,7 @@ int main(int argc, char** argv) {
   try {
     return ctd::train::run(ctd::train::load_config(cfg));
   } catch (const std::exception& e) {
-    std::cerr << "[ctd_train] error: " << e.what() << "\n";
+    std::cerr << "ctd_train: error: " << e.what() << "\n";
     return 1;
   }
 }

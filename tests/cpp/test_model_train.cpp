@@ -3,8 +3,13 @@
 // 57-123 of the reference), against include/ctd/ directly.  Run on a GPU by
 // tests/test_gpu_cpp.py; the CPU oracle (oracle/ember_oracle.h) pins the
 // logits.  Exit status = number of failed tests.
+#include <unistd.h>
+
 #include <cmath>
 #include <cstdio>
+#include <cstring>
+#include <filesystem>
+#include <fstream>
 #include <functional>
 #include <random>
 #include <stdexcept>
@@ -15,6 +20,7 @@
 #include "ctd/nn/kv_cache.h"
 #include "ctd/nn/model.h"
 #include "ctd/optim.h"
+#include "ctd/safetensors.h"
 #include "ctd/tensor.h"
 #include "ember_oracle.h"
 
@@ -311,9 +317,128 @@ void kv_cache_equivalences(TinyCfg c) {
   }
 }
 
+// ------------------------------------------------------------ safetensors
+namespace fs = std::filesystem;
+
+void write_raw(const fs::path& p, const std::string& header, size_t data_bytes) {
+  std::ofstream f(p, std::ios::binary);
+  const uint64_t n = header.size();
+  f.write(reinterpret_cast<const char*>(&n), 8);
+  f.write(header.data(), static_cast<std::streamsize>(n));
+  const std::string data(data_bytes, '\0');
+  f.write(data.data(), static_cast<std::streamsize>(data.size()));
+}
+
+bool throws_with(const std::function<void()>& fn, const std::string& needle) {
+  try {
+    fn();
+  } catch (const std::runtime_error& e) {
+    if (std::string(e.what()).find(needle) != std::string::npos) return true;
+    std::printf("    message was: %s\n", e.what());
+    return false;
+  }
+  return false;
+}
+
+// The writer's header for two tensors inserted as b then a, written out by
+// hand: keys sorted, fields data_offsets / dtype / shape, no spaces, offsets in
+// insertion order, padded with spaces to a multiple of 8 (110 -> 112 bytes).
+void safetensors_format_and_faults(Device dev) {
+  const fs::path dir = fs::temp_directory_path() /
+                       ("ctd_st_" + std::to_string(::getpid()) + (dev.is_hip() ? "_d" : "_h"));
+  fs::create_directories(dir);
+  const float b_vals[2] = {1.0f, 2.0f}, a_vals[2] = {3.0f, -4.5f};
+  const std::vector<std::pair<std::string, Tensor>> items = {
+      {"b", Tensor::from_host(b_vals, {2}, DType::kFloat32, dev)},
+      {"a", Tensor::from_host(a_vals, {1, 2}, DType::kFloat32, dev)}};
+  const fs::path file = dir / "two.safetensors";
+  save_safetensors(items, file);
+  const std::string want =
+      "{\"a\":{\"data_offsets\":[8,16],\"dtype\":\"F32\",\"shape\":[1,2]},"
+      "\"b\":{\"data_offsets\":[0,8],\"dtype\":\"F32\",\"shape\":[2]}}  ";
+  {
+    std::ifstream f(file, std::ios::binary);
+    uint64_t n = 0;
+    f.read(reinterpret_cast<char*>(&n), 8);
+    std::string head(n, '\0');
+    f.read(head.data(), static_cast<std::streamsize>(n));
+    float data[4];
+    f.read(reinterpret_cast<char*>(data), sizeof data);
+    check(n == 112 && head == want, "header bytes");
+    check(data[0] == 1.0f && data[1] == 2.0f && data[2] == 3.0f && data[3] == -4.5f,
+          "data in insertion order");
+    check(fs::file_size(file) == 8 + 112 + 16, "file size");
+  }
+  TensorDict back = load_safetensors(file, dev);
+  std::vector<float> got(2);
+  back.at("a").copy_to_host(got.data());
+  check(back.size() == 2 && back.at("a").shape() == std::vector<int64_t>{1, 2} &&
+            got[0] == 3.0f && got[1] == -4.5f,
+        "round trip");
+  {  // SafetensorsReader::read into caller memory
+    SafetensorsReader r(file);
+    Tensor dst = Tensor::zeros({2}, DType::kFloat32, dev);
+    r.read("b", dst);
+    dst.copy_to_host(got.data());
+    check(got[0] == 1.0f && got[1] == 2.0f && r.find("c") == nullptr, "reader read");
+    Tensor wrong = Tensor::zeros({3}, DType::kFloat32, dev);
+    check(throws_with([&] { r.read("b", wrong); }, "destination differs"), "reader shape check");
+  }
+  const std::string ok_entry = "\"x\":{\"dtype\":\"F32\",\"shape\":[2],\"data_offsets\":[0,8]}";
+  struct Bad {
+    const char* what;
+    std::string header;
+    size_t data;
+    const char* needle;
+  };
+  const Bad bad[] = {
+      {"bad JSON", "{\"x\":", 8, "malformed header"},
+      {"range past the data", "{" + ok_entry + "}", 4, "inconsistent layout"},
+      {"size vs shape", "{\"x\":{\"dtype\":\"F32\",\"shape\":[3],\"data_offsets\":[0,8]}}", 8,
+       "inconsistent layout"},
+      {"overlap", "{" + ok_entry + ",\"y\":{\"dtype\":\"F32\",\"shape\":[1],\"data_offsets\":[4,8]}}",
+       8, "overlap"},
+      {"F16", "{\"x\":{\"dtype\":\"F16\",\"shape\":[4],\"data_offsets\":[0,8]}}", 8,
+       "unsupported dtype"},
+      {"negative extent", "{\"x\":{\"dtype\":\"F32\",\"shape\":[-2],\"data_offsets\":[0,8]}}", 8,
+       "malformed header"},
+  };
+  for (const Bad& b : bad) {
+    const fs::path p = dir / "bad.safetensors";
+    write_raw(p, b.header, b.data);
+    check(throws_with([&] { load_safetensors(p, dev); }, b.needle), b.what);
+  }
+  {  // header length larger than the file
+    const fs::path p = dir / "short.safetensors";
+    std::ofstream f(p, std::ios::binary);
+    const uint64_t n = 1000;
+    f.write(reinterpret_cast<const char*>(&n), 8);
+    f << "{}";
+    f.close();
+    check(throws_with([&] { load_safetensors(p, dev); }, "truncated file"), "truncated");
+  }
+  check(throws_with([&] { load_safetensors(dir / "missing.safetensors", dev); }, "cannot open"),
+        "missing file");
+  const int64_t ids[2] = {1, 2};
+  check(throws_with([&] {
+          save_safetensors({{"i", Tensor::from_host(ids, {2}, DType::kInt64, dev)}}, dir / "i.st");
+        }, "F32 tensors only"),
+        "writer dtype");
+  check(!fs::exists(dir / "i.st") && !fs::exists(dir / "i.st.partial"), "no partial file left");
+  fs::remove_all(dir);
+}
+
 }  // namespace
 
-int main() {
+int main(int argc, char** argv) {
+  // --cpu: only the tests that need no GPU (host tensors only).
+  if (argc > 1 && std::strcmp(argv[1], "--cpu") == 0) {
+    run("Safetensors.FormatAndFaults_Host", [] { safetensors_format_and_faults(kCPU); });
+    std::printf("%d failure(s)\n", g_failed);
+    return g_failed;
+  }
+  run("Safetensors.FormatAndFaults_Host", [] { safetensors_format_and_faults(kCPU); });
+  run("Safetensors.FormatAndFaults_Device", [] { safetensors_format_and_faults(kHIP0); });
   run("ModelTrain.TrainLogitsMatchInferenceLogits",
       [] { train_logits_match_inference_logits(TinyCfg{}); });
   run("ModelTrain.TrainLogitsMatchInferenceLogits_D64",

@@ -67,6 +67,19 @@ def test_gemm_split_plan_without_gpu():
     assert lib.ember_gemm_f32_workspace_bytes(128, 2048, 2048, 1) == 8 * 128 * 2048 * 4
     # the c5 k/v weight gradient (128 tiles, K = 32768 tokens): 12 chunks
     assert lib.ember_gemm_f32_workspace_bytes(1024, 2048, 32768, 1) == 12 * 1024 * 2048 * 4
+    # Weight gradients dW[out, in] = dY^T X of BASELINE configs 2 and 3 (K =
+    # tokens).  Few-tile grids (at most 128 tiles of 128x128) split into
+    # chunks of >= 256, the others into chunks of >= 1024, aiming at 1536 tiles:
+    # Qwen3-0.6B, 4096 tokens: q/o 128 tiles -> 12; k/v 64 -> 16; gate/up/down
+    # 192 tiles -> min(8, 4096/1024) = 4.
+    # LLaMA-3.2-1B, 8192 tokens: q/o 256 tiles -> 6; k/v 64 -> 16;
+    # gate/up/down 1024 tiles -> 2.
+    plans = [(2048, 1024, 4096, 12), (1024, 1024, 4096, 16), (1024, 2048, 4096, 12),
+             (3072, 1024, 4096, 4), (1024, 3072, 4096, 4),
+             (2048, 2048, 8192, 6), (512, 2048, 8192, 16), (8192, 2048, 8192, 2),
+             (2048, 8192, 8192, 2)]
+    for M, N, K, splits in plans:
+        assert lib.ember_gemm_f32_workspace_bytes(M, N, K, 1) == splits * M * N * 4, (M, N, K)
     # enough tiles, or K too short to split: one pass over K
     assert lib.ember_gemm_f32_workspace_bytes(4096, 2048, 2048, 1) == 0
     assert lib.ember_gemm_f32_workspace_bytes(128, 2048, 511, 1) == 0

@@ -74,16 +74,20 @@ def test_host_batch_matches_oracle(tmp_path):
 def test_data_format_errors(tmp_path):
     seq_len = 8
     tp, mp = write_split(tmp_path, "a", np.zeros(2 * seq_len + 1), np.zeros(2 * seq_len))
-    with pytest.raises(TR.CtdError, match="not multiple of seq_len"):
+    with pytest.raises(TR.CtdError, match="not whole documents of 8"):
         TR.host_batch(tp, mp, seq_len, [])
     tp, mp = write_split(tmp_path, "b", np.zeros(2 * seq_len), np.zeros(2 * seq_len - 1))
-    with pytest.raises(TR.CtdError, match="mask size mismatch"):
+    with pytest.raises(TR.CtdError, match="15 mask values for 16 tokens"):
         TR.host_batch(tp, mp, seq_len, [])
     tp, mp = write_split(tmp_path, "c", np.zeros(2 * seq_len), np.zeros(2 * seq_len))
     with pytest.raises(TR.CtdError, match="out of range"):
         TR.host_batch(tp, mp, seq_len, [2])
-    with pytest.raises(TR.CtdError, match="cannot open"):
+    with pytest.raises(TR.CtdError, match="cannot stat"):
         TR.host_batch(os.path.join(tmp_path, "missing.bin"), mp, seq_len, [])
+    # a token file that is not a whole number of int32 values
+    open(os.path.join(tmp_path, "odd.bin"), "wb").write(b"\0" * 33)
+    with pytest.raises(TR.CtdError, match="not a whole number of 4-byte values"):
+        TR.host_batch(os.path.join(tmp_path, "odd.bin"), mp, seq_len, [])
 
 
 # ------------------------------------------------------------ loss.jsonl records
@@ -131,4 +135,4 @@ def test_cli_usage_and_config_error(tmp_path):
     cfg = tmp_path / "config.json"
     cfg.write_text('{"data_dir": "x"}')
     r = subprocess.run([exe, "--config", str(cfg)], capture_output=True, text=True)
-    assert r.returncode == 1 and "[ctd_train] error:" in r.stderr and "init_weights" in r.stderr
+    assert r.returncode == 1 and "ctd_train: error:" in r.stderr and "init_weights" in r.stderr

@@ -41,7 +41,7 @@ def test_bad_request_gives_error_line(req, msg):
     rec = json.loads(lines[0])
     assert list(rec) == ["done", "error", "reason"]          # nlohmann's sorted keys
     assert rec["done"] is True and rec["reason"] == "error" and msg in rec["error"]
-    assert "[ctd_generate] error:" in r.stderr
+    assert "ctd_generate: error:" in r.stderr
 
 
 def test_missing_model_file_is_an_error_reply():
@@ -49,7 +49,7 @@ def test_missing_model_file_is_an_error_reply():
     assert r.returncode == 1
     rec = json.loads(r.stdout)
     assert rec["reason"] == "error" and "cannot open" in rec["error"]
-    assert "[ctd_generate] loading /nonexistent/model.safetensors" in r.stderr
+    assert "ctd_generate: weights /nonexistent/model.safetensors" in r.stderr
 
 
 def test_error_text_is_escaped_json():

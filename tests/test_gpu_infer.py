@@ -455,7 +455,7 @@ def test_generate_greedy_matches_oracle(gen_model):
     assert rc == 0, err
     assert lines == OG.generate(last_logits, req)
     assert json.loads(lines[-1]) == {"done": True, "generated_tokens": 12, "reason": "max_tokens"}
-    assert "[ctd_generate] prefill (6 tok)" in err
+    assert "ctd_generate: prompt of 6 tokens" in err
 
 
 def test_generate_sampled_matches_oracle(gen_model):

@@ -121,7 +121,8 @@ def gemm_ws(a, b, ta, tb, alpha=1.0, beta=0.0, c=None, ws_bytes=None):
 
 
 @pytest.mark.parametrize("ta,tb,K", [(1, 0, 5003), (0, 0, 5003), (0, 1, 5003), (1, 1, 5003),
-                                     (1, 0, 5008), (0, 1, 5008), (0, 1, 1000), (0, 1, 2048)])
+                                     (1, 0, 5008), (0, 1, 5008)]
+                         + [(ta, tb, K) for K in (1000, 2048) for ta in (0, 1) for tb in (0, 1)])
 def test_gemm_split_k_vs_oracle(ta, tb, K):
     # Few output tiles: the K-split path with partials (K % 16 == 0 takes the
     # LDS-DMA kernel, a ragged K the register-staged one), 16 splits of a long K
@@ -471,6 +472,89 @@ def test_attention_fwd_bwd_vs_oracle(B, T, H, Hk, D):
          Hk, D, scale, p(WS), wsb, None)
     assert torch.equal(Ot, O2) and torch.equal(L, L2)
     assert torch.equal(DQ, DQ2) and torch.equal(DK, DK2) and torch.equal(DV, DV2)
+
+
+def _attn_hip(Q, K, Vv, DO, B, T, H, Hk, D, scale):
+    """Forward and backward through the C ABI on device tensors."""
+    Ot, L = empty((B, T, H, D)), empty((B, H, T))
+    call("ember_attn_fwd", p(Q), p(K), p(Vv), p(Ot), p(L), B, T, H, Hk, D, scale, None)
+    wsb = capi.lib().ember_attn_bwd_workspace_bytes(B, T, H)
+    WS = empty((wsb // 4,))
+    DQ, DK, DV = empty((B, T, H, D)), empty((B, T, Hk, D)), empty((B, T, Hk, D))
+    call("ember_attn_bwd", p(Q), p(K), p(Vv), p(Ot), p(L), p(DO), p(DQ), p(DK), p(DV), B, T, H, Hk,
+         D, scale, p(WS), wsb, None)
+    return Ot, L, DQ, DK, DV
+
+
+# The launch layouts of the BASELINE configs: c3 Qwen3-0.6B (64 (batch, head)
+# rows, group 2, D 128), c4 LLaMA-3.2-1B (128 rows, group 4, D 64), c5
+# Qwen3-1.7B (128 rows, group 2, D 128).  Row counts that are multiples of 8
+# above 8 take the XCD regrouping of the work items, and group 4 takes the
+# dK/dV kernel's loop over four query heads per KV head.
+REAL_LAYOUTS = [("c3", 4, 1024, 16, 8, 128), ("c4", 4, 2048, 32, 8, 64),
+                ("c5", 8, 4096, 16, 8, 128)]
+
+
+@pytest.mark.parametrize("name,B,T,H,Hk,D", REAL_LAYOUTS)
+def test_attention_real_layouts_vs_oracle(name, B, T, H, Hk, D):
+    # Every (batch, head) row of the real launch, at T = 256 so the oracle
+    # finishes in seconds.
+    T = 256
+    r = rng({"c3": 31, "c4": 41, "c5": 51}[name])
+    q = r.standard_normal((B, T, H, D)).astype(np.float32)
+    k = r.standard_normal((B, T, Hk, D)).astype(np.float32)
+    v = r.standard_normal((B, T, Hk, D)).astype(np.float32)
+    do = r.standard_normal((B, T, H, D)).astype(np.float32)
+    scale = 1.0 / math.sqrt(D)
+    Ot, L, DQ, DK, DV = _attn_hip(dev(q), dev(k), dev(v), dev(do), B, T, H, Hk, D, scale)
+    o_ref, lse_ref = O.attention_fwd(q, k, v, scale)
+    assert_close(host(Ot), o_ref, name=f"{name} o")
+    assert_close(host(L), lse_ref, name=f"{name} lse")
+    dq_ref, dk_ref, dv_ref = O.attention_bwd(q, k, v, do, scale)
+    assert_close(host(DQ), dq_ref, name=f"{name} dq")
+    assert_close(host(DK), dk_ref, name=f"{name} dk")
+    assert_close(host(DV), dv_ref, name=f"{name} dv")
+
+
+@pytest.mark.parametrize("name,B,T,H,Hk,D", REAL_LAYOUTS)
+def test_attention_real_layouts_full_T_vs_torch(name, B, T, H, Hk, D):
+    # The full launch at the config's own B, T and heads against fp32 torch
+    # autograd of softmax(Q K^T * scale + causal mask) V on the GPU, one
+    # (batch, KV head) group of query heads at a time.
+    g = torch.Generator(device="cuda").manual_seed(7)
+    q = torch.randn(B, T, H, D, device="cuda", generator=g)
+    k = torch.randn(B, T, Hk, D, device="cuda", generator=g)
+    v = torch.randn(B, T, Hk, D, device="cuda", generator=g)
+    do = torch.randn(B, T, H, D, device="cuda", generator=g)
+    scale = 1.0 / math.sqrt(D)
+    Ot, L, DQ, DK, DV = _attn_hip(q, k, v, do, B, T, H, Hk, D, scale)
+    G = H // Hk
+    causal = torch.triu(torch.ones(T, T, dtype=torch.bool, device="cuda"), 1)
+    refs = {n: torch.empty_like(t) for n, t in (("o", Ot), ("dq", DQ), ("dk", DK), ("dv", DV))}
+    ref_lse = torch.empty_like(L)
+    for b in range(B):
+        for j in range(Hk):
+            heads = slice(j * G, (j + 1) * G)
+            qg = q[b, :, heads].permute(1, 0, 2).contiguous().requires_grad_(True)  # [G,T,D]
+            kj = k[b, :, j].contiguous().requires_grad_(True)
+            vj = v[b, :, j].contiguous().requires_grad_(True)
+            s = torch.matmul(qg, kj.t().contiguous()) * scale          # [G,T,T]
+            s = s.masked_fill(causal, -math.inf)
+            og = torch.matmul(torch.softmax(s, -1), vj)
+            og.backward(do[b, :, heads].permute(1, 0, 2).contiguous())
+            refs["o"][b, :, heads] = og.detach().permute(1, 0, 2)
+            refs["dq"][b, :, heads] = qg.grad.permute(1, 0, 2)
+            refs["dk"][b, :, j] = kj.grad
+            refs["dv"][b, :, j] = vj.grad
+            ref_lse[b, heads] = torch.logsumexp(s.detach(), -1)
+    torch.cuda.synchronize()
+    for n, got in (("o", Ot), ("dq", DQ), ("dk", DK), ("dv", DV)):
+        rel = ((got - refs[n]).norm() / refs[n].norm()).item()
+        assert rel < 1e-5, (name, n, rel)
+        err = (got - refs[n]).abs()
+        bound = 1e-4 * refs[n].abs() + 1e-4 * refs[n].abs().max()
+        assert bool((err <= bound).all()), (name, n, err.max().item())
+    assert (L - ref_lse).abs().max().item() < 1e-4
 
 
 def test_attention_full_T_c5_vs_torch_sdpa():

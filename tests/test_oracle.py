@@ -138,37 +138,85 @@ def test_rope_identity_and_norm_and_transpose():
 
 
 def test_rope_matches_complex_rotation_llama3():
+    # Frequencies from the per-band statement (pinned to literals below), not
+    # from the oracle.
+    from tests.golden.make_golden import rope_freqs
     r = rng(7)
     D, theta = 64, 5e5
     x = r.standard_normal((1, 40, 2, D))
-    freqs = [O.rope_freq(i, D, theta, 32.0, 1.0, 4.0, 8192) for i in range(D // 2)]
+    freqs = rope_freqs(D, theta, 32.0, 1.0, 4.0, 8192)
     ref = _rope_complex(x, theta, 3, freqs)
-    np.testing.assert_allclose(O.rope(x, theta, pos0=3, factor=32.0), ref, rtol=1e-10,
-                               atol=1e-12)
+    # the oracle's float arithmetic may land one ulp of a mid-band frequency
+    # away (about 1e-7 rad at these positions)
+    np.testing.assert_allclose(O.rope(x, theta, pos0=3, factor=32.0), ref, rtol=1e-7,
+                               atol=1e-8)
+
+
+# LLaMA-3.2 llama3 settings: D 64, theta 5e5, factor 32,
+# low_freq 1, high_freq 4, original context L 8192.  The mid band
+# (L/4 = 2048 < 2*pi/f <= 8192) holds i = 15, 16, 17.  Expected values worked
+# out by hand from rope.cu:41-45 with f = 5e5^(-i/32):
+#   i  f              2*pi/f       s = (wl-2048)/6144   (1-s) f + s f/32
+#   15 2.13111954e-3  2948.30262   0.146533629          1.8285976285e-3
+#   16 1.41421356e-3  4442.88294   0.389792145          8.8019076638e-4
+#   17 9.38473870e-4  6695.10948   0.756365475          2.5082679882e-4
+LLAMA3_MID = {15: 1.8285976285e-3, 16: 8.8019076638e-4, 17: 2.5082679882e-4}
+
+
+def _llama3_alternatives(i, D=64, theta=5e5, fac=32.0, lf=1.0, hf=4.0, L=8192):
+    """What two plausible mistakes give: HF's weighting and the reference's
+    weights swapped."""
+    base = theta ** (-2.0 * i / D)
+    wl = 2 * math.pi / base
+    s_hf = (L / wl - lf) / (hf - lf)
+    s = (wl - L / hf) / (L / lf - L / hf)
+    return (1 - s_hf) * base / fac + s_hf * base, s * base + (1 - s) * base / fac
+
+
+def test_rope_llama3_mid_band_literals():
+    for i, want in LLAMA3_MID.items():
+        got = O.rope_freq(i, 64, 5e5, 32.0, 1.0, 4.0, 8192)
+        assert got == pytest.approx(want, rel=1e-6), (i, got, want)
+        hf_value, swapped = _llama3_alternatives(i)
+        # a mistaken oracle would be at least 20% away from the literal
+        assert abs(hf_value - want) > 0.2 * want and abs(swapped - want) > 0.2 * want
+
+
+def test_rope_llama3_one_third_weight():
+    # Constructed case: D 4, i 1 gives f = theta^(-1/2); theta = (4096/(2*pi))^2
+    # puts the wavelength at 4096 exactly, so s = (4096-2048)/(8192-2048) = 1/3
+    # and the reference's f' = (2/3) f + (1/3) f/32 = (65/96) f, where HF's
+    # weighting (s' = (8192/4096 - 1)/3 = 1/3 on f, 2/3 on f/32) gives (34/96) f.
+    theta = (4096 / (2 * math.pi)) ** 2
+    base = float(np.float32(theta) ** np.float32(-0.5))
+    got = O.rope_freq(1, 4, theta, 32.0, 1.0, 4.0, 8192)
+    assert got / base == pytest.approx(65 / 96, rel=1e-6)
+    assert abs(got / base - 34 / 96) > 0.3
 
 
 def test_rope_llama3_bands():
-    # rope.cu:37-46 at LLaMA-3.2 settings: factor 32, low 1, high 4, L 8192.
+    from tests.golden.make_golden import rope_freqs
     D, theta = 64, 5e5
     L, lf, hf, fac = 8192, 1.0, 4.0, 32.0
+    closed = rope_freqs(D, theta, fac, lf, hf, L)
+    for i, want in LLAMA3_MID.items():   # the per-band statement is pinned too
+        assert float(closed[i]) == pytest.approx(want, rel=1e-6)
     for i in range(D // 2):
         base = float(np.float32(theta) ** np.float32(-(2.0 * i) / D))
         f = O.rope_freq(i, D, theta, fac, lf, hf, L)
         wl = 2 * math.pi / base
-        if wl < L / hf * 0.999:
-            assert f == pytest.approx(base, rel=1e-6)          # high-frequency band unchanged
-        elif wl > L / lf * 1.001:
-            assert f == pytest.approx(base / fac, rel=1e-6)    # low-frequency band divided
-        else:
-            lo, hi = min(base, base / fac), max(base, base / fac)
-            assert lo * (1 - 1e-6) <= f <= hi * (1 + 1e-6)     # mid band between the two
-    # Mid-band weight of the reference formula (differs from HF): at wavelen
-    # 4096 with L/hf = 2048, L/lf = 8192, smooth = 1/3 on base/factor.
-    smooth = (4096 - 2048) / (8192 - 2048)
-    assert smooth == pytest.approx(1 / 3)
+        if wl <= L / hf:
+            assert f == base                                   # high-frequency band unchanged
+        elif wl > L / lf:
+            assert f == pytest.approx(base / fac, rel=1e-7)    # low-frequency band divided
+        # every band within one float32 ulp of the per-band statement
+        assert abs(np.float32(f) - closed[i]) <= np.spacing(closed[i]), i
     freqs = [O.rope_freq(i, D, theta, fac, lf, hf, L) for i in range(D // 2)]
     assert all(a >= b for a, b in zip(freqs, freqs[1:]))       # monotone in i
     assert O.rope_freq(0, D, theta, fac, lf, hf, L) == 1.0
+    # below factor 1 the scaling is off: every frequency is the plain one
+    plain = rope_freqs(D, theta)
+    assert [O.rope_freq(i, D, theta, 0.0, lf, hf, L) for i in range(D // 2)] == list(plain)
 
 
 # ------------------------------------------------------------- Softmax
@@ -374,9 +422,9 @@ def _torch_block(cfg, w, x):
     if cfg.qk_norm:
         q = F.rms_norm(q, (D,), w["q_norm"], eps=cfg.eps)
         k = F.rms_norm(k, (D,), w["k_norm"], eps=cfg.eps)
-    freqs = torch.tensor([O.rope_freq(i, D, cfg.theta, cfg.rope_factor, cfg.rope_low_freq,
-                                      cfg.rope_high_freq, cfg.rope_orig_max_pos) for i in range(D // 2)],
-                         dtype=torch.float32)
+    from tests.golden.make_golden import rope_freqs
+    freqs = torch.from_numpy(rope_freqs(D, cfg.theta, cfg.rope_factor, cfg.rope_low_freq,
+                                        cfg.rope_high_freq, cfg.rope_orig_max_pos))
     ang = (torch.arange(T, dtype=torch.float32)[:, None] * freqs[None, :]).double()
     cos, sin = torch.cos(ang)[None, :, None, :], torch.sin(ang)[None, :, None, :]
 
