@@ -51,6 +51,7 @@ SIGNATURES = {
     "ember_rmsnorm_fwd": (i32, [vp, vp, vp, vp, i64, i64, f32, vp]),
     "ember_rmsnorm_bwd_workspace_bytes": (sz, [i64, i64]),
     "ember_rmsnorm_bwd": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, f32, vp, sz, vp]),
+    "ember_rmsnorm_bwd_noalloc": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, f32, vp]),
     "ember_rope_freqs_host": (i32, [C.POINTER(f32), i32, f32, f32, f32, f32, i32]),
     "ember_rope": (i32, [vp, vp, i64, i64, i64, i64, i64, C.POINTER(f32), f32, vp]),
     "ember_add": (i32, [vp, vp, vp, i64, vp]),

@@ -7,6 +7,8 @@
 // QK-Norm rows, so one wave covers several rows), rows are read as float4,
 // and dw is reduced deterministically: each block sums its rows in a fixed
 // order into a workspace row, then one pass sums the workspace rows in order.
+#include <mutex>
+
 #include "common.h"
 
 using namespace ember;
@@ -357,6 +359,46 @@ extern "C" int ember_rmsnorm_fwd(const float* x, const float* w, float* y, float
   return launch_status();
 }
 
+// Scratch of ember_rmsnorm_bwd_noalloc: the dw partials in a file-scope device
+// array instead of a caller workspace.  Every GPU the library runs on holds
+// its own copy at its own address until the process ends.  Host code must not
+// pass the array's name to a kernel (on the host it is a stand-in, not a
+// device address): each device's address is looked up once with
+// hipGetSymbolAddress and cached below.
+static __device__ __align__(256) float scratch[EMBER_RMSNORM_BWD_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Address of `scratch` on the current device, looked up on first use there.
+int scratch_on_current_device(hipStream_t st, float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return status_of(e);
+  if (dev < 0 || dev >= kMaxScratchDevices) return EMBER_EINVAL;
+  if (st) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(st, &sdev);
+    if (e != hipSuccess) return status_of(e);
+    if (sdev != dev) return EMBER_EINVAL;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return status_of(e);
+    if (!p) return EMBER_EINVAL;
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return EMBER_OK;
+}
+
+}  // namespace
+
 extern "C" size_t ember_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t H) {
   if (rows <= 0 || H <= 0) return 0;
   const bool vec = H % 4 == 0 && H / 4 <= 16 * 64;
@@ -403,4 +445,21 @@ extern "C" int ember_rmsnorm_bwd(const float* dy, const float* x, const float* w
   column_sum<<<static_cast<unsigned>((H + kWave - 1) / kWave), kColThreads, 0, st>>>(part, dw, nb,
                                                                                   H);
   return launch_status();
+}
+
+extern "C" int ember_rmsnorm_bwd_noalloc(const float* dy, const float* x, const float* w,
+                                         const float* rstd, float* dx, float* dw, int64_t rows,
+                                         int64_t H, float eps, ember_stream_t s) {
+  if (rows < 0 || H <= 0 || !w) return EMBER_EINVAL;
+  if (rows > 0 && (!dy || !x)) return EMBER_EINVAL;
+  const size_t need = ember_rmsnorm_bwd_workspace_bytes(rows, H);
+  if (!dw || need == 0) return ember_rmsnorm_bwd(dy, x, w, rstd, dx, dw, rows, H, eps, nullptr, 0, s);
+  if (need > EMBER_RMSNORM_BWD_SCRATCH_BYTES) return EMBER_ESCRATCH;
+  float* ws = nullptr;
+  const int rc = scratch_on_current_device(as_stream(s), &ws);
+  if (rc) return rc;
+  // Every partial row the kernels read is written first by the same call (the
+  // float4 kernel stores all H columns of each workgroup's row, the scalar one
+  // zeroes its row before adding), so nothing left by an earlier call is read.
+  return ember_rmsnorm_bwd(dy, x, w, rstd, dx, dw, rows, H, eps, ws, need, s);
 }

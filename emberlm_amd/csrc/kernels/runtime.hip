@@ -12,6 +12,7 @@ extern "C" const char* ember_status_string(int status) {
     case EMBER_EWORKSPACE: return "workspace missing or too small";
     case EMBER_EALIGN: return "pointer alignment not met";
     case EMBER_EMASKSUM: return "sum(loss_mask) == 0 in cross-entropy backward";
+    case EMBER_ESCRATCH: return "problem larger than the entry point's fixed scratch";
     default: break;
   }
   if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));

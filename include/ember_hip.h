@@ -36,6 +36,7 @@ enum {
   EMBER_EWORKSPACE = -2, /* workspace missing or too small */
   EMBER_EALIGN = -3,     /* pointer alignment the kernel requires is not met */
   EMBER_EMASKSUM = -4,   /* sum(loss_mask) == 0 in cross-entropy backward */
+  EMBER_ESCRATCH = -5,   /* problem larger than an allocation-free entry's fixed scratch */
   EMBER_NOTREADY = 600   /* ember_event_query: work before the event still pending */
 };
 
@@ -122,6 +123,20 @@ size_t ember_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t H);
 int ember_rmsnorm_bwd(const float* dy, const float* x, const float* w, const float* rstd,
                       float* dx, float* dw, int64_t rows, int64_t H, float eps, void* workspace,
                       size_t workspace_bytes, ember_stream_t s);
+/* ember_rmsnorm_bwd with no workspace argument and no allocation of any kind,
+ * for callers that cannot allocate device memory: code under HIP graph
+ * capture, serving loops and harnesses that forbid hipMalloc.  No counterpart
+ * in the reference.  The dw partials go to one fixed array of
+ * EMBER_RMSNORM_BWD_SCRATCH_BYTES in device memory, one per GPU, held until
+ * the process ends: sizes whose ember_rmsnorm_bwd_workspace_bytes(rows, H)
+ * exceed it return EMBER_ESCRATCH (any row count fits for H <= 4096).  Results
+ * are bitwise those of ember_rmsnorm_bwd.  Every call on a GPU uses that GPU's
+ * one array, so calls that overlap on one GPU (two streams, two threads) race;
+ * the stream must belong to the current device (else EMBER_EINVAL). */
+#define EMBER_RMSNORM_BWD_SCRATCH_BYTES ((size_t)16 << 20)
+int ember_rmsnorm_bwd_noalloc(const float* dy, const float* x, const float* w, const float* rstd,
+                              float* dx, float* dw, int64_t rows, int64_t H, float eps,
+                              ember_stream_t s);
 
 /* ----------------------------------------------------------------- RoPE
  * Frequencies of the D/2 rotation pairs in float, following src/ops/rope.cu:37-46

@@ -61,6 +61,18 @@ def test_argument_validation_without_gpu():
     assert lib.ember_ce_masked_fwd_workspace_bytes(32768) == 32768 * 4
 
 
+def test_noalloc_size_limit_without_gpu():
+    # The allocation-free RMSNorm backward refuses problems whose dw partials
+    # exceed its fixed 16 MiB scratch before touching the device (fake
+    # non-null pointers; nothing is dereferenced or launched).
+    lib = capi.lib()
+    fake = C.c_void_p(256)
+    assert lib.ember_rmsnorm_bwd_workspace_bytes(32768, 8192) == 32 << 20
+    rc = lib.ember_rmsnorm_bwd_noalloc(fake, fake, fake, None, None, fake, 32768, 8192, 1e-6, None)
+    assert rc == -5
+    assert lib.ember_rmsnorm_bwd_noalloc(None, None, fake, None, None, fake, 4, 8, 1e-6, None) == -1
+
+
 def test_gemm_split_plan_without_gpu():
     lib = capi.lib()
     # a short prefill's projection (M = 128, 16 tiles): 8 K chunks of 256
