@@ -254,6 +254,9 @@ def main():
     ap.add_argument("--prefetch-layer", type=int, default=None,
                     help="layer whose re-run in the backward starts that prefetch (-1: none; "
                          "default: the library's estimate for the model and batch)")
+    ap.add_argument("--attn-ds-bytes", type=int, default=None,
+                    help="device bytes the attention backward may keep dS in (0: recompute it; "
+                         "default: the library's)")
     ap.add_argument("--link-probe", action="store_true",
                     help="only the pinned host<->device copy rates of this box (one JSON line)")
     args = ap.parse_args()
@@ -299,6 +302,8 @@ def main():
     log(f"[bench] {args.workload}: {n_params / 1e9:.4f} B params, B={B} T={T}, "
         f"checkpointing={ckpt}, offload={offload}")
 
+    if args.attn_ds_bytes is not None:
+        TR.set_attn_ds_bytes(args.attn_ds_bytes)
     t0 = time.time()
     tr = TR.Trainer(cfg, seed=0, init_std=0.02, norm_value=1.0)
     tr.set_checkpointing(ckpt)
@@ -352,6 +357,9 @@ def main():
              "TN": "gemm_f32_dma<A M-contig, B N-contig> (dW, TN)",
              "TT": "gemm_f32_dma<A M-contig, B K-contig> (TT)"}
     attn = {k: prof.pop(k) for k in ("attn_fwd", "attn_bwd")}
+    # Executed over algorithmic backward flops: 5/4 when dS is kept between the
+    # dK/dV and dQ passes (S recomputed), 7/4 when the dQ pass recomputes S, dP.
+    bwd_exec = 1.75 if args.attn_ds_bytes == 0 else 1.25
     dom = max(prof, key=lambda k: prof[k].total_ms)
     p = prof[dom]
     per_launch_flops = p.flops / max(p.launches, 1)
@@ -408,7 +416,7 @@ def main():
                 "frac_of_fp32_mfma_peak":
                     round(a.flops / (a.total_ms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)
                     if a.total_ms else None,
-                "executed_tflops": round(a.flops * (1.0 if k == "attn_fwd" else 1.75)
+                "executed_tflops": round(a.flops * (1.0 if k == "attn_fwd" else bwd_exec)
                                          / (a.total_ms / 1e3) / 1e12, 2) if a.total_ms else None}
             for k, a in attn.items()},
         "roofline": {"kernel": kname[dom], "bound": "mfma", "achieved": round(achieved, 2),

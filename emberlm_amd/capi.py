@@ -71,6 +71,7 @@ SIGNATURES = {
     "ember_permute": (i32, [vp, vp, i32, C.POINTER(i64), C.POINTER(i32), vp]),
     "ember_attn_fwd": (i32, [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, f32, vp]),
     "ember_attn_bwd_workspace_bytes": (sz, [i64, i64, i64]),
+    "ember_attn_bwd_workspace_bytes_min": (sz, [i64, i64, i64]),
     "ember_attn_bwd": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, f32,
                              vp, sz, vp]),
     "ember_ce_masked_fwd_workspace_bytes": (sz, [i64]),

@@ -2,6 +2,8 @@
 // fused SwiGLU and fused causal attention.  Each public op launches through
 // the C ABI and, when an input requires grad, records a backward node with
 // the reference's gradient formulas (src/ops/*.cu, src/ops/matmul.cpp).
+#include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <utility>
 
@@ -469,10 +471,20 @@ AttnDims attn_dims(const Tensor& q, const Tensor& k, const Tensor& v) {
 
 // Algorithmic FLOPs of the causal forward: S = Q K^T and O = P V over the
 // T(T+1)/2 visible (query, key) pairs.  The backward's four products (dV,
-// dP, dQ, dK) are twice this; the kernels execute 3.5x (S and dP are
-// recomputed in both backward kernels).
+// dP, dQ, dK) are twice this; the kernels execute 2.5x with dS kept (S is
+// recomputed), 3.5x without (S and dP recomputed in both passes).
 double attn_fwd_flops(const AttnDims& d) {
   return 4.0 * static_cast<double>(d.B) * d.H * d.D * (static_cast<double>(d.T) * (d.T + 1) / 2);
+}
+
+std::atomic<int64_t> g_attn_ds_bytes{kAttentionBackwardDsBytes};
+
+// Workspace for ember_attn_bwd: rowsum(dO*O) plus as much of dS as the budget allows.
+size_t attn_bwd_workspace(const AttnDims& d) {
+  const size_t lo = ember_attn_bwd_workspace_bytes_min(d.B, d.T, d.H);
+  const size_t hi = ember_attn_bwd_workspace_bytes(d.B, d.T, d.H);
+  const int64_t budget = g_attn_ds_bytes.load();
+  return budget <= 0 ? lo : std::min(hi, lo + static_cast<size_t>(budget));
 }
 
 struct CausalAttentionBackward : autograd::Node {
@@ -485,7 +497,7 @@ struct CausalAttentionBackward : autograd::Node {
     check_f32(dout, "causal_attention backward", "grad");
     const AttnDims d = attn_dims(q, k, v);
     Tensor dq = empty_like(q), dk = empty_like(k), dv = empty_like(v);
-    const size_t wsb = ember_attn_bwd_workspace_bytes(d.B, d.T, d.H);
+    const size_t wsb = attn_bwd_workspace(d);
     Tensor ws = workspace(wsb);
     void* ev = runtime::gemm_profile_begin();
     CTD_CHECK(ember_attn_bwd(cfp(q), cfp(k), cfp(v), cfp(o), cfp(lse), cfp(dout), fp(dq), fp(dk),
@@ -497,6 +509,10 @@ struct CausalAttentionBackward : autograd::Node {
 };
 
 }  // namespace
+
+void set_attention_backward_ds_bytes(int64_t bytes) {
+  g_attn_ds_bytes.store(bytes < 0 ? kAttentionBackwardDsBytes : bytes);
+}
 
 Tensor causal_attention_impl(const Tensor& q, const Tensor& k, const Tensor& v, float scale,
                              Tensor* lse_out) {

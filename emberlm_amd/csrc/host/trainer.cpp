@@ -15,6 +15,7 @@
 #include <string>
 #include <vector>
 
+#include "ctd/ops/attention.h"
 #include "ctd/allocator.h"
 #include "ctd/generate.h"
 #include "ctd/nn/model.h"
@@ -729,6 +730,10 @@ int ctd_trainer_generate(ctd_trainer_t t, const int64_t* prompt, int64_t P, int3
 
 int ctd_set_head_chunk_rows(int64_t rows) {
   return guarded([&] { ops::set_linear_cross_entropy_chunk_rows(rows); });
+}
+
+int ctd_set_attn_ds_bytes(int64_t bytes) {
+  return guarded([&] { ops::set_attention_backward_ds_bytes(bytes); });
 }
 
 }  // extern "C"

@@ -26,15 +26,29 @@
 //
 // Backward (no atomics, so dK/dV/dQ are bitwise reproducible):
 //   attn_delta:  delta = rowsum(dO * O);
-//   attn_bwd_dq: per 16 queries, S^T = K Q^T and dP^T = V dO^T, then
-//                dQ^T += K^T dS^T (same orientation as the forward);
 //   attn_bwd_dkdv: per 16 keys, S = Q K^T and dP = dO V^T put the key in the
 //                lane, so dV^T += dO^T P and dK^T += Q^T dS accumulate in
 //                registers across every query tile and every query head of
-//                the KV head's group, in a fixed order.
-// Both backward kernels take 64 rows per workgroup (two waves per SIMD at
-// D = 128; 32 rows per wave on 32x32x2 tiles needed more than 256 registers
-// per lane there) and double-buffer their streamed tiles the same way.
+//                the KV head's group, in a fixed order.  With a dS buffer it
+//                also stores dS (fp32, the causal part only, see below);
+//   attn_bwd_dq_ds: dQ^T += K^T dS^T per 16 queries from the stored dS, a
+//                plain product in key order;
+//   attn_bwd_dq (no dS buffer): per 16 queries, S^T = K Q^T and dP^T =
+//                V dO^T recomputed, then dQ^T += K^T dS^T.
+// Counted in units of one T x T x D product per head, the algorithm needs 4
+// (dV, dP, dQ, dK); with the stored dS the kernels execute 5 (S is computed
+// again), with the recompute dQ kernel 7 (S and dP twice).
+// dS layout, per (b, h) row: for each 64-key block kb a strip of 64 key rows
+// by Lr = T32 - 64 kb query columns (T32 = T rounded up to 32), columns
+// starting at query 64 kb, so only the causal part is kept; strips follow
+// each other in kb order (ds_strip_offset).  The dK/dV kernel writes one
+// float4 of four consecutive queries per lane; entries it skips (query tiles
+// no key of a wave sees) are never read, because the dQ kernel masks keys
+// after the query.
+// Every backward kernel takes 64 rows per workgroup (two waves per SIMD at
+// D = 128 for dK/dV and the recompute dQ; 32 rows per wave on 32x32x2 tiles
+// needed more than 256 registers per lane there) and double-buffers its
+// streamed tiles the same way.
 #include "common.h"
 
 using namespace ember;
@@ -68,6 +82,15 @@ __device__ __forceinline__ WorkItem work_item(int ntiles) {
   int rr = L % rows;
   if (rows % 8 == 0) rr = (rr % 8) * (rows / 8) + rr / 8;
   return {L / rows, rr};
+}
+
+// dS strips of one (b, h) row (layout in the header comment).
+__host__ __device__ __forceinline__ int64_t ds_t32(int64_t T) { return (T + 31) / 32 * 32; }
+__host__ __device__ __forceinline__ int64_t ds_strip_offset(int64_t kb, int64_t T32) {
+  return 64 * kb * T32 - 2048 * kb * (kb - 1);
+}
+__host__ __device__ __forceinline__ int64_t ds_row_floats(int64_t T) {
+  return ds_strip_offset((T + 63) / 64, ds_t32(T));
 }
 
 // ROWS rows of D floats staged global -> registers -> LDS by a block of
@@ -421,15 +444,16 @@ template <int D>
 __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta,
-    float* __restrict__ dk, float* __restrict__ dv, int T, int H, int Hk, float scale_log2,
-    float scale) {
+    float* __restrict__ dk, float* __restrict__ dv, float* __restrict__ ds, int row0, int T,
+    int H, int Hk, float scale_log2, float scale) {
   using C = DkvCfg<D>;
   constexpr int NT = D / 16;  // d tiles; float4 groups of a lane's K/V row
   __shared__ __attribute__((aligned(16))) float smem[C::kSmem];
 
   const WorkItem wi = work_item((T + C::kBKeys - 1) / C::kBKeys);
   const int kb = wi.tile;  // small key blocks see the most queries: launched first
-  const int hk = wi.row % Hk, b = wi.row / Hk;
+  const int kvrow = row0 + wi.row;  // (b, hk) of this launch's chunk of rows
+  const int hk = kvrow % Hk, b = kvrow / Hk;
   const int group = H / Hk;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, i = lane & 15;
   const int key0 = kb * C::kBKeys, kw0 = key0 + 16 * w, mykey = kw0 + i;
@@ -452,6 +476,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
   f32x4 adk[NT], adv[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) adk[t] = adv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // This lane's row of the key block's dS strip for the group's first query
+  // head (the chunk-local (b, h) rows of a KV row are consecutive); columns
+  // count queries from key0.
+  const int64_t T32 = ds_t32(T), ds_row = ds_row_floats(T), lr = T32 - key0;
+  float* ds_lane = ds ? ds + static_cast<int64_t>(wi.row) * group * ds_row +
+                            ds_strip_offset(kb, T32) + static_cast<int64_t>(16 * w + i) * lr + 4 * g
+                      : nullptr;
 
   // The streamed sequence: for each query head of the group, the query tiles
   // key0, key0 + 32, ... below T.
@@ -522,6 +554,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
           s[mt][e] = p;
           dp[mt][e] = p * (dp[mt][e] - Es[ql]);
         }
+      if (ds_lane) {  // queries qt0 + 16mt + 4g + (0..3) of this lane's key
+        float* dst = ds_lane + (step / ntile) * ds_row + (qt0 - key0);
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) *reinterpret_cast<f32x4*>(dst + 16 * mt) = dp[mt];
+      }
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -547,6 +584,105 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
       dkr[4 * t + g] = adk[t] * scale;
       dvr[4 * t + g] = adv[t];
     }
+  }
+}
+
+// dQ from the stored dS: dQ^T += K^T dS^T per 16 queries, 64 per workgroup,
+// over 32-key tiles in key order (the same MFMA orientation as attn_bwd_dq,
+// whose dS^T operand this kernel loads instead of recomputing).  K tiles are
+// double-buffered in LDS; the next tile's dS values (eight per lane: keys
+// 16kt + 4g + e, query i) are loaded into registers before the current
+// tile's MFMAs.  Keys after the lane's query, and queries at or past T, read
+// nothing and count as 0.
+template <int D>
+struct DqDsCfg {
+  static constexpr int kBQ = 64, kBK = 32, kKS = D + 4;
+  static constexpr int kBuf = kBK * kKS;
+  static constexpr int kSmem = 2 * kBuf;
+};
+
+template <int D>
+__global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_ds_kernel(
+    const float* __restrict__ k, const float* __restrict__ ds, float* __restrict__ dq, int row0,
+    int T, int H, int Hk, float scale) {
+  using C = DqDsCfg<D>;
+  constexpr int NT = D / 16;
+  __shared__ __attribute__((aligned(16))) float smem[C::kSmem];
+
+  const int nqb = (T + C::kBQ - 1) / C::kBQ;
+  const WorkItem wi = work_item(nqb);
+  const int qb = nqb - 1 - wi.tile;  // longest rows first
+  const int row = row0 + wi.row;     // (b, h)
+  const int h = row % H, b = row / H;
+  const int hk = h / (H / Hk);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, i = lane & 15;
+  const int q0 = qb * C::kBQ, qw0 = q0 + 16 * w, myq = qw0 + i;
+  const int64_t qs = static_cast<int64_t>(H) * D, ks = static_cast<int64_t>(Hk) * D;
+  const float* kbase = k + static_cast<int64_t>(b) * T * ks + static_cast<int64_t>(hk) * D;
+  const int64_t T32 = ds_t32(T);
+  const float* dsrow = ds + static_cast<int64_t>(wi.row) * ds_row_floats(T);
+  const bool live = myq < T;
+
+  // dS^T[key][myq] for keys k0 + 16kt + 4g + e of 32-key tile kbi.
+  auto load_ds = [&](int kbi, float (&dst)[2][4]) {
+    const int k0 = kbi * C::kBK, sb = k0 >> 6;
+    const int64_t lr = T32 - 64 * sb;
+    const float* strip = dsrow + ds_strip_offset(sb, T32) + (myq - 64 * sb);
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int key = k0 + 16 * kt + 4 * g + e;
+        dst[kt][e] = (live && key <= myq) ? strip[static_cast<int64_t>(key - 64 * sb) * lr] : 0.f;
+      }
+  };
+
+  f32x4 acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int kend = min(T, q0 + C::kBQ);
+  const int nkb = (kend + C::kBK - 1) / C::kBK;
+  RowTile<D, C::kBK> tk;
+  float cur[2][4], nxt[2][4];
+  tk.load(kbase, ks, T);
+  load_ds(0, cur);
+  tk.store(smem, C::kKS);
+  __syncthreads();
+
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int k0 = kb * C::kBK;
+    const bool more = kb + 1 < nkb;
+    if (more) {
+      tk.load(kbase + static_cast<int64_t>(k0 + C::kBK) * ks, ks, T - k0 - C::kBK);
+      load_ds(kb + 1, nxt);
+    }
+    const float* Ks = smem + (kb & 1) * C::kBuf;
+    if (k0 <= qw0 + 15) {  // some key of the tile is seen by some query of this wave
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = (16 * kt + 4 * g + e) * C::kKS;
+#pragma unroll
+          for (int t = 0; t < NT; ++t) acc[t] = mfma16(Ks[r + 16 * t + i], cur[kt][e], acc[t]);
+        }
+    }
+    if (more) {
+      tk.store(smem + ((kb + 1) & 1) * C::kBuf, C::kKS);
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cur[kt][e] = nxt[kt][e];
+    }
+    __syncthreads();
+  }
+
+  if (live) {
+    f32x4* dqr = reinterpret_cast<f32x4*>(dq + static_cast<int64_t>(b) * T * qs +
+                                          static_cast<int64_t>(h) * D + myq * qs);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) dqr[4 * t + g] = acc[t] * scale;
   }
 }
 
@@ -582,9 +718,67 @@ extern "C" int ember_attn_fwd(const float* q, const float* k, const float* v, fl
   return launch_status();
 }
 
+namespace {
+
+size_t delta_bytes(int64_t B, int64_t T, int64_t H) {
+  return static_cast<size_t>((B * T * H * 4 + 255) / 256 * 256);
+}
+
+template <int D>
+int launch_bwd(const float* q, const float* k, const float* v, const float* o, const float* lse,
+               const float* dout, float* dq, float* dk, float* dv, int64_t B, int64_t T,
+               int64_t H, int64_t Hk, float scale, char* ws, size_t ws_bytes, hipStream_t st) {
+  float* delta = reinterpret_cast<float*>(ws);
+  const int64_t rows = B * T * H;
+  const int Ti = static_cast<int>(T), Hi = static_cast<int>(H), Hki = static_cast<int>(Hk);
+  const float sl = scale * kLog2e;
+  constexpr int RPB = kThreads / (D / 4);
+  attn_delta_kernel<D><<<static_cast<unsigned>((rows + RPB - 1) / RPB), kThreads, 0, st>>>(
+      o, dout, delta, rows, Ti, Hi);
+  int rc = launch_status();
+  if (rc) return rc;
+  static_assert(DqCfg<D>::kBQ == 64 && DqDsCfg<D>::kBQ == 64, "dQ grids assume 64 queries");
+  static_assert(DkvCfg<D>::kBKeys == 64, "dK/dV grid assumes 64 keys");
+  const unsigned nqb = static_cast<unsigned>((T + 63) / 64);
+  const int64_t group = H / Hk, kv_rows = B * Hk;
+  const size_t dlt = delta_bytes(B, T, H);
+  const size_t kv_row_bytes = static_cast<size_t>(group * ds_row_floats(T)) * sizeof(float);
+  int64_t chunk = static_cast<int64_t>((ws_bytes - dlt) / kv_row_bytes);
+  if (chunk < 1) {  // no room for dS: dQ recomputes S and dP
+    attn_bwd_dq_kernel<D><<<dim3(nqb * static_cast<unsigned>(B * H)), kThreads, 0, st>>>(
+        q, k, v, dout, lse, delta, dq, Ti, Hi, Hki, sl, scale);
+    if ((rc = launch_status())) return rc;
+    attn_bwd_dkdv_kernel<D><<<dim3(nqb * static_cast<unsigned>(kv_rows)), kThreads, 0, st>>>(
+        q, k, v, dout, lse, delta, dk, dv, nullptr, 0, Ti, Hi, Hki, sl, scale);
+    return launch_status();
+  }
+  // Chunks of KV rows whose dS fits; a multiple of 8 rows keeps the XCD
+  // regrouping of the work items.
+  if (chunk < kv_rows && chunk >= 8) chunk -= chunk % 8;
+  if (chunk > kv_rows) chunk = kv_rows;
+  float* ds = reinterpret_cast<float*>(ws + dlt);
+  for (int64_t r0 = 0; r0 < kv_rows; r0 += chunk) {
+    const int64_t n = kv_rows - r0 < chunk ? kv_rows - r0 : chunk;
+    attn_bwd_dkdv_kernel<D><<<dim3(nqb * static_cast<unsigned>(n)), kThreads, 0, st>>>(
+        q, k, v, dout, lse, delta, dk, dv, ds, static_cast<int>(r0), Ti, Hi, Hki, sl, scale);
+    if ((rc = launch_status())) return rc;
+    attn_bwd_dq_ds_kernel<D><<<dim3(nqb * static_cast<unsigned>(n * group)), kThreads, 0, st>>>(
+        k, ds, dq, static_cast<int>(r0 * group), Ti, Hi, Hki, scale);
+    if ((rc = launch_status())) return rc;
+  }
+  return EMBER_OK;
+}
+
+}  // namespace
+
 extern "C" size_t ember_attn_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H) {
   if (B <= 0 || T <= 0 || H <= 0) return 0;
-  return static_cast<size_t>(B * T * H) * sizeof(float);
+  return delta_bytes(B, T, H) + static_cast<size_t>(B * H * ds_row_floats(T)) * sizeof(float);
+}
+
+extern "C" size_t ember_attn_bwd_workspace_bytes_min(int64_t B, int64_t T, int64_t H) {
+  if (B <= 0 || T <= 0 || H <= 0) return 0;
+  return delta_bytes(B, T, H);
 }
 
 extern "C" int ember_attn_bwd(const float* q, const float* k, const float* v, const float* o,
@@ -596,37 +790,13 @@ extern "C" int ember_attn_bwd(const float* q, const float* k, const float* v, co
   if (B == 0 || T == 0) return EMBER_OK;
   if (!q || !k || !v || !o || !lse || !dout || !dq || !dk || !dv) return EMBER_EINVAL;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(dout) ||
-      !aligned16(dq) || !aligned16(dk) || !aligned16(dv))
+      !aligned16(dq) || !aligned16(dk) || !aligned16(dv) || !aligned16(workspace))
     return EMBER_EALIGN;
-  if (!workspace || workspace_bytes < ember_attn_bwd_workspace_bytes(B, T, H))
-    return EMBER_EWORKSPACE;
-  float* delta = static_cast<float*>(workspace);
-  hipStream_t st = as_stream(s);
-  const int64_t rows = B * T * H;
-  const int Ti = static_cast<int>(T), Hi = static_cast<int>(H), Hki = static_cast<int>(Hk);
-  const float sl = scale * kLog2e;
-  static_assert(DqCfg<64>::kBQ == 64 && DqCfg<128>::kBQ == 64, "dQ grid assumes 64 queries");
-  static_assert(DkvCfg<64>::kBKeys == 64 && DkvCfg<128>::kBKeys == 64, "dK/dV grid assumes 64 keys");
-  const dim3 gq(static_cast<unsigned>((T + 63) / 64 * H * B));
-  const dim3 gk(static_cast<unsigned>((T + 63) / 64 * Hk * B));
-  if (D == 64) {
-    attn_delta_kernel<64><<<static_cast<unsigned>((rows + 15) / 16), kThreads, 0, st>>>(
-        o, dout, delta, rows, Ti, Hi);
-    if ((rc = launch_status())) return rc;
-    attn_bwd_dq_kernel<64><<<gq, kThreads, 0, st>>>(q, k, v, dout, lse, delta, dq, Ti, Hi, Hki,
-                                                    sl, scale);
-    if ((rc = launch_status())) return rc;
-    attn_bwd_dkdv_kernel<64><<<gk, kThreads, 0, st>>>(q, k, v, dout, lse, delta, dk, dv, Ti, Hi,
-                                                      Hki, sl, scale);
-  } else {
-    attn_delta_kernel<128><<<static_cast<unsigned>((rows + 7) / 8), kThreads, 0, st>>>(
-        o, dout, delta, rows, Ti, Hi);
-    if ((rc = launch_status())) return rc;
-    attn_bwd_dq_kernel<128><<<gq, kThreads, 0, st>>>(q, k, v, dout, lse, delta, dq, Ti, Hi, Hki,
-                                                     sl, scale);
-    if ((rc = launch_status())) return rc;
-    attn_bwd_dkdv_kernel<128><<<gk, kThreads, 0, st>>>(q, k, v, dout, lse, delta, dk, dv, Ti, Hi,
-                                                       Hki, sl, scale);
-  }
-  return launch_status();
+  if (!workspace || workspace_bytes < delta_bytes(B, T, H)) return EMBER_EWORKSPACE;
+  char* ws = static_cast<char*>(workspace);
+  if (D == 64)
+    return launch_bwd<64>(q, k, v, o, lse, dout, dq, dk, dv, B, T, H, Hk, scale, ws,
+                          workspace_bytes, as_stream(s));
+  return launch_bwd<128>(q, k, v, o, lse, dout, dq, dk, dv, B, T, H, Hk, scale, ws,
+                         workspace_bytes, as_stream(s));
 }

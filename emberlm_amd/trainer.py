@@ -96,6 +96,7 @@ _SIGS = {
     "ctd_trainer_forward_cached": (i32, [vp, vp, lptr, i64, i64, i32, i32, fptr, i64]),
     "ctd_sample": (i32, [fptr, i64, i64, f32, i32, f32, u64, i32, i32, lptr]),
     "ctd_set_head_chunk_rows": (i32, [i64]),
+    "ctd_set_attn_ds_bytes": (i32, [i64]),
     "ctd_trainer_generate": (i32, [vp, lptr, i64, i32, f32, i32, f32, u64, i64, lptr,
                                    C.POINTER(C.c_double), C.POINTER(C.c_double)]),
 }
@@ -380,6 +381,11 @@ def sample(logits, temperature=1.0, top_k=0, top_p=0.0, seed=0, draws=1, on_devi
     _ck(lib().ctd_sample(p, B, V, temperature, top_k, top_p, seed, draws, int(on_device),
                          out.ctypes.data_as(lptr)), "sample")
     return out
+
+
+def set_attn_ds_bytes(nbytes):
+    """Device bytes the attention backward may keep dS in (-1 default, 0 none)."""
+    _ck(lib().ctd_set_attn_ds_bytes(int(nbytes)), "set_attn_ds_bytes")
 
 
 def set_head_chunk_rows(rows):

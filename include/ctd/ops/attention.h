@@ -10,6 +10,16 @@ namespace ctd::ops {
 // q [B,T,H,D], k/v [B,T,Hk,D] -> o [B,T,H,D]; H % Hk == 0, D in {64, 128}.
 // Autograd-aware: saves q, k, v, o and the per-row log-sum-exp.
 Tensor causal_attention(const Tensor& q, const Tensor& k, const Tensor& v, float scale);
+// Device memory the backward may use to keep dS between its dK/dV and dQ
+// passes (ember_attn_bwd): less than a layer's full dS splits the pass into
+// chunks of KV heads, 0 recomputes dS in the dQ pass instead; -1 restores the
+// default (kAttentionBackwardDsBytes).  Results do not depend on it.  The
+// default holds Qwen3-1.7B's dS at B=8, T=4096 (4.4 GB per layer) in two
+// chunks, which leaves the step's peak HBM where it is (the workspace is live
+// only while a layer's backward runs) at 1.7% more attention-backward time
+// than one chunk; smaller models fit in one.
+constexpr int64_t kAttentionBackwardDsBytes = 2500000000;
+void set_attention_backward_ds_bytes(int64_t bytes);
 // Forward only; lse (if non-null) receives the [B,H,T] log-sum-exp.
 Tensor causal_attention_impl(const Tensor& q, const Tensor& k, const Tensor& v, float scale,
                              Tensor* lse = nullptr);

@@ -198,6 +198,10 @@ int ctd_trainer_generate(ctd_trainer_t t, const int64_t* prompt, int64_t P, int3
  * 0 = automatic). */
 int ctd_set_head_chunk_rows(int64_t rows);
 
+/* Device bytes the attention backward may keep dS in
+ * (ops::set_attention_backward_ds_bytes; -1 = default, 0 = recompute). */
+int ctd_set_attn_ds_bytes(int64_t bytes);
+
 #ifdef __cplusplus
 }
 #endif

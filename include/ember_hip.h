@@ -201,12 +201,19 @@ int ember_attn_fwd(const float* q, const float* k, const float* v, float* o, flo
                    int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D, float scale,
                    ember_stream_t s);
 /* Backward of ember_attn_fwd: dq [B,T,H,D], dk/dv [B,T,Hk,D] (written, summed
- * over each KV head's query group in a fixed order: deterministic).
- * workspace >= ember_attn_bwd_workspace_bytes(). Replaces BmmBackward,
- * SoftmaxBackward, CausalMaskBackward, MulScalarBackward, RepeatKvBackward and
- * PermuteBackward of the chain (matmul.cpp:137-152, softmax.cu:54-80,
- * mask.cu:41-52, repeat_kv.cu:29-43, permute.cu). */
+ * over each KV head's query group in a fixed order: deterministic).  Replaces
+ * BmmBackward, SoftmaxBackward, CausalMaskBackward, MulScalarBackward,
+ * RepeatKvBackward and PermuteBackward of the chain (matmul.cpp:137-152,
+ * softmax.cu:54-80, mask.cu:41-52, repeat_kv.cu:29-43, permute.cu).
+ * The workspace holds rowsum(dO*O) ([B,H,T]) and, when it is large enough, dS
+ * for the causal part of as many KV heads' query groups as fit (4*T^2/2 bytes
+ * per (batch, query head) roughly); the dQ product then reads dS instead of
+ * recomputing it, and the work runs in chunks of KV heads.
+ * ember_attn_bwd_workspace_bytes: the size that keeps all of dS (fastest);
+ * ember_attn_bwd_workspace_bytes_min: the smallest accepted (no dS kept).
+ * Any size in between works; dq, dk and dv do not depend on the chunking. */
 size_t ember_attn_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H);
+size_t ember_attn_bwd_workspace_bytes_min(int64_t B, int64_t T, int64_t H);
 int ember_attn_bwd(const float* q, const float* k, const float* v, const float* o,
                    const float* lse, const float* dout, float* dq, float* dk, float* dv,
                    int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D, float scale,

@@ -474,16 +474,65 @@ def test_attention_fwd_bwd_vs_oracle(B, T, H, Hk, D):
     assert torch.equal(DQ, DQ2) and torch.equal(DK, DK2) and torch.equal(DV, DV2)
 
 
-def _attn_hip(Q, K, Vv, DO, B, T, H, Hk, D, scale):
-    """Forward and backward through the C ABI on device tensors."""
+def _attn_hip(Q, K, Vv, DO, B, T, H, Hk, D, scale, wsb=None):
+    """Forward and backward through the C ABI on device tensors (the backward
+    with `wsb` bytes of workspace, by default all it can use)."""
     Ot, L = empty((B, T, H, D)), empty((B, H, T))
     call("ember_attn_fwd", p(Q), p(K), p(Vv), p(Ot), p(L), B, T, H, Hk, D, scale, None)
-    wsb = capi.lib().ember_attn_bwd_workspace_bytes(B, T, H)
-    WS = empty((wsb // 4,))
+    if wsb is None:
+        wsb = capi.lib().ember_attn_bwd_workspace_bytes(B, T, H)
+    WS = empty(((wsb + 3) // 4,))
     DQ, DK, DV = empty((B, T, H, D)), empty((B, T, Hk, D)), empty((B, T, Hk, D))
     call("ember_attn_bwd", p(Q), p(K), p(Vv), p(Ot), p(L), p(DO), p(DQ), p(DK), p(DV), B, T, H, Hk,
          D, scale, p(WS), wsb, None)
     return Ot, L, DQ, DK, DV
+
+
+def _ds_row_floats(T):
+    # dS strips of one (batch, head): 64 key rows x (T32 - 64 kb) queries
+    T32 = (T + 31) // 32 * 32
+    return sum(64 * (T32 - 64 * kb) for kb in range((T + 63) // 64))
+
+
+@pytest.mark.parametrize("B,T,H,Hk,D", [
+    (2, 300, 8, 2, 64),     # 4 KV rows, ragged T (T32 = 320)
+    (4, 130, 8, 1, 128),    # 4 KV rows of group 8, D 128
+    (1, 200, 32, 8, 64),    # 8 KV rows of group 4 (the c4 head layout)
+    (2, 96, 32, 8, 64),     # 16 KV rows: chunks of 8 keep the XCD regrouping
+])
+def test_attention_bwd_workspace_paths(B, T, H, Hk, D):
+    # The backward keeps dS in the workspace when it fits, in chunks of KV rows
+    # when only part fits, and recomputes it with the minimum workspace.  dK
+    # and dV come from the same arithmetic on every path (bitwise equal); dQ
+    # is bitwise equal across chunkings and within tolerance of the oracle on
+    # both dQ kernels.
+    r = rng(B * 1000 + T + H)
+    q = r.standard_normal((B, T, H, D)).astype(np.float32)
+    k = r.standard_normal((B, T, Hk, D)).astype(np.float32)
+    v = r.standard_normal((B, T, Hk, D)).astype(np.float32)
+    do = r.standard_normal((B, T, H, D)).astype(np.float32)
+    scale = 1.0 / math.sqrt(D)
+    lib = capi.lib()
+    lo = lib.ember_attn_bwd_workspace_bytes_min(B, T, H)
+    hi = lib.ember_attn_bwd_workspace_bytes(B, T, H)
+    kv_row = (H // Hk) * _ds_row_floats(T) * 4
+    assert lo == (B * T * H * 4 + 255) // 256 * 256 and hi == lo + B * Hk * kv_row
+    Q, K, Vv, DO = dev(q), dev(k), dev(v), dev(do)
+    runs = {}
+    for name, wsb in [("full", hi), ("one", lo + kv_row), ("three", lo + 3 * kv_row + 100),
+                      ("eight", lo + 8 * kv_row), ("min", lo)]:
+        _, _, DQ, DK, DV = _attn_hip(Q, K, Vv, DO, B, T, H, Hk, D, scale, wsb)
+        runs[name] = (host(DQ), host(DK), host(DV))
+    dq_ref, dk_ref, dv_ref = O.attention_bwd(q, k, v, do, scale)
+    for name, (dq, dk, dv) in runs.items():
+        assert np.array_equal(dk, runs["full"][1]) and np.array_equal(dv, runs["full"][2]), name
+        if name != "min":
+            assert np.array_equal(dq, runs["full"][0]), name
+    for name in ("full", "min"):
+        dq, dk, dv = runs[name]
+        assert_close(dq, dq_ref, name=f"{name} dq")
+        assert_close(dk, dk_ref, name=f"{name} dk")
+        assert_close(dv, dv_ref, name=f"{name} dv")
 
 
 # The launch layouts of the BASELINE configs: c3 Qwen3-0.6B (64 (batch, head)
@@ -528,6 +577,10 @@ def test_attention_real_layouts_full_T_vs_torch(name, B, T, H, Hk, D):
     do = torch.randn(B, T, H, D, device="cuda", generator=g)
     scale = 1.0 / math.sqrt(D)
     Ot, L, DQ, DK, DV = _attn_hip(q, k, v, do, B, T, H, Hk, D, scale)
+    # the recompute path (minimum workspace) at the same full size
+    _, _, DQm, DKm, DVm = _attn_hip(q, k, v, do, B, T, H, Hk, D, scale,
+                                    capi.lib().ember_attn_bwd_workspace_bytes_min(B, T, H))
+    assert torch.equal(DK, DKm) and torch.equal(DV, DVm)
     G = H // Hk
     causal = torch.triu(torch.ones(T, T, dtype=torch.bool, device="cuda"), 1)
     refs = {n: torch.empty_like(t) for n, t in (("o", Ot), ("dq", DQ), ("dk", DK), ("dv", DV))}
@@ -548,7 +601,7 @@ def test_attention_real_layouts_full_T_vs_torch(name, B, T, H, Hk, D):
             refs["dv"][b, :, j] = vj.grad
             ref_lse[b, heads] = torch.logsumexp(s.detach(), -1)
     torch.cuda.synchronize()
-    for n, got in (("o", Ot), ("dq", DQ), ("dk", DK), ("dv", DV)):
+    for n, got in (("o", Ot), ("dq", DQ), ("dk", DK), ("dv", DV), ("dq", DQm)):
         rel = ((got - refs[n]).norm() / refs[n].norm()).item()
         assert rel < 1e-5, (name, n, rel)
         err = (got - refs[n]).abs()
