@@ -12,8 +12,8 @@ weights ~N(0,0.02), norm weights 1.
 
 Prints ONE JSON line: tokens/s (B*T per second), peak HBM, the GEMM roofline
 (HIP events around every GEMM launch of the timed steps) and a CPU baseline
-(the scalar CPU oracle timed on a bounded sample of the same workload and
-extrapolated; 1 core).
+(the reference's scalar fp32 CPU test ops on one host core
+measured in full, this workload extrapolated from measured slices).
 """
 from __future__ import annotations
 
@@ -46,69 +46,119 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(cfg, B, T, budget_s=20.0):
-    """Scalar CPU oracle (double, 1 thread) on a bounded sample, extrapolated to one step.
-
-    Sample: one decoder block forward+backward (the backward recomputes the block,
-    as checkpointing does) on s tokens at full hidden width; one attention head
-    forward+backward at T_s; the tied LM head for r rows.  Per-token costs scale
-    linearly to B*T tokens and L layers, attention by (T/T_s)^2 * H * B * L, the
-    head by B*T rows x 3 GEMMs (forward, dX, dW)."""
+def _ref_block(rng, d, H, Hk, D, I, qk_norm, norm_std):
+    """Block weights ~N(0, 0.02) in float32; norm weights 1, or ~N(0, 0.02)
+    too when norm_std."""
     import numpy as np
-    import oracle as O
+    n = lambda *sh: (0.02 * rng.standard_normal(sh)).astype(np.float32)  # noqa: E731
+    norm = (lambda k: n(k)) if norm_std else (lambda k: np.ones(k, np.float32))
+    w = {"input_layernorm": norm(d), "post_attention_layernorm": norm(d),
+         "q_proj": n(H * D, d), "k_proj": n(Hk * D, d), "v_proj": n(Hk * D, d),
+         "o_proj": n(d, H * D), "gate_proj": n(I, d), "up_proj": n(I, d), "down_proj": n(d, I)}
+    if qk_norm:
+        w["q_norm"], w["k_norm"] = norm(D), norm(D)
+    return w
+
+
+def cpu_baseline(cfg, B, T):
+    """The reference's scalar fp32 CPU ops as its unit tests write them
+    (oracle/ref_f32.c: mm_cpu, rms_norm_cpu, softmax_cpu, rope_cpu, silu, the
+    AdamW closed form; the backward formulas are that file's scalar restatement
+    of the reference kernels), built -O2 and run on one host core.
+
+    1. BASELINE config 0 in full, measured: one SmolLM2-135M block at B=1,
+       T=256 forward+backward without and with checkpointing, and one AdamW
+       step over its 3.54 M weights.
+    2. The benchmark workload, extrapolated from measured slices (a full step
+       would take days): one block forward + recompute + backward on s tokens
+       at full width (scaled by tokens and layers), one attention head forward
+       (twice: forward and recompute) + backward at T_s (scaled by (T/T_s)^2,
+       heads, batch and layers), the tied LM head + masked CE on r rows x V_s
+       vocabulary rows (scaled by tokens and V), and AdamW over 4 M weights
+       (scaled by the parameter count)."""
+    import numpy as np
+    from oracle import ref_f32 as RF
 
     rng = np.random.default_rng(0)
+    t = time.perf_counter
+
+    # 1. config 0 in full
+    c1 = RF.BlockCfg(d=576, H=9, Hk=3, Dh=64, I=1536, eps=1e-5, theta=1e5)
+    w1 = _ref_block(rng, 576, 9, 3, 64, 1536, False, True)
+    x = rng.standard_normal((256, 576)).astype(np.float32)
+    dy = rng.standard_normal((256, 576)).astype(np.float32)
+    t0 = t()
+    RF.block_fwd_bwd(c1, w1, x, dy, checkpoint=False)
+    t_off = t() - t0
+    t0 = t()
+    _, _, g1 = RF.block_fwd_bwd(c1, w1, x, dy, checkpoint=True)
+    t_on = t() - t0
+    t0 = t()
+    for k, p in w1.items():
+        RF.adamw(p, g1[k], np.zeros_like(p), np.zeros_like(p), 1e-4, 0.9, 0.95, 1e-8,
+                 0.1 if p.ndim == 2 else 0.0, 1)
+    t_adam1 = t() - t0
+
+    # 2. the workload's slices
     d, I, H, Hk, D, V, L = (cfg.hidden_size, cfg.intermediate_size, cfg.num_heads,
                             cfg.num_kv_heads, cfg.head_dim, cfg.vocab_size, cfg.num_layers)
-    oc = O.make_cfg(vocab=V, hidden=d, inter=I, layers=1, heads=H, kv_heads=Hk, head_dim=D,
-                    eps=cfg.rms_norm_eps, theta=cfg.rope_theta, rope_factor=cfg.rope_factor,
-                    qk_norm=cfg.qk_norm)
-    w = {"input_layernorm": np.ones(d), "post_attention_layernorm": np.ones(d),
-         "q_proj": 0.02 * rng.standard_normal((H * D, d)),
-         "k_proj": 0.02 * rng.standard_normal((Hk * D, d)),
-         "v_proj": 0.02 * rng.standard_normal((Hk * D, d)),
-         "o_proj": 0.02 * rng.standard_normal((d, H * D)),
-         "gate_proj": 0.02 * rng.standard_normal((I, d)),
-         "up_proj": 0.02 * rng.standard_normal((I, d)),
-         "down_proj": 0.02 * rng.standard_normal((d, I))}
-    if cfg.qk_norm:
-        w["q_norm"] = np.ones(D)
-        w["k_norm"] = np.ones(D)
-    s = 48
-    x = rng.standard_normal((1, s, d))
-    t0 = time.perf_counter()
-    O.block_bwd(oc, w, x, rng.standard_normal((1, s, d)))  # forward + recompute + backward
-    t_block = time.perf_counter() - t0
-    Ts = 256
-    q = rng.standard_normal((1, Ts, 1, D))
-    t0 = time.perf_counter()
-    O.attention_fwd(q, q, q)
-    O.attention_bwd(q, q, q, q)
-    t_attn = time.perf_counter() - t0
-    r, Vs = 1, min(V, 16384)  # head cost is linear in the vocabulary rows
-    hn = rng.standard_normal((r, d))
-    E = 0.02 * rng.standard_normal((Vs, d))
-    t0 = time.perf_counter()
-    O.matmul(hn, E, False, True)
-    t_head = (time.perf_counter() - t0) * V / Vs
-    sample_s = t_block + t_attn + t_head
+    cb = RF.BlockCfg(d=d, H=H, Hk=Hk, Dh=D, I=I, eps=cfg.rms_norm_eps, theta=cfg.rope_theta)
+    wb = _ref_block(rng, d, H, Hk, D, I, bool(cfg.qk_norm), False)
+    s = 16
+    xs = rng.standard_normal((s, d)).astype(np.float32)
+    t0 = t()
+    RF.block_fwd_bwd(cb, wb, xs, xs, checkpoint=True)
+    t_block = t() - t0
+    Ts = 512
+    q = rng.standard_normal((Ts, D)).astype(np.float32)
+    t0 = t()
+    RF.attention_head(q, q, q)
+    t_afwd = t() - t0
+    t0 = t()
+    RF.attention_head(q, q, q, q)
+    t_afb = t() - t0
+    r, Vs = 2, min(V, 16384)
+    hs = rng.standard_normal((r, d)).astype(np.float32)
+    E = (0.02 * rng.standard_normal((Vs, d))).astype(np.float32)
+    t0 = t()
+    RF.lm_head_ce(hs, E, rng.integers(0, Vs, r), np.ones(r, np.float32))
+    t_head = t() - t0
+    na = 1 << 22
+    pa = rng.standard_normal(na).astype(np.float32)
+    t0 = t()
+    RF.adamw(pa, pa, np.zeros_like(pa), np.zeros_like(pa), 1e-4, 0.9, 0.95, 1e-8, 0.1, 1)
+    t_adam = t() - t0
+    from emberlm_amd import trainer as TR
+    P = TR.param_count(cfg)
     N = B * T
-    step_s = (t_block / s * N * L
-              + t_attn * (T / Ts) ** 2 * H * B * L
-              + t_head / r * N * 3)
+    # the block sample's own attention over s tokens is negligible beside its projections
+    step_s = (t_block / s * N * L + (t_afwd + t_afb) * (T / Ts) ** 2 * H * B * L
+              + t_head / r * N * (V / Vs) + t_adam * P / na)
+    sample_s = t_off + t_on + t_adam1 + t_block + t_afwd + t_afb + t_head + t_adam
+    ncpu = os.cpu_count()
     return {
         "value": N / step_s,
         "unit": "tokens/s",
         "cores": 1,
+        "cores_of": ncpu,
         "kind": "port",
-        "sample": (f"scalar fp64 CPU oracle, 1 thread: one block fwd+recompute+bwd on {s} tokens "
-                   f"({t_block:.2f}s), one head attention fwd+bwd at T={Ts} ({t_attn:.2f}s), "
-                   f"tied LM head for {r} row x {Vs} vocab rows (scaled to V: {t_head:.2f}s); "
-                   f"extrapolated linearly in tokens "
-                   f"and layers, attention by T^2; sample {sample_s:.1f}s, extrapolated step "
-                   f"{step_s:.0f}s"),
+        "sample": (f"the reference's scalar fp32 CPU test ops (mm_cpu, rms_norm_cpu, softmax_cpu, "
+                   f"rope_cpu, silu, AdamW closed form) composed into the block, LM head and "
+                   f"AdamW, 1 thread of {ncpu}; value extrapolated to this workload's step from "
+                   f"a block fwd+recompute+bwd on {s} tokens ({t_block:.2f}s), one attention head "
+                   f"fwd x2 + bwd at T={Ts} ({t_afwd + t_afb:.2f}s, scaled by T^2), the LM head + "
+                   f"CE on {r} rows x {Vs} vocab rows ({t_head:.2f}s) and AdamW on {na} weights "
+                   f"({t_adam:.3f}s): extrapolated step {step_s:.0f}s; sample {sample_s:.1f}s"),
+        "config0_measured": {
+            "workload": "one SmolLM2-135M block, B1 T256 (BASELINE configs[0])",
+            "fwd_bwd_s": round(t_off, 3),
+            "fwd_bwd_checkpoint_s": round(t_on, 3),
+            "recompute_overhead": round(t_on / t_off - 1.0, 4),
+            "adamw_step_s": round(t_adam1, 4),
+            "tokens_per_s_checkpoint_plus_adamw": round(256 / (t_on + t_adam1), 2),
+        },
         "cpu_model": _cpu_model(),
-        "nproc": os.cpu_count(),
+        "nproc": ncpu,
     }
 
 
