@@ -8,7 +8,10 @@
 //   - a node is released as soon as it has run (its saved tensors with it)
 //     instead of being kept alive until backward returns
 //     (keep_alive, autograd.cu:170, 251); the walked graph is consumed, and a
-//     second backward through it throws;
+//     second backward through it throws, unless the backward was asked to
+//     retain the graph (then nodes keep their saved tensors, a leaf's first
+//     gradient is copied rather than aliased so later passes add into
+//     storage only the leaf holds, and the graph can be walked again);
 //   - fan-in accumulation is done out of place when the slot's storage is
 //     shared (e.g. AddBackward hands the same grad to both inputs without
 //     copying it), in place otherwise.
@@ -19,11 +22,21 @@
 
 #include "ctd/autograd.h"
 #include "ctd/runtime.h"
+#include "ember_hip.h"
 
 namespace ctd::autograd {
 
 namespace {
 thread_local bool g_grad_enabled = true;
+thread_local bool g_retain_graph = false;
+
+Tensor copy_of(const Tensor& t) {
+  Tensor c = Tensor::empty(t.shape(), t.dtype(), t.device());
+  if (t.nbytes())
+    CTD_CHECK(ember_memcpy_async(c.data_ptr(), t.data_ptr(), t.nbytes(), 2,
+                                 runtime::compute_stream()));
+  return c;
+}
 
 struct AccumulateGrad : public Node {
   std::weak_ptr<AutogradMeta> leaf_meta;
@@ -34,7 +47,9 @@ struct AccumulateGrad : public Node {
     if (!meta) return {};
     const Tensor& g = grads_out[0];
     if (!meta->grad.storage()) {
-      meta->grad = g;
+      // With the graph retained, g may be a node's saved tensor that a later
+      // pass returns again: the leaf gets its own copy to add into.
+      meta->grad = g_retain_graph ? copy_of(g) : g;
     } else {
       accumulate_inplace(meta->grad, g);
     }
@@ -45,6 +60,7 @@ struct AccumulateGrad : public Node {
 }  // namespace
 
 bool is_grad_enabled() { return g_grad_enabled; }
+bool graph_retained() { return g_retain_graph; }
 NoGradGuard::NoGradGuard() : prev_(g_grad_enabled) { g_grad_enabled = false; }
 NoGradGuard::~NoGradGuard() { g_grad_enabled = prev_; }
 
@@ -127,9 +143,17 @@ Tensor ones_like_scalar(const Tensor& t) {
   return Tensor::from_host(&one, t.shape(), t.dtype(), t.device());
 }
 
-void run_backward(const std::shared_ptr<AutogradMeta>& root_meta, Tensor root_grad) {
+struct RetainScope {
+  bool prev;
+  explicit RetainScope(bool on) : prev(g_retain_graph) { g_retain_graph = on; }
+  ~RetainScope() { g_retain_graph = prev; }
+};
+
+void run_backward(const std::shared_ptr<AutogradMeta>& root_meta, Tensor root_grad,
+                  bool retain) {
   if (!root_meta || !root_meta->grad_fn)
     throw std::runtime_error("backward: this tensor has no grad_fn");
+  const RetainScope scope(retain);
   Node* const root = root_meta->grad_fn.get();
   const uint32_t root_nr = root_meta->output_nr;
   if (root->consumed)
@@ -195,6 +219,7 @@ void run_backward(const std::shared_ptr<AutogradMeta>& root_meta, Tensor root_gr
       if (it != indeg.end() && --it->second == 0) ready.push(p);
     }
     out_grads.clear();
+    if (retain) continue;
     // Consume the node: its edges and (when no tensor still refers to it) the
     // node itself with its saved tensors.
     if (!n->next_edges.empty()) n->consumed = true;
@@ -260,14 +285,18 @@ void Tensor::zero_grad_() {
   if (autograd_meta_) autograd_meta_->grad = Tensor{};
 }
 
-void Tensor::backward() {
+void Tensor::backward() { backward(false); }
+
+void Tensor::backward(bool retain_graph) {
   if (!autograd_meta_ || !autograd_meta_->grad_fn)
     throw std::runtime_error("backward: this tensor has no grad_fn");
-  autograd::run_backward(autograd_meta_, autograd::ones_like_scalar(*this));
+  autograd::run_backward(autograd_meta_, autograd::ones_like_scalar(*this), retain_graph);
 }
 
-void Tensor::backward(const Tensor& grad_output) {
-  autograd::run_backward(autograd_meta_, grad_output);
+void Tensor::backward(const Tensor& grad_output) { backward(grad_output, false); }
+
+void Tensor::backward(const Tensor& grad_output, bool retain_graph) {
+  autograd::run_backward(autograd_meta_, grad_output, retain_graph);
 }
 
 Tensor Tensor::detach() const {

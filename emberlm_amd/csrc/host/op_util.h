@@ -30,6 +30,13 @@ inline const float* cfp(const Tensor& t) { return static_cast<const float*>(t.da
 
 inline Tensor empty_like(const Tensor& t) { return Tensor::empty(t.shape(), t.dtype(), t.device()); }
 
+// Drops a backward node's saved tensors once it has run, unless the backward
+// pass retains its graph for another pass (autograd::graph_retained()).
+template <typename... Ts>
+void release_saved(Ts&... ts) {
+  if (!autograd::graph_retained()) ((ts = Tensor{}), ...);
+}
+
 // Scratch buffer from the caching allocator (freed when the returned tensor dies).
 inline Tensor workspace(size_t bytes) {
   return Tensor::empty({static_cast<int64_t>((bytes + 3) / 4)}, DType::kFloat32, kHIP0);

@@ -71,8 +71,7 @@ struct MatmulBackward : autograd::Node {
     autograd::NoGradGuard ng;
     const bool na = next_edges.at(0).node != nullptr, nb = next_edges.at(1).node != nullptr;
     auto [dA, dB] = matmul_like_backward(go.at(0), a, b, ta, tb, na, nb, matmul_impl);
-    a = Tensor{};
-    b = Tensor{};
+    release_saved(a, b);
     return {dA, dB};
   }
 };
@@ -85,8 +84,7 @@ struct BmmBackward : autograd::Node {
     autograd::NoGradGuard ng;
     const bool na = next_edges.at(0).node != nullptr, nb = next_edges.at(1).node != nullptr;
     auto [dA, dB] = matmul_like_backward(go.at(0), a, b, ta, tb, na, nb, bmm_impl);
-    a = Tensor{};
-    b = Tensor{};
+    release_saved(a, b);
     return {dA, dB};
   }
 };
@@ -188,7 +186,7 @@ struct RmsNormBackward : autograd::Node {
     check_f32(go.at(0), "rms_norm backward", "grad");
     auto r = rms_bwd(go[0], x, w, &rstd, eps, next_edges.at(0).node != nullptr,
                      next_edges.at(1).node != nullptr);
-    x = w = rstd = Tensor{};
+    release_saved(x, w, rstd);
     return {r.first, r.second};
   }
 };
@@ -323,7 +321,7 @@ struct MulBackward : autograd::Node {
     Tensor da, db;
     if (next_edges.at(0).node) da = mul_impl(go.at(0), b);
     if (next_edges.at(1).node) db = mul_impl(go.at(0), a);
-    a = b = Tensor{};
+    release_saved(a, b);
     return {da, db};
   }
 };
@@ -334,7 +332,7 @@ struct SiluBackward : autograd::Node {
   std::vector<Tensor> backward(const std::vector<Tensor>& go) override {
     autograd::NoGradGuard ng;
     Tensor dx = silu_backward_impl(x, go.at(0));
-    x = Tensor{};
+    release_saved(x);
     return {dx};
   }
 };
@@ -347,7 +345,7 @@ struct SwigluBackward : autograd::Node {
     check_f32(go.at(0), "swiglu backward", "grad");
     Tensor dg = empty_like(g), du = empty_like(u);
     CTD_CHECK(ember_swiglu_bwd(cfp(g), cfp(u), cfp(go[0]), fp(dg), fp(du), g.numel(), S()));
-    g = u = Tensor{};
+    release_saved(g, u);
     return {dg, du};
   }
 };
@@ -503,7 +501,7 @@ struct CausalAttentionBackward : autograd::Node {
     CTD_CHECK(ember_attn_bwd(cfp(q), cfp(k), cfp(v), cfp(o), cfp(lse), cfp(dout), fp(dq), fp(dk),
                              fp(dv), d.B, d.T, d.H, d.Hk, d.D, scale, ws.data_ptr(), wsb, S()));
     runtime::gemm_profile_end(ev, 2.0 * attn_fwd_flops(d), runtime::kProfileAttnBwd);
-    q = k = v = o = lse = Tensor{};
+    release_saved(q, k, v, o, lse);
     return {dq, dk, dv};
   }
 };

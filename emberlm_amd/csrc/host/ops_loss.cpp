@@ -59,12 +59,15 @@ struct CrossEntropyMaskedBackward : autograd::Node {
     if (!(ms > 0.0f))
       throw std::runtime_error("cross_entropy_masked: sum(loss_mask) == 0 in backward");
     const int64_t N = logits.shape()[0], V = logits.shape()[1];
-    // Overwrite the logits when this node is their only holder (saves a full [N,V] buffer).
-    Tensor dlogits = logits.storage().use_count() == 1 ? logits : empty_like(logits);
+    // Overwrite the logits when this node is their only holder and will not
+    // run again (saves a full [N,V] buffer).
+    Tensor dlogits = logits.storage().use_count() == 1 && !autograd::graph_retained()
+                         ? logits
+                         : empty_like(logits);
     CTD_CHECK(ember_ce_masked_bwd(cfp(logits), static_cast<const int64_t*>(targets.data_ptr()),
                                   cfp(mask), cfp(lse), cfp(dy), cfp(mask_sum), N, V, fp(dlogits),
                                   S()));
-    logits = targets = mask = lse = mask_sum = Tensor{};
+    release_saved(logits, targets, mask, lse, mask_sum);
     return {dlogits, Tensor{}, Tensor{}};
   }
 };
@@ -135,14 +138,22 @@ struct LinearCrossEntropyBackward : autograd::Node {
     if (!(ms > 0.0f))
       throw std::runtime_error("cross_entropy_masked: sum(loss_mask) == 0 in backward");
     dy.copy_to_host(&g);
+    // Scaled in place, unless the graph is kept for another pass, which needs
+    // the gradients for an upstream gradient of 1 again.
+    const bool keep = autograd::graph_retained();
+    Tensor gh = want_h ? dh : Tensor{}, gw = want_w ? dw : Tensor{};
     if (g != 1.0f) {
-      if (want_h) CTD_CHECK(ember_scale(cfp(dh), g, fp(dh), dh.numel(), S()));
-      if (want_w) CTD_CHECK(ember_scale(cfp(dw), g, fp(dw), dw.numel(), S()));
+      if (want_h) {
+        if (keep) gh = empty_like(dh);
+        CTD_CHECK(ember_scale(cfp(dh), g, fp(gh), dh.numel(), S()));
+      }
+      if (want_w) {
+        if (keep) gw = empty_like(dw);
+        CTD_CHECK(ember_scale(cfp(dw), g, fp(gw), dw.numel(), S()));
+      }
     }
-    std::vector<Tensor> out = {want_h ? dh : Tensor{}, want_w ? dw : Tensor{}, Tensor{},
-                               Tensor{}};
-    dh = dw = mask_sum = Tensor{};
-    return out;
+    release_saved(dh, dw, mask_sum);
+    return {gh, gw, Tensor{}, Tensor{}};
   }
 };
 
@@ -245,7 +256,7 @@ struct EmbeddingBackward : autograd::Node {
   std::vector<Tensor> backward(const std::vector<Tensor>& go) override {
     autograd::NoGradGuard ng;
     Tensor dw = embedding_backward_impl(ids, go.at(0), vocab);
-    ids = Tensor{};
+    release_saved(ids);
     return {Tensor{}, dw};
   }
 };

@@ -22,7 +22,7 @@ struct SoftmaxBackward : autograd::Node {
   std::vector<Tensor> backward(const std::vector<Tensor>& go) override {
     autograd::NoGradGuard ng;
     Tensor dx = softmax_backward_impl(y, go.at(0));
-    y = Tensor{};
+    release_saved(y);
     return {dx};
   }
 };

@@ -23,7 +23,8 @@ class Node {
   virtual std::vector<Tensor> backward(const std::vector<Tensor>& grads_out) = 0;
   virtual const char* name() const { return "Node"; }
   std::vector<Edge> next_edges;
-  // Set once a backward pass has run this node and released its edges.
+  // Set once a backward pass that does not retain the graph has run this
+  // node and released its edges.
   bool consumed = false;
 };
 
@@ -36,6 +37,13 @@ struct AutogradMeta {
 };
 
 bool is_grad_enabled();
+
+// True while a backward pass runs that keeps its graph for another pass
+// (Tensor::backward(..., retain_graph = true)).  Nodes then keep their saved
+// tensors and never overwrite them; otherwise each node drops them once it
+// has run.  A nested backward (the recompute inside checkpoint) has its own
+// setting.
+bool graph_retained();
 
 class NoGradGuard {
  public:

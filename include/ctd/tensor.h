@@ -59,6 +59,12 @@ class Tensor {
   void zero_grad_();
   void backward();
   void backward(const Tensor& grad_output);
+  // retain_graph = true keeps the graph (nodes and their saved tensors) so
+  // that another backward can run through it, as the reference's engine
+  // always does (src/core/autograd.cu:158-237); the default releases each
+  // node as soon as it has run.
+  void backward(bool retain_graph);
+  void backward(const Tensor& grad_output, bool retain_graph);
   Tensor detach() const;
 
   const std::shared_ptr<autograd::AutogradMeta>& autograd_meta() const { return autograd_meta_; }

@@ -5,6 +5,7 @@
 // logits.  Exit status = number of failed tests.
 #include <unistd.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -19,6 +20,7 @@
 #include "ctd/autograd.h"
 #include "ctd/nn/kv_cache.h"
 #include "ctd/nn/model.h"
+#include "ctd/ops/repeat_kv.h"
 #include "ctd/optim.h"
 #include "ctd/safetensors.h"
 #include "ctd/tensor.h"
@@ -317,6 +319,72 @@ void kv_cache_equivalences(TinyCfg c) {
   }
 }
 
+// Tensor::backward(..., retain_graph = true) keeps the graph, as the
+// reference's engine always does (src/core/autograd.cu:158-237): a second
+// pass through it adds the same gradients again (x + x is exact, so every
+// gradient is exactly twice the first pass's), through checkpointed layers
+// too and through a loss scaled before backward (the fused LM head's node
+// then scales into fresh buffers); a last pass without retaining consumes the
+// graph, after which another backward throws, as the default always does.
+void retained_graph_repeat_backward(bool checkpointing, float upstream) {
+  const int B = 2, T = 6;
+  std::vector<int64_t> hx = {1, 4, 0, 6, 7, 2, 3, 5, 2, 2, 1, 0};
+  std::vector<int64_t> hy = {4, 0, 6, 3, 2, 3, 5, 1, 7, 6, 5, 4};
+  std::mt19937 rng(7);
+  TinyCfg c{32, 128, 2, 1, 64, 64, 2, 1e-5f, 1e4f};
+  nn::Model m = build_tiny(c, rng, /*grad=*/true);
+  m.gradient_checkpointing = checkpointing;
+  Tensor x = Tensor::from_host(hx.data(), {B, T}, DType::kInt64, kHIP0);
+  Tensor y = Tensor::from_host(hy.data(), {B, T}, DType::kInt64, kHIP0);
+  std::vector<Tensor> ps = params_of(m);
+
+  Tensor loss = m.forward_train(x, y);
+  Tensor root = upstream == 1.0f ? loss : ops::mul_scalar(loss, upstream);
+  root.backward(/*retain_graph=*/true);
+  std::vector<std::vector<float>> g1;
+  for (Tensor& p : ps) g1.push_back(host(p.grad()));
+  root.backward(/*retain_graph=*/true);
+  bool doubled = true;
+  for (size_t i = 0; i < ps.size(); ++i) {
+    const std::vector<float> g2 = host(ps[i].grad());
+    for (size_t j = 0; j < g2.size(); ++j) doubled = doubled && g2[j] == 2.0f * g1[i][j];
+  }
+  check(doubled, "second pass through the retained graph doubles every gradient");
+  root.backward();  // consumes the graph
+  double worst = 0.0;
+  for (size_t i = 0; i < ps.size(); ++i) {
+    const std::vector<float> g3 = host(ps[i].grad());
+    for (size_t j = 0; j < g3.size(); ++j)
+      worst = std::max(worst, std::abs(static_cast<double>(g3[j]) - 3.0 * g1[i][j]) /
+                                  (1e-30 + std::abs(3.0 * g1[i][j])));
+  }
+  check(worst < 1e-6, "third pass adds the same gradients once more");
+  bool threw = false;
+  try {
+    root.backward();
+  } catch (const std::runtime_error&) {
+    threw = true;
+  }
+  check(threw, "a consumed graph refuses another backward");
+
+  // The default (no retain) consumes the graph on its first pass.
+  for (Tensor& p : ps) p.zero_grad_();
+  Tensor l2 = m.forward_train(x, y);
+  l2.backward();
+  threw = false;
+  try {
+    l2.backward();
+  } catch (const std::runtime_error&) {
+    threw = true;
+  }
+  check(threw, "default backward consumes the graph");
+  if (upstream == 1.0f) {  // and gives the first retained pass's gradients
+    bool same = true;
+    for (size_t i = 0; i < ps.size(); ++i) same = same && host(ps[i].grad()) == g1[i];
+    check(same, "retained and default passes give the same gradients");
+  }
+}
+
 // ------------------------------------------------------------ safetensors
 namespace fs = std::filesystem;
 
@@ -439,6 +507,11 @@ int main(int argc, char** argv) {
   }
   run("Safetensors.FormatAndFaults_Host", [] { safetensors_format_and_faults(kCPU); });
   run("Safetensors.FormatAndFaults_Device", [] { safetensors_format_and_faults(kHIP0); });
+  run("Autograd.RetainedGraphRepeatBackward", [] { retained_graph_repeat_backward(false, 1.0f); });
+  run("Autograd.RetainedGraphRepeatBackward_Checkpointed",
+      [] { retained_graph_repeat_backward(true, 1.0f); });
+  run("Autograd.RetainedGraphRepeatBackward_ScaledLoss",
+      [] { retained_graph_repeat_backward(true, 0.25f); });
   run("ModelTrain.TrainLogitsMatchInferenceLogits",
       [] { train_logits_match_inference_logits(TinyCfg{}); });
   run("ModelTrain.TrainLogitsMatchInferenceLogits_D64",
