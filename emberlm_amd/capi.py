@@ -80,8 +80,9 @@ SIGNATURES = {
     "ember_ce_masked_rows": (i32, [vp, vp, vp, i64, i64, vp, vp, vp]),
     "ember_ce_masked_reduce": (i32, [vp, vp, i64, vp, vp, vp]),
     "ember_embedding_fwd": (i32, [vp, vp, vp, i64, i64, i64, vp]),
-    "ember_embedding_bwd_workspace_bytes": (sz, [i64, i64]),
+    "ember_embedding_bwd_workspace_bytes": (sz, [i64, i64, i64]),
     "ember_embedding_bwd": (i32, [vp, vp, vp, i64, i64, i64, i32, vp, sz, vp]),
+    "ember_sgd": (i32, [vp, vp, i64, f32, vp]),
     "ember_adamw": (i32, [vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, f32, f32, vp]),
     "ember_adamw_bounded": (i32, [vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, f32, f32, i32, vp]),
     "ember_sumsq_workspace_bytes": (sz, [i32]),

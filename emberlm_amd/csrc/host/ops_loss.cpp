@@ -281,7 +281,7 @@ Tensor embedding_backward_impl(const Tensor& ids, const Tensor& dy, int64_t voca
   require(n > 0 ? dy.numel() % n == 0 : true, "embedding_backward: dy shape mismatch");
   const int64_t H = n ? dy.numel() / n : dy.shape().back();
   Tensor dw = Tensor::empty({vocab, H}, DType::kFloat32, dy.device());
-  const size_t wsb = ember_embedding_bwd_workspace_bytes(n, vocab);
+  const size_t wsb = ember_embedding_bwd_workspace_bytes(n, H, vocab);
   Tensor ws = wsb ? workspace(wsb) : Tensor{};
   CTD_CHECK(ember_embedding_bwd(static_cast<const int64_t*>(ids.data_ptr()), cfp(dy), fp(dw), n, H,
                                 vocab, /*accumulate=*/0, wsb ? ws.data_ptr() : nullptr, wsb, S()));

@@ -55,6 +55,31 @@ namespace {
 constexpr int kUpdateBlocks = 1024;
 }  // namespace
 
+// ------------------------------------------------------------------ SGD
+// src/core/optim.cu:23-48 of the reference: every parameter must require grad;
+// step() updates those that have a gradient, one launch each.
+SGD::SGD(std::vector<Tensor> params, float lr) : params_(std::move(params)), lr_(lr) {
+  for (const Tensor& p : params_)
+    if (!p.requires_grad()) throw std::runtime_error("SGD: param does not require grad");
+}
+
+void SGD::step() {
+  for (Tensor& p : params_) {
+    Tensor g = p.grad();
+    if (!g.storage()) continue;
+    if (g.shape() != p.shape()) throw std::runtime_error("SGD: param/grad shape mismatch");
+    if (p.dtype() != DType::kFloat32 || g.dtype() != DType::kFloat32)
+      throw std::runtime_error("SGD: fp32 only");
+    CTD_CHECK(ember_sgd(static_cast<float*>(p.data_ptr()), static_cast<const float*>(g.data_ptr()),
+                        p.numel(), lr_, runtime::compute_stream()));
+  }
+}
+
+void SGD::zero_grad() {
+  for (Tensor& p : params_) p.zero_grad_();
+}
+
+// ---------------------------------------------------------------- AdamW
 AdamW::AdamW(std::vector<Tensor> params, float lr, float weight_decay, float beta1, float beta2,
              float eps, bool offload)
     : AdamW(std::vector<ParamGroup>{ParamGroup{std::move(params), lr, weight_decay}}, beta1, beta2,

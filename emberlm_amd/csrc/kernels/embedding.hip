@@ -2,11 +2,22 @@
 //
 // Reference: embedding_kernel_f32 / embedding_backward_kernel_f32
 // (src/ops/embedding.cu:15-39), whose backward atomically adds every token's
-// gradient row into dW[id] (order-dependent fp32 sums).  Here each block owns
-// a range of kIdsPerBlock vocabulary rows, scans the id list in order, compacts
-// the positions that hit its range with a wave ballot (keeping ascending
-// order), and adds those dy rows into its dW rows one after another, so every
-// dW row is the same left-to-right sum on every run.
+// gradient row into dW[id] (order-dependent fp32 sums).  Both backward forms
+// here sum each dW row in a fixed order, so it is the same on every run:
+//   - with a workspace (ember_embedding_bwd_workspace_bytes): the token
+//     positions are sorted by id with a stable radix sort (hipCUB), cut into
+//     windows of 64 sorted entries; one workgroup per window sums each run of
+//     equal ids in position order into a partial row, and one workgroup per
+//     window then adds up, for every id whose run starts in it, the partials
+//     of the windows the run spans, in window order, into dW.  The work per
+//     token is bounded however the ids repeat: a batch of one repeated id
+//     (padding) spreads over n/64 workgroups instead of one serial chain.
+//   - without one: each block owns kIdsPerBlock vocabulary rows, scans the id
+//     list in order, compacts the positions that hit its range with a wave
+//     ballot (keeping ascending order), and adds those dy rows into its dW
+//     rows one after another.
+#include <hipcub/hipcub.hpp>
+
 #include "common.h"
 
 using namespace ember;
@@ -67,6 +78,111 @@ __global__ __launch_bounds__(kThreads) void embedding_bwd_kernel(const int64_t* 
   }
 }
 
+// --- sorted form -----------------------------------------------------------
+constexpr int kWin = 64;  // sorted entries per window
+
+// keys = ids (out-of-range ids become V and sort last), vals = positions.
+__global__ __launch_bounds__(kThreads) void emb_sort_prep(const int64_t* __restrict__ ids,
+                                                          uint32_t* __restrict__ keys,
+                                                          uint32_t* __restrict__ vals, int64_t n,
+                                                          int64_t V) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const int64_t id = ids[i];
+  keys[i] = static_cast<uint32_t>(id >= 0 && id < V ? id : V);
+  vals[i] = static_cast<uint32_t>(i);
+}
+
+// Window w: the sum, in position order, of the dy rows of each run of equal
+// keys among sorted entries [64w, 64w + 64), written to part[64w + k] for the
+// window's k-th run.
+__global__ __launch_bounds__(kThreads) void emb_window_sums(const uint32_t* __restrict__ keys,
+                                                            const uint32_t* __restrict__ vals,
+                                                            const float* __restrict__ dy,
+                                                            float* __restrict__ part, int64_t n,
+                                                            int64_t H, int64_t V) {
+  __shared__ uint32_t k_s[kWin], v_s[kWin];
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kWin;
+  const int cnt = static_cast<int>(n - e0 < kWin ? n - e0 : kWin);
+  if (threadIdx.x < cnt) {
+    k_s[threadIdx.x] = keys[e0 + threadIdx.x];
+    v_s[threadIdx.x] = vals[e0 + threadIdx.x];
+  }
+  __syncthreads();
+  for (int64_t c = threadIdx.x; c < H; c += kThreads) {
+    float acc = 0.f;
+    int k = 0;
+    for (int e = 0; e < cnt; ++e) {
+      const uint32_t key = k_s[e];
+      if (key >= V) break;  // invalid ids sort last
+      acc += dy[static_cast<int64_t>(v_s[e]) * H + c];
+      if (e + 1 == cnt || k_s[e + 1] != key) {
+        part[(e0 + k) * H + c] = acc;
+        acc = 0.f;
+        ++k;
+      }
+    }
+  }
+}
+
+// Window w: for each run that starts in it (not a continuation of the
+// previous window's last run), dW[key] += its partial + the partials of the
+// following windows the run continues into, in window order.
+__global__ __launch_bounds__(kThreads) void emb_window_combine(const uint32_t* __restrict__ keys,
+                                                               const float* __restrict__ part,
+                                                               float* __restrict__ dw, int64_t n,
+                                                               int64_t H, int64_t V) {
+  __shared__ uint32_t k_s[kWin];
+  const int64_t nwin = (n + kWin - 1) / kWin;
+  const int64_t w = blockIdx.x;
+  const int64_t e0 = w * kWin;
+  const int cnt = static_cast<int>(n - e0 < kWin ? n - e0 : kWin);
+  if (threadIdx.x < cnt) k_s[threadIdx.x] = keys[e0 + threadIdx.x];
+  __syncthreads();
+  const bool continued = w > 0 && keys[e0 - 1] == k_s[0];
+  int k = 0;
+  for (int e = 0; e < cnt; ++e) {
+    const uint32_t key = k_s[e];
+    if (key >= V) break;
+    const bool run_end = e + 1 == cnt || k_s[e + 1] != key;
+    if (!run_end) continue;
+    const bool owned = !(k == 0 && continued);
+    const bool last_in_window = e + 1 == cnt;
+    if (owned) {
+      for (int64_t c = threadIdx.x; c < H; c += kThreads) {
+        float t = part[(e0 + k) * H + c];
+        // a run ending at the window's end may continue into the next ones
+        for (int64_t w2 = w + 1; last_in_window && w2 < nwin; ++w2) {
+          const int64_t f = w2 * kWin;
+          if (keys[f] != key) break;
+          t += part[f * H + c];  // the continuation is window w2's first run
+          const int64_t fend = f + kWin < n ? f + kWin : n;
+          if (keys[fend - 1] != key) break;  // the run ends inside window w2
+        }
+        dw[static_cast<int64_t>(key) * H + c] += t;
+      }
+    }
+    ++k;
+  }
+}
+
+int emb_key_bits(int64_t V) {
+  int b = 1;
+  while ((int64_t{1} << b) <= V) ++b;  // keys run up to V (invalid ids)
+  return b;
+}
+
+size_t emb_sort_temp_bytes(int64_t n, int64_t V) {
+  size_t b = 0;
+  const hipError_t e = hipcub::DeviceRadixSort::SortPairs(
+      nullptr, b, static_cast<const uint32_t*>(nullptr), static_cast<uint32_t*>(nullptr),
+      static_cast<const uint32_t*>(nullptr), static_cast<uint32_t*>(nullptr), static_cast<int>(n),
+      0, emb_key_bits(V));
+  return e == hipSuccess ? b : 0;
+}
+
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
 }  // namespace
 
 extern "C" int ember_embedding_fwd(const int64_t* ids, const float* w, float* out, int64_t n,
@@ -79,17 +195,17 @@ extern "C" int ember_embedding_fwd(const int64_t* ids, const float* w, float* ou
   return launch_status();
 }
 
-extern "C" size_t ember_embedding_bwd_workspace_bytes(int64_t n, int64_t V) {
-  (void)n;
-  (void)V;
-  return 0;
+extern "C" size_t ember_embedding_bwd_workspace_bytes(int64_t n, int64_t H, int64_t V) {
+  if (n <= 0 || H <= 0 || V <= 0 || n > 0x7fffffff || V >= 0x7fffffff) return 0;
+  const size_t temp = emb_sort_temp_bytes(n, V);
+  if (!temp) return 0;
+  return 4 * align256(static_cast<size_t>(n) * 4) + align256(static_cast<size_t>(n * H) * 4) +
+         align256(temp);
 }
 
 extern "C" int ember_embedding_bwd(const int64_t* ids, const float* dy, float* dw, int64_t n,
                                    int64_t H, int64_t V, int accumulate, void* workspace,
                                    size_t workspace_bytes, ember_stream_t s) {
-  (void)workspace;
-  (void)workspace_bytes;
   if (n < 0 || H <= 0 || V <= 0 || !dw) return EMBER_EINVAL;
   if (n > 0 && (!ids || !dy)) return EMBER_EINVAL;
   if (!accumulate) {
@@ -97,9 +213,34 @@ extern "C" int ember_embedding_bwd(const int64_t* ids, const float* dy, float* d
     if (rc) return rc;
   }
   if (n == 0) return EMBER_OK;
+  hipStream_t st = as_stream(s);
+  const size_t need = workspace ? ember_embedding_bwd_workspace_bytes(n, H, V) : 0;
+  if (need && workspace_bytes >= need) {
+    char* p = static_cast<char*>(workspace);
+    const size_t keyb = align256(static_cast<size_t>(n) * 4);
+    uint32_t* keys_in = reinterpret_cast<uint32_t*>(p);
+    uint32_t* vals_in = reinterpret_cast<uint32_t*>(p + keyb);
+    uint32_t* keys = reinterpret_cast<uint32_t*>(p + 2 * keyb);
+    uint32_t* vals = reinterpret_cast<uint32_t*>(p + 3 * keyb);
+    float* part = reinterpret_cast<float*>(p + 4 * keyb);
+    char* temp = p + 4 * keyb + align256(static_cast<size_t>(n * H) * 4);
+    size_t temp_bytes = need - 4 * keyb - align256(static_cast<size_t>(n * H) * 4);
+    emb_sort_prep<<<static_cast<unsigned>((n + kThreads - 1) / kThreads), kThreads, 0, st>>>(
+        ids, keys_in, vals_in, n, V);
+    int rc = launch_status();
+    if (rc) return rc;
+    rc = status_of(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, keys_in, keys, vals_in,
+                                                      vals, static_cast<int>(n), 0,
+                                                      emb_key_bits(V), st));
+    if (rc) return rc;
+    const unsigned nwin = static_cast<unsigned>((n + kWin - 1) / kWin);
+    emb_window_sums<<<nwin, kThreads, 0, st>>>(keys, vals, dy, part, n, H, V);
+    if ((rc = launch_status())) return rc;
+    emb_window_combine<<<nwin, kThreads, 0, st>>>(keys, part, dw, n, H, V);
+    return launch_status();
+  }
   const int64_t nb = (V + kIdsPerBlock - 1) / kIdsPerBlock;
   if (nb > 0x7fffffff) return EMBER_EINVAL;
-  embedding_bwd_kernel<<<static_cast<unsigned>(nb), kThreads, 0, as_stream(s)>>>(ids, dy, dw, n, H,
-                                                                                 V);
+  embedding_bwd_kernel<<<static_cast<unsigned>(nb), kThreads, 0, st>>>(ids, dy, dw, n, H, V);
   return launch_status();
 }

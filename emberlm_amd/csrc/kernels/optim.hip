@@ -132,6 +132,44 @@ __global__ __launch_bounds__(kPartsThreads) void sum_parts(const float* __restri
 
 }  // namespace
 
+namespace {
+
+// p -= lr * g, two roundings (contraction is off in this file).
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void sgd_kernel(float* __restrict__ p,
+                                                       const float* __restrict__ g, int64_t n,
+                                                       float lr) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (VEC) {
+    for (int64_t i = tid; i < n / 4; i += stride) {
+      f32x4 pp = reinterpret_cast<f32x4*>(p)[i];
+      const f32x4 gg = reinterpret_cast<const f32x4*>(g)[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pp[e] = pp[e] - lr * gg[e];
+      reinterpret_cast<f32x4*>(p)[i] = pp;
+    }
+    for (int64_t i = n / 4 * 4 + tid; i < n; i += stride) p[i] = p[i] - lr * g[i];
+  } else {
+    for (int64_t i = tid; i < n; i += stride) p[i] = p[i] - lr * g[i];
+  }
+}
+
+}  // namespace
+
+extern "C" int ember_sgd(float* p, const float* g, int64_t n, float lr, ember_stream_t s) {
+  if (n < 0) return EMBER_EINVAL;
+  if (n == 0) return EMBER_OK;
+  if (!p || !g) return EMBER_EINVAL;
+  const bool vec = aligned16(p) && aligned16(g);
+  const unsigned grid = grid_1d(vec ? (n + 3) / 4 : n, kThreads, 65536);
+  if (vec)
+    sgd_kernel<true><<<grid, kThreads, 0, as_stream(s)>>>(p, g, n, lr);
+  else
+    sgd_kernel<false><<<grid, kThreads, 0, as_stream(s)>>>(p, g, n, lr);
+  return launch_status();
+}
+
 extern "C" int ember_adamw(float* p, const float* g, float* m, float* v, int64_t n, float lr,
                            float beta1, float beta2, float eps, float wd, float bc1, float bc2,
                            ember_stream_t s) {

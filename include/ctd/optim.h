@@ -1,6 +1,6 @@
 #pragma once
-// AdamW (decoupled weight decay) with optional host-offloaded m/v, and global
-// grad-norm clipping (mirrors include/ctd/optim.h of the reference).
+// SGD, AdamW (decoupled weight decay) with optional host-offloaded m/v, and
+// global grad-norm clipping (mirrors include/ctd/optim.h of the reference).
 //
 //   m = b1 m + (1-b1) g;  v = b2 v + (1-b2) g^2
 //   p <- p - lr ( (m/(1-b1^t)) / (sqrt(v/(1-b2^t)) + eps) + wd p )
@@ -25,6 +25,19 @@
 #include "ctd/tensor.h"
 
 namespace ctd::optim {
+
+// Plain SGD, p <- p - lr * g for every parameter with a gradient (the
+// reference's include/ctd/optim.h:11-20; it has no momentum or weight decay).
+class SGD {
+ public:
+  explicit SGD(std::vector<Tensor> params, float lr);
+  void step();
+  void zero_grad();
+
+ private:
+  std::vector<Tensor> params_;
+  float lr_;
+};
 
 struct ParamGroup {
   std::vector<Tensor> params;

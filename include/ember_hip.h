@@ -345,13 +345,24 @@ int ember_ce_masked_reduce(const float* row_loss, const float* mask, int64_t N, 
  * out[i,:] = w[ids[i],:] (src/ops/embedding.cu:15-24). */
 int ember_embedding_fwd(const int64_t* ids, const float* w, float* out, int64_t n, int64_t H,
                         int64_t V, ember_stream_t s);
-/* dw[v,:] (+)= sum over i with ids[i]==v of dy[i,:], summed in increasing i
- * (deterministic, no atomics); accumulate=0 zero-fills dw first.  Replaces the
- * atomicAdd scatter of src/ops/embedding.cu:28-39, 71-87. */
-size_t ember_embedding_bwd_workspace_bytes(int64_t n, int64_t V);
+/* dw[v,:] (+)= sum over i with ids[i]==v of dy[i,:] (deterministic, no
+ * atomics); accumulate=0 zero-fills dw first.  Replaces the atomicAdd scatter
+ * of src/ops/embedding.cu:28-39, 71-87.  With a workspace of
+ * ember_embedding_bwd_workspace_bytes(n, H, V) (queried on the device that
+ * runs the call; 0 when unavailable) the positions are sorted by id and each
+ * id's rows summed in fixed-size windows of the sorted order, then across the
+ * windows in order, so a much-repeated id costs no more than n/64 workgroups;
+ * with none, one workgroup per 128 vocabulary rows sums its hits in
+ * increasing i, one after another. */
+size_t ember_embedding_bwd_workspace_bytes(int64_t n, int64_t H, int64_t V);
 int ember_embedding_bwd(const int64_t* ids, const float* dy, float* dw, int64_t n, int64_t H,
                         int64_t V, int accumulate, void* workspace, size_t workspace_bytes,
                         ember_stream_t s);
+
+/* -------------------------------------------------------------------- SGD
+ * p -= lr * g, as p - (lr * g) with two roundings (sgd_step_kernel_f32,
+ * src/core/optim.cu:14-20, launched per parameter by SGD::step, optim.cu:29-44). */
+int ember_sgd(float* p, const float* g, int64_t n, float lr, ember_stream_t s);
 
 /* ------------------------------------------------------------------ AdamW
  * m = b1 m + (1-b1) g; v = b2 v + (1-b2) g^2;

@@ -20,6 +20,7 @@
 #include "ctd/autograd.h"
 #include "ctd/nn/kv_cache.h"
 #include "ctd/nn/model.h"
+#include "ctd/ops/elementwise.h"
 #include "ctd/ops/repeat_kv.h"
 #include "ctd/optim.h"
 #include "ctd/safetensors.h"
@@ -385,6 +386,39 @@ void retained_graph_repeat_backward(bool checkpointing, float upstream) {
   }
 }
 
+// optim::SGD (the reference's include/ctd/optim.h:11-20): p <- p - lr * g for
+// parameters with a gradient, untouched otherwise; zero_grad drops the grads;
+// a parameter that does not require grad is rejected.
+void sgd_step() {
+  std::mt19937 rng(3);
+  Tensor a = rand_tensor({300}, rng, 1.0f, true);
+  Tensor b = rand_tensor({17}, rng, 1.0f, true);
+  const std::vector<float> a0 = host(a), b0 = host(b);
+  // y = a * c with a constant c: backward(ones) leaves a.grad = c
+  std::vector<float> ga(300);
+  for (size_t i = 0; i < 300; ++i) ga[i] = 0.5f * static_cast<float>(i % 7) - 1.0f;
+  const std::vector<float> ones(300, 1.0f);
+  ops::mul(a, Tensor::from_host(ga.data(), {300}, DType::kFloat32, kHIP0))
+      .backward(Tensor::from_host(ones.data(), {300}, DType::kFloat32, kHIP0));
+  optim::SGD opt({a, b}, 0.1f);
+  opt.step();
+  const std::vector<float> a1 = host(a), b1 = host(b);
+  bool ok = true;
+  for (size_t i = 0; i < 300; ++i) ok = ok && a1[i] == a0[i] - 0.1f * ga[i];
+  check(ok, "SGD: p - lr g");
+  check(b1 == b0, "SGD: parameters without a gradient are untouched");
+  opt.zero_grad();
+  check(!a.grad().storage(), "SGD: zero_grad drops the gradient");
+  Tensor c = rand_tensor({4}, rng, 1.0f, false);
+  bool threw = false;
+  try {
+    optim::SGD bad({c}, 0.1f);
+  } catch (const std::runtime_error&) {
+    threw = true;
+  }
+  check(threw, "SGD: a parameter without requires_grad is rejected");
+}
+
 // ------------------------------------------------------------ safetensors
 namespace fs = std::filesystem;
 
@@ -507,6 +541,7 @@ int main(int argc, char** argv) {
   }
   run("Safetensors.FormatAndFaults_Host", [] { safetensors_format_and_faults(kCPU); });
   run("Safetensors.FormatAndFaults_Device", [] { safetensors_format_and_faults(kHIP0); });
+  run("Optim.SGD", [] { sgd_step(); });
   run("Autograd.RetainedGraphRepeatBackward", [] { retained_graph_repeat_backward(false, 1.0f); });
   run("Autograd.RetainedGraphRepeatBackward_Checkpointed",
       [] { retained_graph_repeat_backward(true, 1.0f); });

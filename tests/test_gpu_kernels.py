@@ -351,6 +351,56 @@ def test_embedding_kat_and_bwd():
     assert_close(host(DW2)[:300], 2 * O.embedding_bwd(ids, dy, V)[:300], name="emb accumulate")
 
 
+def _emb_bwd(ids, dy, V, accumulate=0, dw=None, sorted_path=True):
+    n, H = dy.shape
+    lib = capi.lib()
+    wsb = lib.ember_embedding_bwd_workspace_bytes(n, H, V) if sorted_path else 0
+    assert (wsb > 0) == sorted_path
+    WS = empty((max(wsb // 4, 1),))
+    DW = dev(dw) if dw is not None else empty((V, H))
+    call("ember_embedding_bwd", p(dev(ids)), p(dev(dy)), p(DW), n, H, V, accumulate,
+         p(WS) if wsb else None, wsb, None)
+    return DW
+
+
+@pytest.mark.parametrize("case", ["repeats", "one_id", "mostly_one", "long_runs", "invalid"])
+def test_embedding_bwd_sorted_vs_oracle(case):
+    # The sorted-window form: random ids with repeats, a batch of one repeated id
+    # (every window continues the same run), 90% one id, runs longer than a
+    # window, and ids outside [0, V) (skipped).  Deterministic over repeat calls
+    # and equal to the oracle's sums; accumulate adds onto dw.
+    r = rng(21)
+    V, H = 5000, 2048 if case in ("one_id", "mostly_one") else 96
+    n = 32768 if case in ("one_id", "mostly_one") else 3000
+    if case == "repeats":
+        ids = r.integers(0, 300, n)
+    elif case == "one_id":
+        ids = np.full(n, 17)
+    elif case == "mostly_one":
+        ids = np.where(r.random(n) < 0.9, 4999, r.integers(0, V, n))
+    elif case == "long_runs":
+        ids = np.repeat(r.integers(0, V, 20), 150)[:n]
+    else:
+        ids = r.integers(-3, V + 3, n)
+    ids = ids.astype(np.int64)
+    dy = r.standard_normal((n, H)).astype(np.float32)
+    valid = (ids >= 0) & (ids < V)
+    ref = O.embedding_bwd(np.where(valid, ids, 0), dy * valid[:, None], V)
+    DW = _emb_bwd(ids, dy, V)
+    got = host(DW)
+    hit = np.unique(ids[valid])
+    assert_close(got[hit], ref[hit], name=f"emb {case}")
+    miss = np.setdiff1d(np.arange(V), hit)
+    assert (got[miss] == 0).all()
+    assert torch.equal(DW, _emb_bwd(ids, dy, V))
+    base = r.standard_normal((V, H)).astype(np.float32)
+    acc = host(_emb_bwd(ids, dy, V, accumulate=1, dw=base))
+    assert_close(acc[hit], base[hit] + ref[hit], name=f"emb {case} accumulate")
+    assert np.array_equal(acc[miss], base[miss])
+    if case == "repeats":  # the scan form (no workspace) agrees within tolerance
+        assert_close(host(_emb_bwd(ids, dy, V, sorted_path=False))[hit], ref[hit], name="scan")
+
+
 # ---------------------------------------------------------------- AdamW
 def test_adamw_vs_oracle():
     r = rng(7)
@@ -430,6 +480,23 @@ def test_sumsq_multi():
     assert abs(first - ref) <= 1e-5 * ref
     call("ember_sumsq_multi", ptrs, sizes, 2, p(out), p(ws), wsb, None)
     assert host(out)[0] == first
+
+
+def test_sgd_exact():
+    # p - lr * g with two float32 roundings (float4 path and a ragged tail on
+    # the scalar one); gradients of 0 leave p unchanged.
+    r = rng(12)
+    for n, off in ((1_000_003, 0), (1001, 1)):
+        p0 = r.standard_normal(n + off).astype(np.float32)
+        g = r.standard_normal(n + off).astype(np.float32)
+        g[:7] = 0.0
+        P, G = dev(p0), dev(g)
+        call("ember_sgd", C.c_void_p(P.data_ptr() + 4 * off), C.c_void_p(G.data_ptr() + 4 * off), n,
+             0.01, None)
+        lr = np.float32(0.01)
+        want = p0.copy()
+        want[off:] = (p0[off:] - (lr * g[off:]).astype(np.float32)).astype(np.float32)
+        assert np.array_equal(host(P), want)
 
 
 # ------------------------------------------------------------ attention
