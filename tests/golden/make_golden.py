@@ -112,11 +112,9 @@ def grad_names(c):
 
 
 def summarised_grads(c):
-    """Indices of the parameters whose gradients a fixture keeps: the
-    embedding (tied head), all of layer 0, the last layer's down projection
-    and the final norm."""
-    n = len(grad_names(c))
-    return list(range(1 + len(block_keys(c)))) + [n - 2, n - 1]
+    """Indices of the parameters whose gradients a fixture keeps: all of them,
+    in collect_parameters order."""
+    return list(range(len(grad_names(c))))
 
 
 def rope_freqs(D, theta, factor=0.0, low_freq=1.0, high_freq=4.0, orig_max_pos=8192):
