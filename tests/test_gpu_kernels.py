@@ -165,6 +165,10 @@ def test_gemm_split_k_weight_gradient_shape_vs_torch():
     (0, 1, 33000, 1000, 48), (0, 0, 33000, 1000, 48), (1, 0, 33000, 1000, 48),
     (1, 1, 33000, 1000, 48),                        # LDS-DMA kernel, M, N off the tile grid
     (0, 1, 33001, 999, 48),                         # LDS-DMA, K-contiguous rows clamped
+    # one and two 16-k stages: the peeled k loop's DMA-free tail only
+    (0, 1, 33000, 1000, 16), (0, 0, 33000, 1000, 32), (1, 0, 33000, 1000, 16),
+    (1, 1, 33000, 1000, 32), (0, 1, 500, 300, 16), (1, 0, 500, 300, 32),
+    (0, 1, 500, 300, 64),                           # 128x128 tiles, two stages of DMA ahead
 ])
 def test_gemm_large_tile_ragged_vs_oracle(ta, tb, M, N, K):
     # Enough tiles for the 256x128 kernels, with M and N off the tile grid.
