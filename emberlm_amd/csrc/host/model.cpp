@@ -160,12 +160,14 @@ Tensor train_hidden(const Model& m, const Tensor& input_ids) {
     const TransformerBlock& layer = m.layers[i];
     if (m.gradient_checkpointing) {
       // checkpoint() runs fn under no-grad in the forward pass and with grad
-      // enabled when the backward pass re-runs it.
+      // enabled when the backward pass re-runs it; the re-run only
+      // back-propagates through its result, so the block skips computing it.
       const int li = static_cast<int>(i);
       h = autograd::checkpoint(
           [&m, &layer, li](const Tensor& x) {
-            if (m.recompute_hook && autograd::is_grad_enabled()) m.recompute_hook(li);
-            return layer.forward_train(x);
+            if (!autograd::is_grad_enabled()) return layer.forward_train(x);
+            if (m.recompute_hook) m.recompute_hook(li);
+            return layer.forward_train_for_backward(x);
           },
           h);
     } else {

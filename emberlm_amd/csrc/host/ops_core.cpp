@@ -119,6 +119,24 @@ Tensor matmul(const Tensor& a, const Tensor& b, bool transa, bool transb) {
   return y;
 }
 
+Tensor matmul_graph_only(const Tensor& a, const Tensor& b, bool transa, bool transb,
+                         const Tensor& values) {
+  const MM d = mm_dims(a, b, transa, transb, "matmul_graph_only");
+  require(values.is_contiguous() && values.numel() == d.M * d.N,
+          "matmul_graph_only: values must be M*N contiguous elements");
+  Tensor y = values.detach().reshape({d.M, d.N});
+  if (autograd::any_requires_grad({a, b})) {
+    auto node = std::make_shared<MatmulBackward>();
+    node->a = a.detach();
+    node->b = b.detach();
+    node->ta = transa;
+    node->tb = transb;
+    node->next_edges = autograd::collect_next_edges({a, b});
+    autograd::set_history(y, std::move(node));
+  }
+  return y;
+}
+
 Tensor bmm_impl(const Tensor& a, const Tensor& b, bool transa, bool transb) {
   check_f32(a, "bmm", "a");
   check_f32(b, "bmm", "b");
@@ -361,6 +379,18 @@ Tensor add_impl(const Tensor& a, const Tensor& b) {
 
 Tensor add(const Tensor& a, const Tensor& b) {
   Tensor y = add_impl(a, b);
+  if (autograd::any_requires_grad({a, b})) {
+    auto node = std::make_shared<AddBackward>();
+    node->next_edges = autograd::collect_next_edges({a, b});
+    autograd::set_history(y, std::move(node));
+  }
+  return y;
+}
+
+Tensor add_graph_only(const Tensor& a, const Tensor& b, const Tensor& values) {
+  check_binary(a, b, "add_graph_only");
+  require(values.shape() == a.shape(), "add_graph_only: values must have the operands' shape");
+  Tensor y = values.detach();
   if (autograd::any_requires_grad({a, b})) {
     auto node = std::make_shared<AddBackward>();
     node->next_edges = autograd::collect_next_edges({a, b});

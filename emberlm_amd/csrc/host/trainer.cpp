@@ -360,9 +360,13 @@ int ctd_trainer_block_step(ctd_trainer_t t, int64_t layer, const float* x, const
     const int64_t d = tr->model.config.hidden_size;
     Tensor xin = Tensor::from_host(x, {B, T, d}, DType::kFloat32, kHIP0);
     xin.requires_grad_(true);
-    Tensor y = checkpoint ? autograd::checkpoint(
-                                [&blk](const Tensor& v) { return blk.forward_train(v); }, xin)
-                          : blk.forward_train(xin);
+    // The checkpoint's re-run in the backward pass takes the model's form,
+    // which records the block output's graph without computing it.
+    auto fn = [&blk](const Tensor& v) {
+      return autograd::is_grad_enabled() ? blk.forward_train_for_backward(v)
+                                         : blk.forward_train(v);
+    };
+    Tensor y = checkpoint ? autograd::checkpoint(fn, xin) : blk.forward_train(xin);
     if (y_out) y.copy_to_host(y_out);
     Tensor g = Tensor::from_host(dy, {B, T, d}, DType::kFloat32, kHIP0);
     y.backward(g);

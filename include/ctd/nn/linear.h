@@ -21,6 +21,21 @@ struct Linear {
     out_shape.back() = out;
     return y2d.reshape(out_shape);
   }
+
+  // forward(x)'s autograd graph without the product: the result is a view of
+  // `values` (forward(x)'s shape).  See ops::matmul_graph_only.
+  Tensor forward_graph_only(const Tensor& x, const Tensor& values) const {
+    const int64_t in = weight.shape()[1];
+    const int64_t out = weight.shape()[0];
+    const auto& sh = x.shape();
+    if (sh.back() != in) throw std::runtime_error("Linear: in_features mismatch");
+    const int64_t leading = x.numel() / in;
+    Tensor y2d = ops::matmul_graph_only(x.reshape({leading, in}), weight, /*transa=*/false,
+                                        /*transb=*/true, values);
+    std::vector<int64_t> out_shape(sh.begin(), sh.end());
+    out_shape.back() = out;
+    return y2d.reshape(out_shape);
+  }
 };
 
 }  // namespace ctd::nn

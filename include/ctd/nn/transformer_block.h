@@ -59,6 +59,22 @@ struct TransformerBlock {
     Tensor m = mlp.forward(h2);
     return ops::add(h, m);
   }
+
+  // forward_train(x) for a checkpoint's recompute, whose backward reads only
+  // the graph of the block's output: down_proj and the last residual add are
+  // recorded but not run, so the returned tensor has forward_train(x)'s
+  // grad_fn and h's values (not the block's output).  Its gradients are
+  // forward_train's, kernel for kernel.  The checkpointed forward already
+  // computed the real output: it is the next block's saved input.
+  Tensor forward_train_for_backward(const Tensor& x) const {
+    Tensor h1 = input_layernorm.forward(x);
+    Tensor a = self_attn.forward_train(h1);
+    Tensor h = ops::add(x, a);
+    Tensor h2 = post_attention_layernorm.forward(h);
+    Tensor act = ops::swiglu(mlp.gate_proj.forward(h2), mlp.up_proj.forward(h2));
+    Tensor m = mlp.down_proj.forward_graph_only(act, h);
+    return ops::add_graph_only(h, m, h);
+  }
 };
 
 }  // namespace ctd::nn

@@ -7,6 +7,9 @@ namespace ctd::ops {
 
 Tensor add(const Tensor& a, const Tensor& b);
 Tensor add_impl(const Tensor& a, const Tensor& b);
+// add()'s backward node without the sum: a view of `values` (a's shape, left
+// as they are) carrying that node; see matmul_graph_only.  Added in this build.
+Tensor add_graph_only(const Tensor& a, const Tensor& b, const Tensor& values);
 Tensor mul(const Tensor& a, const Tensor& b);
 Tensor mul_impl(const Tensor& a, const Tensor& b);
 // SiLU: y = x * sigmoid(x).

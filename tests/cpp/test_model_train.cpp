@@ -21,6 +21,7 @@
 #include "ctd/nn/kv_cache.h"
 #include "ctd/nn/model.h"
 #include "ctd/ops/elementwise.h"
+#include "ctd/ops/matmul.h"
 #include "ctd/ops/repeat_kv.h"
 #include "ctd/optim.h"
 #include "ctd/safetensors.h"
@@ -530,6 +531,61 @@ void safetensors_format_and_faults(Device dev) {
   fs::remove_all(dir);
 }
 
+// The recompute form of a block (TransformerBlock::forward_train_for_backward)
+// records the graph of the block's output without computing its last GEMM
+// and residual add: back-propagating an upstream gradient through it must
+// give every gradient of forward_train bit for bit, and its result must be
+// h's storage, values untouched.
+void block_graph_only_recompute_matches_forward_train() {
+  TinyCfg c{32, 128, 2, 1, 64, 64, 1, 1e-5f, 1e4f};
+  std::mt19937 rng(11);
+  nn::Model m = build_tiny(c, rng, true);
+  const nn::TransformerBlock& blk = m.layers[0];
+  const int64_t B = 2, T = 24;
+  Tensor x0 = rand_tensor({B, T, c.D}, rng, 1.0f, false);
+  Tensor dy = rand_tensor({B, T, c.D}, rng, 1.0f, false);
+  auto params = [&] {
+    const auto& a = blk.self_attn;
+    return std::vector<Tensor>{blk.input_layernorm.weight, blk.post_attention_layernorm.weight,
+                               a.q_proj.weight, a.k_proj.weight, a.v_proj.weight,
+                               a.o_proj.weight, blk.mlp.gate_proj.weight,
+                               blk.mlp.up_proj.weight, blk.mlp.down_proj.weight};
+  };
+  auto run_once = [&](bool graph_only, std::vector<float>* y_host) {
+    for (auto& p : params()) p.zero_grad_();
+    Tensor x = x0.detach();
+    x.requires_grad_(true);
+    Tensor y = graph_only ? blk.forward_train_for_backward(x) : blk.forward_train(x);
+    if (y_host) *y_host = host(y);
+    y.backward(dy);
+    std::vector<std::vector<float>> g{host(x.grad())};
+    for (auto& p : params()) g.push_back(host(p.grad()));
+    return g;
+  };
+  std::vector<float> y_full, y_graph;
+  const auto g_full = run_once(false, &y_full);
+  const auto g_graph = run_once(true, &y_graph);
+  check(g_full.size() == g_graph.size(), "same gradient count");
+  for (size_t i = 0; i < g_full.size() && i < g_graph.size(); ++i)
+    check(g_full[i] == g_graph[i], "gradient " + std::to_string(i) + " bitwise equal");
+
+  // The graph-only result holds h = x + attn(norm(x)), not the block output.
+  autograd::NoGradGuard ng;
+  Tensor h = ops::add(x0, blk.self_attn.forward_train(blk.input_layernorm.forward(x0)));
+  check(host(h) == y_graph, "graph-only result holds h's values");
+  check(y_full != y_graph, "the block output differs from h");
+
+  // ops-level: the result is a view of `values`, which are left as they were.
+  Tensor a2 = rand_tensor({5, 8}, rng, 1.0f, true), w = rand_tensor({3, 8}, rng, 1.0f, true);
+  Tensor vals = rand_tensor({15}, rng, 1.0f, false);
+  const std::vector<float> before = host(vals);
+  Tensor y2 = ops::matmul_graph_only(a2, w, false, true, vals);
+  check(y2.shape() == std::vector<int64_t>{5, 3}, "matmul_graph_only shape");
+  check(y2.storage() == vals.storage() && host(vals) == before, "matmul_graph_only is a view");
+  check(throws_with([&] { ops::matmul_graph_only(a2, w, false, true, a2); }, "M*N"),
+        "matmul_graph_only rejects values of another size");
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -542,6 +598,8 @@ int main(int argc, char** argv) {
   run("Safetensors.FormatAndFaults_Host", [] { safetensors_format_and_faults(kCPU); });
   run("Safetensors.FormatAndFaults_Device", [] { safetensors_format_and_faults(kHIP0); });
   run("Optim.SGD", [] { sgd_step(); });
+  run("Autograd.BlockGraphOnlyRecompute",
+      [] { block_graph_only_recompute_matches_forward_train(); });
   run("Autograd.RetainedGraphRepeatBackward", [] { retained_graph_repeat_backward(false, 1.0f); });
   run("Autograd.RetainedGraphRepeatBackward_Checkpointed",
       [] { retained_graph_repeat_backward(true, 1.0f); });
