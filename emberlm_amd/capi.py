@@ -48,6 +48,8 @@ SIGNATURES = {
     "ember_gemm_f32_workspace_bytes": (sz, [i64, i64, i64, i64]),
     "ember_gemm_f32_ws": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, i64, vp, i64, i64, f32, vp,
                                 i64, i64, i64, vp, sz, vp]),
+    "ember_gemm_f32_dyn": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp, i64,
+                                 vp, i64, i32, vp, sz, vp]),
     "ember_rmsnorm_fwd": (i32, [vp, vp, vp, vp, i64, i64, f32, vp]),
     "ember_rmsnorm_bwd_workspace_bytes": (sz, [i64, i64]),
     "ember_rmsnorm_bwd": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, f32, vp, sz, vp]),
@@ -78,6 +80,11 @@ SIGNATURES = {
     "ember_ce_masked_fwd": (i32, [vp, vp, vp, i64, i64, vp, vp, vp, vp, sz, vp]),
     "ember_ce_masked_bwd": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, vp, vp]),
     "ember_ce_masked_rows": (i32, [vp, vp, vp, i64, i64, vp, vp, vp]),
+    "ember_mask_rows": (i32, [vp, i64, vp, vp, vp]),
+    "ember_rows_gather": (i32, [vp, i64, i64, vp, vp, i64, i64, vp, vp]),
+    "ember_rows_scatter": (i32, [vp, i64, vp, vp, i64, i64, vp, i64, vp]),
+    "ember_ce_masked_rows_idx": (i32, [vp, vp, vp, vp, vp, i64, i64, i64, vp, vp, vp]),
+    "ember_ce_masked_bwd_idx": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, vp, vp, vp, vp]),
     "ember_ce_masked_reduce": (i32, [vp, vp, i64, vp, vp, vp]),
     "ember_embedding_fwd": (i32, [vp, vp, vp, i64, i64, i64, vp]),
     "ember_embedding_bwd_workspace_bytes": (sz, [i64, i64, i64]),

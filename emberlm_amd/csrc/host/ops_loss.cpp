@@ -104,6 +104,7 @@ Tensor cross_entropy_masked(const Tensor& logits, const Tensor& targets,
 namespace {
 
 std::atomic<int64_t> g_head_chunk_rows{0};
+std::atomic<bool> g_head_active_rows{true};
 
 // Rows per chunk: at most ~2.5 GB of logits, a multiple of 256, at least 256.
 int64_t head_chunk_rows(int64_t N, int64_t V) {
@@ -123,6 +124,71 @@ void head_gemm(bool ta, bool tb, int64_t M, int64_t N, int64_t K, const float* A
                               accumulate ? 1.0f : 0.0f, C, ldc, 0, 1,
                               wsb ? ws.data_ptr() : nullptr, wsb, S()));
   runtime::gemm_profile_end(ev, 2.0 * M * N * K, 2 * ta + tb);
+}
+
+// head_gemm with M (dim 0) or K (dim 1) cut on the device to the chunk's
+// active rows, count[0] - base.
+void head_gemm_dyn(bool ta, bool tb, int64_t M, int64_t N, int64_t K, const float* A,
+                   int64_t lda, const float* B, int64_t ldb, float* C, int64_t ldc,
+                   bool accumulate, const int64_t* count, int64_t base, int dim) {
+  const size_t wsb = dim == 0 ? ember_gemm_f32_workspace_bytes(M, N, K, 1) : 0;
+  Tensor ws = wsb ? workspace(wsb) : Tensor{};
+  void* ev = runtime::gemm_profile_begin();
+  CTD_CHECK(ember_gemm_f32_dyn(ta, tb, M, N, K, 1.0f, A, lda, B, ldb, accumulate ? 1.0f : 0.0f,
+                               C, ldc, count, base, dim, wsb ? ws.data_ptr() : nullptr, wsb, S()));
+  // Algorithmic flops: the chunk's active rows only.
+  const int64_t ext = dim == 0 ? M : K;
+  runtime::gemm_profile_end_rows(ev, 2.0 * M * N * K / static_cast<double>(ext), count, base,
+                                 ext, 2 * ta + tb);
+}
+
+int64_t round16(int64_t x) { return (x + 15) / 16 * 16; }
+
+// The LM head + loss over only the rows whose mask value is nonzero: they are
+// listed on the device (ember_mask_rows) and taken `rows` at a time, so the
+// three GEMMs run on those rows only, sized on the device.  Row losses land
+// at their batch rows (zeros elsewhere), so the loss is the one-pass-per-row
+// result bit for bit; dh rows of masked-out tokens are 0, as they are when
+// computed.
+void head_loss_active_rows(const Tensor& h, const Tensor& w, const int64_t* tg,
+                           const Tensor& loss_mask, int64_t rows, Tensor& lse,
+                           Tensor& row_loss, const Tensor& one, const Tensor& mask_sum,
+                           Tensor& dh, Tensor& dw) {
+  const int64_t N = h.shape()[0], H = h.shape()[1], V = w.shape()[0];
+  const Device dev = h.device();
+  const bool grad = one.defined();
+  Tensor list = Tensor::empty({N + 1}, DType::kInt64, dev);
+  int64_t* idx = static_cast<int64_t*>(list.data_ptr());
+  const int64_t* count = idx + N;
+  CTD_CHECK(ember_mask_rows(cfp(loss_mask), N, idx, idx + N, S()));
+  CTD_CHECK(ember_fill(fp(row_loss), N, 0.0f, S()));
+  if (dh.defined()) CTD_CHECK(ember_fill(fp(dh), N * H, 0.0f, S()));
+  // Chunks of whole 16-row stages, so that only the last one is ragged and the
+  // device-side row counts, clamped to a chunk, never run into the next one.
+  rows = round16(rows);
+  const int64_t cap = rows;
+  Tensor logits = Tensor::empty({cap, V}, DType::kFloat32, dev);
+  Tensor hc = Tensor::empty({cap, H}, DType::kFloat32, dev);
+  Tensor dhc = dh.defined() ? Tensor::empty({cap, H}, DType::kFloat32, dev) : Tensor{};
+  for (int64_t r0 = 0; r0 < N; r0 += rows) {
+    const int64_t n = std::min(rows, N - r0);  // the chunk's capacity; active rows on the device
+    CTD_CHECK(ember_rows_gather(cfp(h), H, H, idx, count, r0, cap, fp(hc), S()));
+    head_gemm_dyn(false, true, round16(n), V, H, cfp(hc), H, cfp(w), H, fp(logits), V, false,
+                  count, r0, 0);
+    CTD_CHECK(ember_ce_masked_rows_idx(cfp(logits), tg, cfp(loss_mask), idx, count, r0, n, V,
+                                       fp(lse) + r0, fp(row_loss), S()));
+    if (!grad) continue;
+    CTD_CHECK(ember_ce_masked_bwd_idx(cfp(logits), tg, cfp(loss_mask), cfp(lse) + r0, idx, count,
+                                      r0, n, V, cfp(one), cfp(mask_sum), fp(logits), S()));
+    if (dh.defined()) {
+      head_gemm_dyn(false, false, n, H, V, cfp(logits), V, cfp(w), H, fp(dhc), H, false, count,
+                    r0, 0);
+      CTD_CHECK(ember_rows_scatter(cfp(dhc), H, idx, count, r0, n, fp(dh), H, S()));
+    }
+    if (dw.defined())
+      head_gemm_dyn(true, false, V, H, round16(n), cfp(logits), V, cfp(hc), H, fp(dw), H, r0 > 0,
+                    count, r0, 1);
+  }
 }
 
 struct LinearCrossEntropyBackward : autograd::Node {
@@ -164,6 +230,8 @@ void set_linear_cross_entropy_chunk_rows(int64_t rows) {
   g_head_chunk_rows.store(rows);
 }
 
+void set_linear_cross_entropy_active_rows(bool on) { g_head_active_rows.store(on); }
+
 Tensor linear_cross_entropy_masked(const Tensor& h, const Tensor& w, const Tensor& targets,
                                    const Tensor& loss_mask) {
   check_f32(h, "linear_cross_entropy_masked", "h");
@@ -195,7 +263,15 @@ Tensor linear_cross_entropy_masked(const Tensor& h, const Tensor& w, const Tenso
     if (want_h) dh = Tensor::empty({N, H}, DType::kFloat32, dev);
     if (want_w) dw = Tensor::empty({V, H}, DType::kFloat32, dev);  // running dlogits^T h
   }
-  if (N > 0) {
+  // The active-row form needs the LDS-DMA GEMM's shapes: H, V in whole
+  // 16-k stages, 16-byte aligned operands.
+  const bool active_rows = g_head_active_rows.load() && N > 0 && H % 16 == 0 && V % 16 == 0 &&
+                           reinterpret_cast<uintptr_t>(h.data_ptr()) % 16 == 0 &&
+                           reinterpret_cast<uintptr_t>(w.data_ptr()) % 16 == 0;
+  if (active_rows) {
+    head_loss_active_rows(h, w, tg, loss_mask, head_chunk_rows(N, V), lse, row_loss, one,
+                          mask_sum, dh, dw);
+  } else if (N > 0) {
     const int64_t rows = head_chunk_rows(N, V);
     Tensor logits = Tensor::empty({rows, V}, DType::kFloat32, dev);
     for (int64_t r0 = 0; r0 < N; r0 += rows) {

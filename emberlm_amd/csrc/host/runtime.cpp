@@ -6,6 +6,7 @@
 // rounded size so the training loop never reaches the driver after its first
 // step (hipFree would also synchronise the device), and it keeps the
 // high-water mark of live bytes that the peak-HBM figure is read from.
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -118,6 +119,16 @@ struct GemmProfiler {
   std::vector<std::pair<ember_event_t, ember_event_t>> spans;
   std::vector<double> flops;
   std::vector<int> variant;
+  // Launches sized on the device: flops = per_row * clamp(slot - base, 0, max)
+  // with the row count copied into a device slot when the launch is queued.
+  struct DynRows {
+    size_t span;
+    int64_t slot, base, max;
+    double per_row;
+  };
+  std::vector<DynRows> dyn;
+  int64_t* slots = nullptr;  // kSlots int64 on the device, allocated on first use
+  static constexpr int64_t kSlots = 1 << 16;
   ember_event_t get() {
     if (!pool.empty()) {
       ember_event_t e = pool.back();
@@ -161,10 +172,42 @@ void gemm_profile_end(void* begin, double flops, int variant) {
   p.variant.push_back(variant >= 0 && variant < kProfileVariants ? variant : 0);
 }
 
+void gemm_profile_end_rows(void* begin, double flops_per_row, const int64_t* count,
+                           int64_t base, int64_t max_rows, int variant) {
+  if (!begin) return;
+  auto& p = prof();
+  std::lock_guard<std::mutex> lk(p.mu);
+  if (!p.slots)
+    check(ember_device_malloc(reinterpret_cast<void**>(&p.slots),
+                              GemmProfiler::kSlots * sizeof(int64_t)),
+          "gemm profiler slots");
+  if (static_cast<int64_t>(p.dyn.size()) >= GemmProfiler::kSlots)
+    throw std::runtime_error("gemm profiler: too many device-sized launches between collects");
+  const int64_t slot = static_cast<int64_t>(p.dyn.size());
+  check(ember_memcpy_async(p.slots + slot, count, sizeof(int64_t), 2, compute_stream()),
+        "gemm profiler count copy");
+  ember_event_t e = p.get();
+  check(ember_event_record(e, compute_stream()), "gemm profiler record");
+  p.dyn.push_back({p.spans.size(), slot, base, max_rows, flops_per_row});
+  p.spans.emplace_back(begin, e);
+  p.flops.push_back(0.0);
+  p.variant.push_back(variant >= 0 && variant < kProfileVariants ? variant : 0);
+}
+
 void gemm_profile_collect(int64_t* launches, double* flops, double* total_ms) {
   auto& p = prof();
   std::lock_guard<std::mutex> lk(p.mu);
   synchronize();
+  if (!p.dyn.empty()) {
+    std::vector<int64_t> counts(p.dyn.size());
+    check(ember_memcpy(counts.data(), p.slots, counts.size() * sizeof(int64_t), 1),
+          "gemm profiler counts");
+    for (const auto& d : p.dyn) {
+      const int64_t rows = std::min(std::max<int64_t>(counts[d.slot] - d.base, 0), d.max);
+      p.flops[d.span] = d.per_row * static_cast<double>(rows);
+    }
+    p.dyn.clear();
+  }
   for (int v = 0; v < kProfileVariants; ++v) {
     launches[v] = 0;
     flops[v] = 0.0;

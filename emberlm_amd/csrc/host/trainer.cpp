@@ -736,6 +736,10 @@ int ctd_set_head_chunk_rows(int64_t rows) {
   return guarded([&] { ops::set_linear_cross_entropy_chunk_rows(rows); });
 }
 
+int ctd_set_head_active_rows(int32_t on) {
+  return guarded([&] { ops::set_linear_cross_entropy_active_rows(on != 0); });
+}
+
 int ctd_set_attn_ds_bytes(int64_t bytes) {
   return guarded([&] { ops::set_attention_backward_ds_bytes(bytes); });
 }

@@ -51,7 +51,18 @@ struct GemmArgs {
   int64_t kchunk;  // > 0: blockIdx.y is a K split of this many k (last one clipped)
   float alpha, beta;
   int tiles_m, tiles_n;
+  // Optional extent read from device memory at run time (LDS-DMA kernel and
+  // the split-K reduce only): v = clamp(*dyn - dyn_base, 0, static extent);
+  // dyn_dim 0: rows of C beyond v are not needed (whole tiles past v exit);
+  // dyn_dim 1: K becomes v rounded up to 16 (operand rows up to there are read).
+  const int64_t* dyn = nullptr;
+  int64_t dyn_base = 0;
+  int dyn_dim = 0;
 };
+
+__device__ __forceinline__ int64_t dyn_extent(const GemmArgs& a, int64_t full) {
+  return min(max(*a.dyn - a.dyn_base, int64_t{0}), full);
+}
 
 template <bool KC, int ROWS, int BK>
 struct Stage {
@@ -406,9 +417,17 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_dma(GemmArgs a) {
   const float* __restrict__ A = a.A + bz * a.sA;
   const float* __restrict__ B = a.B + bz * a.sB;
   float* __restrict__ C = a.C + bz * a.sC;
-  const int64_t K = a.kchunk > 0 ? min(a.kchunk, a.K - bz * a.kchunk) : a.K;
+  int64_t K = a.kchunk > 0 ? min(a.kchunk, a.K - bz * a.kchunk) : a.K;
   const int64_t m0 = static_cast<int64_t>(tm) * BM;
   const int64_t n0 = static_cast<int64_t>(tn) * BN;
+  if (a.dyn) {  // uniform per block: the whole block leaves or none of it
+    if (a.dyn_dim == 0) {
+      if (m0 >= dyn_extent(a, a.M)) return;
+    } else {
+      K = min(K, (dyn_extent(a, K) + 15) / 16 * 16);
+      if (K == 0 && a.beta == 1.f) return;  // C stays as it is
+    }
+  }
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -554,12 +573,14 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_dma(GemmArgs a) {
 template <bool VEC>
 __global__ __launch_bounds__(kThreads) void splitk_reduce(const float* __restrict__ P, float* C,
                                                           int64_t M, int64_t N, int64_t ldc,
-                                                          int S, float alpha, float beta) {
+                                                          int S, float alpha, float beta,
+                                                          const int64_t* dyn, int64_t dyn_base) {
   const int64_t per = VEC ? 4 : 1;
   const int64_t cols = N / per;
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (i >= M * cols) return;
   const int64_t m = i / cols, n = (i % cols) * per;
+  if (dyn && m >= min(max(*dyn - dyn_base, int64_t{0}), M)) return;  // rows not needed
   const int64_t plane = M * N;
   if (VEC) {
     f32x4 s = *reinterpret_cast<const f32x4*>(P + m * N + n);
@@ -769,19 +790,23 @@ extern "C" size_t ember_gemm_f32_workspace_bytes(int64_t M, int64_t N, int64_t K
   return p.splits > 1 ? static_cast<size_t>(p.splits * M * N) * sizeof(float) : 0;
 }
 
-extern "C" int ember_gemm_f32_ws(int transa, int transb, int64_t M, int64_t N, int64_t K,
-                                 float alpha, const float* A, int64_t lda, int64_t sA,
-                                 const float* B, int64_t ldb, int64_t sB, float beta, float* C,
-                                 int64_t ldc, int64_t sC, int64_t batch, void* workspace,
-                                 size_t workspace_bytes, ember_stream_t s) {
-  int rc = check_args(transa, transb, M, N, K, A, lda, B, ldb, C, ldc, batch);
-  if (rc || M == 0 || N == 0) return rc;
+namespace {
+
+// One GEMM call; `dyn` (may be null) is the device-side extent of GemmArgs.
+int gemm_run(int transa, int transb, int64_t M, int64_t N, int64_t K, float alpha,
+             const float* A, int64_t lda, int64_t sA, const float* B, int64_t ldb, int64_t sB,
+             float beta, float* C, int64_t ldc, int64_t sC, int64_t batch, void* workspace,
+             size_t workspace_bytes, const int64_t* dyn, int64_t dyn_base, int dyn_dim,
+             hipStream_t st) {
+  int rc = EMBER_OK;
   GemmArgs a{A, B, C, M, N, K, lda, ldb, ldc, sA, sB, sC, 0, alpha, beta, 0, 0};
+  a.dyn = dyn;
+  a.dyn_base = dyn_base;
+  a.dyn_dim = dyn_dim;
   const bool vec = aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0) &&
                    (batch == 1 || (sA % 4 == 0 && sB % 4 == 0));
-  hipStream_t st = as_stream(s);
   const bool a_kc = !transa, b_kc = transb != 0;
-  if (batch == 1 && M <= kSkinnyMaxM && a_kc && b_kc && vec && K > 0 && K % 4 == 0 &&
+  if (!dyn && batch == 1 && M <= kSkinnyMaxM && a_kc && b_kc && vec && K > 0 && K % 4 == 0 &&
       N <= int64_t{kSkinnyRows} * 0x7fffffff) {
     if (M == 1) return launch_skinny<1>(A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, st);
     if (M == 2) return launch_skinny<2>(A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, st);
@@ -790,8 +815,9 @@ extern "C" int ember_gemm_f32_ws(int transa, int transb, int64_t M, int64_t N, i
   }
   Plan p = make_plan(M, N, K, batch);
   if (p.splits > 1 &&
-      (!workspace || workspace_bytes < static_cast<size_t>(p.splits * M * N) * sizeof(float)))
-    p.splits = 1;  // no room for partials: one pass over K
+      ((dyn && dyn_dim == 1) || !workspace ||
+       workspace_bytes < static_cast<size_t>(p.splits * M * N) * sizeof(float)))
+    p.splits = 1;  // no room for partials, or K itself is decided on the device
   if (p.splits > 1) {
     // Split s computes A[:, s*kchunk ...] B[s*kchunk ..., :] into plane s.
     GemmArgs sp = a;
@@ -811,22 +837,55 @@ extern "C" int ember_gemm_f32_ws(int transa, int transb, int64_t M, int64_t N, i
     const bool rvec = (N % 4 == 0) && (ldc % 4 == 0) && aligned16(C);
     const int64_t items = M * (rvec ? N / 4 : N);
     const unsigned blocks = static_cast<unsigned>(cdiv(items, kThreads));
+    const int64_t* rdyn = dyn_dim == 0 ? dyn : nullptr;
     if (rvec)
       splitk_reduce<true><<<blocks, kThreads, 0, st>>>(static_cast<const float*>(workspace), C, M,
                                                        N, ldc, static_cast<int>(p.splits),
-                                                       alpha, beta);
+                                                       alpha, beta, rdyn, dyn_base);
     else
       splitk_reduce<false><<<blocks, kThreads, 0, st>>>(static_cast<const float*>(workspace), C,
                                                         M, N, ldc, static_cast<int>(p.splits),
-                                                        alpha, beta);
+                                                        alpha, beta, rdyn, dyn_base);
     return launch_status();
   }
   const bool dma = vec && K % 16 == 0 && (a_kc || M % 4 == 0) && (b_kc || N % 4 == 0) &&
                    (batch == 1 || (sA % 4 == 0 && sB % 4 == 0));
   if (dma && p.big) return launch_dma<256, 128, 2>(a, a_kc, b_kc, batch, st);
   if (dma) return launch_dma<128, 128, 3>(a, a_kc, b_kc, batch, st);
+  if (dyn) return EMBER_EINVAL;  // only the LDS-DMA kernels read a device-side extent
   if (p.big) return launch_t<256, 128, 2>(a, a_kc, b_kc, batch, vec, st);
   return launch_t<128, 128, 3>(a, a_kc, b_kc, batch, vec, st);
+}
+
+}  // namespace
+
+extern "C" int ember_gemm_f32_ws(int transa, int transb, int64_t M, int64_t N, int64_t K,
+                                 float alpha, const float* A, int64_t lda, int64_t sA,
+                                 const float* B, int64_t ldb, int64_t sB, float beta, float* C,
+                                 int64_t ldc, int64_t sC, int64_t batch, void* workspace,
+                                 size_t workspace_bytes, ember_stream_t s) {
+  int rc = check_args(transa, transb, M, N, K, A, lda, B, ldb, C, ldc, batch);
+  if (rc || M == 0 || N == 0) return rc;
+  return gemm_run(transa, transb, M, N, K, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, batch,
+                  workspace, workspace_bytes, nullptr, 0, 0, as_stream(s));
+}
+
+extern "C" int ember_gemm_f32_dyn(int transa, int transb, int64_t M, int64_t N, int64_t K,
+                                  float alpha, const float* A, int64_t lda, const float* B,
+                                  int64_t ldb, float beta, float* C, int64_t ldc,
+                                  const int64_t* count, int64_t base, int dim, void* workspace,
+                                  size_t workspace_bytes, ember_stream_t s) {
+  int rc = check_args(transa, transb, M, N, K, A, lda, B, ldb, C, ldc, 1);
+  if (rc) return rc;
+  if (!count || (dim != 0 && dim != 1) || base < 0) return EMBER_EINVAL;
+  // The LDS-DMA kernels' conditions: 16-byte rows and K in whole 16-k stages.
+  const bool a_kc = !transa, b_kc = transb != 0;
+  if (!aligned16(A) || !aligned16(B) || lda % 4 != 0 || ldb % 4 != 0 || K % 16 != 0 ||
+      (!a_kc && M % 4 != 0) || (!b_kc && N % 4 != 0))
+    return EMBER_EINVAL;
+  if (M == 0 || N == 0) return EMBER_OK;
+  return gemm_run(transa, transb, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1,
+                  workspace, workspace_bytes, count, base, dim, as_stream(s));
 }
 
 extern "C" int ember_gemm_f32(int transa, int transb, int64_t M, int64_t N, int64_t K,

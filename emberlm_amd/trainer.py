@@ -96,6 +96,7 @@ _SIGS = {
     "ctd_trainer_forward_cached": (i32, [vp, vp, lptr, i64, i64, i32, i32, fptr, i64]),
     "ctd_sample": (i32, [fptr, i64, i64, f32, i32, f32, u64, i32, i32, lptr]),
     "ctd_set_head_chunk_rows": (i32, [i64]),
+    "ctd_set_head_active_rows": (i32, [i32]),
     "ctd_set_attn_ds_bytes": (i32, [i64]),
     "ctd_trainer_generate": (i32, [vp, lptr, i64, i32, f32, i32, f32, u64, i64, lptr,
                                    C.POINTER(C.c_double), C.POINTER(C.c_double)]),
@@ -391,6 +392,11 @@ def set_attn_ds_bytes(nbytes):
 def set_head_chunk_rows(rows):
     """Rows per chunk of the fused LM head + loss (0 = automatic)."""
     _ck(lib().ctd_set_head_chunk_rows(rows), "set_head_chunk_rows")
+
+
+def set_head_active_rows(on):
+    """Whether the fused LM head + loss skips rows whose mask value is 0."""
+    _ck(lib().ctd_set_head_active_rows(int(bool(on))), "set_head_active_rows")
 
 
 def train_run(config_path):

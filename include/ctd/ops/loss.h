@@ -21,10 +21,16 @@ Tensor cross_entropy_masked_impl(const Tensor& logits, const Tensor& targets,
 // gradient the chunk's dlogits, dh and dW (for an upstream gradient of 1) are
 // formed right there; backward scales them by the upstream gradient.  The
 // loss equals cross_entropy_masked's bit for bit; same error on sum(mask) == 0.
+// When H and V are multiples of 16, only rows whose mask value is nonzero go
+// through the head (listed and counted on the device): masked-out rows add
+// nothing to the loss and get dh = 0, as they would if computed.
 Tensor linear_cross_entropy_masked(const Tensor& h, const Tensor& w, const Tensor& targets,
                                    const Tensor& loss_mask);
 // Rows per chunk of linear_cross_entropy_masked (process-wide); 0 restores the
 // automatic choice (about 2.5 GB of logits per chunk).
 void set_linear_cross_entropy_chunk_rows(int64_t rows);
+// Whether linear_cross_entropy_masked computes only the active rows where it
+// can (default true; false runs every row, for comparisons).
+void set_linear_cross_entropy_active_rows(bool on);
 
 }  // namespace ctd::ops

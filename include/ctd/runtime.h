@@ -49,6 +49,10 @@ void* gemm_profile_begin();                     // null when disabled
 // variant of the launch: 2*transa + transb for a GEMM (which kernel
 // instantiation ran), kProfileAttnFwd / kProfileAttnBwd for fused attention.
 void gemm_profile_end(void* begin, double flops, int variant);
+// The same for a launch sized on the device: its flops are flops_per_row times
+// clamp(*count - base, 0, max_rows), the count read when the record is collected.
+void gemm_profile_end_rows(void* begin, double flops_per_row, const int64_t* count,
+                           int64_t base, int64_t max_rows, int variant);
 constexpr int kProfileAttnFwd = 4;
 constexpr int kProfileAttnBwd = 5;
 constexpr int kProfileVariants = 6;

@@ -197,6 +197,9 @@ int ctd_trainer_generate(ctd_trainer_t t, const int64_t* prompt, int64_t P, int3
 /* Rows per chunk of the fused LM head + loss (ops::set_linear_cross_entropy_chunk_rows;
  * 0 = automatic). */
 int ctd_set_head_chunk_rows(int64_t rows);
+/* Whether the fused LM head + loss skips rows whose mask value is 0
+ * (ops::set_linear_cross_entropy_active_rows; default 1). */
+int ctd_set_head_active_rows(int32_t on);
 
 /* Device bytes the attention backward may keep dS in
  * (ops::set_attention_backward_ds_bytes; -1 = default, 0 = recompute). */

@@ -109,6 +109,23 @@ int ember_gemm_f32_ws(int transa, int transb, int64_t M, int64_t N, int64_t K, f
                       const float* A, int64_t lda, int64_t sA, const float* B, int64_t ldb,
                       int64_t sB, float beta, float* C, int64_t ldc, int64_t sC, int64_t batch,
                       void* workspace, size_t workspace_bytes, ember_stream_t s);
+/* ember_gemm_f32_ws (batch 1) with one extent known only on the device, so a
+ * caller can size a product by a count a kernel produced without waiting for
+ * it on the host.  v = clamp(*count - base, 0, extent):
+ *   dim 0: only rows [0, v) of C are wanted; whole row tiles past v are
+ *          skipped, rows of a tile that straddles v are written too.
+ *   dim 1: K becomes v rounded up to a multiple of 16; the operands' k rows
+ *          [v, that) are read and must hold finite values (zeros contribute
+ *          nothing).  With v = 0 and beta = 1, C is left untouched.
+ * Requires 16-byte aligned A and B, lda and ldb multiples of 4, K % 16 == 0 and
+ * M (N) % 4 == 0 when A (B) is MN-contiguous; otherwise EMBER_EINVAL.  The
+ * workspace is ember_gemm_f32_ws's (a K split only with dim 0).  Used by
+ * the LM head to compute only rows whose loss-mask value is nonzero.  Added in
+ * this build; the reference sizes every product on the host. */
+int ember_gemm_f32_dyn(int transa, int transb, int64_t M, int64_t N, int64_t K, float alpha,
+                       const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+                       float* C, int64_t ldc, const int64_t* count, int64_t base, int dim,
+                       void* workspace, size_t workspace_bytes, ember_stream_t s);
 
 /* -------------------------------------------------------------- RMSNorm
  * y = x * rsqrt(mean(x^2) + eps) * w over rows of length H; rstd[rows] (may be
@@ -340,6 +357,35 @@ int ember_ce_masked_rows(const float* logits, const int64_t* tgt, const float* m
                          int64_t V, float* lse, float* row_loss, ember_stream_t s);
 int ember_ce_masked_reduce(const float* row_loss, const float* mask, int64_t N, float* loss,
                            float* mask_sum, ember_stream_t s);
+
+/* Rows whose loss-mask value is 0 add nothing to the loss or to any gradient,
+ * so the chunked LM head can compute the others only (added in this build; the
+ * reference's ce_masked kernels run every row, loss.cu:253-329):
+ *   ember_mask_rows: idx[0 .. *count) = the rows r < N with mask[r] != 0 (NaN
+ *     counts as nonzero), ascending; idx holds N entries.
+ * The calls below work on a chunk of R rows whose row j is batch row
+ * idx[base + j], for j < n = clamp(*count - base, 0, R), all read on the device:
+ *   ember_rows_gather: dst [R, H] contiguous; row j = src row idx[base + j]
+ *     (src row stride ld) for j < n, zeros for j in [n, round_up(n, 256)) (the
+ *     row tile of a GEMM over the chunk), later rows untouched.
+ *   ember_rows_scatter: dst row idx[base + j] (stride ld) = src row j, j < n.
+ *   ember_ce_masked_rows_idx / _bwd_idx: ember_ce_masked_rows / _bwd over the
+ *     chunk's n rows of logits [R, V]; lse is per chunk row, tgt, mask and
+ *     row_loss are per batch row (row_loss of other rows is not written). */
+int ember_mask_rows(const float* mask, int64_t N, int64_t* idx, int64_t* count,
+                    ember_stream_t s);
+int ember_rows_gather(const float* src, int64_t ld, int64_t H, const int64_t* idx,
+                      const int64_t* count, int64_t base, int64_t R, float* dst,
+                      ember_stream_t s);
+int ember_rows_scatter(const float* src, int64_t H, const int64_t* idx, const int64_t* count,
+                       int64_t base, int64_t R, float* dst, int64_t ld, ember_stream_t s);
+int ember_ce_masked_rows_idx(const float* logits, const int64_t* tgt, const float* mask,
+                             const int64_t* idx, const int64_t* count, int64_t base, int64_t R,
+                             int64_t V, float* lse, float* row_loss, ember_stream_t s);
+int ember_ce_masked_bwd_idx(const float* logits, const int64_t* tgt, const float* mask,
+                            const float* lse, const int64_t* idx, const int64_t* count,
+                            int64_t base, int64_t R, int64_t V, const float* dloss,
+                            const float* mask_sum, float* dlogits, ember_stream_t s);
 
 /* -------------------------------------------------------------- embedding
  * out[i,:] = w[ids[i],:] (src/ops/embedding.cu:15-24). */

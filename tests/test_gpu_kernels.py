@@ -329,6 +329,168 @@ def test_ce_zero_mask_loss_is_zero():
     assert host(loss)[0] == 0.0 and host(ms)[0] == 0.0
 
 
+# ------------------------------------------ LM head over the active rows
+def _mask_rows(mask):
+    """idx, count of ember_mask_rows on the device (count as a device tensor)."""
+    N = mask.shape[0]
+    M = dev(mask)
+    idx = torch.full((max(N, 1),), -7, dtype=torch.int64, device="cuda")
+    cnt = torch.full((1,), -7, dtype=torch.int64, device="cuda")
+    call("ember_mask_rows", p(M), N, p(idx), p(cnt), None)
+    return idx, cnt
+
+
+@pytest.mark.parametrize("N", [0, 1, 1000, 32768, 100003])
+def test_mask_rows_lists_nonzero_rows(N):
+    r = rng(N)
+    mask = np.where(r.random(N) < 0.45, 0.0, r.standard_normal(N)).astype(np.float32)
+    if N > 10:
+        mask[3], mask[5], mask[7] = np.nan, -0.0, -2.0   # NaN counts, -0 does not
+    idx, cnt = _mask_rows(mask)
+    want = np.nonzero(mask != 0)[0]
+    assert host(cnt)[0] == len(want)
+    assert np.array_equal(host(idx)[: len(want)], want)
+    if N > 10:
+        assert 3 in want and 5 not in want and 7 in want
+
+
+@pytest.mark.parametrize("H", [72, 30])   # float4 and scalar rows
+def test_rows_gather_scatter(H):
+    N, R = 3000, 1024
+    r = rng(H)
+    mask = (r.random(N) < 0.5).astype(np.float32)
+    src = r.standard_normal((N, H)).astype(np.float32)
+    idx, cnt = _mask_rows(mask)
+    act = np.nonzero(mask)[0]
+    S_ = dev(src)
+    for base in (0, 512, 1400, len(act), len(act) + 5):
+        n = min(max(len(act) - base, 0), R)
+        D_ = torch.full((R, H), 5.0, device="cuda")
+        call("ember_rows_gather", p(S_), H, H, p(idx), p(cnt), base, R, p(D_), None)
+        d = host(D_)
+        fill = min(R, -(-n // 256) * 256)
+        assert np.array_equal(d[:n], src[act[base:base + n]])
+        assert (d[n:fill] == 0).all() and (d[fill:] == 5.0).all()
+        O_ = torch.full((N, H), 9.0, device="cuda")
+        call("ember_rows_scatter", p(D_), H, p(idx), p(cnt), base, R, p(O_), H, None)
+        o = host(O_)
+        rows = act[base:base + n]
+        assert np.array_equal(o[rows], src[rows])
+        rest = np.ones(N, bool)
+        rest[rows] = False
+        assert (o[rest] == 9.0).all()
+
+
+@pytest.mark.parametrize("V", [4096, 1001])
+def test_ce_rows_idx_equal_all_rows_bitwise(V):
+    # The active-rows CE over gathered logits rows gives the all-rows kernels'
+    # lse, row loss and dlogits bits for those rows.
+    N, R, base = 300, 128, 64
+    r = rng(V)
+    logits = (r.standard_normal((N, V)) * 2).astype(np.float32)
+    tgt = r.integers(0, V, N).astype(np.int64)
+    mask = (r.random(N) > 0.4).astype(np.float32)
+    L, T_, M = dev(logits), dev(tgt), dev(mask)
+    lse_f, rl_f = empty((N,)), empty((N,))
+    call("ember_ce_masked_rows", p(L), p(T_), p(M), N, V, p(lse_f), p(rl_f), None)
+    ms = dev(np.array([mask.sum()], np.float32))
+    dl = dev(np.array([0.7], np.float32))
+    D_ = empty((N, V))
+    call("ember_ce_masked_bwd", p(L), p(T_), p(M), p(lse_f), p(dl), p(ms), N, V, p(D_), None)
+    idx, cnt = _mask_rows(mask)
+    act = np.nonzero(mask)[0]
+    n = min(len(act) - base, R)
+    Lc = empty((R, V))
+    call("ember_rows_gather", p(L), V, V, p(idx), p(cnt), base, R, p(Lc), None)
+    lse_c, rl = empty((R,)), torch.zeros(N, device="cuda")
+    call("ember_ce_masked_rows_idx", p(Lc), p(T_), p(M), p(idx), p(cnt), base, R, V, p(lse_c),
+         p(rl), None)
+    rows = act[base:base + n]
+    assert np.array_equal(host(lse_c)[:n], host(lse_f)[rows])
+    rl_h = host(rl)
+    assert np.array_equal(rl_h[rows], host(rl_f)[rows])
+    others = np.ones(N, bool)
+    others[rows] = False
+    assert (rl_h[others] == 0).all()
+    call("ember_ce_masked_bwd_idx", p(Lc), p(T_), p(M), p(lse_c), p(idx), p(cnt), base, R, V,
+         p(dl), p(ms), p(Lc), None)
+    assert np.array_equal(host(Lc)[:n], host(D_)[rows])
+
+
+def _gemm_dyn(a, b, ta, tb, count, base, dim, beta=0.0, c=None, alpha=1.0):
+    A, B = dev(a), dev(b)
+    M = a.shape[1] if ta else a.shape[0]
+    K = a.shape[0] if ta else a.shape[1]
+    N = b.shape[0] if tb else b.shape[1]
+    Cm = dev(c) if c is not None else torch.full((M, N), 7.0, device="cuda")
+    wsb = int(capi.lib().ember_gemm_f32_workspace_bytes(M, N, K, 1)) if dim == 0 else 0
+    ws = empty((max(wsb // 4, 1),))
+    cnt = dev(np.array([count], np.int64))
+    call("ember_gemm_f32_dyn", int(ta), int(tb), M, N, K, alpha, p(A), a.shape[1], p(B),
+         b.shape[1], beta, p(Cm), N, p(cnt), base, dim, p(ws), wsb, None)
+    return host(Cm)
+
+
+@pytest.mark.parametrize("ta,tb,M,N,K,count,base", [
+    (0, 1, 4096, 1200, 64, 4096, 0),      # every row
+    (0, 1, 4096, 1200, 64, 1000, 0),
+    (0, 1, 4096, 1200, 64, 1300, 300),     # count - base = 1000
+    (0, 1, 4096, 1200, 64, 0, 0),          # nothing: C untouched
+    (0, 1, 4096, 1200, 64, 99999, 10),     # clamped to M
+    (0, 1, 8192, 4096, 32, 5000, 0),       # 256x128 tiles
+    (0, 0, 512, 256, 8192, 300, 0),        # NN with a K split: partials + reduce
+    (0, 0, 512, 256, 8192, 0, 0),
+])
+def test_gemm_dyn_rows_vs_oracle(ta, tb, M, N, K, count, base):
+    r = rng(M + N + K + count)
+    a = r.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    b = r.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    got = _gemm_dyn(a, b, ta, tb, count, base, 0)
+    v = min(max(count - base, 0), M)
+    if v:
+        assert_close(got[:v], O.matmul(a[:v], b, ta, tb), name="gemm dyn rows")
+    past = -(-v // 256) * 256
+    assert (got[past:] == 7.0).all()   # whole row tiles past v are skipped
+
+
+@pytest.mark.parametrize("M,N,K,count,beta", [
+    (1024, 512, 4096, 4096, 0.0), (1024, 512, 4096, 1000, 0.0), (1024, 512, 4096, 17, 0.0),
+    (1024, 512, 4096, 1000, 1.0), (1024, 512, 4096, 0, 1.0), (1024, 512, 4096, 0, 0.0),
+    (33000, 1024, 64, 40, 0.0),            # 256x128 tiles
+])
+def test_gemm_dyn_k_vs_oracle(M, N, K, count, beta):
+    # TN (dW form): rows [v, round16(v)) of both operands are zero, rows past
+    # that hold values the product must not read.
+    r = rng(M + K + count)
+    a = r.standard_normal((K, M)).astype(np.float32)
+    b = r.standard_normal((K, N)).astype(np.float32)
+    v = min(count, K)
+    k16 = -(-v // 16) * 16
+    a[v:k16] = 0
+    b[v:k16] = 0
+    c = r.standard_normal((M, N)).astype(np.float32)
+    got = _gemm_dyn(a, b, 1, 0, count, 0, 1, beta=beta, c=c)
+    ref = beta * c.astype(np.float64)
+    if v:
+        ref = ref + O.matmul(a[:v], b[:v], True, False)
+    if v == 0 and beta == 1.0:
+        assert np.array_equal(got, c)
+    else:
+        assert_close(got, ref, name="gemm dyn k")
+
+
+def test_gemm_dyn_rejects_shapes_off_the_dma_path():
+    A = empty((64, 40))
+    cnt = dev(np.array([10], np.int64))
+    Cm = empty((64, 64))
+    with pytest.raises(capi.EmberError):   # K = 40 is not whole 16-k stages
+        capi.call("ember_gemm_f32_dyn", 0, 1, 64, 64, 40, 1.0, p(A), 40, p(A), 40, 0.0, p(Cm),
+                  64, p(cnt), 0, 0, None, 0, None)
+    with pytest.raises(capi.EmberError):   # dim must be 0 or 1
+        capi.call("ember_gemm_f32_dyn", 0, 1, 64, 64, 32, 1.0, p(A), 40, p(A), 40, 0.0, p(Cm),
+                  64, p(cnt), 0, 2, None, 0, None)
+
+
 # ------------------------------------------------------------ embedding
 def test_embedding_kat_and_bwd():
     V, H = 7, 5

@@ -220,8 +220,10 @@ def test_c4_llama32_1b_two_layers_vs_golden():
     _model_step_vs_golden(MG.C4, c, "c4_model.npz")
 
 
-def tiny_cfg(qk_norm=False, llama3=False, D=64):
-    return TR.make_config(vocab_size=1000, hidden_size=128, intermediate_size=256, num_layers=2,
+def tiny_cfg(qk_norm=False, llama3=False, D=64, vocab=1000):
+    # vocab 1000 takes the LM head's all-rows form, a multiple of 16 (1024) the
+    # form that computes only rows with a nonzero mask value.
+    return TR.make_config(vocab_size=vocab, hidden_size=128, intermediate_size=256, num_layers=2,
                           num_heads=4, num_kv_heads=2, head_dim=D, qk_norm=int(qk_norm),
                           rms_norm_eps=1e-6 if qk_norm else 1e-5,
                           rope_theta=5e5 if llama3 else 1e4, rope_factor=32.0 if llama3 else 0.0,
@@ -237,14 +239,20 @@ def batch(c, B, T, seed):
     return row[:, :T], row[:, 1:], mask
 
 
-@pytest.mark.parametrize("qk_norm,llama3,D", [(False, False, 64), (True, False, 128),
-                                              (False, True, 64),
-                                              # head sizes outside the fused kernels' 64/128:
-                                              # the reference's bmm/mask/softmax chain
-                                              (True, False, 16), (False, True, 32),
-                                              (False, False, 8)])
-def test_tiny_model_loss_and_grads_vs_oracle(qk_norm, llama3, D):
-    c = tiny_cfg(qk_norm, llama3, D)
+@pytest.mark.parametrize("qk_norm,llama3,D,vocab", [(False, False, 64, 1000),
+                                                    (True, False, 128, 1000),
+                                                    (False, True, 64, 1000),
+                                                    # head sizes outside the fused kernels'
+                                                    # 64/128: the reference's
+                                                    # bmm/mask/softmax chain
+                                                    (True, False, 16, 1000),
+                                                    (False, True, 32, 1000),
+                                                    (False, False, 8, 1000),
+                                                    # LM head over the active rows only
+                                                    (True, False, 128, 1024),
+                                                    (False, True, 64, 1024)])
+def test_tiny_model_loss_and_grads_vs_oracle(qk_norm, llama3, D, vocab):
+    c = tiny_cfg(qk_norm, llama3, D, vocab)
     tr = TR.Trainer(c, seed=1, init_std=0.1, norm_value=None)
     ids, tg, mask = batch(c, 2, 96, seed=2)
     tr.set_batch(ids, tg, mask)
@@ -277,12 +285,18 @@ def test_tiny_model_loss_and_grads_vs_oracle(qk_norm, llama3, D):
     tr.close()
 
 
-def test_chunked_lm_head_loss_equals_single_chunk():
+@pytest.mark.parametrize("vocab,dead_rows", [(1000, 0), (1024, 0), (1024, 100)])
+def test_chunked_lm_head_loss_equals_single_chunk(vocab, dead_rows):
     """The LM head + loss run a chunk of rows at a time; the loss does not
     depend on the chunking (bitwise), the gradients only through the order dW
-    is summed in, and both match the oracle."""
-    c = tiny_cfg(qk_norm=True, D=64)
+    is summed in.  vocab 1024 takes the active-rows form, where chunks hold
+    active rows only (dead_rows: the first rows all masked out, so that a
+    whole chunk's worth of rows has nothing to compute); its loss is the
+    all-rows form's (set_head_active_rows(False)) bit for bit and its
+    gradients equal within fp32 rounding."""
+    c = tiny_cfg(qk_norm=True, D=64, vocab=vocab)
     ids, tg, mask = batch(c, 2, 96, seed=8)
+    mask.reshape(-1)[:dead_rows] = 0
     runs = []
     for rows in (0, 64, 40):   # automatic (one chunk), 3 chunks, 5 chunks (ragged)
         TR.set_head_chunk_rows(rows)
@@ -291,6 +305,16 @@ def test_chunked_lm_head_loss_equals_single_chunk():
         loss = tr.forward_backward(True)
         runs.append((loss, [tr.get_grad(i) for i in range(tr.num_params())], tr.names))
         tr.close()
+    if vocab % 16 == 0:  # the same model with every row through the head
+        TR.set_head_active_rows(False)
+        try:
+            tr = TR.Trainer(c, seed=4, init_std=0.1, norm_value=None)
+            tr.set_batch(ids, tg, mask)
+            loss = tr.forward_backward(True)
+            runs.append((loss, [tr.get_grad(i) for i in range(tr.num_params())], tr.names))
+            tr.close()
+        finally:
+            TR.set_head_active_rows(True)
     TR.set_head_chunk_rows(0)
     base_loss, base_grads, names = runs[0]
     for loss, grads, _ in runs[1:]:
