@@ -151,6 +151,15 @@ __device__ __forceinline__ void tile_coords(const GemmArgs& a, int& tm, int& tn)
   const int tiles = a.tiles_m * a.tiles_n;
   int t = blockIdx.x;
   if ((tiles & 7) == 0) t = (t & 7) * (tiles >> 3) + (t >> 3);
+  if (a.dyn && a.dyn_dim == 0) {
+    // Row tiles past a count read on the device are skipped.  Each XCD takes
+    // a range of whole columns (every row tile of them), so each keeps the
+    // same share of the work that remains whatever the count; with groups of
+    // tile rows per XCD, the XCDs holding the first rows would do it all.
+    tm = t % a.tiles_m;
+    tn = t / a.tiles_m;
+    return;
+  }
   const int width = kGroupM * a.tiles_n;
   const int group = t / width;
   const int first = group * kGroupM;
