@@ -280,7 +280,7 @@ def _cpu_model():
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=15)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--workload", default="qwen3-1.7b", choices=sorted(WORKLOADS))
     ap.add_argument("--no-checkpointing", action="store_true")

@@ -498,32 +498,34 @@ def test_c5_offloaded_steps_equal_on_device_full_size():
     # for bit.  The offloaded state is one 6.9 GB pinned buffer each for m and v
     # (byte offsets past 2^32), cut into 16M-float chunks that cross parameter
     # boundaries, and the embedding's 20 chunks are prefetched during the
-    # backward at the default layer; the second step reads back what the first
-    # wrote.
+    # backward at the default layer (a), or not at all (p); the second step
+    # reads back what the first wrote.
     c = TR.preset("qwen3-1.7b")
     a = TR.Trainer(c, seed=0, init_std=0.02)
+    p = TR.Trainer(c, seed=0, init_std=0.02)
     b = TR.Trainer(c, seed=0, init_std=0.02)
     a.make_optimizer(lr=1e-4, weight_decay=0.1, offload=True)
+    p.make_optimizer(lr=1e-4, weight_decay=0.1, offload=True)
+    p.set_prefetch_chunks(0)
     b.make_optimizer(lr=1e-4, weight_decay=0.1, offload=False)
-    for t in (a, b):
+    for t in (a, p, b):
         t.set_checkpointing(True)
     for step in range(2):
-        la = lb = None
-        for t in (a, b):
+        losses = []
+        for t in (a, p, b):
             t.synthetic_batch(8, 4096, seed=step, masked=True)
-            st = t.train_step(1.0)
-            if t is a:
-                la = st.loss
-            else:
-                lb = st.loss
-        assert la == lb, (step, la, lb)
+            losses.append(t.train_step(1.0).loss)
+        assert losses[0] == losses[1] == losses[2], (step, losses)
     ms, nbytes, prefetched = a.offload_stats()
     assert nbytes > 2 ** 32 and prefetched > 0
+    assert p.offload_stats()[2] == 0
     for i in range(a.num_params()):
-        assert np.array_equal(a.get_param(i), b.get_param(i)), a.names[i]
-        ma, va = a.opt_state(i)
+        want = b.get_param(i)
         mb, vb = b.opt_state(i)
-        assert np.array_equal(ma, mb), a.names[i]
-        assert np.array_equal(va, vb), a.names[i]
-    a.close()
-    b.close()
+        for t in (a, p):
+            assert np.array_equal(t.get_param(i), want), a.names[i]
+            mt, vt = t.opt_state(i)
+            assert np.array_equal(mt, mb), a.names[i]
+            assert np.array_equal(vt, vb), a.names[i]
+    for t in (a, p, b):
+        t.close()
