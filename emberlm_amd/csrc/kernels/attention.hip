@@ -501,7 +501,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
     if (threadIdx.x < C::kBQ) {
       const int t = qt0 + static_cast<int>(threadIdx.x);
       const int64_t srow = (static_cast<int64_t>(b) * H + h) * T;
-      tl = t < T ? lse[srow + t] * kLog2e : 0.f;
+      tl = t < T ? lse[srow + t] : 0.f;  // scaled at the LDS store: no wait here
       te = t < T ? delta[srow + t] : 0.f;
     }
   };
@@ -509,7 +509,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
     tq.store(buf, C::kQS);
     tdo.store(buf + C::kBQ * C::kQS, C::kQS);
     if (threadIdx.x < C::kBQ) {
-      buf[2 * C::kBQ * C::kQS + threadIdx.x] = tl;
+      buf[2 * C::kBQ * C::kQS + threadIdx.x] = tl * kLog2e;
       buf[2 * C::kBQ * C::kQS + C::kBQ + threadIdx.x] = te;
     }
   };
