@@ -323,6 +323,23 @@ def test_chunked_lm_head_loss_equals_single_chunk(vocab, dead_rows):
             assert_close(g, b, rtol=1e-5, name=name)
 
 
+@pytest.mark.parametrize("vocab", [1000, 1024])
+def test_lm_head_loss_with_every_row_masked_out(vocab):
+    # The reference's masked CE: a zero mask gives loss 0 in the forward and an
+    # error in the backward (sum(loss_mask) == 0, loss.cu:382-408), through the
+    # all-rows form (vocab 1000) and the active-rows form, which then finds no
+    # rows at all (vocab 1024).
+    c = tiny_cfg(qk_norm=True, D=64, vocab=vocab)
+    ids, tg, mask = batch(c, 2, 64, seed=3)
+    mask[:] = 0
+    tr = TR.Trainer(c, seed=1, init_std=0.1, norm_value=None)
+    tr.set_batch(ids, tg, mask)
+    assert tr.forward_backward(False) == 0.0
+    with pytest.raises(TR.CtdError, match=r"sum\(loss_mask\) == 0"):
+        tr.forward_backward(True)
+    tr.close()
+
+
 def test_offload_equals_on_device_over_steps():
     c = tiny_cfg(qk_norm=True, D=128)
     a = TR.Trainer(c, seed=3, init_std=0.05)
