@@ -443,6 +443,9 @@ def main():
         "hbm_device_used_gb": round(mem.device_used / 1e9, 3),
         "pinned_host_gb": round(mem.pinned_host / 1e9, 3),
         "active_tokens_per_s": round(mask_sum / (ms_step / 1e3), 2),
+        # The fused LM head + loss computes only rows whose mask value is
+        # nonzero (the rest add nothing to the loss or any gradient).
+        "lm_head_rows": {"computed": int(mask_sum), "of": B * T},
         "phase_ms": {k: round(avg(k + "_ms"), 2) for k in
                      ("forward", "backward", "clip", "optimizer", "optimizer_stream")},
         "loss": round(times[-1].loss, 5),
