@@ -31,7 +31,7 @@
 //                registers across every query tile and every query head of
 //                the KV head's group, in a fixed order.  With a dS buffer it
 //                also stores dS (fp32, the causal part only, see below);
-//   attn_bwd_dq_ds: dQ^T += K^T dS^T per 16 queries from the stored dS, a
+//   attn_bwd_dq_ds: dQ^T += K^T dS^T per 32 queries from the stored dS, a
 //                plain product in key order;
 //   attn_bwd_dq (no dS buffer): per 16 queries, S^T = K Q^T and dP^T =
 //                V dO^T recomputed, then dQ^T += K^T dS^T.
@@ -45,10 +45,11 @@
 // float4 of four consecutive queries per lane; entries it skips (query tiles
 // no key of a wave sees) are never read, because the dQ kernel masks keys
 // after the query.
-// Every backward kernel takes 64 rows per workgroup (two waves per SIMD at
-// D = 128 for dK/dV and the recompute dQ; 32 rows per wave on 32x32x2 tiles
-// needed more than 256 registers per lane there) and double-buffers its
-// streamed tiles the same way.
+// The dK/dV and recompute-dQ kernels take 64 rows per workgroup (two waves
+// per SIMD at D = 128; 32 rows per wave on 32x32x2 tiles needed more than 256
+// registers per lane there), the dQ-from-dS kernel 128 queries (32 per wave,
+// three waves per SIMD at D = 128); all double-buffer their streamed tiles the
+// same way.
 #include "common.h"
 
 using namespace ember;
@@ -122,56 +123,12 @@ struct RowTile {
   }
 };
 
-// A tile of ROWS rows of D floats copied global -> LDS by
-// global_load_lds_dwordx4: 16 bytes per lane, one 1 KB block of kRpi = 256/D
-// rows per wave-instruction, no registers and no LDS store instructions.
-// Row r goes to block r % kBlocks, slot r / kBlocks, and the blocks sit
-// 1 KB + 16 B apart, so consecutive rows start 16 bytes apart modulo 256 B
-// (D = 128: each row of a 16-row half in its own block), and every read
-// offset in the kernels below is a lane base plus an immediate.
-template <int D, int ROWS, int WAVES>
-struct DmaTile {
-  static constexpr int kChunks = D / 4;              // 16-byte chunks per row
-  static constexpr int kRpi = 64 / kChunks;          // rows per block
-  static constexpr int kBlocks = ROWS / kRpi;
-  static constexpr int kBlockStride = 256 + 4;       // floats
-  static constexpr int kFloats = kBlocks * kBlockStride;
-  static constexpr int kInsts = kBlocks / WAVES;     // per wave
-  static_assert(kRpi * kChunks == 64 && ROWS % kRpi == 0, "rows do not fill 1 KB blocks");
-  static_assert(kBlocks % WAVES == 0, "tile does not split evenly over the waves");
-  __device__ __forceinline__ static int at(int row, int col) {
-    return (row % kBlocks) * kBlockStride + (row / kBlocks) * D + col;
-  }
-  // Rows [0, ROWS) of src (row stride gstride floats) into lds; rows at or
-  // past valid (>= 1) re-read row valid - 1, whose products are masked out.
-  __device__ __forceinline__ static void issue(float* lds, const float* src, int64_t gstride,
-                                               int valid, int w, int lane) {
-#if defined(__HIP_DEVICE_COMPILE__)  // the host pass would drop the kernel's launch stub
-#pragma unroll
-    for (int q = 0; q < kInsts; ++q) {
-      const int blk = w + WAVES * q;
-      const int row = blk + kBlocks * (lane / kChunks);
-      const int64_t srow = min(row, valid - 1);
-      __builtin_amdgcn_global_load_lds(src + srow * gstride + 4 * (lane % kChunks),
-                                       lds + kBlockStride * blk, 16, 0, 0);
-    }
-#endif
-  }
-};
-
-// s_waitcnt vmcnt(0) lgkmcnt(0).
-__device__ __forceinline__ void wait_all_mem() {
-  __builtin_amdgcn_s_waitcnt((7 << 4) | (0 << 8));
-}
-
 // ------------------------------------------------------------------ forward
 // Forward.  A wave owns 16 queries and a workgroup of eight waves 128, so
-// every K/V tile in LDS serves 128 queries, and at 110 registers per lane
+// every K/V tile in LDS serves 128 queries, and at 124 registers per lane
 // (D = 128) four waves fit on a SIMD (32 queries per wave on 32x32x2 tiles
-// took 239 and two waves: 1.14x slower at B=8, T=4096, H=16, Hk=8).  The
-// next K/V tile is copied into the other LDS buffer by DMA while this one is
-// used (1.2% faster than staging it through registers).  Per 32-key tile
-// (halves kt of 16 keys):
+// took 239 and two waves: 1.14x slower at B=8, T=4096, H=16, Hk=8).  Per
+// 32-key tile (halves kt of 16 keys):
 //   S^T = K Q^T (m = key, n = query): MFMA step 4t+j contracts over
 //   d = 16t + 4g + j, each K fragment one b128 LDS read, Q in registers;
 //   register e of s[kt] in lane (g, i) is the score of key 16kt + 4g + e for
@@ -182,9 +139,8 @@ __device__ __forceinline__ void wait_all_mem() {
 //   operand one b32 LDS read of V.
 template <int D>
 struct FwdCfg {
-  static constexpr int kThreads = 512, kBQ = 128, kBK = 32;
-  static constexpr int kTile = DmaTile<D, kBK, kThreads / 64>::kFloats;
-  static constexpr int kBuf = 2 * kTile;  // one K+V stage
+  static constexpr int kThreads = 512, kBQ = 128, kBK = 32, kKS = D + 4;
+  static constexpr int kBuf = 2 * kBK * kKS;  // one K+V stage
   static constexpr int kSmem = 2 * kBuf;
 };
 
@@ -224,24 +180,22 @@ __global__ __launch_bounds__(FwdCfg<D>::kThreads, 2) void attn_fwd_kernel(
 
   const int kend = min(T, q0 + C::kBQ);
   const int nkb = (kend + C::kBK - 1) / C::kBK;
-  using Tile = DmaTile<D, C::kBK, C::kThreads / 64>;
-  const int wu = __builtin_amdgcn_readfirstlane(w);
-  Tile::issue(smem, kbase, ks, T, wu, lane);
-  Tile::issue(smem + C::kTile, vbase, ks, T, wu, lane);
-  wait_all_mem();
+  RowTile<D, C::kBK, C::kThreads> tk, tv;
+  tk.load(kbase, ks, T);
+  tv.load(vbase, ks, T);
+  tk.store(smem, C::kKS);
+  tv.store(smem + C::kBK * C::kKS, C::kKS);
   __syncthreads();
 
   for (int kb = 0; kb < nkb; ++kb) {
     const int k0 = kb * C::kBK;
     const bool more = kb + 1 < nkb;
-    if (more) {  // the next K/V tile lands in the other buffer during this one
-      float* nb = smem + ((kb + 1) & 1) * C::kBuf;
-      const int64_t off = static_cast<int64_t>(k0 + C::kBK) * ks;
-      Tile::issue(nb, kbase + off, ks, T - k0 - C::kBK, wu, lane);
-      Tile::issue(nb + C::kTile, vbase + off, ks, T - k0 - C::kBK, wu, lane);
+    if (more) {
+      tk.load(kbase + static_cast<int64_t>(k0 + C::kBK) * ks, ks, T - k0 - C::kBK);
+      tv.load(vbase + static_cast<int64_t>(k0 + C::kBK) * ks, ks, T - k0 - C::kBK);
     }
     const float* Ks = smem + (kb & 1) * C::kBuf;
-    const float* Vs = Ks + C::kTile;
+    const float* Vs = Ks + C::kBK * C::kKS;
     if (k0 <= qw0 + 15) {  // some key of the tile is seen by some query of this wave
       f32x4 s[2];
 #pragma unroll
@@ -251,7 +205,7 @@ __global__ __launch_bounds__(FwdCfg<D>::kThreads, 2) void attn_fwd_kernel(
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
           const f32x4 kf =
-              *reinterpret_cast<const f32x4*>(Ks + Tile::at(16 * kt + i, 16 * t + 4 * g));
+              *reinterpret_cast<const f32x4*>(Ks + (16 * kt + i) * C::kKS + 16 * t + 4 * g);
 #pragma unroll
           for (int j = 0; j < 4; ++j) s[kt] = mfma16(kf[j], qreg[t][j], s[kt]);
         }
@@ -288,13 +242,16 @@ __global__ __launch_bounds__(FwdCfg<D>::kThreads, 2) void attn_fwd_kernel(
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int row = 16 * kt + 4 * g + e;
+          const int row = (16 * kt + 4 * g + e) * C::kKS;
 #pragma unroll
-          for (int t = 0; t < NT; ++t)
-            acc[t] = mfma16(Vs[Tile::at(row, 16 * t + i)], s[kt][e], acc[t]);
+          for (int t = 0; t < NT; ++t) acc[t] = mfma16(Vs[row + 16 * t + i], s[kt][e], acc[t]);
         }
     }
-    wait_all_mem();  // this wave's DMA of the next tile has landed
+    if (more) {
+      float* nb = smem + ((kb + 1) & 1) * C::kBuf;
+      tk.store(nb, C::kKS);
+      tv.store(nb + C::kBK * C::kKS, C::kKS);
+    }
     __syncthreads();
   }
 
@@ -631,16 +588,19 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
   }
 }
 
-// dQ from the stored dS: dQ^T += K^T dS^T per 16 queries, 64 per workgroup,
-// over 32-key tiles in key order (the same MFMA orientation as attn_bwd_dq,
-// whose dS^T operand this kernel loads instead of recomputing).  K tiles are
-// double-buffered in LDS; the next tile's dS values (eight per lane: keys
-// 16kt + 4g + e, query i) are loaded into registers before the current
-// tile's MFMAs.  Keys after the lane's query, and queries at or past T, read
-// nothing and count as 0.
+// dQ from the stored dS: dQ^T += K^T dS^T (m = d, n = query, contraction
+// over keys), 32 queries per wave as two 16-query MFMA tiles, so that every
+// b32 LDS read of K feeds two MFMAs; 128 queries per workgroup, over 32-key
+// tiles in key order.  K tiles are double-buffered in LDS; the next tile's dS
+// values (sixteen per lane: keys 16kt + 4g + e for queries i and 16 + i of
+// the wave) are loaded into registers before the current tile's MFMAs.  Keys
+// after a lane's query, and queries at or past T, read nothing and count as
+// 0, which adds exact zeros: every dQ element sums the same products in the
+// same key order as a 16-query tiling would.
 template <int D>
 struct DqDsCfg {
-  static constexpr int kBQ = 64, kBK = 32, kKS = D + 4;
+  static constexpr int kWQ = 32;  // queries per wave
+  static constexpr int kBQ = 4 * kWQ, kBK = 32, kKS = D + 4;
   static constexpr int kBuf = kBK * kKS;
   static constexpr int kSmem = 2 * kBuf;
 };
@@ -660,35 +620,43 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_ds_kernel(
   const int h = row % H, b = row / H;
   const int hk = h / (H / Hk);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, i = lane & 15;
-  const int q0 = qb * C::kBQ, qw0 = q0 + 16 * w, myq = qw0 + i;
+  const int q0 = qb * C::kBQ, qw0 = q0 + C::kWQ * w;
   const int64_t qs = static_cast<int64_t>(H) * D, ks = static_cast<int64_t>(Hk) * D;
   const float* kbase = k + static_cast<int64_t>(b) * T * ks + static_cast<int64_t>(hk) * D;
   const int64_t T32 = ds_t32(T);
   const float* dsrow = ds + static_cast<int64_t>(wi.row) * ds_row_floats(T);
-  const bool live = myq < T;
 
-  // dS^T[key][myq] for keys k0 + 16kt + 4g + e of 32-key tile kbi.
-  auto load_ds = [&](int kbi, float (&dst)[2][4]) {
+  // dS^T[key][query] for keys k0 + 16kt + 4g + e of 32-key tile kbi and the
+  // lane's queries qw0 + 16n + i.
+  auto load_ds = [&](int kbi, float (&dst)[2][2][4]) {
     const int k0 = kbi * C::kBK, sb = k0 >> 6;
     const int64_t lr = T32 - 64 * sb;
-    const float* strip = dsrow + ds_strip_offset(sb, T32) + (myq - 64 * sb);
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+    for (int n = 0; n < 2; ++n) {
+      const int myq = qw0 + 16 * n + i;
+      const float* strip = dsrow + ds_strip_offset(sb, T32) + (myq - 64 * sb);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int key = k0 + 16 * kt + 4 * g + e;
-        dst[kt][e] = (live && key <= myq) ? strip[static_cast<int64_t>(key - 64 * sb) * lr] : 0.f;
-      }
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int key = k0 + 16 * kt + 4 * g + e;
+          dst[n][kt][e] = (myq < T && key <= myq)
+                              ? strip[static_cast<int64_t>(key - 64 * sb) * lr]
+                              : 0.f;
+        }
+    }
   };
 
-  f32x4 acc[NT];
+  f32x4 acc[2][NT];
 #pragma unroll
-  for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int n = 0; n < 2; ++n)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[n][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int kend = min(T, q0 + C::kBQ);
   const int nkb = (kend + C::kBK - 1) / C::kBK;
   RowTile<D, C::kBK> tk;
-  float cur[2][4], nxt[2][4];
+  float cur[2][2][4], nxt[2][2][4];
   tk.load(kbase, ks, T);
   load_ds(0, cur);
   tk.store(smem, C::kKS);
@@ -702,31 +670,41 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_ds_kernel(
       load_ds(kb + 1, nxt);
     }
     const float* Ks = smem + (kb & 1) * C::kBuf;
-    if (k0 <= qw0 + 15) {  // some key of the tile is seen by some query of this wave
+    if (k0 <= qw0 + C::kWQ - 1) {  // some key of the tile is seen by some query of this wave
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = (16 * kt + 4 * g + e) * C::kKS;
 #pragma unroll
-          for (int t = 0; t < NT; ++t) acc[t] = mfma16(Ks[r + 16 * t + i], cur[kt][e], acc[t]);
+          for (int t = 0; t < NT; ++t) {
+            const float kv = Ks[r + 16 * t + i];
+#pragma unroll
+            for (int n = 0; n < 2; ++n) acc[n][t] = mfma16(kv, cur[n][kt][e], acc[n][t]);
+          }
         }
     }
     if (more) {
       tk.store(smem + ((kb + 1) & 1) * C::kBuf, C::kKS);
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+      for (int n = 0; n < 2; ++n)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) cur[kt][e] = nxt[kt][e];
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) cur[n][kt][e] = nxt[n][kt][e];
     }
     __syncthreads();
   }
 
-  if (live) {
-    f32x4* dqr = reinterpret_cast<f32x4*>(dq + static_cast<int64_t>(b) * T * qs +
-                                          static_cast<int64_t>(h) * D + myq * qs);
 #pragma unroll
-    for (int t = 0; t < NT; ++t) dqr[4 * t + g] = acc[t] * scale;
+  for (int n = 0; n < 2; ++n) {
+    const int myq = qw0 + 16 * n + i;
+    if (myq < T) {
+      f32x4* dqr = reinterpret_cast<f32x4*>(dq + static_cast<int64_t>(b) * T * qs +
+                                            static_cast<int64_t>(h) * D + myq * qs);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) dqr[4 * t + g] = acc[n][t] * scale;
+    }
   }
 }
 
@@ -781,9 +759,10 @@ int launch_bwd(const float* q, const float* k, const float* v, const float* o, c
       o, dout, delta, rows, Ti, Hi);
   int rc = launch_status();
   if (rc) return rc;
-  static_assert(DqCfg<D>::kBQ == 64 && DqDsCfg<D>::kBQ == 64, "dQ grids assume 64 queries");
+  static_assert(DqCfg<D>::kBQ == 64, "recompute dQ grid assumes 64 queries");
   static_assert(DkvCfg<D>::kBKeys == 64, "dK/dV grid assumes 64 keys");
   const unsigned nqb = static_cast<unsigned>((T + 63) / 64);
+  const unsigned nqb_ds = static_cast<unsigned>((T + DqDsCfg<D>::kBQ - 1) / DqDsCfg<D>::kBQ);
   const int64_t group = H / Hk, kv_rows = B * Hk;
   const size_t dlt = delta_bytes(B, T, H);
   const size_t kv_row_bytes = static_cast<size_t>(group * ds_row_floats(T)) * sizeof(float);
@@ -806,7 +785,8 @@ int launch_bwd(const float* q, const float* k, const float* v, const float* o, c
     attn_bwd_dkdv_kernel<D><<<dim3(nqb * static_cast<unsigned>(n)), kThreads, 0, st>>>(
         q, k, v, dout, lse, delta, dk, dv, ds, static_cast<int>(r0), Ti, Hi, Hki, sl, scale);
     if ((rc = launch_status())) return rc;
-    attn_bwd_dq_ds_kernel<D><<<dim3(nqb * static_cast<unsigned>(n * group)), kThreads, 0, st>>>(
+    attn_bwd_dq_ds_kernel<D><<<dim3(nqb_ds * static_cast<unsigned>(n * group)), kThreads, 0,
+                               st>>>(
         k, ds, dq, static_cast<int>(r0 * group), Ti, Hi, Hki, scale);
     if ((rc = launch_status())) return rc;
   }
