@@ -137,6 +137,26 @@ Tensor matmul_graph_only(const Tensor& a, const Tensor& b, bool transa, bool tra
   return y;
 }
 
+Tensor matmul_add(const Tensor& a, const Tensor& b, bool transa, bool transb, const Tensor& d) {
+  const MM dm = mm_dims(a, b, transa, transb, "matmul_add");
+  check_f32(d, "matmul_add", "d");
+  require(d.device() == a.device() && d.is_contiguous() && d.dim() == 2 &&
+              d.shape()[0] == dm.M && d.shape()[1] == dm.N,
+          "matmul_add: d must be a contiguous [M, N] tensor on the operands' device");
+  Tensor y = Tensor::empty({dm.M, dm.N}, DType::kFloat32, a.device());
+  const size_t wsb = ember_gemm_f32_workspace_bytes(dm.M, dm.N, dm.K, 1);
+  Tensor ws = wsb ? workspace(wsb) : Tensor{};
+  void* ev = runtime::gemm_profile_begin();
+  CTD_CHECK(ember_gemm_f32_add(transa, transb, dm.M, dm.N, dm.K, 1.0f, cfp(a), dm.lda, cfp(b),
+                               dm.ldb, cfp(d), dm.N, fp(y), dm.N, wsb ? ws.data_ptr() : nullptr,
+                               wsb, S()));
+  runtime::gemm_profile_end(ev, 2.0 * dm.M * dm.N * dm.K, 2 * transa + transb);
+  if (!autograd::any_requires_grad({a, b, d})) return y;
+  // The graph of add(d, matmul(a, b)) over the fused values.
+  Tensor m = matmul_graph_only(a, b, transa, transb, y);
+  return add_graph_only(d, m, y);
+}
+
 Tensor bmm_impl(const Tensor& a, const Tensor& b, bool transa, bool transb) {
   check_f32(a, "bmm", "a");
   check_f32(b, "bmm", "b");

@@ -58,7 +58,17 @@ struct GemmArgs {
   const int64_t* dyn = nullptr;
   int64_t dyn_base = 0;
   int dyn_dim = 0;
+  // Optional addend (single GEMMs only): C = alpha op(A) op(B) + beta D, with
+  // D = C when null.  D may be C itself (ldd = ldc), never a shifted overlap.
+  const float* D = nullptr;
+  int64_t ldd = 0;
 };
+
+// The beta term's source for element (row, col) of the current C.
+__device__ __forceinline__ const float* addend(const GemmArgs& a, const float* dst, int64_t row,
+                                               int64_t col) {
+  return a.D ? a.D + row * a.ldd + col : dst;
+}
 
 __device__ __forceinline__ int64_t dyn_extent(const GemmArgs& a, int64_t full) {
   return min(max(*a.dyn - a.dyn_base, int64_t{0}), full);
@@ -300,7 +310,7 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_mfma(GemmArgs a) {
         if (row < a.M) {
           float* dst = C + row * a.ldc + col;
           const float v = a.alpha * acc[i][j][e];
-          *dst = (a.beta != 0.f) ? v + a.beta * *dst : v;
+          *dst = (a.beta != 0.f) ? v + a.beta * *addend(a, dst, row, col) : v;
         }
       }
     }
@@ -434,7 +444,7 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_dma(GemmArgs a) {
       if (m0 >= dyn_extent(a, a.M)) return;
     } else {
       K = min(K, (dyn_extent(a, K) + 15) / 16 * 16);
-      if (K == 0 && a.beta == 1.f) return;  // C stays as it is
+      if (K == 0 && a.beta == 1.f && !a.D) return;  // C stays as it is
     }
   }
 
@@ -571,19 +581,21 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_dma(GemmArgs a) {
         if (row < a.M) {
           float* dst = C + row * a.ldc + col;
           const float v = a.alpha * acc[i][j][e];
-          *dst = (a.beta != 0.f) ? v + a.beta * *dst : v;
+          *dst = (a.beta != 0.f) ? v + a.beta * *addend(a, dst, row, col) : v;
         }
       }
     }
 }
 
-// C = alpha * sum_{s<S} P[s] + beta * C, the split partials summed in order.
-// P is [S][M][N] dense; four columns per thread when the rows allow it.
+// C = alpha * sum_{s<S} P[s] + beta * D (D = C when null), the split partials
+// summed in order.  P is [S][M][N] dense; four columns per thread when the
+// rows allow it.
 template <bool VEC>
 __global__ __launch_bounds__(kThreads) void splitk_reduce(const float* __restrict__ P, float* C,
                                                           int64_t M, int64_t N, int64_t ldc,
                                                           int S, float alpha, float beta,
-                                                          const int64_t* dyn, int64_t dyn_base) {
+                                                          const int64_t* dyn, int64_t dyn_base,
+                                                          const float* D, int64_t ldd) {
   const int64_t per = VEC ? 4 : 1;
   const int64_t cols = N / per;
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
@@ -599,8 +611,9 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce(const float* __restric
       for (int e = 0; e < 4; ++e) s[e] += t[e];
     }
     f32x4* dst = reinterpret_cast<f32x4*>(C + m * ldc + n);
+    const f32x4* src = D ? reinterpret_cast<const f32x4*>(D + m * ldd + n) : dst;
     f32x4 out;
-    const f32x4 old = beta != 0.f ? *dst : f32x4{0.f, 0.f, 0.f, 0.f};
+    const f32x4 old = beta != 0.f ? *src : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int e = 0; e < 4; ++e) out[e] = beta != 0.f ? alpha * s[e] + beta * old[e] : alpha * s[e];
     *dst = out;
@@ -608,7 +621,8 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce(const float* __restric
     float s = P[m * N + n];
     for (int k = 1; k < S; ++k) s += P[k * plane + m * N + n];
     float* dst = C + m * ldc + n;
-    *dst = beta != 0.f ? alpha * s + beta * *dst : alpha * s;
+    const float* src = D ? D + m * ldd + n : dst;
+    *dst = beta != 0.f ? alpha * s + beta * *src : alpha * s;
   }
 }
 
@@ -627,9 +641,10 @@ template <int MR>
 __global__ __launch_bounds__(kThreads) void gemm_skinny_nt(const float* __restrict__ A,
                                                            int64_t lda,
                                                            const float* __restrict__ B,
-                                                           int64_t ldb, float* __restrict__ C,
-                                                           int64_t ldc, int M, int64_t N,
-                                                           int64_t K, float alpha, float beta) {
+                                                           int64_t ldb, float* C, int64_t ldc,
+                                                           int M, int64_t N, int64_t K,
+                                                           float alpha, float beta,
+                                                           const float* D, int64_t ldd) {
   constexpr int NR = kSkinnyRows;
   __shared__ float red[kThreads / kWave][NR * MR];
   const int lane = threadIdx.x & (kWave - 1);
@@ -693,7 +708,8 @@ __global__ __launch_bounds__(kThreads) void gemm_skinny_nt(const float* __restri
 #pragma unroll
       for (int q = 0; q < kThreads / kWave; ++q) s += red[q][idx];
       float* c = C + m * ldc + n;
-      *c = beta != 0.f ? alpha * s + beta * *c : alpha * s;
+      const float* src = D ? D + m * ldd + n : c;
+      *c = beta != 0.f ? alpha * s + beta * *src : alpha * s;
     }
   }
 }
@@ -701,10 +717,10 @@ __global__ __launch_bounds__(kThreads) void gemm_skinny_nt(const float* __restri
 template <int MR>
 int launch_skinny(const float* A, int64_t lda, const float* B, int64_t ldb, float* C,
                   int64_t ldc, int64_t M, int64_t N, int64_t K, float alpha, float beta,
-                  hipStream_t st) {
+                  const float* D, int64_t ldd, hipStream_t st) {
   const unsigned grid = static_cast<unsigned>((N + kSkinnyRows - 1) / kSkinnyRows);
   gemm_skinny_nt<MR><<<grid, kThreads, 0, st>>>(A, lda, B, ldb, C, ldc, static_cast<int>(M), N,
-                                                 K, alpha, beta);
+                                                 K, alpha, beta, D, ldd);
   return launch_status();
 }
 
@@ -806,21 +822,24 @@ int gemm_run(int transa, int transb, int64_t M, int64_t N, int64_t K, float alph
              const float* A, int64_t lda, int64_t sA, const float* B, int64_t ldb, int64_t sB,
              float beta, float* C, int64_t ldc, int64_t sC, int64_t batch, void* workspace,
              size_t workspace_bytes, const int64_t* dyn, int64_t dyn_base, int dyn_dim,
-             hipStream_t st) {
+             const float* D, int64_t ldd, hipStream_t st) {
   int rc = EMBER_OK;
   GemmArgs a{A, B, C, M, N, K, lda, ldb, ldc, sA, sB, sC, 0, alpha, beta, 0, 0};
   a.dyn = dyn;
   a.dyn_base = dyn_base;
   a.dyn_dim = dyn_dim;
+  a.D = D;
+  a.ldd = ldd;
   const bool vec = aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0) &&
                    (batch == 1 || (sA % 4 == 0 && sB % 4 == 0));
   const bool a_kc = !transa, b_kc = transb != 0;
   if (!dyn && batch == 1 && M <= kSkinnyMaxM && a_kc && b_kc && vec && K > 0 && K % 4 == 0 &&
       N <= int64_t{kSkinnyRows} * 0x7fffffff) {
-    if (M == 1) return launch_skinny<1>(A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, st);
-    if (M == 2) return launch_skinny<2>(A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, st);
-    if (M <= 4) return launch_skinny<4>(A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, st);
-    return launch_skinny<8>(A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, st);
+    auto skinny = M == 1 ? launch_skinny<1>
+                  : M == 2 ? launch_skinny<2>
+                  : M <= 4 ? launch_skinny<4>
+                           : launch_skinny<8>;
+    return skinny(A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, D, ldd, st);
   }
   Plan p = make_plan(M, N, K, batch);
   if (p.splits > 1 &&
@@ -843,18 +862,19 @@ int gemm_run(int transa, int transb, int64_t M, int64_t N, int64_t K, float alph
     if ((rc = dma ? launch_dma<128, 128, 3>(sp, a_kc, b_kc, p.splits, st)
                   : launch_t<128, 128, 3>(sp, a_kc, b_kc, p.splits, vec, st)))
       return rc;
-    const bool rvec = (N % 4 == 0) && (ldc % 4 == 0) && aligned16(C);
+    const bool rvec = (N % 4 == 0) && (ldc % 4 == 0) && aligned16(C) &&
+                      (!D || (ldd % 4 == 0 && aligned16(D)));
     const int64_t items = M * (rvec ? N / 4 : N);
     const unsigned blocks = static_cast<unsigned>(cdiv(items, kThreads));
     const int64_t* rdyn = dyn_dim == 0 ? dyn : nullptr;
     if (rvec)
       splitk_reduce<true><<<blocks, kThreads, 0, st>>>(static_cast<const float*>(workspace), C, M,
                                                        N, ldc, static_cast<int>(p.splits),
-                                                       alpha, beta, rdyn, dyn_base);
+                                                       alpha, beta, rdyn, dyn_base, D, ldd);
     else
       splitk_reduce<false><<<blocks, kThreads, 0, st>>>(static_cast<const float*>(workspace), C,
                                                         M, N, ldc, static_cast<int>(p.splits),
-                                                        alpha, beta, rdyn, dyn_base);
+                                                        alpha, beta, rdyn, dyn_base, D, ldd);
     return launch_status();
   }
   const bool dma = vec && K % 16 == 0 && (a_kc || M % 4 == 0) && (b_kc || N % 4 == 0) &&
@@ -876,7 +896,26 @@ extern "C" int ember_gemm_f32_ws(int transa, int transb, int64_t M, int64_t N, i
   int rc = check_args(transa, transb, M, N, K, A, lda, B, ldb, C, ldc, batch);
   if (rc || M == 0 || N == 0) return rc;
   return gemm_run(transa, transb, M, N, K, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, batch,
-                  workspace, workspace_bytes, nullptr, 0, 0, as_stream(s));
+                  workspace, workspace_bytes, nullptr, 0, 0, nullptr, 0, as_stream(s));
+}
+
+extern "C" int ember_gemm_f32_add(int transa, int transb, int64_t M, int64_t N, int64_t K,
+                                  float alpha, const float* A, int64_t lda, const float* B,
+                                  int64_t ldb, const float* D, int64_t ldd, float* C, int64_t ldc,
+                                  void* workspace, size_t workspace_bytes, ember_stream_t s) {
+  int rc = check_args(transa, transb, M, N, K, A, lda, B, ldb, C, ldc, 1);
+  if (rc || M == 0 || N == 0) return rc;
+  if (!D || ldd < N) return EMBER_EINVAL;
+  if (D != C) {  // D is C itself or lies wholly apart from it
+    const auto c0 = reinterpret_cast<uintptr_t>(C), d0 = reinterpret_cast<uintptr_t>(D);
+    const uintptr_t c1 = c0 + static_cast<uintptr_t>((M - 1) * ldc + N) * sizeof(float);
+    const uintptr_t d1 = d0 + static_cast<uintptr_t>((M - 1) * ldd + N) * sizeof(float);
+    if (d0 < c1 && c0 < d1) return EMBER_EINVAL;
+  } else if (ldd != ldc) {
+    return EMBER_EINVAL;
+  }
+  return gemm_run(transa, transb, M, N, K, alpha, A, lda, 0, B, ldb, 0, 1.0f, C, ldc, 0, 1,
+                  workspace, workspace_bytes, nullptr, 0, 0, D, ldd, as_stream(s));
 }
 
 extern "C" int ember_gemm_f32_dyn(int transa, int transb, int64_t M, int64_t N, int64_t K,
@@ -894,7 +933,7 @@ extern "C" int ember_gemm_f32_dyn(int transa, int transb, int64_t M, int64_t N, 
     return EMBER_EINVAL;
   if (M == 0 || N == 0) return EMBER_OK;
   return gemm_run(transa, transb, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1,
-                  workspace, workspace_bytes, count, base, dim, as_stream(s));
+                  workspace, workspace_bytes, count, base, dim, nullptr, 0, as_stream(s));
 }
 
 extern "C" int ember_gemm_f32(int transa, int transb, int64_t M, int64_t N, int64_t K,

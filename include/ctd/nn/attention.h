@@ -66,6 +66,11 @@ struct Attention {
   // kv, this call's K/V go to cache rows [position_start, position_start+T)
   // and the queries attend over rows [0, position_start+T).
   Tensor forward(const Tensor& x, KVLayer* kv = nullptr, int position_start = 0) const {
+    return o_proj.forward(forward_context(x, kv, position_start));
+  }
+
+  // forward() up to o_proj: the attention output, [B, T, H * D].
+  Tensor forward_context(const Tensor& x, KVLayer* kv = nullptr, int position_start = 0) const {
     autograd::NoGradGuard ng;
     const int64_t B = x.shape()[0];
     const int64_t T = x.shape()[1];
@@ -101,11 +106,14 @@ struct Attention {
     } else {
       A = ops::offset_attention(Q, K, V, position_start, scale);
     }
-    return o_proj.forward(A.reshape({B, T, static_cast<int64_t>(H) * D}));
+    return A.reshape({B, T, static_cast<int64_t>(H) * D});
   }
 
   // Training forward (autograd-aware), positions start at 0.
-  Tensor forward_train(const Tensor& x) const {
+  Tensor forward_train(const Tensor& x) const { return o_proj.forward(forward_train_context(x)); }
+
+  // forward_train() up to o_proj: the attention output, [B, T, H * D].
+  Tensor forward_train_context(const Tensor& x) const {
     const int64_t B = x.shape()[0];
     const int64_t T = x.shape()[1];
     const int H = num_heads, Hk = num_kv_heads, D = head_dim;
@@ -127,7 +135,7 @@ struct Attention {
       Tensor Vr = ops::permute(ops::repeat_kv_heads(V, group()), {0, 2, 1, 3});
       A = attention_chain(Q, Kr, Vr, 0, scale);
     }
-    return o_proj.forward(A.reshape({B, T, static_cast<int64_t>(H) * D}));
+    return A.reshape({B, T, static_cast<int64_t>(H) * D});
   }
 };
 

@@ -17,6 +17,13 @@ struct MLP {
     Tensor u = up_proj.forward(x);
     return down_proj.forward(ops::swiglu(g, u));
   }
+
+  // residual + forward(x), the add done by the down projection's GEMM.
+  Tensor forward_add(const Tensor& x, const Tensor& residual) const {
+    Tensor g = gate_proj.forward(x);
+    Tensor u = up_proj.forward(x);
+    return down_proj.forward_add(ops::swiglu(g, u), residual);
+  }
 };
 
 }  // namespace ctd::nn

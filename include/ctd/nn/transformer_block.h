@@ -26,11 +26,9 @@ struct TransformerBlock {
         Attention::fused_head_dim(self_attn.head_dim))
       return decode_step(x, *kv, position_start);
     Tensor h1 = input_layernorm.forward(x);
-    Tensor a = self_attn.forward(h1, kv, position_start);
-    Tensor h = ops::add(x, a);
+    Tensor h = self_attn.o_proj.forward_add(self_attn.forward_context(h1, kv, position_start), x);
     Tensor h2 = post_attention_layernorm.forward(h);
-    Tensor m = mlp.forward(h2);
-    return ops::add(h, m);
+    return mlp.forward_add(h2, h);
   }
 
   Tensor decode_step(const Tensor& x, KVLayer& kv, int position_start) const {
@@ -51,13 +49,13 @@ struct TransformerBlock {
     return ops::decode_linear(m, Tensor{}, 0.0f, {mlp.down_proj.weight}, {h})[0];
   }
 
+  // The residual adds run inside the o_proj and down_proj GEMMs (bitwise the
+  // same as ops::add after the product, same autograd graph).
   Tensor forward_train(const Tensor& x) const {
     Tensor h1 = input_layernorm.forward(x);
-    Tensor a = self_attn.forward_train(h1);
-    Tensor h = ops::add(x, a);
+    Tensor h = self_attn.o_proj.forward_add(self_attn.forward_train_context(h1), x);
     Tensor h2 = post_attention_layernorm.forward(h);
-    Tensor m = mlp.forward(h2);
-    return ops::add(h, m);
+    return mlp.forward_add(h2, h);
   }
 
   // forward_train(x) for a checkpoint's recompute, whose backward reads only
@@ -68,8 +66,7 @@ struct TransformerBlock {
   // computed the real output: it is the next block's saved input.
   Tensor forward_train_for_backward(const Tensor& x) const {
     Tensor h1 = input_layernorm.forward(x);
-    Tensor a = self_attn.forward_train(h1);
-    Tensor h = ops::add(x, a);
+    Tensor h = self_attn.o_proj.forward_add(self_attn.forward_train_context(h1), x);
     Tensor h2 = post_attention_layernorm.forward(h);
     Tensor act = ops::swiglu(mlp.gate_proj.forward(h2), mlp.up_proj.forward(h2));
     Tensor m = mlp.down_proj.forward_graph_only(act, h);

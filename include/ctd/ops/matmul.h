@@ -16,6 +16,12 @@ Tensor matmul_impl(const Tensor& a, const Tensor& b, bool transa, bool transb);
 Tensor matmul_graph_only(const Tensor& a, const Tensor& b, bool transa, bool transb,
                          const Tensor& values);
 
+// d + matmul(a, b, transa, transb) in one GEMM (the add done as the product
+// is stored, bitwise equal to the two ops), with both ops' backward nodes:
+// the residual connections of a block.  d is [M, N] contiguous.  Added in
+// this build; the reference runs matmul and then ops::add.
+Tensor matmul_add(const Tensor& a, const Tensor& b, bool transa, bool transb, const Tensor& d);
+
 // Batched matmul: a [B, Ma, Ka], b [B, Mb, Kb] -> [B, M, N].
 Tensor bmm(const Tensor& a, const Tensor& b, bool transa = false, bool transb = false);
 Tensor bmm_impl(const Tensor& a, const Tensor& b, bool transa, bool transb);

@@ -100,10 +100,10 @@ int ember_gemm_f32(int transa, int transb, int64_t M, int64_t N, int64_t K, floa
  * reproducible run to run.  ember_gemm_f32_workspace_bytes gives the size this
  * call can use (0: no split for this shape); a smaller or NULL workspace runs
  * the unsplit kernel.  ember_gemm_f32 is this call with no workspace. */
-/* Both entry points run products with at most 8 rows (M <= 8, batch 1, A and
- * B K-contiguous i.e. transa = 0 and transb = 1, 16-byte aligned, K % 4 == 0:
- * Linear forward of a decode step) on a skinny kernel that streams B at HBM
- * rate instead of on the MFMA tiles. */
+/* These entry points and ember_gemm_f32_add run products with at most 8 rows
+ * (M <= 8, batch 1, A and B K-contiguous i.e. transa = 0 and transb = 1,
+ * 16-byte aligned, K % 4 == 0: Linear forward of a decode step) on a skinny
+ * kernel that streams B at HBM rate instead of on the MFMA tiles. */
 size_t ember_gemm_f32_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t batch);
 int ember_gemm_f32_ws(int transa, int transb, int64_t M, int64_t N, int64_t K, float alpha,
                       const float* A, int64_t lda, int64_t sA, const float* B, int64_t ldb,
@@ -126,6 +126,20 @@ int ember_gemm_f32_dyn(int transa, int transb, int64_t M, int64_t N, int64_t K, 
                        const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
                        float* C, int64_t ldc, const int64_t* count, int64_t base, int dim,
                        void* workspace, size_t workspace_bytes, ember_stream_t s);
+/* C = alpha op(A) op(B) + D (batch 1): a product and a residual add in one
+ * pass, the add done where the product is stored (the split-K reduce when K
+ * is split).  Replaces the matmul + ops::add pairs of the block's residual
+ * connections (include/ctd/nn/transformer_block.h:21, 24 with
+ * src/ops/matmul.cpp:38-47 and the add kernel, src/ops/elementwise.cu:14-20,
+ * 89-101); element for element the same float additions as the product
+ * stored and then added, so the results are bitwise equal.  D is [M][ldd],
+ * ldd >= N; it may be C itself (ldd == ldc, the same as beta = 1) but must
+ * not otherwise overlap C (EMBER_EINVAL).  The workspace is
+ * ember_gemm_f32_ws's. */
+int ember_gemm_f32_add(int transa, int transb, int64_t M, int64_t N, int64_t K, float alpha,
+                       const float* A, int64_t lda, const float* B, int64_t ldb, const float* D,
+                       int64_t ldd, float* C, int64_t ldc, void* workspace,
+                       size_t workspace_bytes, ember_stream_t s);
 
 /* -------------------------------------------------------------- RMSNorm
  * y = x * rsqrt(mean(x^2) + eps) * w over rows of length H; rstd[rows] (may be

@@ -491,6 +491,64 @@ def test_gemm_dyn_rejects_shapes_off_the_dma_path():
                   64, p(cnt), 0, 2, None, 0, None)
 
 
+# ------------------------------------------------- product + residual add
+def _gemm_ws(A, B, ta, tb, M, N, K, lda, ldb):
+    wsb = int(capi.lib().ember_gemm_f32_workspace_bytes(M, N, K, 1))
+    ws = empty((max(wsb // 4, 1),))
+    Cm = empty((M, N))
+    call("ember_gemm_f32_ws", int(ta), int(tb), M, N, K, 1.0, p(A), lda, 0, p(B), ldb, 0, 0.0,
+         p(Cm), N, 0, 1, p(ws), wsb, None)
+    return Cm, ws, wsb
+
+
+@pytest.mark.parametrize("ta,tb,M,N,K", [
+    (0, 1, 4096, 2048, 512),    # Linear forward shape: 256x128 DMA tiles
+    (0, 1, 300, 200, 64),       # 128x128 DMA tiles, ragged edges
+    (0, 0, 1000, 300, 48),      # NN
+    (1, 0, 256, 128, 8192),     # TN with a K split: the reduce adds D
+    (1, 1, 200, 150, 70),       # K not whole 16-k stages: register-staged kernel
+    (0, 1, 5, 1000, 256),       # M <= 8: skinny kernel
+    (0, 1, 100, 64, 0),         # K = 0: C = D
+])
+def test_gemm_add_bitwise_equals_product_then_add(ta, tb, M, N, K):
+    """ember_gemm_f32_add = the same product stored, then one IEEE add per
+    element (torch's add here), bit for bit; D separate and D = C."""
+    r = rng(M + 3 * N + 7 * K)
+    a = r.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    b = r.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    d = r.standard_normal((M, N)).astype(np.float32)
+    A, B, Dd = dev(a), dev(b), dev(d)
+    lda, ldb = a.shape[1], b.shape[1]
+    prod, ws, wsb = _gemm_ws(A, B, ta, tb, M, N, K, lda, ldb)
+    want = host(prod + Dd)
+    Cm = empty((M, N))
+    call("ember_gemm_f32_add", int(ta), int(tb), M, N, K, 1.0, p(A), lda, p(B), ldb, p(Dd), N,
+         p(Cm), N, p(ws), wsb, None)
+    assert np.array_equal(host(Cm), want)
+    C2 = Dd.clone()                 # D aliased to C: the beta = 1 form
+    call("ember_gemm_f32_add", int(ta), int(tb), M, N, K, 1.0, p(A), lda, p(B), ldb, p(C2), N,
+         p(C2), N, p(ws), wsb, None)
+    assert np.array_equal(host(C2), want)
+    if K:
+        assert_close(host(Cm), O.matmul(a, b, ta, tb) + d, name="gemm add")
+
+
+def test_gemm_add_rejects_overlap_and_short_rows():
+    A = empty((64, 32))
+    buf = empty((65, 64))
+    D, Cm = buf[1:], buf[:64]       # D starts one row into C
+    with pytest.raises(capi.EmberError):
+        capi.call("ember_gemm_f32_add", 0, 1, 64, 64, 32, 1.0, p(A), 32, p(A), 32, p(D), 64,
+                  p(Cm), 64, None, 0, None)
+    C2 = empty((64, 64))
+    with pytest.raises(capi.EmberError):   # ldd < N
+        capi.call("ember_gemm_f32_add", 0, 1, 64, 64, 32, 1.0, p(A), 32, p(A), 32, p(C2), 32,
+                  p(C2), 64, None, 0, None)
+    with pytest.raises(capi.EmberError):   # D = C with another row stride
+        capi.call("ember_gemm_f32_add", 0, 1, 32, 32, 32, 1.0, p(A), 32, p(A), 32, p(C2), 64,
+                  p(C2), 32, None, 0, None)
+
+
 # ------------------------------------------------------------ embedding
 def test_embedding_kat_and_bwd():
     V, H = 7, 5
