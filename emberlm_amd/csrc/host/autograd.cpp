@@ -136,6 +136,28 @@ void accumulate_slot(Tensor& slot, const Tensor& incoming) {
   }
 }
 
+// For each edge of n: the gradient its input already holds, when nothing but
+// the engine holds that storage and no earlier edge of n targets the same
+// slot (so a node may add into it in place); else an empty tensor.
+std::vector<Tensor> partial_sums(const Node& n,
+                                 std::unordered_map<Node*, std::vector<Tensor>>& grads_in) {
+  std::vector<Tensor> out(n.next_edges.size());
+  for (size_t i = 0; i < n.next_edges.size(); ++i) {
+    const Edge& e = n.next_edges[i];
+    if (!e.node) continue;
+    bool repeated = false;
+    for (size_t j = 0; j < i; ++j)
+      repeated = repeated || (n.next_edges[j].node == e.node &&
+                              n.next_edges[j].input_nr == e.input_nr);
+    if (repeated) continue;
+    auto it = grads_in.find(e.node.get());
+    if (it == grads_in.end() || it->second.size() <= e.input_nr) continue;
+    const Tensor& slot = it->second[e.input_nr];
+    if (slot.storage() && slot.storage().use_count() == 1) out[i] = slot;
+  }
+  return out;
+}
+
 Tensor ones_like_scalar(const Tensor& t) {
   if (t.dtype() != DType::kFloat32) throw std::runtime_error("backward: fp32 only");
   if (t.numel() != 1) throw std::runtime_error("backward: only scalar loss is supported");
@@ -193,10 +215,16 @@ void run_backward(const std::shared_ptr<AutogradMeta>& root_meta, Tensor root_gr
     Node* n = ready.front();
     ready.pop();
     std::vector<Tensor> out_grads;
+    std::vector<Tensor> partials;
     {
       std::vector<Tensor> grads = std::move(grads_in[n]);
       grads_in.erase(n);
-      out_grads = n->backward(grads);
+      if (n->accepts_partials()) {
+        partials = partial_sums(*n, grads_in);
+        out_grads = n->backward_with_partials(grads, partials);
+      } else {
+        out_grads = n->backward(grads);
+      }
     }
     if (out_grads.size() != n->next_edges.size())
       throw std::runtime_error(std::string("backward: node ") + n->name() +
@@ -206,7 +234,10 @@ void run_backward(const std::shared_ptr<AutogradMeta>& root_meta, Tensor root_gr
       if (!e.node) continue;
       Tensor& incoming = out_grads[i];
       Node* p = e.node.get();
-      if (incoming.storage()) {
+      const bool added = i < partials.size() && partials[i].storage() &&
+                         incoming.storage() == partials[i].storage();
+      if (i < partials.size()) partials[i] = Tensor{};  // the slot's storage is exclusive again
+      if (incoming.storage() && !added) {  // (added: the node summed into the slot)
         auto& slots = grads_in[p];
         if (slots.size() <= e.input_nr) slots.resize(e.input_nr + 1);
         if (!slots[e.input_nr].storage()) {

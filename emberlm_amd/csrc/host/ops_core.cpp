@@ -63,14 +63,47 @@ std::pair<Tensor, Tensor> matmul_like_backward(const Tensor& dy, const Tensor& a
   return {dA, dB};
 }
 
+// c += op(x) op(y) on the GEMM (beta = 1): the same float additions as the
+// product stored and then accumulated into c.
+void matmul_accumulate(const Tensor& x, const Tensor& y, bool tx, bool ty, Tensor& c) {
+  const MM d = mm_dims(x, y, tx, ty, "matmul");
+  const size_t wsb = ember_gemm_f32_workspace_bytes(d.M, d.N, d.K, 1);
+  Tensor ws = wsb ? workspace(wsb) : Tensor{};
+  void* ev = runtime::gemm_profile_begin();
+  CTD_CHECK(ember_gemm_f32_ws(tx, ty, d.M, d.N, d.K, 1.0f, cfp(x), d.lda, 0, cfp(y), d.ldb, 0,
+                              1.0f, fp(c), d.N, 0, 1, wsb ? ws.data_ptr() : nullptr, wsb, S()));
+  runtime::gemm_profile_end(ev, 2.0 * d.M * d.N * d.K, 2 * tx + ty);
+}
+
 struct MatmulBackward : autograd::Node {
   Tensor a, b;
   bool ta = false, tb = false;
   const char* name() const override { return "MatmulBackward"; }
   std::vector<Tensor> backward(const std::vector<Tensor>& go) override {
+    return backward_with_partials(go, {});
+  }
+  // dA goes straight into a partial sum the engine already holds for a
+  // (another consumer's gradient), by a beta = 1 GEMM: the fan-in add of
+  // src/core/autograd.cu's accumulate step done where dA is stored.
+  bool accepts_partials() const override { return true; }
+  std::vector<Tensor> backward_with_partials(const std::vector<Tensor>& go,
+                                             const std::vector<Tensor>& partials) override {
     autograd::NoGradGuard ng;
     const bool na = next_edges.at(0).node != nullptr, nb = next_edges.at(1).node != nullptr;
-    auto [dA, dB] = matmul_like_backward(go.at(0), a, b, ta, tb, na, nb, matmul_impl);
+    const Tensor* into = partials.empty() ? nullptr : &partials[0];
+    const bool fold = na && into && into->storage() && into->dtype() == DType::kFloat32 &&
+                      into->device() == a.device() && into->is_contiguous() &&
+                      into->shape() == a.shape();
+    auto [dA, dB] = matmul_like_backward(go.at(0), a, b, ta, tb, na && !fold, nb, matmul_impl);
+    if (fold) {
+      // dA's operands per the same table: op(x) op(y) with (x, y, tx, ty).
+      Tensor acc = *into;
+      if (!ta && !tb) matmul_accumulate(go[0], b, false, true, acc);
+      else if (ta && !tb) matmul_accumulate(b, go[0], false, true, acc);
+      else if (!ta && tb) matmul_accumulate(go[0], b, false, false, acc);
+      else matmul_accumulate(b, go[0], true, true, acc);
+      dA = acc;
+    }
     release_saved(a, b);
     return {dA, dB};
   }

@@ -21,6 +21,18 @@ class Node {
  public:
   virtual ~Node() = default;
   virtual std::vector<Tensor> backward(const std::vector<Tensor>& grads_out) = 0;
+  // A node that accepts partials is run through backward_with_partials: for
+  // each edge whose input already holds a gradient from an earlier node, in
+  // storage nothing else holds, partials[edge] is that running sum (else
+  // empty).  The node may add its own gradient for the edge into it in place
+  // and return that same tensor for the edge; the engine then adds nothing.
+  // Added in this build (the reference always returns a new gradient).
+  virtual bool accepts_partials() const { return false; }
+  virtual std::vector<Tensor> backward_with_partials(const std::vector<Tensor>& grads_out,
+                                                     const std::vector<Tensor>& partials) {
+    (void)partials;
+    return backward(grads_out);
+  }
   virtual const char* name() const { return "Node"; }
   std::vector<Edge> next_edges;
   // Set once a backward pass that does not retain the graph has run this

@@ -117,9 +117,10 @@ struct Attention {
     const int64_t B = x.shape()[0];
     const int64_t T = x.shape()[1];
     const int H = num_heads, Hk = num_kv_heads, D = head_dim;
-    Tensor Q = q_proj.forward(x).reshape({B, T, H, D});
-    Tensor K = k_proj.forward(x).reshape({B, T, Hk, D});
-    Tensor V = v_proj.forward(x).reshape({B, T, Hk, D});
+    Tensor x2 = q_proj.rows(x);  // one view for the three projections
+    Tensor Q = q_proj.forward(x2).reshape({B, T, H, D});
+    Tensor K = k_proj.forward(x2).reshape({B, T, Hk, D});
+    Tensor V = v_proj.forward(x2).reshape({B, T, Hk, D});
     if (has_qk_norm()) {
       Q = q_norm.forward(Q);
       K = k_norm.forward(K);

@@ -11,47 +11,47 @@ struct Linear {
   Tensor weight;  // [out, in]
 
   Tensor forward(const Tensor& x) const {
-    const int64_t in = weight.shape()[1];
-    const int64_t out = weight.shape()[0];
-    const auto& sh = x.shape();
-    if (sh.back() != in) throw std::runtime_error("Linear: in_features mismatch");
-    const int64_t leading = x.numel() / in;
-    Tensor y2d = ops::matmul(x.reshape({leading, in}), weight, /*transa=*/false, /*transb=*/true);
-    std::vector<int64_t> out_shape(sh.begin(), sh.end());
-    out_shape.back() = out;
-    return y2d.reshape(out_shape);
+    return shaped(ops::matmul(rows(x), weight, /*transa=*/false, /*transb=*/true), out_shape(x));
   }
 
   // residual + forward(x) as one GEMM whose store does the add (bitwise equal
-  // to the two ops, same backward); residual has forward(x)'s shape.
+  // to the two ops, same backward); residual has forward(x)'s elements and
+  // shapes the result.
   Tensor forward_add(const Tensor& x, const Tensor& residual) const {
-    const int64_t in = weight.shape()[1];
     const int64_t out = weight.shape()[0];
-    const auto& sh = x.shape();
-    if (sh.back() != in) throw std::runtime_error("Linear: in_features mismatch");
-    const int64_t leading = x.numel() / in;
-    std::vector<int64_t> out_shape(sh.begin(), sh.end());
-    out_shape.back() = out;
-    if (residual.shape() != out_shape)
+    Tensor x2 = rows(x);
+    if (residual.shape().back() != out || residual.numel() != x2.shape()[0] * out)
       throw std::runtime_error("Linear: residual shape mismatch");
-    Tensor y2d = ops::matmul_add(x.reshape({leading, in}), weight, /*transa=*/false,
-                                 /*transb=*/true, residual.reshape({leading, out}));
-    return y2d.reshape(out_shape);
+    Tensor r2 = residual.dim() == 2 ? residual : residual.reshape({x2.shape()[0], out});
+    return shaped(ops::matmul_add(x2, weight, /*transa=*/false, /*transb=*/true, r2),
+                  residual.shape());
   }
 
   // forward(x)'s autograd graph without the product: the result is a view of
-  // `values` (forward(x)'s shape).  See ops::matmul_graph_only.
+  // `values` (forward(x)'s elements).  See ops::matmul_graph_only.
   Tensor forward_graph_only(const Tensor& x, const Tensor& values) const {
+    return shaped(ops::matmul_graph_only(rows(x), weight, /*transa=*/false, /*transb=*/true,
+                                         values),
+                  out_shape(x));
+  }
+
+  // x as [leading, in_features]: x itself when it is 2-D already, so that
+  // projections of one input share its node and their input gradients meet
+  // in one place (where the engine adds them inside the second GEMM).
+  Tensor rows(const Tensor& x) const {
     const int64_t in = weight.shape()[1];
-    const int64_t out = weight.shape()[0];
-    const auto& sh = x.shape();
-    if (sh.back() != in) throw std::runtime_error("Linear: in_features mismatch");
-    const int64_t leading = x.numel() / in;
-    Tensor y2d = ops::matmul_graph_only(x.reshape({leading, in}), weight, /*transa=*/false,
-                                        /*transb=*/true, values);
-    std::vector<int64_t> out_shape(sh.begin(), sh.end());
-    out_shape.back() = out;
-    return y2d.reshape(out_shape);
+    if (x.shape().back() != in) throw std::runtime_error("Linear: in_features mismatch");
+    return x.dim() == 2 ? x : x.reshape({x.numel() / in, in});
+  }
+
+ private:
+  std::vector<int64_t> out_shape(const Tensor& x) const {
+    std::vector<int64_t> sh(x.shape().begin(), x.shape().end());
+    sh.back() = weight.shape()[0];
+    return sh;
+  }
+  static Tensor shaped(const Tensor& y2d, const std::vector<int64_t>& shape) {
+    return y2d.shape() == shape ? y2d : y2d.reshape(shape);
   }
 };
 

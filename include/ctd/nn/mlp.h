@@ -18,11 +18,16 @@ struct MLP {
     return down_proj.forward(ops::swiglu(g, u));
   }
 
-  // residual + forward(x), the add done by the down projection's GEMM.
+  // residual + forward(x), the add done by the down projection's GEMM; gate
+  // and up read one [tokens, hidden] view of x.
   Tensor forward_add(const Tensor& x, const Tensor& residual) const {
-    Tensor g = gate_proj.forward(x);
-    Tensor u = up_proj.forward(x);
-    return down_proj.forward_add(ops::swiglu(g, u), residual);
+    return down_proj.forward_add(activation(x), residual);
+  }
+
+  // silu(gate(x)) * up(x) as [tokens, intermediate].
+  Tensor activation(const Tensor& x) const {
+    Tensor x2 = gate_proj.rows(x);
+    return ops::swiglu(gate_proj.forward(x2), up_proj.forward(x2));
   }
 };
 

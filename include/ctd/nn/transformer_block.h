@@ -68,9 +68,8 @@ struct TransformerBlock {
     Tensor h1 = input_layernorm.forward(x);
     Tensor h = self_attn.o_proj.forward_add(self_attn.forward_train_context(h1), x);
     Tensor h2 = post_attention_layernorm.forward(h);
-    Tensor act = ops::swiglu(mlp.gate_proj.forward(h2), mlp.up_proj.forward(h2));
-    Tensor m = mlp.down_proj.forward_graph_only(act, h);
-    return ops::add_graph_only(h, m, h);
+    Tensor m = mlp.down_proj.forward_graph_only(mlp.activation(h2), h);
+    return ops::add_graph_only(h, m.reshape(h.shape()), h);
   }
 };
 

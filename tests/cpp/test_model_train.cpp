@@ -586,6 +586,34 @@ void block_graph_only_recompute_matches_forward_train() {
         "matmul_graph_only rejects values of another size");
 }
 
+// A matmul whose input already holds another consumer's gradient adds its
+// own into it inside the GEMM (beta = 1).  The input gradient must be bitwise
+// what the engine's separate adds give when each product reads its own view
+// of x (so nothing can be folded), for an unsplit and a split-K product.
+void fan_in_fold_matches_separate_adds() {
+  std::mt19937 rng(12);
+  for (int64_t O : {96, 2048}) {
+    const int64_t N = 300, K = 64;
+    Tensor x0 = rand_tensor({N, K}, rng, 1.0f, false);
+    Tensor w1 = rand_tensor({O, K}, rng, 0.1f, false), w2 = rand_tensor({O, K}, rng, 0.1f, false),
+           w3 = rand_tensor({O, K}, rng, 0.1f, false);
+    Tensor dy = rand_tensor({N, O}, rng, 1.0f, false);
+    auto run_once = [&](bool shared) {
+      Tensor x = x0.detach();
+      x.requires_grad_(true);
+      auto view = [&] { return shared ? x : x.reshape({N, K}); };
+      Tensor y = ops::add(ops::add(ops::matmul(view(), w1, false, true),
+                                   ops::matmul(view(), w2, false, true)),
+                          ops::matmul(view(), w3, false, true));
+      y.backward(dy);
+      return host(x.grad());
+    };
+    const std::vector<float> folded = run_once(true), separate = run_once(false);
+    check(folded == separate, "fan-in folded into the GEMM is bitwise the separate adds, O = " +
+                                  std::to_string(O));
+  }
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -600,6 +628,7 @@ int main(int argc, char** argv) {
   run("Optim.SGD", [] { sgd_step(); });
   run("Autograd.BlockGraphOnlyRecompute",
       [] { block_graph_only_recompute_matches_forward_train(); });
+  run("Autograd.FanInFoldMatchesSeparateAdds", [] { fan_in_fold_matches_separate_adds(); });
   run("Autograd.RetainedGraphRepeatBackward", [] { retained_graph_repeat_backward(false, 1.0f); });
   run("Autograd.RetainedGraphRepeatBackward_Checkpointed",
       [] { retained_graph_repeat_backward(true, 1.0f); });
