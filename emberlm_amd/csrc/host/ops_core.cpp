@@ -353,6 +353,61 @@ Tensor rope_transpose_impl(const Tensor& x, int position_start, float theta,
   return y;
 }
 
+namespace {
+
+struct QkNormRopeBackward : autograd::Node {
+  Tensor x, w, rstd;
+  float eps = 1e-6f;
+  int position_start = 0;
+  RopeArgs args{};
+  const char* name() const override { return "QkNormRopeBackward"; }
+  std::vector<Tensor> backward(const std::vector<Tensor>& go) override {
+    autograd::NoGradGuard ng;
+    check_f32(go.at(0), "qk_norm_rope backward", "grad");
+    const bool need_dx = next_edges.at(0).node != nullptr;
+    const bool need_dw = next_edges.at(1).node != nullptr;
+    const int64_t rows = args.B * args.T * args.H;
+    Tensor dx = need_dx ? empty_like(x) : Tensor{};
+    Tensor dw = need_dw ? empty_like(w) : Tensor{};
+    const size_t wsb = need_dw ? ember_rmsnorm_bwd_workspace_bytes(rows, args.D) : 0;
+    Tensor ws = wsb ? workspace(wsb) : Tensor{};
+    CTD_CHECK(ember_qknorm_rope_bwd(cfp(go[0]), cfp(x), cfp(w), cfp(rstd),
+                                    need_dx ? fp(dx) : nullptr, need_dw ? fp(dw) : nullptr, rows,
+                                    args.H, args.T, args.D, eps, position_start, args.freqs,
+                                    wsb ? ws.data_ptr() : nullptr, wsb, S()));
+    release_saved(x, w, rstd);
+    return {dx, dw};
+  }
+};
+
+}  // namespace
+
+Tensor qk_norm_rope(const Tensor& x, const Tensor& weight, float eps, int position_start,
+                    float theta, const RopeScaling& scaling) {
+  check_norm(x, weight);
+  const RopeArgs a = rope_args(x, theta, scaling);
+  if ((a.D != 64 && a.D != 128) || !x.is_contiguous())
+    return rope(rms_norm(x, weight, eps), position_start, theta, scaling);
+  const int64_t rows = a.B * a.T * a.H;
+  const bool grad = autograd::any_requires_grad({x, weight});
+  Tensor y = empty_like(x);
+  Tensor rstd = grad ? Tensor::empty({rows}, DType::kFloat32, x.device()) : Tensor{};
+  CTD_CHECK(ember_qknorm_rope_fwd(cfp(x), cfp(weight), fp(y), grad ? fp(rstd) : nullptr, rows,
+                                  a.H, a.T, a.D, eps, position_start, a.freqs, S()));
+  if (grad) {
+    auto node = std::make_shared<QkNormRopeBackward>();
+    node->x = x.detach();
+    node->w = weight.detach();
+    node->rstd = rstd;
+    node->eps = eps;
+    node->position_start = position_start;
+    node->args = a;
+    node->next_edges = autograd::collect_next_edges({x, weight});
+    autograd::set_history(y, std::move(node));
+  }
+  return y;
+}
+
 Tensor rope(const Tensor& x, int position_start, float theta, const RopeScaling& scaling) {
   Tensor y = rope_impl(x, position_start, theta, scaling);
   if (autograd::any_requires_grad({x})) {

@@ -10,6 +10,7 @@
 #include <mutex>
 
 #include "common.h"
+#include "rope_math.h"
 
 using namespace ember;
 
@@ -130,6 +131,23 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_scalar(const float* __re
   for (int64_t i = threadIdx.x; i < H; i += kThreads) y[row * H + i] = xr[i] * s * w[i];
 }
 
+// The backward's per-element arithmetic with its roundings spelled out (the
+// products written here are rounded, the rest is fused), so that this file's
+// two backward kernels give the same bits whatever the compiler would
+// contract in each context:  c += g w x,  dx = s (g w - x k),  dw += g x s.
+__device__ __forceinline__ float bwd_c_term(float c, float g, float w, float x) {
+#pragma clang fp contract(off)
+  return fmaf(x, g * w, c);
+}
+__device__ __forceinline__ float bwd_dx(float s, float g, float w, float x, float k) {
+#pragma clang fp contract(off)
+  return s * fmaf(g, w, -(x * k));
+}
+__device__ __forceinline__ float bwd_dw_term(float acc, float g, float x, float s) {
+#pragma clang fp contract(off)
+  return fmaf(g * x, s, acc);
+}
+
 // Backward, float4 path.  Block b handles rows b*RPB + slot + k*grid*RPB.
 // MAXC = float4 chunks per lane (H/4/LPR rounded up) kept as dw partials.
 template <int LPR, int MAXC>
@@ -172,7 +190,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             ss = fmaf(v[e], v[e], ss);
-            c += g[e] * ww[e] * v[e];
+            c = bwd_c_term(c, g[e], ww[e], v[e]);
           }
         }
       }
@@ -190,8 +208,8 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
         f32x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          o[e] = s * (g[e] * ww[e] - v[e] * k);
-          acc[j][e] += g[e] * v[e] * s;
+          o[e] = bwd_dx(s, g[e], ww[e], v[e], k);
+          acc[j][e] = bwd_dw_term(acc[j][e], g[e], v[e], s);
         }
         if (dx) reinterpret_cast<f32x4*>(dx + row * H)[ci] = o;
       }
@@ -238,6 +256,178 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_scalar(
       if (dx) dx[row * H + i] = s * (gr[i] * w[i] - xr[i] * s * s * c * invH);
       if (dw_part) dw_part[blockIdx.x * H + i] += gr[i] * xr[i] * s;
     }
+  }
+}
+
+// ------------------------------------------------ QK-Norm + RoPE, fused
+// Per-head RMSNorm and then the rotation in one pass over q or k: rows of
+// H = 4 * LPR floats, one float4 per lane (LPR = 16 or 32: D = 64 or 128),
+// row r = (b * T + t) * heads + h.  The norm is rmsnorm_fwd_reg<LPR, 1>'s
+// arithmetic and the rotation rope_kernel's (rope_math.h), so the result is
+// bitwise those two kernels run one after the other.  Element i's partner
+// i +- D/2 sits in lane sub ^ LPR/2 of the same row and comes over by a lane
+// shuffle; pair index i = 4 (sub % (LPR/2)) + e.  A workgroup's rows cover
+// few tokens (one when heads is a multiple of its row count), so it computes
+// each of their D/2 sines and cosines once, into LDS.
+struct RopeRows {
+  int64_t T, pos0;
+  int heads;
+  float sign;  // a run-time value, as in rope_kernel, so both compile alike
+  RopeFreqs fr;
+};
+
+template <int LPR>
+struct RopeTable {
+  static constexpr int kRows = kThreads / LPR, kPairs = 2 * LPR;
+  float cs[kRows][kPairs], sn[kRows][kPairs];
+};
+
+// Sines and cosines of the tokens of rows [row0, row0 + kRows) (clipped to
+// rows), token j at tok0 + j; the workgroup's threads share the work.
+template <int LPR>
+__device__ __forceinline__ void fill_rope_table(RopeTable<LPR>& tb, int64_t row0, int64_t rows,
+                                                const RopeRows& rr, int64_t& tok0) {
+  constexpr int P = RopeTable<LPR>::kPairs;
+  tok0 = row0 / rr.heads;
+  const int64_t last = min(row0 + RopeTable<LPR>::kRows, rows) - 1;
+  const int ntok = static_cast<int>(last / rr.heads - tok0 + 1);
+  for (int idx = threadIdx.x; idx < ntok * P; idx += kThreads) {
+    const int j = idx / P, i = idx % P;
+    float sn, cs;
+    rope_sincos(rr.pos0 + (tok0 + j) % rr.T, rr.fr.f[i], rr.sign, sn, cs);
+    tb.cs[j][i] = cs;
+    tb.sn[j][i] = sn;
+  }
+}
+
+template <int LPR>
+__device__ __forceinline__ f32x4 rotate_row_chunk(const f32x4& o, int sub, int j,
+                                                  const RopeTable<LPR>& tb) {
+  constexpr int HALF = LPR / 2;
+  f32x4 p, out;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) p[e] = __shfl_xor(o[e], HALF, kWave);
+  const bool first = sub < HALF;
+  const int i0 = 4 * (sub % HALF);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float cs = tb.cs[j][i0 + e], sn = tb.sn[j][i0 + e];
+    out[e] = first ? rope_first(o[e], p[e], cs, sn) : rope_second(p[e], o[e], cs, sn);
+  }
+  return out;
+}
+
+// The same rotation with the sines computed in registers: lanes sub and
+// sub ^ LPR/2 need the same four, so each computes two and they swap.  (For
+// the backward's grid-stride loop, where a shared table costs a barrier per
+// step.)
+template <int LPR>
+__device__ __forceinline__ f32x4 rotate_row_chunk_regs(const f32x4& o, int sub, int64_t row,
+                                                       const RopeRows& rr) {
+  constexpr int HALF = LPR / 2;
+  const bool first = sub < HALF;
+  const int i0 = 4 * (sub % HALF);
+  const int64_t pos = rr.pos0 + (row / rr.heads) % rr.T;
+  float cs[4], sn[4];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int mine = first ? q : 2 + q, theirs = first ? 2 + q : q;
+    rope_sincos(pos, rr.fr.f[i0 + mine], rr.sign, sn[mine], cs[mine]);
+    cs[theirs] = __shfl_xor(cs[mine], HALF, kWave);
+    sn[theirs] = __shfl_xor(sn[mine], HALF, kWave);
+  }
+  f32x4 p, out;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) p[e] = __shfl_xor(o[e], HALF, kWave);
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    out[e] = first ? rope_first(o[e], p[e], cs[e], sn[e]) : rope_second(p[e], o[e], cs[e], sn[e]);
+  return out;
+}
+
+template <int LPR>
+__global__ __launch_bounds__(kThreads) void qknorm_rope_fwd(const float* __restrict__ x,
+                                                            const float* __restrict__ w,
+                                                            float* __restrict__ y,
+                                                            float* __restrict__ rstd,
+                                                            int64_t rows, float eps,
+                                                            RopeRows rr) {
+  constexpr int RPB = kThreads / LPR;
+  constexpr int64_t H = 4 * LPR;
+  __shared__ RopeTable<LPR> tb;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * RPB;
+  int64_t tok0;
+  fill_rope_table<LPR>(tb, row0, rows, rr, tok0);
+  const int64_t row = row0 + threadIdx.x / LPR;
+  const int sub = threadIdx.x % LPR;
+  const bool live = row < rows;  // the same for every lane of a row's group
+  const int64_t r = live ? row : rows - 1;
+  const f32x4 v = reinterpret_cast<const f32x4*>(x + r * H)[sub];
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) ss = fmaf(v[e], v[e], ss);
+  ss = group_sum(ss, LPR);
+  const float s = 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
+  if (live && rstd && sub == 0) rstd[row] = s;
+  const f32x4 ww = reinterpret_cast<const f32x4*>(w)[sub];
+  f32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = v[e] * s * ww[e];
+  __syncthreads();  // the table is filled
+  const f32x4 out = rotate_row_chunk<LPR>(o, sub, static_cast<int>(r / rr.heads - tok0), tb);
+  if (live) reinterpret_cast<f32x4*>(y + row * H)[sub] = out;
+}
+
+// Backward (rr.sign = -1): dy through the rotation's transpose (rope_kernel
+// with sign -1), then rmsnorm_bwd_vec<LPR, 1>'s arithmetic, dw partials per
+// block likewise.
+template <int LPR>
+__global__ __launch_bounds__(kThreads) void qknorm_rope_bwd(
+    const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ w,
+    const float* __restrict__ rstd, float* __restrict__ dx, float* __restrict__ dw_part,
+    int64_t rows, float eps, RopeRows rr) {
+  constexpr int RPB = kThreads / LPR;
+  constexpr int64_t H = 4 * LPR;
+  extern __shared__ __attribute__((aligned(16))) float red[];  // [RPB][H]
+  const int slot = threadIdx.x / LPR;
+  const int sub = threadIdx.x % LPR;
+  const float invH = 1.0f / static_cast<float>(H);
+  const f32x4 ww = reinterpret_cast<const f32x4*>(w)[sub];
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int64_t step = static_cast<int64_t>(gridDim.x) * RPB;
+  for (int64_t row0 = static_cast<int64_t>(blockIdx.x) * RPB; row0 < rows; row0 += step) {
+    const int64_t row = row0 + slot;
+    const bool live = row < rows;
+    const int64_t r = live ? row : rows - 1;
+    const f32x4 v = reinterpret_cast<const f32x4*>(x + r * H)[sub];
+    const f32x4 g =
+        rotate_row_chunk_regs<LPR>(reinterpret_cast<const f32x4*>(dy + r * H)[sub], sub, r, rr);
+    float ss = 0.f, c = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      ss = fmaf(v[e], v[e], ss);
+      c = bwd_c_term(c, g[e], ww[e], v[e]);
+    }
+    ss = group_sum(ss, LPR);
+    c = group_sum(c, LPR);
+    if (!live) continue;
+    const float s = rstd ? rstd[row] : 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
+    const float k = s * s * c * invH;
+    f32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o[e] = bwd_dx(s, g[e], ww[e], v[e], k);
+      acc[e] = bwd_dw_term(acc[e], g[e], v[e], s);
+    }
+    if (dx) reinterpret_cast<f32x4*>(dx + row * H)[sub] = o;
+  }
+  if (!dw_part) return;
+  reinterpret_cast<f32x4*>(red + slot * H)[sub] = acc;
+  __syncthreads();
+  for (int64_t col = threadIdx.x; col < H; col += kThreads) {
+    float t = 0.f;
+    for (int sl = 0; sl < RPB; ++sl) t += red[sl * H + col];
+    dw_part[static_cast<int64_t>(blockIdx.x) * H + col] = t;
   }
 }
 
@@ -444,6 +634,80 @@ extern "C" int ember_rmsnorm_bwd(const float* dy, const float* x, const float* w
   if (rc || !dw) return rc;
   column_sum<<<static_cast<unsigned>((H + kWave - 1) / kWave), kColThreads, 0, st>>>(part, dw, nb,
                                                                                   H);
+  return launch_status();
+}
+
+namespace {
+
+// Checks shared by the fused QK-Norm + RoPE entries; fills the rows' RoPE
+// arguments.
+int qknorm_rope_rows(int64_t rows, int64_t heads, int64_t T, int64_t D, int64_t pos0,
+                     const float* freqs_host, float sign, RopeRows* rr) {
+  if (rows < 0 || heads <= 0 || T <= 0 || (D != 64 && D != 128) || !freqs_host ||
+      heads > 0x7fffffff || rows % (heads * T) != 0)
+    return EMBER_EINVAL;
+  rr->T = T;
+  rr->pos0 = pos0;
+  rr->heads = static_cast<int>(heads);
+  rr->sign = sign;
+  for (int i = 0; i < kRopeMaxPairs; ++i) rr->fr.f[i] = i < D / 2 ? freqs_host[i] : 0.f;
+  return EMBER_OK;
+}
+
+}  // namespace
+
+extern "C" int ember_qknorm_rope_fwd(const float* x, const float* w, float* y, float* rstd,
+                                     int64_t rows, int64_t heads, int64_t T, int64_t D, float eps,
+                                     int64_t pos0, const float* freqs_host, ember_stream_t s) {
+  RopeRows rr;
+  int rc = qknorm_rope_rows(rows, heads, T, D, pos0, freqs_host, 1.0f, &rr);
+  if (rc || rows == 0) return rc;
+  if (!x || !w || !y) return EMBER_EINVAL;
+  if (!aligned16(x) || !aligned16(w) || !aligned16(y)) return EMBER_EALIGN;
+  const int lpr = static_cast<int>(D / 4);
+  const int64_t nb = (rows + kThreads / lpr - 1) / (kThreads / lpr);
+  if (nb > 0x7fffffff) return EMBER_EINVAL;
+  hipStream_t st = as_stream(s);
+  if (D == 64)
+    qknorm_rope_fwd<16><<<static_cast<unsigned>(nb), kThreads, 0, st>>>(x, w, y, rstd, rows, eps,
+                                                                       rr);
+  else
+    qknorm_rope_fwd<32><<<static_cast<unsigned>(nb), kThreads, 0, st>>>(x, w, y, rstd, rows, eps,
+                                                                       rr);
+  return launch_status();
+}
+
+extern "C" int ember_qknorm_rope_bwd(const float* dy, const float* x, const float* w,
+                                     const float* rstd, float* dx, float* dw, int64_t rows,
+                                     int64_t heads, int64_t T, int64_t D, float eps,
+                                     int64_t pos0, const float* freqs_host, void* workspace,
+                                     size_t workspace_bytes, ember_stream_t s) {
+  RopeRows rr;
+  int rc = qknorm_rope_rows(rows, heads, T, D, pos0, freqs_host, -1.0f, &rr);
+  if (rc) return rc;
+  if (!w) return EMBER_EINVAL;
+  if (rows == 0) return dw ? ember_fill(dw, D, 0.f, s) : EMBER_OK;
+  if (!dy || !x) return EMBER_EINVAL;
+  if (!aligned16(dy) || !aligned16(x) || !aligned16(w) || (dx && !aligned16(dx)))
+    return EMBER_EALIGN;
+  const int64_t nb = bwd_blocks(rows, D, true);
+  float* part = nullptr;
+  if (dw) {
+    if (!workspace || workspace_bytes < static_cast<size_t>(nb) * D * sizeof(float))
+      return EMBER_EWORKSPACE;
+    part = static_cast<float*>(workspace);
+  }
+  hipStream_t st = as_stream(s);
+  const size_t lds = part ? static_cast<size_t>(kThreads) * 4 * sizeof(float) : 0;  // [RPB][D]
+  if (D == 64)
+    qknorm_rope_bwd<16><<<static_cast<unsigned>(nb), kThreads, lds, st>>>(dy, x, w, rstd, dx,
+                                                                         part, rows, eps, rr);
+  else
+    qknorm_rope_bwd<32><<<static_cast<unsigned>(nb), kThreads, lds, st>>>(dy, x, w, rstd, dx,
+                                                                         part, rows, eps, rr);
+  if ((rc = launch_status()) || !dw) return rc;
+  column_sum<<<static_cast<unsigned>((D + kWave - 1) / kWave), kColThreads, 0, st>>>(part, dw, nb,
+                                                                                  D);
   return launch_status();
 }
 

@@ -12,16 +12,14 @@
 #include <cmath>
 
 #include "common.h"
+#include "rope_math.h"
 
 using namespace ember;
 
 namespace {
 
-constexpr int kMaxPairs = 128;  // D <= 256
-
-struct Freqs {
-  float f[kMaxPairs];
-};
+constexpr int kMaxPairs = kRopeMaxPairs;
+using Freqs = RopeFreqs;
 
 __global__ __launch_bounds__(256) void rope_kernel(const float* x,
                                                    float* y, int64_t BT, int64_t T,
@@ -33,10 +31,8 @@ __global__ __launch_bounds__(256) void rope_kernel(const float* x,
   const int half = D / 2;
   if (tok >= BT || i >= half) return;
   const int64_t t = tok % T;
-  const float ang = static_cast<float>(pos0 + t) * fr.f[i];
   float sn, cs;
-  sincosf(ang, &sn, &cs);
-  sn *= sign;
+  rope_sincos(pos0 + t, fr.f[i], sign, sn, cs);
   const float* xb = x + tok * H * D;
   float* yb = y + tok * H * D;
   // Up to kHeads heads' pairs are loaded before any is stored (y may be x,
@@ -53,8 +49,8 @@ __global__ __launch_bounds__(256) void rope_kernel(const float* x,
 #pragma unroll
     for (int j = 0; j < kHeads; ++j)
       if (h0 + j < H) {
-        yb[(h0 + j) * D + i] = a[j] * cs - b[j] * sn;
-        yb[(h0 + j) * D + i + half] = a[j] * sn + b[j] * cs;
+        yb[(h0 + j) * D + i] = rope_first(a[j], b[j], cs, sn);
+        yb[(h0 + j) * D + i + half] = rope_second(a[j], b[j], cs, sn);
       }
   }
 }

@@ -79,11 +79,14 @@ struct Attention {
     Tensor K = k_proj.forward(x).reshape({B, T, Hk, D});
     Tensor V = v_proj.forward(x).reshape({B, T, Hk, D});
     if (has_qk_norm()) {
-      Q = q_norm.forward(Q);
-      K = k_norm.forward(K);
+      Q = ops::qk_norm_rope(Q, q_norm.weight, q_norm.eps, position_start, rope_theta,
+                            rope_scaling);
+      K = ops::qk_norm_rope(K, k_norm.weight, k_norm.eps, position_start, rope_theta,
+                            rope_scaling);
+    } else {
+      ops::apply_rope_inplace(Q, position_start, rope_theta, rope_scaling);
+      ops::apply_rope_inplace(K, position_start, rope_theta, rope_scaling);
     }
-    ops::apply_rope_inplace(Q, position_start, rope_theta, rope_scaling);
-    ops::apply_rope_inplace(K, position_start, rope_theta, rope_scaling);
     const float scale = 1.0f / std::sqrt(static_cast<float>(D));
     Tensor A;
     if (kv != nullptr) {
@@ -121,12 +124,13 @@ struct Attention {
     Tensor Q = q_proj.forward(x2).reshape({B, T, H, D});
     Tensor K = k_proj.forward(x2).reshape({B, T, Hk, D});
     Tensor V = v_proj.forward(x2).reshape({B, T, Hk, D});
-    if (has_qk_norm()) {
-      Q = q_norm.forward(Q);
-      K = k_norm.forward(K);
+    if (has_qk_norm()) {  // QK-Norm and RoPE in one pass each (bitwise the two ops)
+      Q = ops::qk_norm_rope(Q, q_norm.weight, q_norm.eps, 0, rope_theta, rope_scaling);
+      K = ops::qk_norm_rope(K, k_norm.weight, k_norm.eps, 0, rope_theta, rope_scaling);
+    } else {
+      Q = ops::rope(Q, /*position_start=*/0, rope_theta, rope_scaling);
+      K = ops::rope(K, /*position_start=*/0, rope_theta, rope_scaling);
     }
-    Q = ops::rope(Q, /*position_start=*/0, rope_theta, rope_scaling);
-    K = ops::rope(K, /*position_start=*/0, rope_theta, rope_scaling);
     const float scale = 1.0f / std::sqrt(static_cast<float>(D));
     Tensor A;
     if (fused_head_dim(D)) {

@@ -27,4 +27,11 @@ Tensor rope_impl(const Tensor& x, int position_start, float theta,
 Tensor rope_transpose_impl(const Tensor& x, int position_start, float theta,
                            const RopeScaling& scaling = {});
 
+// rope(rms_norm(x, weight, eps), ...) with one backward node: x [B, T, H, D]
+// normalised over D per head (QK-Norm) and rotated, in one pass when D is 64
+// or 128 (bitwise the two ops), by the two ops otherwise.  Added in this
+// build; the reference runs RMSNorm::forward and then rope.
+Tensor qk_norm_rope(const Tensor& x, const Tensor& weight, float eps, int position_start,
+                    float theta, const RopeScaling& scaling = {});
+
 }  // namespace ctd::ops

@@ -183,6 +183,24 @@ int ember_rope_freqs_host(float* freqs_out, int D, float theta, float factor,
 int ember_rope(const float* x, float* y, int64_t B, int64_t T, int64_t H, int64_t D,
                int64_t pos0, const float* freqs_host, float sign, ember_stream_t s);
 
+/* Per-head QK-Norm followed by RoPE in one pass: y = R(angle) (x * rstd * w)
+ * over rows = B*T*heads rows of D floats (row (b*T + t)*heads + h, position
+ * pos0 + t), bitwise ember_rmsnorm_fwd then ember_rope (sign 1); rstd[rows]
+ * may be NULL.  The backward is bitwise ember_rope (sign -1) then
+ * ember_rmsnorm_bwd: dx and dw (either may be NULL; dw through the workspace
+ * that ember_rmsnorm_bwd_workspace_bytes(rows, D) sizes).  D = 64 or 128,
+ * 16-byte aligned rows, freqs_host as for ember_rope.  Replaces the
+ * q_norm / k_norm then rope pair of Attention::forward_train and forward
+ * (include/ctd/nn/attention.h:115-121 and 58-64 of the reference; norm.cu:17-49,
+ * rope.cu:17-56) and the two backward nodes. */
+int ember_qknorm_rope_fwd(const float* x, const float* w, float* y, float* rstd, int64_t rows,
+                          int64_t heads, int64_t T, int64_t D, float eps, int64_t pos0,
+                          const float* freqs_host, ember_stream_t s);
+int ember_qknorm_rope_bwd(const float* dy, const float* x, const float* w, const float* rstd,
+                          float* dx, float* dw, int64_t rows, int64_t heads, int64_t T,
+                          int64_t D, float eps, int64_t pos0, const float* freqs_host,
+                          void* workspace, size_t workspace_bytes, ember_stream_t s);
+
 /* --------------------------------------------------------- elementwise
  * Replace src/ops/elementwise.cu:15-69, repeat_kv.cu:45-51 and
  * autograd.cu:88-93 (addinto). */

@@ -256,6 +256,56 @@ def test_rope_roundtrip_identity():
     assert (z - x).abs().max().item() < 1e-5
 
 
+@pytest.mark.parametrize("B,T,H,D,theta,factor,pos0", [
+    (2, 64, 16, 128, 1e6, 0.0, 0),      # Qwen3 q heads
+    (1, 37, 8, 128, 1e6, 0.0, 5),       # k heads, ragged row count, offset positions
+    (2, 50, 3, 64, 5e5, 32.0, 0),       # D = 64 with llama3 frequencies
+    (1, 4096, 2, 128, 1e6, 0.0, 0),     # full T: large angles
+])
+def test_qknorm_rope_bitwise_equals_norm_then_rope(B, T, H, D, theta, factor, pos0):
+    """The fused QK-Norm + RoPE kernels against ember_rmsnorm_* and ember_rope
+    run one after the other (each pinned against the oracle above): forward
+    y and rstd, backward dx and dw, bit for bit."""
+    r = rng(B * T * H + D)
+    rows, eps = B * T * H, 1e-6
+    x = r.standard_normal((B, T, H, D)).astype(np.float32)
+    w = (1.0 + 0.1 * r.standard_normal(D)).astype(np.float32)
+    dy = r.standard_normal((B, T, H, D)).astype(np.float32)
+    X, W, DY = dev(x), dev(w), dev(dy)
+    fr = freqs(D, theta, factor)
+    # separate kernels
+    Yn, RS, Yr = empty((B, T, H, D)), empty((rows,)), empty((B, T, H, D))
+    call("ember_rmsnorm_fwd", p(X), p(W), p(Yn), p(RS), rows, D, eps, None)
+    call("ember_rope", p(Yn), p(Yr), B, T, H, D, pos0, fr, 1.0, None)
+    G, DX, DW = empty((B, T, H, D)), empty((B, T, H, D)), empty((D,))
+    ws_n = int(capi.lib().ember_rmsnorm_bwd_workspace_bytes(rows, D))
+    WS = empty((max(ws_n // 4, 1),))
+    call("ember_rope", p(DY), p(G), B, T, H, D, pos0, fr, -1.0, None)
+    call("ember_rmsnorm_bwd", p(G), p(X), p(W), p(RS), p(DX), p(DW), rows, D, eps, p(WS), ws_n,
+         None)
+    # fused
+    Y, RS2, DX2, DW2 = empty((B, T, H, D)), empty((rows,)), empty((B, T, H, D)), empty((D,))
+    call("ember_qknorm_rope_fwd", p(X), p(W), p(Y), p(RS2), rows, H, T, D, eps, pos0, fr, None)
+    call("ember_qknorm_rope_bwd", p(DY), p(X), p(W), p(RS2), p(DX2), p(DW2), rows, H, T, D, eps,
+         pos0, fr, p(WS), ws_n, None)
+    assert torch.equal(Y, Yr) and torch.equal(RS2, RS)
+    assert torch.equal(DX2, DX) and torch.equal(DW2, DW)
+    # dx alone, no rstd (recomputed), as the separate kernels do it
+    DX3 = empty((B, T, H, D))
+    call("ember_qknorm_rope_bwd", p(DY), p(X), p(W), None, p(DX3), None, rows, H, T, D, eps,
+         pos0, fr, None, 0, None)
+    call("ember_rmsnorm_bwd", p(G), p(X), p(W), None, p(DX), None, rows, D, eps, None, 0, None)
+    assert torch.equal(DX3, DX)
+
+
+def test_qknorm_rope_rejects_other_head_dims():
+    X = empty((4, 96))
+    fr = freqs(96, 1e6)
+    with pytest.raises(capi.EmberError):
+        capi.call("ember_qknorm_rope_fwd", p(X), p(X[0]), p(X), None, 4, 2, 2, 96, 1e-6, 0, fr,
+                  None)
+
+
 # ----------------------------------------------------------- elementwise
 def test_elementwise_vs_oracle():
     r = rng(5)
