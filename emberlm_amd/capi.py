@@ -58,6 +58,7 @@ SIGNATURES = {
                                     sz, vp]),
     "ember_rmsnorm_bwd_workspace_bytes": (sz, [i64, i64]),
     "ember_rmsnorm_bwd": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, f32, vp, sz, vp]),
+    "ember_rmsnorm_bwd_accumulate": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, f32, vp, sz, vp]),
     "ember_rmsnorm_bwd_noalloc": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, f32, vp]),
     "ember_rope_freqs_host": (i32, [C.POINTER(f32), i32, f32, f32, f32, f32, i32]),
     "ember_rope": (i32, [vp, vp, i64, i64, i64, i64, i64, C.POINTER(f32), f32, vp]),

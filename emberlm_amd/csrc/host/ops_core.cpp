@@ -84,7 +84,7 @@ struct MatmulBackward : autograd::Node {
   }
   // dA goes straight into a partial sum the engine already holds for a
   // (another consumer's gradient), by a beta = 1 GEMM: the fan-in add of
-  // src/core/autograd.cu's accumulate step done where dA is stored.
+  // src/core/autograd.cu:86-118 done where dA is stored.
   bool accepts_partials() const override { return true; }
   std::vector<Tensor> backward_with_partials(const std::vector<Tensor>& go,
                                              const std::vector<Tensor>& partials) override {
@@ -234,17 +234,20 @@ void check_norm(const Tensor& x, const Tensor& w) {
   require(w.dim() == 1 && w.shape()[0] == x.shape().back(), "rms_norm: weight shape mismatch");
 }
 
+// dx and dw; with `into`, dx is added into that tensor (which is returned).
 std::pair<Tensor, Tensor> rms_bwd(const Tensor& dy, const Tensor& x, const Tensor& w,
-                                  const Tensor* rstd, float eps, bool need_dx, bool need_dw) {
+                                  const Tensor* rstd, float eps, bool need_dx, bool need_dw,
+                                  const Tensor* into = nullptr) {
   const int64_t H = x.shape().back();
   const int64_t rows = x.numel() / H;
-  Tensor dx = need_dx ? empty_like(x) : Tensor{};
+  Tensor dx = into ? *into : need_dx ? empty_like(x) : Tensor{};
   Tensor dw = need_dw ? empty_like(w) : Tensor{};
   const size_t wsb = need_dw ? ember_rmsnorm_bwd_workspace_bytes(rows, H) : 0;
   Tensor ws = wsb ? workspace(wsb) : Tensor{};
-  CTD_CHECK(ember_rmsnorm_bwd(cfp(dy), cfp(x), cfp(w), rstd ? cfp(*rstd) : nullptr,
-                              need_dx ? fp(dx) : nullptr, need_dw ? fp(dw) : nullptr, rows, H, eps,
-                              wsb ? ws.data_ptr() : nullptr, wsb, S()));
+  auto fn = into ? ember_rmsnorm_bwd_accumulate : ember_rmsnorm_bwd;
+  CTD_CHECK(fn(cfp(dy), cfp(x), cfp(w), rstd ? cfp(*rstd) : nullptr,
+               dx.storage() ? fp(dx) : nullptr, need_dw ? fp(dw) : nullptr, rows, H, eps,
+               wsb ? ws.data_ptr() : nullptr, wsb, S()));
   return {dx, dw};
 }
 
@@ -253,10 +256,22 @@ struct RmsNormBackward : autograd::Node {
   float eps = 1e-5f;
   const char* name() const override { return "RmsNormBackward"; }
   std::vector<Tensor> backward(const std::vector<Tensor>& go) override {
+    return backward_with_partials(go, {});
+  }
+  // dx goes straight into the running sum the engine already holds for x
+  // (the residual stream's other gradient), as MatmulBackward does for dA.
+  bool accepts_partials() const override { return true; }
+  std::vector<Tensor> backward_with_partials(const std::vector<Tensor>& go,
+                                             const std::vector<Tensor>& partials) override {
     autograd::NoGradGuard ng;
     check_f32(go.at(0), "rms_norm backward", "grad");
-    auto r = rms_bwd(go[0], x, w, &rstd, eps, next_edges.at(0).node != nullptr,
-                     next_edges.at(1).node != nullptr);
+    const bool need_dx = next_edges.at(0).node != nullptr;
+    const Tensor* into = partials.empty() ? nullptr : &partials[0];
+    const bool fold = need_dx && into && into->storage() && into->dtype() == DType::kFloat32 &&
+                      into->device() == x.device() && into->is_contiguous() &&
+                      into->shape() == x.shape();
+    auto r = rms_bwd(go[0], x, w, &rstd, eps, need_dx, next_edges.at(1).node != nullptr,
+                     fold ? into : nullptr);
     release_saved(x, w, rstd);
     return {r.first, r.second};
   }

@@ -154,7 +154,7 @@ template <int LPR, int MAXC>
 __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
     const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ w,
     const float* __restrict__ rstd, float* __restrict__ dx, float* __restrict__ dw_part,
-    int64_t rows, int64_t H, float eps) {
+    int64_t rows, int64_t H, float eps, bool acc_dx) {
   constexpr int RPB = kThreads / LPR;
   extern __shared__ __attribute__((aligned(16))) float red[];  // [RPB][H]
   const int slot = threadIdx.x / LPR;
@@ -211,7 +211,15 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
           o[e] = bwd_dx(s, g[e], ww[e], v[e], k);
           acc[j][e] = bwd_dw_term(acc[j][e], g[e], v[e], s);
         }
-        if (dx) reinterpret_cast<f32x4*>(dx + row * H)[ci] = o;
+        if (dx) {
+          f32x4* dst = reinterpret_cast<f32x4*>(dx + row * H) + ci;
+          if (acc_dx) {  // dx += this gradient (one add, as ember_accumulate)
+            const f32x4 old = *dst;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = old[e] + o[e];
+          }
+          *dst = o;
+        }
       }
     }
   }
@@ -234,7 +242,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
 __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_scalar(
     const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ w,
     const float* __restrict__ rstd, float* __restrict__ dx, float* __restrict__ dw_part,
-    int64_t rows, int64_t H, float eps) {
+    int64_t rows, int64_t H, float eps, bool acc_dx) {
   __shared__ float red[kThreads / kWave];
   const float invH = 1.0f / static_cast<float>(H);
   for (int64_t col0 = 0; col0 < H; col0 += kThreads) {
@@ -253,7 +261,10 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_scalar(
     c = block_sum(c, red);
     const float s = rstd ? rstd[row] : 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
     for (int64_t i = threadIdx.x; i < H; i += kThreads) {
-      if (dx) dx[row * H + i] = s * (gr[i] * w[i] - xr[i] * s * s * c * invH);
+      if (dx) {
+        const float d = s * (gr[i] * w[i] - xr[i] * s * s * c * invH);
+        dx[row * H + i] = acc_dx ? dx[row * H + i] + d : d;
+      }
       if (dw_part) dw_part[blockIdx.x * H + i] += gr[i] * xr[i] * s;
     }
   }
@@ -483,14 +494,15 @@ int64_t bwd_blocks(int64_t rows, int64_t H, bool vec) {
 
 template <int LPR>
 int launch_bwd_lpr(int64_t nb, const float* dy, const float* x, const float* w, const float* rstd,
-                   float* dx, float* part, int64_t rows, int64_t H, float eps, hipStream_t st) {
+                   float* dx, float* part, int64_t rows, int64_t H, float eps, bool acc_dx,
+                   hipStream_t st) {
   const int64_t chunks = (H / 4 + LPR - 1) / LPR;
   const size_t lds = static_cast<size_t>(kThreads / LPR) * H * sizeof(float);
   if (lds > 64 * 1024) return EMBER_EINVAL;
 #define EMBER_BWD_CASE(MC)                                                                     \
   if (chunks <= MC) {                                                                          \
     rmsnorm_bwd_vec<LPR, MC><<<static_cast<unsigned>(nb), kThreads, part ? lds : 0, st>>>(     \
-        dy, x, w, rstd, dx, part, rows, H, eps);                                               \
+        dy, x, w, rstd, dx, part, rows, H, eps, acc_dx);                                       \
     return launch_status();                                                                    \
   }
   EMBER_BWD_CASE(1)
@@ -595,10 +607,11 @@ extern "C" size_t ember_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t H) {
   return static_cast<size_t>(bwd_blocks(rows, H, vec)) * H * sizeof(float);
 }
 
-extern "C" int ember_rmsnorm_bwd(const float* dy, const float* x, const float* w,
-                                 const float* rstd, float* dx, float* dw, int64_t rows, int64_t H,
-                                 float eps, void* workspace, size_t workspace_bytes,
-                                 ember_stream_t s) {
+namespace {
+
+int rmsnorm_bwd_run(const float* dy, const float* x, const float* w, const float* rstd, float* dx,
+                    float* dw, int64_t rows, int64_t H, float eps, bool acc_dx, void* workspace,
+                    size_t workspace_bytes, ember_stream_t s) {
   if (rows < 0 || H <= 0 || !w) return EMBER_EINVAL;
   if (rows > 0 && (!dy || !x)) return EMBER_EINVAL;
   hipStream_t st = as_stream(s);
@@ -617,24 +630,46 @@ extern "C" int ember_rmsnorm_bwd(const float* dy, const float* x, const float* w
   }
   int rc;
   if (vec) {
+    int (*fn)(int64_t, const float*, const float*, const float*, const float*, float*, float*,
+              int64_t, int64_t, float, bool, hipStream_t);
     switch (lanes_per_row(H)) {
-      case 1: rc = launch_bwd_lpr<1>(nb, dy, x, w, rstd, dx, part, rows, H, eps, st); break;
-      case 2: rc = launch_bwd_lpr<2>(nb, dy, x, w, rstd, dx, part, rows, H, eps, st); break;
-      case 4: rc = launch_bwd_lpr<4>(nb, dy, x, w, rstd, dx, part, rows, H, eps, st); break;
-      case 8: rc = launch_bwd_lpr<8>(nb, dy, x, w, rstd, dx, part, rows, H, eps, st); break;
-      case 16: rc = launch_bwd_lpr<16>(nb, dy, x, w, rstd, dx, part, rows, H, eps, st); break;
-      case 32: rc = launch_bwd_lpr<32>(nb, dy, x, w, rstd, dx, part, rows, H, eps, st); break;
-      default: rc = launch_bwd_lpr<64>(nb, dy, x, w, rstd, dx, part, rows, H, eps, st); break;
+      case 1: fn = launch_bwd_lpr<1>; break;
+      case 2: fn = launch_bwd_lpr<2>; break;
+      case 4: fn = launch_bwd_lpr<4>; break;
+      case 8: fn = launch_bwd_lpr<8>; break;
+      case 16: fn = launch_bwd_lpr<16>; break;
+      case 32: fn = launch_bwd_lpr<32>; break;
+      default: fn = launch_bwd_lpr<64>; break;
     }
+    rc = fn(nb, dy, x, w, rstd, dx, part, rows, H, eps, acc_dx, st);
   } else {
     rmsnorm_bwd_scalar<<<static_cast<unsigned>(nb), kThreads, 0, st>>>(dy, x, w, rstd, dx, part,
-                                                                       rows, H, eps);
+                                                                       rows, H, eps, acc_dx);
     rc = launch_status();
   }
   if (rc || !dw) return rc;
   column_sum<<<static_cast<unsigned>((H + kWave - 1) / kWave), kColThreads, 0, st>>>(part, dw, nb,
                                                                                   H);
   return launch_status();
+}
+
+}  // namespace
+
+extern "C" int ember_rmsnorm_bwd(const float* dy, const float* x, const float* w,
+                                 const float* rstd, float* dx, float* dw, int64_t rows, int64_t H,
+                                 float eps, void* workspace, size_t workspace_bytes,
+                                 ember_stream_t s) {
+  return rmsnorm_bwd_run(dy, x, w, rstd, dx, dw, rows, H, eps, false, workspace, workspace_bytes,
+                         s);
+}
+
+extern "C" int ember_rmsnorm_bwd_accumulate(const float* dy, const float* x, const float* w,
+                                            const float* rstd, float* dx, float* dw,
+                                            int64_t rows, int64_t H, float eps, void* workspace,
+                                            size_t workspace_bytes, ember_stream_t s) {
+  if (!dx) return EMBER_EINVAL;
+  return rmsnorm_bwd_run(dy, x, w, rstd, dx, dw, rows, H, eps, true, workspace, workspace_bytes,
+                         s);
 }
 
 namespace {
@@ -717,7 +752,8 @@ extern "C" int ember_rmsnorm_bwd_noalloc(const float* dy, const float* x, const 
   if (rows < 0 || H <= 0 || !w) return EMBER_EINVAL;
   if (rows > 0 && (!dy || !x)) return EMBER_EINVAL;
   const size_t need = ember_rmsnorm_bwd_workspace_bytes(rows, H);
-  if (!dw || need == 0) return ember_rmsnorm_bwd(dy, x, w, rstd, dx, dw, rows, H, eps, nullptr, 0, s);
+  if (!dw || need == 0)
+    return ember_rmsnorm_bwd(dy, x, w, rstd, dx, dw, rows, H, eps, nullptr, 0, s);
   if (need > EMBER_RMSNORM_BWD_SCRATCH_BYTES) return EMBER_ESCRATCH;
   float* ws = nullptr;
   const int rc = scratch_on_current_device(as_stream(s), &ws);

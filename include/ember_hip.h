@@ -154,6 +154,15 @@ size_t ember_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t H);
 int ember_rmsnorm_bwd(const float* dy, const float* x, const float* w, const float* rstd,
                       float* dx, float* dw, int64_t rows, int64_t H, float eps, void* workspace,
                       size_t workspace_bytes, ember_stream_t s);
+/* ember_rmsnorm_bwd with dx accumulated: dx += the input gradient (dx must
+ * hold the running sum; one add per element, as ember_accumulate after
+ * ember_rmsnorm_bwd, so the same bits).  For an input whose other consumers'
+ * gradients already sit in dx, e.g. the residual stream of a block (the
+ * reference's autograd adds them in its fan-in, src/core/autograd.cu:86-118). */
+int ember_rmsnorm_bwd_accumulate(const float* dy, const float* x, const float* w,
+                                 const float* rstd, float* dx, float* dw, int64_t rows, int64_t H,
+                                 float eps, void* workspace, size_t workspace_bytes,
+                                 ember_stream_t s);
 /* ember_rmsnorm_bwd with no workspace argument and no allocation of any kind,
  * for callers that cannot allocate device memory: code under HIP graph
  * capture, serving loops and harnesses that forbid hipMalloc.  No counterpart

@@ -612,6 +612,24 @@ void fan_in_fold_matches_separate_adds() {
     check(folded == separate, "fan-in folded into the GEMM is bitwise the separate adds, O = " +
                                   std::to_string(O));
   }
+  // The residual stream: an RMSNorm's dx added into x's running sum.
+  for (int64_t H : {128, 2048, 130}) {
+    const int64_t N = 77;
+    Tensor x0 = rand_tensor({N, H}, rng, 1.0f, false);
+    Tensor w = rand_tensor({H}, rng, 0.1f, false);
+    Tensor dy = rand_tensor({N, H}, rng, 1.0f, false);
+    auto run_once = [&](bool shared) {
+      Tensor x = x0.detach();
+      x.requires_grad_(true);
+      Tensor xn = shared ? x : x.reshape({N, H});
+      Tensor y = ops::add(ops::rms_norm(xn, w, 1e-6f), x);
+      y.backward(dy);
+      return host(x.grad());
+    };
+    const std::vector<float> folded = run_once(true), separate = run_once(false);
+    check(folded == separate, "RMSNorm dx folded into the running sum is bitwise the separate "
+                              "add, H = " + std::to_string(H));
+  }
 }
 
 }  // namespace

@@ -220,6 +220,27 @@ def test_rmsnorm_full_size_c5():
     assert ((y - ref).abs().max() / ref.abs().max()).item() < 1e-5
 
 
+@pytest.mark.parametrize("rows,H", [(300, 2048), (1000, 128), (77, 576), (50, 130)])
+def test_rmsnorm_bwd_accumulate_bitwise(rows, H):
+    """dx += the input gradient: bitwise ember_rmsnorm_bwd followed by one add
+    per element (the float4 paths at 2048, 128 and 576, the scalar one at 130)."""
+    r = rng(rows + H)
+    x = r.standard_normal((rows, H)).astype(np.float32)
+    w = (1.0 + 0.1 * r.standard_normal(H)).astype(np.float32)
+    dy = r.standard_normal((rows, H)).astype(np.float32)
+    d0 = r.standard_normal((rows, H)).astype(np.float32)
+    X, W, DY, D0 = dev(x), dev(w), dev(dy), dev(d0)
+    ws_n = int(capi.lib().ember_rmsnorm_bwd_workspace_bytes(rows, H))
+    WS = empty((max(ws_n // 4, 1),))
+    DX, DW, DW2 = empty((rows, H)), empty((H,)), empty((H,))
+    call("ember_rmsnorm_bwd", p(DY), p(X), p(W), None, p(DX), p(DW), rows, H, 1e-6, p(WS), ws_n,
+         None)
+    ACC = D0.clone()
+    call("ember_rmsnorm_bwd_accumulate", p(DY), p(X), p(W), None, p(ACC), p(DW2), rows, H, 1e-6,
+         p(WS), ws_n, None)
+    assert torch.equal(ACC, D0 + DX) and torch.equal(DW2, DW)
+
+
 # ----------------------------------------------------------------- RoPE
 def freqs(D, theta, factor=0.0):
     out = (C.c_float * (D // 2))()
