@@ -150,11 +150,12 @@ __device__ __forceinline__ float bwd_dw_term(float acc, float g, float x, float 
 
 // Backward, float4 path.  Block b handles rows b*RPB + slot + k*grid*RPB.
 // MAXC = float4 chunks per lane (H/4/LPR rounded up) kept as dw partials.
-template <int LPR, int MAXC>
+// ACC: dx += the gradient (dx holds a running sum, read with the row).
+template <int LPR, int MAXC, bool ACC>
 __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
     const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ w,
     const float* __restrict__ rstd, float* __restrict__ dx, float* __restrict__ dw_part,
-    int64_t rows, int64_t H, float eps, bool acc_dx) {
+    int64_t rows, int64_t H, float eps) {
   constexpr int RPB = kThreads / LPR;
   extern __shared__ __attribute__((aligned(16))) float red[];  // [RPB][H]
   const int slot = threadIdx.x / LPR;
@@ -173,7 +174,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
     const f32x4* xr = reinterpret_cast<const f32x4*>(x + (live ? row : 0) * H);
     const f32x4* gr = reinterpret_cast<const f32x4*>(dy + (live ? row : 0) * H);
     // The row's x and dy chunks stay in registers for the dx pass below.
-    f32x4 xv[MAXC], gv[MAXC];
+    f32x4 xv[MAXC], gv[MAXC], ov[ACC ? MAXC : 1];  // ov: dx's running sum (ACC)
     float ss = 0.f, c = 0.f;
     if (live) {
 #pragma unroll
@@ -181,6 +182,14 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
         const int64_t ci = sub + static_cast<int64_t>(j) * LPR;
         xv[j] = ci < nc ? xr[ci] : f32x4{0.f, 0.f, 0.f, 0.f};
         gv[j] = ci < nc ? gr[ci] : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+      if constexpr (ACC) {  // loaded with the row, not behind the sums below
+#pragma unroll
+        for (int j = 0; j < MAXC; ++j) {
+          const int64_t ci = sub + static_cast<int64_t>(j) * LPR;
+          ov[j] = ci < nc ? reinterpret_cast<const f32x4*>(dx + row * H)[ci]
+                          : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
       }
 #pragma unroll
       for (int j = 0; j < MAXC; ++j) {
@@ -212,13 +221,11 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
           acc[j][e] = bwd_dw_term(acc[j][e], g[e], v[e], s);
         }
         if (dx) {
-          f32x4* dst = reinterpret_cast<f32x4*>(dx + row * H) + ci;
-          if (acc_dx) {  // dx += this gradient (one add, as ember_accumulate)
-            const f32x4 old = *dst;
+          if constexpr (ACC) {  // dx += this gradient (one add, as ember_accumulate)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = old[e] + o[e];
+            for (int e = 0; e < 4; ++e) o[e] = ov[j][e] + o[e];
           }
-          *dst = o;
+          reinterpret_cast<f32x4*>(dx + row * H)[ci] = o;
         }
       }
     }
@@ -501,8 +508,9 @@ int launch_bwd_lpr(int64_t nb, const float* dy, const float* x, const float* w, 
   if (lds > 64 * 1024) return EMBER_EINVAL;
 #define EMBER_BWD_CASE(MC)                                                                     \
   if (chunks <= MC) {                                                                          \
-    rmsnorm_bwd_vec<LPR, MC><<<static_cast<unsigned>(nb), kThreads, part ? lds : 0, st>>>(     \
-        dy, x, w, rstd, dx, part, rows, H, eps, acc_dx);                                       \
+    auto kern = acc_dx ? rmsnorm_bwd_vec<LPR, MC, true> : rmsnorm_bwd_vec<LPR, MC, false>;     \
+    kern<<<static_cast<unsigned>(nb), kThreads, part ? lds : 0, st>>>(dy, x, w, rstd, dx, part, \
+                                                                     rows, H, eps);            \
     return launch_status();                                                                    \
   }
   EMBER_BWD_CASE(1)
