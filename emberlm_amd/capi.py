@@ -52,8 +52,6 @@ SIGNATURES = {
                                  vp, i64, i32, vp, sz, vp]),
     "ember_gemm_f32_add": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, vp, i64, vp,
                                  i64, vp, sz, vp]),
-    "ember_gemm_f32_swiglu": (i32, [i32, i32, i64, i64, i64, vp, i64, vp, i64, vp, i64, vp, i64,
-                                    vp, i64, vp, sz, vp]),
     "ember_rmsnorm_fwd": (i32, [vp, vp, vp, vp, i64, i64, f32, vp]),
     "ember_qknorm_rope_fwd": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, f32, i64, vp, vp]),
     "ember_qknorm_rope_bwd": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, f32, i64, vp, vp,

@@ -599,33 +599,6 @@ Tensor swiglu(const Tensor& g, const Tensor& u) {
   return h;
 }
 
-Tensor matmul_swiglu(const Tensor& a, const Tensor& b, bool transa, bool transb, const Tensor& g) {
-  const MM dm = mm_dims(a, b, transa, transb, "matmul_swiglu");
-  check_f32(g, "matmul_swiglu", "g");
-  require(g.device() == a.device() && g.dim() == 2 && g.shape()[0] == dm.M &&
-              g.shape()[1] == dm.N,
-          "matmul_swiglu: g must be a contiguous [M, N] tensor on the operands' device");
-  const bool grad = autograd::any_requires_grad({a, b, g});
-  Tensor h = Tensor::empty({dm.M, dm.N}, DType::kFloat32, a.device());
-  Tensor u = grad ? Tensor::empty({dm.M, dm.N}, DType::kFloat32, a.device()) : Tensor{};
-  const size_t wsb = ember_gemm_f32_workspace_bytes(dm.M, dm.N, dm.K, 1);
-  Tensor ws = wsb ? workspace(wsb) : Tensor{};
-  void* ev = runtime::gemm_profile_begin();
-  CTD_CHECK(ember_gemm_f32_swiglu(transa, transb, dm.M, dm.N, dm.K, cfp(a), dm.lda, cfp(b),
-                                  dm.ldb, cfp(g), dm.N, fp(h), dm.N, grad ? fp(u) : nullptr, dm.N,
-                                  wsb ? ws.data_ptr() : nullptr, wsb, S()));
-  runtime::gemm_profile_end(ev, 2.0 * dm.M * dm.N * dm.K, 2 * transa + transb);
-  if (!grad) return h;
-  // The graph of swiglu(g, matmul(a, b)) over the fused values.
-  Tensor ut = matmul_graph_only(a, b, transa, transb, u);
-  auto node = std::make_shared<SwigluBackward>();
-  node->g = g.detach();
-  node->u = ut.detach();
-  node->next_edges = autograd::collect_next_edges({g, ut});
-  autograd::set_history(h, std::move(node));
-  return h;
-}
-
 // =============================================================== attention
 namespace {
 

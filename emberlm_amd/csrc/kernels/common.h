@@ -28,11 +28,6 @@ inline unsigned grid_1d(int64_t n, int threads, int64_t cap = 1 << 20) {
   return static_cast<unsigned>(g);
 }
 
-// Logistic sigmoid with the accurate expf (the reference's backward form,
-// elementwise.cu); shared so that every kernel computing SwiGLU gives the
-// same bits.
-__device__ __forceinline__ float sigmoidf_acc(float v) { return 1.0f / (1.0f + expf(-v)); }
-
 // Full-wave (64-lane) reductions through DPP-free shuffles.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

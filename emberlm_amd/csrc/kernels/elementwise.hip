@@ -14,6 +14,8 @@ namespace {
 
 constexpr int kThreads = 256;
 
+__device__ __forceinline__ float sigmoidf_acc(float v) { return 1.0f / (1.0f + expf(-v)); }
+
 enum class Op { kAdd, kSub, kMul, kScale, kAccum, kSilu, kSiluBwd, kSwigluFwd };
 
 template <Op OP>

@@ -62,34 +62,12 @@ struct GemmArgs {
   // D = C when null.  D may be C itself (ldd = ldc), never a shifted overlap.
   const float* D = nullptr;
   int64_t ldd = 0;
-  // Epilogue form (single GEMMs only): kEpiStore as above; kEpiSwiglu:
-  // C = silu(D) * v with v = alpha op(A) op(B) and D the gate values (SwiGLU
-  // of the gate and this product), and E = v when E is set.
-  int epi = 0;
-  float* E = nullptr;
-  int64_t lde = 0;
 };
-
-enum : int { kEpiStore = 0, kEpiSwiglu = 1 };
 
 // The beta term's source for element (row, col) of the current C.
 __device__ __forceinline__ const float* addend(const GemmArgs& a, const float* dst, int64_t row,
                                                int64_t col) {
   return a.D ? a.D + row * a.ldd + col : dst;
-}
-
-// Stores element (row, col) of C (the current batch's), v = alpha * product.
-// The SwiGLU form is the arithmetic of ember_swiglu_fwd, element for element.
-__device__ __forceinline__ void epi_store(const GemmArgs& a, float* C, int64_t row, int64_t col,
-                                          float v) {
-  float* dst = C + row * a.ldc + col;
-  if (a.epi == kEpiSwiglu) {
-    const float gv = a.D[row * a.ldd + col];
-    if (a.E) a.E[row * a.lde + col] = v;
-    *dst = gv * sigmoidf_acc(gv) * v;
-  } else {
-    *dst = (a.beta != 0.f) ? v + a.beta * *addend(a, dst, row, col) : v;
-  }
 }
 
 __device__ __forceinline__ int64_t dyn_extent(const GemmArgs& a, int64_t full) {
@@ -329,7 +307,11 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_mfma(GemmArgs a) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int64_t row = m0 + wm * (BM / 2) + i * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
-        if (row < a.M) epi_store(a, C, row, col, a.alpha * acc[i][j][e]);
+        if (row < a.M) {
+          float* dst = C + row * a.ldc + col;
+          const float v = a.alpha * acc[i][j][e];
+          *dst = (a.beta != 0.f) ? v + a.beta * *addend(a, dst, row, col) : v;
+        }
       }
     }
 }
@@ -596,22 +578,24 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_dma(GemmArgs a) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int64_t row = m0 + wm * (BM / 2) + i * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
-        if (row < a.M) epi_store(a, C, row, col, a.alpha * acc[i][j][e]);
+        if (row < a.M) {
+          float* dst = C + row * a.ldc + col;
+          const float v = a.alpha * acc[i][j][e];
+          *dst = (a.beta != 0.f) ? v + a.beta * *addend(a, dst, row, col) : v;
+        }
       }
     }
 }
 
 // C = alpha * sum_{s<S} P[s] + beta * D (D = C when null), the split partials
-// summed in order; with epi = kEpiSwiglu, C = silu(D) * v and E = v for
-// v = alpha * sum (epi_store's forms).  P is [S][M][N] dense; four columns per
-// thread when the rows allow it.
+// summed in order.  P is [S][M][N] dense; four columns per thread when the
+// rows allow it.
 template <bool VEC>
 __global__ __launch_bounds__(kThreads) void splitk_reduce(const float* __restrict__ P, float* C,
                                                           int64_t M, int64_t N, int64_t ldc,
                                                           int S, float alpha, float beta,
                                                           const int64_t* dyn, int64_t dyn_base,
-                                                          const float* D, int64_t ldd, int epi,
-                                                          float* E, int64_t lde) {
+                                                          const float* D, int64_t ldd) {
   const int64_t per = VEC ? 4 : 1;
   const int64_t cols = N / per;
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
@@ -629,18 +613,6 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce(const float* __restric
     f32x4* dst = reinterpret_cast<f32x4*>(C + m * ldc + n);
     const f32x4* src = D ? reinterpret_cast<const f32x4*>(D + m * ldd + n) : dst;
     f32x4 out;
-    if (epi == kEpiSwiglu) {
-      const f32x4 gv = *src;
-      f32x4 v;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[e] = alpha * s[e];
-        out[e] = gv[e] * sigmoidf_acc(gv[e]) * v[e];
-      }
-      if (E) *reinterpret_cast<f32x4*>(E + m * lde + n) = v;
-      *dst = out;
-      return;
-    }
     const f32x4 old = beta != 0.f ? *src : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int e = 0; e < 4; ++e) out[e] = beta != 0.f ? alpha * s[e] + beta * old[e] : alpha * s[e];
@@ -650,12 +622,6 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce(const float* __restric
     for (int k = 1; k < S; ++k) s += P[k * plane + m * N + n];
     float* dst = C + m * ldc + n;
     const float* src = D ? D + m * ldd + n : dst;
-    if (epi == kEpiSwiglu) {
-      const float gv = *src, v = alpha * s;
-      if (E) E[m * lde + n] = v;
-      *dst = gv * sigmoidf_acc(gv) * v;
-      return;
-    }
     *dst = beta != 0.f ? alpha * s + beta * *src : alpha * s;
   }
 }
@@ -678,8 +644,7 @@ __global__ __launch_bounds__(kThreads) void gemm_skinny_nt(const float* __restri
                                                            int64_t ldb, float* C, int64_t ldc,
                                                            int M, int64_t N, int64_t K,
                                                            float alpha, float beta,
-                                                           const float* D, int64_t ldd, int epi,
-                                                           float* E, int64_t lde) {
+                                                           const float* D, int64_t ldd) {
   constexpr int NR = kSkinnyRows;
   __shared__ float red[kThreads / kWave][NR * MR];
   const int lane = threadIdx.x & (kWave - 1);
@@ -744,13 +709,7 @@ __global__ __launch_bounds__(kThreads) void gemm_skinny_nt(const float* __restri
       for (int q = 0; q < kThreads / kWave; ++q) s += red[q][idx];
       float* c = C + m * ldc + n;
       const float* src = D ? D + m * ldd + n : c;
-      if (epi == kEpiSwiglu) {  // epi_store's SwiGLU form
-        const float gv = *src, v = alpha * s;
-        if (E) E[m * lde + n] = v;
-        *c = gv * sigmoidf_acc(gv) * v;
-      } else {
-        *c = beta != 0.f ? alpha * s + beta * *src : alpha * s;
-      }
+      *c = beta != 0.f ? alpha * s + beta * *src : alpha * s;
     }
   }
 }
@@ -758,11 +717,10 @@ __global__ __launch_bounds__(kThreads) void gemm_skinny_nt(const float* __restri
 template <int MR>
 int launch_skinny(const float* A, int64_t lda, const float* B, int64_t ldb, float* C,
                   int64_t ldc, int64_t M, int64_t N, int64_t K, float alpha, float beta,
-                  const float* D, int64_t ldd, int epi, float* E, int64_t lde,
-                  hipStream_t st) {
+                  const float* D, int64_t ldd, hipStream_t st) {
   const unsigned grid = static_cast<unsigned>((N + kSkinnyRows - 1) / kSkinnyRows);
   gemm_skinny_nt<MR><<<grid, kThreads, 0, st>>>(A, lda, B, ldb, C, ldc, static_cast<int>(M), N,
-                                                 K, alpha, beta, D, ldd, epi, E, lde);
+                                                 K, alpha, beta, D, ldd);
   return launch_status();
 }
 
@@ -859,24 +817,12 @@ extern "C" size_t ember_gemm_f32_workspace_bytes(int64_t M, int64_t N, int64_t K
 
 namespace {
 
-// Two [M][ld] row-major regions of N columns are the same (same start and
-// row stride) or share no byte.
-bool same_or_apart(const float* p, int64_t ldp, const float* q, int64_t ldq, int64_t M,
-                   int64_t N) {
-  if (p == q) return ldp == ldq;
-  const auto p0 = reinterpret_cast<uintptr_t>(p), q0 = reinterpret_cast<uintptr_t>(q);
-  const uintptr_t p1 = p0 + static_cast<uintptr_t>((M - 1) * ldp + N) * sizeof(float);
-  const uintptr_t q1 = q0 + static_cast<uintptr_t>((M - 1) * ldq + N) * sizeof(float);
-  return !(p0 < q1 && q0 < p1);
-}
-
 // One GEMM call; `dyn` (may be null) is the device-side extent of GemmArgs.
 int gemm_run(int transa, int transb, int64_t M, int64_t N, int64_t K, float alpha,
              const float* A, int64_t lda, int64_t sA, const float* B, int64_t ldb, int64_t sB,
              float beta, float* C, int64_t ldc, int64_t sC, int64_t batch, void* workspace,
              size_t workspace_bytes, const int64_t* dyn, int64_t dyn_base, int dyn_dim,
-             const float* D, int64_t ldd, hipStream_t st, int epi = kEpiStore,
-             float* E = nullptr, int64_t lde = 0) {
+             const float* D, int64_t ldd, hipStream_t st) {
   int rc = EMBER_OK;
   GemmArgs a{A, B, C, M, N, K, lda, ldb, ldc, sA, sB, sC, 0, alpha, beta, 0, 0};
   a.dyn = dyn;
@@ -884,9 +830,6 @@ int gemm_run(int transa, int transb, int64_t M, int64_t N, int64_t K, float alph
   a.dyn_dim = dyn_dim;
   a.D = D;
   a.ldd = ldd;
-  a.epi = epi;
-  a.E = E;
-  a.lde = lde;
   const bool vec = aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0) &&
                    (batch == 1 || (sA % 4 == 0 && sB % 4 == 0));
   const bool a_kc = !transa, b_kc = transb != 0;
@@ -896,7 +839,7 @@ int gemm_run(int transa, int transb, int64_t M, int64_t N, int64_t K, float alph
                   : M == 2 ? launch_skinny<2>
                   : M <= 4 ? launch_skinny<4>
                            : launch_skinny<8>;
-    return skinny(A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, D, ldd, epi, E, lde, st);
+    return skinny(A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, D, ldd, st);
   }
   Plan p = make_plan(M, N, K, batch);
   if (p.splits > 1 &&
@@ -914,29 +857,24 @@ int gemm_run(int transa, int transb, int64_t M, int64_t N, int64_t K, float alph
     sp.kchunk = p.kchunk;
     sp.alpha = 1.f;
     sp.beta = 0.f;
-    sp.epi = kEpiStore;  // plain partials; the reduce applies the epilogue
-    sp.E = nullptr;
     const bool dma = vec && p.kchunk % 16 == 0 && K % 16 == 0 && (a_kc || M % 4 == 0) &&
                      (b_kc || N % 4 == 0);
     if ((rc = dma ? launch_dma<128, 128, 3>(sp, a_kc, b_kc, p.splits, st)
                   : launch_t<128, 128, 3>(sp, a_kc, b_kc, p.splits, vec, st)))
       return rc;
     const bool rvec = (N % 4 == 0) && (ldc % 4 == 0) && aligned16(C) &&
-                      (!D || (ldd % 4 == 0 && aligned16(D))) &&
-                      (!E || (lde % 4 == 0 && aligned16(E)));
+                      (!D || (ldd % 4 == 0 && aligned16(D)));
     const int64_t items = M * (rvec ? N / 4 : N);
     const unsigned blocks = static_cast<unsigned>(cdiv(items, kThreads));
     const int64_t* rdyn = dyn_dim == 0 ? dyn : nullptr;
     if (rvec)
       splitk_reduce<true><<<blocks, kThreads, 0, st>>>(static_cast<const float*>(workspace), C, M,
                                                        N, ldc, static_cast<int>(p.splits),
-                                                       alpha, beta, rdyn, dyn_base, D, ldd, epi,
-                                                       E, lde);
+                                                       alpha, beta, rdyn, dyn_base, D, ldd);
     else
       splitk_reduce<false><<<blocks, kThreads, 0, st>>>(static_cast<const float*>(workspace), C,
                                                         M, N, ldc, static_cast<int>(p.splits),
-                                                        alpha, beta, rdyn, dyn_base, D, ldd,
-                                                        epi, E, lde);
+                                                        alpha, beta, rdyn, dyn_base, D, ldd);
     return launch_status();
   }
   const bool dma = vec && K % 16 == 0 && (a_kc || M % 4 == 0) && (b_kc || N % 4 == 0) &&
@@ -968,26 +906,16 @@ extern "C" int ember_gemm_f32_add(int transa, int transb, int64_t M, int64_t N, 
   int rc = check_args(transa, transb, M, N, K, A, lda, B, ldb, C, ldc, 1);
   if (rc || M == 0 || N == 0) return rc;
   if (!D || ldd < N) return EMBER_EINVAL;
-  if (!same_or_apart(D, ldd, C, ldc, M, N)) return EMBER_EINVAL;
+  if (D != C) {  // D is C itself or lies wholly apart from it
+    const auto c0 = reinterpret_cast<uintptr_t>(C), d0 = reinterpret_cast<uintptr_t>(D);
+    const uintptr_t c1 = c0 + static_cast<uintptr_t>((M - 1) * ldc + N) * sizeof(float);
+    const uintptr_t d1 = d0 + static_cast<uintptr_t>((M - 1) * ldd + N) * sizeof(float);
+    if (d0 < c1 && c0 < d1) return EMBER_EINVAL;
+  } else if (ldd != ldc) {
+    return EMBER_EINVAL;
+  }
   return gemm_run(transa, transb, M, N, K, alpha, A, lda, 0, B, ldb, 0, 1.0f, C, ldc, 0, 1,
                   workspace, workspace_bytes, nullptr, 0, 0, D, ldd, as_stream(s));
-}
-
-extern "C" int ember_gemm_f32_swiglu(int transa, int transb, int64_t M, int64_t N, int64_t K,
-                                     const float* A, int64_t lda, const float* B, int64_t ldb,
-                                     const float* G, int64_t ldg, float* C, int64_t ldc, float* U,
-                                     int64_t ldu, void* workspace, size_t workspace_bytes,
-                                     ember_stream_t s) {
-  int rc = check_args(transa, transb, M, N, K, A, lda, B, ldb, C, ldc, 1);
-  if (rc || M == 0 || N == 0) return rc;
-  if (!G || ldg < N || (U && ldu < N)) return EMBER_EINVAL;
-  if (!same_or_apart(G, ldg, C, ldc, M, N) ||
-      (U && (!same_or_apart(U, ldu, C, ldc, M, N) || !same_or_apart(U, ldu, G, ldg, M, N) ||
-             U == C || U == G)))
-    return EMBER_EINVAL;
-  return gemm_run(transa, transb, M, N, K, 1.0f, A, lda, 0, B, ldb, 0, 0.0f, C, ldc, 0, 1,
-                  workspace, workspace_bytes, nullptr, 0, 0, G, ldg, as_stream(s), kEpiSwiglu,
-                  U, ldu);
 }
 
 extern "C" int ember_gemm_f32_dyn(int transa, int transb, int64_t M, int64_t N, int64_t K,

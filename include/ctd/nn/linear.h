@@ -27,16 +27,6 @@ struct Linear {
                   residual.shape());
   }
 
-  // swiglu(gate, forward(x)) as one GEMM whose store applies the activation
-  // (bitwise equal to the ops, same backward); gate has forward(x)'s shape.
-  Tensor forward_swiglu(const Tensor& x, const Tensor& gate) const {
-    const std::vector<int64_t> sh = out_shape(x);
-    if (gate.shape() != sh) throw std::runtime_error("Linear: gate shape mismatch");
-    Tensor x2 = rows(x);
-    Tensor g2 = gate.dim() == 2 ? gate : gate.reshape({x2.shape()[0], weight.shape()[0]});
-    return shaped(ops::matmul_swiglu(x2, weight, /*transa=*/false, /*transb=*/true, g2), sh);
-  }
-
   // forward(x)'s autograd graph without the product: the result is a view of
   // `values` (forward(x)'s elements).  See ops::matmul_graph_only.
   Tensor forward_graph_only(const Tensor& x, const Tensor& values) const {

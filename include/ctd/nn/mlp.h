@@ -24,11 +24,10 @@ struct MLP {
     return down_proj.forward_add(activation(x), residual);
   }
 
-  // silu(gate(x)) * up(x) as [tokens, intermediate], the SwiGLU applied by
-  // the up projection's GEMM as it stores (bitwise the separate ops).
+  // silu(gate(x)) * up(x) as [tokens, intermediate].
   Tensor activation(const Tensor& x) const {
     Tensor x2 = gate_proj.rows(x);
-    return up_proj.forward_swiglu(x2, gate_proj.forward(x2));
+    return ops::swiglu(gate_proj.forward(x2), up_proj.forward(x2));
   }
 };
 

@@ -22,13 +22,6 @@ Tensor matmul_graph_only(const Tensor& a, const Tensor& b, bool transa, bool tra
 // this build; the reference runs matmul and then ops::add.
 Tensor matmul_add(const Tensor& a, const Tensor& b, bool transa, bool transb, const Tensor& d);
 
-// swiglu(g, matmul(a, b, transa, transb)) in one GEMM (the activation done as
-// the product is stored, bitwise equal to the two ops), with both ops'
-// backward nodes (the product is kept for the SwiGLU backward only when a
-// gradient is needed).  g is [M, N] contiguous.  Added in this build; the
-// reference runs the up projection, silu and mul one by one.
-Tensor matmul_swiglu(const Tensor& a, const Tensor& b, bool transa, bool transb, const Tensor& g);
-
 // Batched matmul: a [B, Ma, Ka], b [B, Mb, Kb] -> [B, M, N].
 Tensor bmm(const Tensor& a, const Tensor& b, bool transa = false, bool transb = false);
 Tensor bmm_impl(const Tensor& a, const Tensor& b, bool transa, bool transb);

@@ -141,20 +141,6 @@ int ember_gemm_f32_add(int transa, int transb, int64_t M, int64_t N, int64_t K, 
                        int64_t ldd, float* C, int64_t ldc, void* workspace,
                        size_t workspace_bytes, ember_stream_t s);
 
-/* C = silu(G) * P and, when U is not NULL, U = P, for P = op(A) op(B) (batch
- * 1): the up projection and the SwiGLU of the gate G in one pass, the
- * activation computed where P is stored (the split-K reduce when K is split).
- * Element for element ember_swiglu_fwd(G, P) after the product, so the bits
- * are the same.  Replaces the up_proj matmul + silu + mul of MLP::forward
- * (include/ctd/nn/mlp.h:16-21 of the reference; src/ops/matmul.cpp:38-47,
- * src/ops/elementwise.cu:31-55).  G may be C itself (ldg == ldc); otherwise
- * G, C and U must not overlap (EMBER_EINVAL).  The workspace is
- * ember_gemm_f32_ws's. */
-int ember_gemm_f32_swiglu(int transa, int transb, int64_t M, int64_t N, int64_t K,
-                          const float* A, int64_t lda, const float* B, int64_t ldb,
-                          const float* G, int64_t ldg, float* C, int64_t ldc, float* U,
-                          int64_t ldu, void* workspace, size_t workspace_bytes, ember_stream_t s);
-
 /* -------------------------------------------------------------- RMSNorm
  * y = x * rsqrt(mean(x^2) + eps) * w over rows of length H; rstd[rows] (may be
  * NULL) receives rsqrt(mean(x^2)+eps).  Replaces rms_norm_kernel_f32

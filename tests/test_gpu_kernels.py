@@ -604,40 +604,6 @@ def test_gemm_add_bitwise_equals_product_then_add(ta, tb, M, N, K):
         assert_close(host(Cm), O.matmul(a, b, ta, tb) + d, name="gemm add")
 
 
-@pytest.mark.parametrize("ta,tb,M,N,K", [
-    (0, 1, 4096, 2048, 512),    # up projection shape: 256x128 DMA tiles
-    (0, 1, 300, 200, 64),       # 128x128 DMA tiles, ragged edges
-    (0, 0, 1000, 300, 48),      # NN
-    (1, 0, 256, 128, 8192),     # K split: the reduce applies the activation
-    (1, 1, 200, 150, 70),       # register-staged kernel
-    (0, 1, 5, 1000, 256),       # M <= 8: skinny kernel
-])
-def test_gemm_swiglu_bitwise_equals_product_then_swiglu(ta, tb, M, N, K):
-    """ember_gemm_f32_swiglu = the product stored, then ember_swiglu_fwd (each
-    pinned against the oracle elsewhere), bit for bit; the product itself in
-    U; the activation written over G in place."""
-    r = rng(2 * M + N + K)
-    a = r.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
-    b = (0.3 * r.standard_normal((N, K) if tb else (K, N))).astype(np.float32)
-    g = (2.0 * r.standard_normal((M, N))).astype(np.float32)
-    A, B, G = dev(a), dev(b), dev(g)
-    lda, ldb = a.shape[1], b.shape[1]
-    prod, ws, wsb = _gemm_ws(A, B, ta, tb, M, N, K, lda, ldb)
-    want = empty((M, N))
-    call("ember_swiglu_fwd", p(G), p(prod), p(want), M * N, None)
-    Cm, U = empty((M, N)), empty((M, N))
-    call("ember_gemm_f32_swiglu", int(ta), int(tb), M, N, K, p(A), lda, p(B), ldb, p(G), N,
-         p(Cm), N, p(U), N, p(ws), wsb, None)
-    assert torch.equal(Cm, want) and torch.equal(U, prod)
-    G2 = G.clone()               # in place over the gate, no product kept
-    call("ember_gemm_f32_swiglu", int(ta), int(tb), M, N, K, p(A), lda, p(B), ldb, p(G2), N,
-         p(G2), N, None, 0, p(ws), wsb, None)
-    assert torch.equal(G2, want)
-    with pytest.raises(capi.EmberError):   # U must not be C
-        capi.call("ember_gemm_f32_swiglu", int(ta), int(tb), M, N, K, p(A), lda, p(B), ldb,
-                  p(G), N, p(Cm), N, p(Cm), N, p(ws), wsb, None)
-
-
 def test_gemm_add_rejects_overlap_and_short_rows():
     A = empty((64, 32))
     buf = empty((65, 64))
