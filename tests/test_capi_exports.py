@@ -89,12 +89,14 @@ def test_gemm_split_plan_without_gpu():
     # chunks of >= 256, the others into chunks of >= 1024, aiming at 1536 tiles:
     # Qwen3-0.6B, 4096 tokens: q/o 128 tiles -> 12; k/v 64 -> 16; gate/up/down
     # 192 tiles -> min(8, 4096/1024) = 4.
-    # LLaMA-3.2-1B, 8192 tokens: q/o 256 tiles -> 6; k/v 64 -> 16;
-    # gate/up/down 1024 tiles -> 2.
+    # LLaMA-3.2-1B, 8192 tokens: q/o 256 tiles -> 128 of 256x128, 8 chunks (two
+    # whole waves); k/v 64 -> 16; gate/up/down 1024 tiles -> 512 of 256x128, 2.
+    # c5 (32768 tokens): q/o 128 of 256x128 -> 8; gate/up/down 384 -> 4.
     plans = [(2048, 1024, 4096, 12), (1024, 1024, 4096, 16), (1024, 2048, 4096, 12),
              (3072, 1024, 4096, 4), (1024, 3072, 4096, 4),
-             (2048, 2048, 8192, 6), (512, 2048, 8192, 16), (8192, 2048, 8192, 2),
-             (2048, 8192, 8192, 2)]
+             (2048, 2048, 8192, 8), (512, 2048, 8192, 16), (8192, 2048, 8192, 2),
+             (2048, 8192, 8192, 2), (2048, 2048, 32768, 8), (6144, 2048, 32768, 4),
+             (2048, 6144, 32768, 4)]
     for M, N, K, splits in plans:
         assert lib.ember_gemm_f32_workspace_bytes(M, N, K, 1) == splits * M * N * 4, (M, N, K)
     # enough tiles, or K too short to split: one pass over K

@@ -143,6 +143,51 @@ def test_gemm_split_k_vs_oracle(ta, tb, K):
     assert_close(one, ref, name="unsplit")
 
 
+@pytest.mark.parametrize("ta,tb,M,N,K", [
+    (1, 0, 2048, 2048, 32768),   # c5 q/o weight gradient: 8 splits on 256x128 tiles
+    (1, 0, 6144, 2048, 32768),   # gate/up: 4 splits
+    (0, 0, 4096, 2048, 8192),    # NN (the LM head's dh form): 4 splits
+])
+def test_gemm_split_k_on_256_tiles_vs_torch(ta, tb, M, N, K):
+    """The K split on 256x128 tiles against an fp64 product on the GPU, and
+    bitwise the same on a second call (fixed-order reduce)."""
+    g = torch.Generator(device="cuda").manual_seed(M + K)
+    a = torch.randn((K, M) if ta else (M, K), device="cuda", generator=g)
+    b = torch.randn((N, K) if tb else (K, N), device="cuda", generator=g)
+    wsb = int(capi.lib().ember_gemm_f32_workspace_bytes(M, N, K, 1))
+    assert wsb >= 4 * M * N * 4   # the split path
+    ws = empty((wsb // 4,))
+    out, out2 = empty((M, N)), empty((M, N))
+    for o in (out, out2):
+        call("ember_gemm_f32_ws", ta, tb, M, N, K, 1.0, p(a), a.shape[1], 0, p(b), b.shape[1], 0,
+             0.0, p(o), N, 0, 1, p(ws), wsb, None)
+    ad, bd = a.double(), b.double()
+    ref = ((ad.t() if ta else ad) @ (bd.t() if tb else bd)).float()
+    rel = ((out - ref).norm() / ref.norm()).item()
+    assert rel < 1e-5, rel
+    assert torch.equal(out, out2)
+
+
+def test_gemm_dyn_rows_split_on_256_tiles_vs_torch():
+    """The device-sized GEMM (rows of C wanted up to a count) on the 256x128
+    K split: rows below the count match an fp64 product, whole row tiles past
+    it are left alone."""
+    M, N, K, count = 4096, 2048, 8192, 1000
+    g = torch.Generator(device="cuda").manual_seed(3)
+    a = torch.randn(M, K, device="cuda", generator=g)
+    b = torch.randn(K, N, device="cuda", generator=g)
+    wsb = int(capi.lib().ember_gemm_f32_workspace_bytes(M, N, K, 1))
+    ws = empty((wsb // 4,))
+    out = torch.full((M, N), 7.0, device="cuda")
+    cnt = dev(np.array([count], np.int64))
+    call("ember_gemm_f32_dyn", 0, 0, M, N, K, 1.0, p(a), K, p(b), N, 0.0, p(out), N, p(cnt), 0,
+         0, p(ws), wsb, None)
+    ref = (a[:count].double() @ b.double()).float()
+    rel = ((out[:count] - ref).norm() / ref.norm()).item()
+    assert rel < 1e-5, rel
+    assert bool((out[1024:] == 7.0).all())   # tiles of 256 rows past the count
+
+
 def test_gemm_split_k_weight_gradient_shape_vs_torch():
     # c5 k/v weight gradient: dW[1024,2048] = dY^T X over 32768 tokens (TN).
     M, N, K = 1024, 2048, 32768
