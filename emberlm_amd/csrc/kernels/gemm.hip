@@ -763,14 +763,15 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch) {
   // latency-bound on its one pass over K: chunks of at least 256 from K = 512.
   const bool few = 2 * tiles <= kCUs;
   const int64_t min_chunk = few ? 256 : 1024;
-  // A K split on 256x128 tiles when a whole number of waves of them (two per
-  // CU) is at least two waves: 2-4% faster than the 128x128 split on the
-  // weight-gradient shapes that allows (e.g. 2048x2048 and 6144x2048 over
-  // 32768 tokens), which a partial last wave made up to 8% slower.
-  if (batch == 1 && !few && K >= 4096) {
+  // A K split on 256x128 tiles, in chunks of at least 1024, when a whole
+  // number of waves of them (two per CU) is at least two waves: 2-4% faster
+  // than the 128x128 split on the weight-gradient shapes that allows (e.g.
+  // 1024x2048, 2048x2048 and 6144x2048 over 32768 tokens), which a partial
+  // last wave made up to 8% slower.
+  if (batch == 1 && K >= 4096) {
     int64_t s = cdiv(4 * kCUs, big_tiles);
     while (s < 16 && (big_tiles * s) % (2 * kCUs) != 0) ++s;
-    if (s >= 2 && s <= K / min_chunk && (big_tiles * s) % (2 * kCUs) == 0) {
+    if (s >= 2 && s <= K / 1024 && (big_tiles * s) % (2 * kCUs) == 0) {
       p.big = true;
       p.kchunk = cdiv(cdiv(K, s), kBK) * kBK;
       p.splits = cdiv(K, p.kchunk);

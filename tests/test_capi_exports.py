@@ -82,8 +82,9 @@ def test_gemm_split_plan_without_gpu():
     lib = capi.lib()
     # a short prefill's projection (M = 128, 16 tiles): 8 K chunks of 256
     assert lib.ember_gemm_f32_workspace_bytes(128, 2048, 2048, 1) == 8 * 128 * 2048 * 4
-    # the c5 k/v weight gradient (128 tiles, K = 32768 tokens): 12 chunks
-    assert lib.ember_gemm_f32_workspace_bytes(1024, 2048, 32768, 1) == 12 * 1024 * 2048 * 4
+    # the c5 k/v weight gradient (64 tiles of 256x128, K = 32768 tokens): 16
+    # chunks, two whole waves
+    assert lib.ember_gemm_f32_workspace_bytes(1024, 2048, 32768, 1) == 16 * 1024 * 2048 * 4
     # Weight gradients dW[out, in] = dY^T X of BASELINE configs 2 and 3 (K =
     # tokens).  Few-tile grids (at most 128 tiles of 128x128) split into
     # chunks of >= 256, the others into chunks of >= 1024, aiming at 1536 tiles:
