@@ -440,7 +440,10 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_dma(GemmArgs a) {
   using TA = DmaTile<A_KC, BM>;
   using TB = DmaTile<B_KC, BN>;
   constexpr int FI = BM / 64, FJ = BN / 64;
-  constexpr int NR = FI * (A_KC ? 1 : 4) + FJ * (B_KC ? 1 : 4);
+  // An M-contiguous A on 256-row tiles is read as b128 rows of four
+  // consecutive tile rows (see load_a), one read per MFMA k-step of a slab.
+  constexpr bool kPermA = !A_KC && FI == 4;
+  constexpr int NR = (A_KC ? FI : kPermA ? 4 : 4 * FI) + FJ * (B_KC ? 1 : 4);
   constexpr int NM = 4 * FI * FJ;
   constexpr int kStage = TA::kFloats + TB::kFloats;
   __shared__ __attribute__((aligned(1024))) float lds[3 * kStage];  // 3-stage ring
@@ -486,6 +489,26 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_dma(GemmArgs a) {
     offB[s] = u + wn * (BN / 2) * 16;
   }
   const int mbA = (wm * (BM / 2)) >> 2, mbB = (wn * (BN / 2)) >> 2;
+  // A fragments of slab s.  With kPermA, MFMA tile i's row slot x holds tile
+  // row wm * (BM / 2) + 4x + i (not 32i + x): the b128 at k-row 8s + 4g + j,
+  // chunk mbA + r (swizzled as stored) is then lane (g, r)'s k-step-j value
+  // for all four tiles.  Each output element sums the same products in the
+  // same k order either way; only the rows' places in the registers move,
+  // which the epilogue undoes.
+  auto load_a = [&](const float* st, int s, f32x4 (&fa)[FI]) {
+    if constexpr (kPermA) {
+      const int off = 4 * ((mbA + r) ^ (8 * g));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(st + (8 * s + 4 * g + j) * BM + off);
+#pragma unroll
+        for (int i = 0; i < FI; ++i) fa[i][j] = v[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < FI; ++i) fa[i] = dma_frag<A_KC, BM>(st, offA[s], i, s, g, r, mbA);
+    }
+  };
   f32x16 acc[FI][FJ];
 #pragma unroll
   for (int i = 0; i < FI; ++i)
@@ -509,8 +532,7 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_dma(GemmArgs a) {
   block_barrier();
   float* st0 = lds;
   f32x4 fa0[FI], fb0[FJ], fa1[FI], fb1[FJ];
-#pragma unroll
-  for (int i = 0; i < FI; ++i) fa0[i] = dma_frag<A_KC, BM>(st0, offA[0], i, 0, g, r, mbA);
+  load_a(st0, 0, fa0);
 #pragma unroll
   for (int j = 0; j < FJ; ++j) fb0[j] = dma_frag<B_KC, BN>(st0 + TA::kFloats, offB[0], j, 0, g, r, mbB);
 
@@ -529,8 +551,7 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_dma(GemmArgs a) {
     float* cur = lds + ic * kStage;
     float* nxt = lds + (ic == 2 ? 0 : ic + 1) * kStage;
     float* nx2 = lds + (ic == 0 ? 2 : ic - 1) * kStage;
-#pragma unroll
-    for (int i = 0; i < FI; ++i) fa1[i] = dma_frag<A_KC, BM>(cur, offA[1], i, 1, g, r, mbA);
+    load_a(cur, 1, fa1);
 #pragma unroll
     for (int j = 0; j < FJ; ++j) fb1[j] = dma_frag<B_KC, BN>(cur + TA::kFloats, offB[1], j, 1, g, r, mbB);
     if constexpr (kDma && !kLateDma) {
@@ -567,8 +588,7 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_dma(GemmArgs a) {
     else
       wait_vm_lgkm0<0>();
     block_barrier();
-#pragma unroll
-    for (int i = 0; i < FI; ++i) fa0[i] = dma_frag<A_KC, BM>(nxt, offA[0], i, 0, g, r, mbA);
+    load_a(nxt, 0, fa0);
 #pragma unroll
     for (int j = 0; j < FJ; ++j) fb0[j] = dma_frag<B_KC, BN>(nxt + TA::kFloats, offB[0], j, 0, g, r, mbB);
 #pragma unroll
@@ -593,7 +613,8 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_dma(GemmArgs a) {
       if (col >= a.N) continue;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int64_t row = m0 + wm * (BM / 2) + i * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+        const int x = 8 * (e >> 2) + 4 * g + (e & 3);  // the MFMA tile's row slot
+        const int64_t row = m0 + wm * (BM / 2) + (kPermA ? 4 * x + i : i * 32 + x);
         if (row < a.M) {
           float* dst = C + row * a.ldc + col;
           const float v = a.alpha * acc[i][j][e];
