@@ -64,6 +64,22 @@ __device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Accumulators over d with permuted row slots: tile 4hq + c, row slot
+// x = 4g + e holds d = 64hq + 4x + c (so that one b128 LDS read of d = 64hq +
+// 4i .. +3 is the A operand of four tiles).  Writes lane (g, i)'s values of
+// one row (query or key i) as float4s at d = 64hq + 16g + 4e, times mul.
+template <int NT>
+__device__ __forceinline__ void store_d_row(f32x4* row, const f32x4 (&acc)[NT], int g,
+                                            float mul) {
+#pragma unroll
+  for (int hq = 0; hq < NT / 4; ++hq)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      row[16 * hq + 4 * g + e] =
+          f32x4{acc[4 * hq][e], acc[4 * hq + 1][e], acc[4 * hq + 2][e], acc[4 * hq + 3][e]} *
+          mul;
+}
+
 // 2^x on the transcendental unit (inputs here are <= 0 or -inf).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -135,8 +151,11 @@ struct RowTile {
 //   query i: a query's running max is reduced over its four lanes (g), and
 //   its running sum is kept per lane and added up at the end;
 //   O^T += V^T P^T (m = d, n = query, contraction over the 4 keys
-//   {16kt + 4g + e : g}): P is the B operand straight from s[kt], the A
-//   operand one b32 LDS read of V.
+//   {16kt + 4g + e : g}): P is the B operand straight from s[kt]; the A
+//   operand of tile 4hq + c, row slot x, is d = 64hq + 4x + c, so one b128
+//   LDS read of V (d = 64hq + 4i .. +3) feeds the four tiles 4hq .. 4hq + 3.
+//   Each element of O sums the same products in the same order as with
+//   d = 16t + x; only its register moves.
 template <int D>
 struct FwdCfg {
   static constexpr int kThreads = 512, kBQ = 128, kBK = 32, kKS = D + 4;
@@ -244,7 +263,12 @@ __global__ __launch_bounds__(FwdCfg<D>::kThreads, 2) void attn_fwd_kernel(
         for (int e = 0; e < 4; ++e) {
           const int row = (16 * kt + 4 * g + e) * C::kKS;
 #pragma unroll
-          for (int t = 0; t < NT; ++t) acc[t] = mfma16(Vs[row + 16 * t + i], s[kt][e], acc[t]);
+          for (int hq = 0; hq < NT / 4; ++hq) {
+            const f32x4 vv = *reinterpret_cast<const f32x4*>(Vs + row + 64 * hq + 4 * i);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              acc[4 * hq + c] = mfma16(vv[c], s[kt][e], acc[4 * hq + c]);
+          }
         }
     }
     if (more) {
@@ -259,11 +283,7 @@ __global__ __launch_bounds__(FwdCfg<D>::kThreads, 2) void attn_fwd_kernel(
   l_tot += __shfl_xor(l_tot, 32, kWave);
   if (myq < T) {
     if (g == 0) lse[(static_cast<int64_t>(b) * H + h) * T + myq] = (m_run + log2f(l_tot)) * kLn2;
-    // Accumulator tile t, lane (g, i), register e holds d = 16t + 4g + e of query i.
-    f32x4* orow = reinterpret_cast<f32x4*>(o + qoff + myq * qs);
-    const float inv = 1.0f / l_tot;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) orow[4 * t + g] = acc[t] * inv;
+    store_d_row(reinterpret_cast<f32x4*>(o + qoff + myq * qs), acc, g, 1.0f / l_tot);
   }
 }
 
@@ -300,7 +320,8 @@ __global__ __launch_bounds__(kThreads) void attn_delta_kernel(const float* __res
 //   read and the Q / dO rows sit in registers in the matching order;
 //   dS^T comes out with the query in the lane and keys 16kt + 4g + e in the
 //   registers, which is the B operand of dQ^T += K^T dS^T (m = d, contraction
-//   over the 4 keys {16kt + 4g + e : g}); its A operand is one b32 LDS read.
+//   over the 4 keys {16kt + 4g + e : g}); its A operand comes from b128 LDS
+//   reads of K, one per four d tiles (the permuted row slots of store_d_row).
 // The query's lse and delta are per-lane scalars.
 template <int D>
 struct DqCfg {
@@ -402,7 +423,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
         for (int e = 0; e < 4; ++e) {
           const int row = (16 * kt + 4 * g + e) * C::kKS;
 #pragma unroll
-          for (int t = 0; t < NT; ++t) acc[t] = mfma16(Ks[row + 16 * t + i], s[kt][e], acc[t]);
+          for (int hq = 0; hq < NT / 4; ++hq) {
+            const f32x4 kv = *reinterpret_cast<const f32x4*>(Ks + row + 64 * hq + 4 * i);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              acc[4 * hq + c] = mfma16(kv[c], s[kt][e], acc[4 * hq + c]);
+          }
         }
     }
     if (more) {
@@ -413,12 +439,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
     __syncthreads();
   }
 
-  // Accumulator tile t, lane (g, i), register e holds d = 16t + 4g + e of query i.
-  if (myq < T) {
-    f32x4* dqr = reinterpret_cast<f32x4*>(dq + qoff + myq * qs);
-#pragma unroll
-    for (int t = 0; t < NT; ++t) dqr[4 * t + g] = acc[t] * scale;
-  }
+  if (myq < T) store_d_row(reinterpret_cast<f32x4*>(dq + qoff + myq * qs), acc, g, scale);
 }
 
 // dK/dV on 16x16x4 MFMA tiles.  A wave owns 16 keys, a workgroup 64, so a
@@ -433,7 +454,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
 //   P and dS come out with the key in the lane (n = l%16) and queries
 //   16mt + 4g + e in the registers, which is exactly the B operand of
 //   dV^T += dO^T P and dK^T += Q^T dS (m = d, n = key, contraction over the
-//   4 queries {16mt + 4g + e : g}); their A operand is one b32 LDS read.
+//   4 queries {16mt + 4g + e : g}); their A operand comes from b128 LDS
+//   reads of dO and Q, one per four d tiles (the permuted row slots of
+//   store_d_row).
 template <int D>
 struct DkvCfg {
   static constexpr int kBKeys = 64, kBQ = 32, kQS = D + 4;
@@ -566,9 +589,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
         for (int e = 0; e < 4; ++e) {
           const int row = (16 * mt + 4 * g + e) * C::kQS;
 #pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            adv[t] = mfma16(Ds[row + 16 * t + i], s[mt][e], adv[t]);
-            adk[t] = mfma16(Qs[row + 16 * t + i], dp[mt][e], adk[t]);
+          for (int hq = 0; hq < NT / 4; ++hq) {
+            const f32x4 ov = *reinterpret_cast<const f32x4*>(Ds + row + 64 * hq + 4 * i);
+            const f32x4 qv = *reinterpret_cast<const f32x4*>(Qs + row + 64 * hq + 4 * i);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              adv[4 * hq + c] = mfma16(ov[c], s[mt][e], adv[4 * hq + c]);
+              adk[4 * hq + c] = mfma16(qv[c], dp[mt][e], adk[4 * hq + c]);
+            }
           }
         }
     }
@@ -576,15 +604,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
     __syncthreads();
   }
 
-  // Accumulator tile t, lane (g, i), register e holds d = 16t + 4g + e of key i.
   if (mykey < T) {
-    f32x4* dkr = reinterpret_cast<f32x4*>(dk + koff + mykey * ks);
-    f32x4* dvr = reinterpret_cast<f32x4*>(dv + koff + mykey * ks);
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      dkr[4 * t + g] = adk[t] * scale;
-      dvr[4 * t + g] = adv[t];
-    }
+    store_d_row(reinterpret_cast<f32x4*>(dk + koff + mykey * ks), adk, g, scale);
+    store_d_row(reinterpret_cast<f32x4*>(dv + koff + mykey * ks), adv, g, 1.0f);
   }
 }
 
@@ -702,6 +724,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_ds_kernel(
     if (myq < T) {
       f32x4* dqr = reinterpret_cast<f32x4*>(dq + static_cast<int64_t>(b) * T * qs +
                                             static_cast<int64_t>(h) * D + myq * qs);
+      // Accumulator tile t, lane (g, i), register e holds d = 16t + 4g + e.
 #pragma unroll
       for (int t = 0; t < NT; ++t) dqr[4 * t + g] = acc[n][t] * scale;
     }
