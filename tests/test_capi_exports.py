@@ -102,6 +102,7 @@ def test_gemm_split_plan_without_gpu():
         assert lib.ember_gemm_f32_workspace_bytes(M, N, K, 1) == splits * M * N * 4, (M, N, K)
     # enough tiles, or K too short to split: one pass over K
     assert lib.ember_gemm_f32_workspace_bytes(4096, 2048, 2048, 1) == 0
+    assert lib.ember_gemm_f32_workspace_bytes(8196, 4096, 512, 1) == 0  # 1056 tiles of 256x128
     assert lib.ember_gemm_f32_workspace_bytes(128, 2048, 511, 1) == 0
 
 

@@ -168,6 +168,28 @@ def test_gemm_split_k_on_256_tiles_vs_torch(ta, tb, M, N, K):
     assert torch.equal(out, out2)
 
 
+@pytest.mark.parametrize("ta,tb", [(1, 0), (1, 1)])
+def test_gemm_m_contiguous_a_on_256_tiles_ragged_rows(ta, tb):
+    """An M-contiguous A on the unsplit 256x128 kernel (its tile rows sit
+    permuted in the MFMA registers and are mapped back in the store), with a
+    last row tile holding 4 rows: every row of C against an fp64 product, the
+    rows past M (a guard band after C) left alone."""
+    M, N, K = 8196, 4096, 512          # 33 x 32 tiles of 256 x 128: the unsplit big-tile plan
+    g = torch.Generator(device="cuda").manual_seed(11 + tb)
+    a = torch.randn(K, M, device="cuda", generator=g)
+    b = torch.randn((N, K) if tb else (K, N), device="cuda", generator=g)
+    buf = torch.full((M + 8, N), 7.0, device="cuda")
+    call("ember_gemm_f32_ws", ta, tb, M, N, K, 1.0, p(a), M, 0, p(b), b.shape[1], 0, 0.0,
+         p(buf), N, 0, 1, None, 0, None)
+    ad, bd = a.double(), b.double()
+    ref = (ad.t() @ (bd.t() if tb else bd)).float()
+    rel = ((buf[:M] - ref).norm() / ref.norm()).item()
+    assert rel < 1e-5, rel
+    row_rel = ((buf[:M] - ref).norm(dim=1) / ref.norm(dim=1)).max().item()
+    assert row_rel < 1e-5, row_rel     # no row lost or swapped
+    assert torch.equal(buf[M:], torch.full((8, N), 7.0, device="cuda"))
+
+
 def test_gemm_dyn_rows_split_on_256_tiles_vs_torch():
     """The device-sized GEMM (rows of C wanted up to a count) on the 256x128
     K split: rows below the count match an fp64 product, whole row tiles past
