@@ -307,6 +307,9 @@ def main():
     ap.add_argument("--attn-ds-bytes", type=int, default=None,
                     help="device bytes the attention backward may keep dS in (0: recompute it; "
                          "default: the library's)")
+    ap.add_argument("--alloc-history", default=None,
+                    help="write the device allocator's history of the timed steps to this file "
+                         "(replayable on the host: emberlm_amd.trainer.alloc_replay)")
     ap.add_argument("--link-probe", action="store_true",
                     help="only the pinned host<->device copy rates of this box (one JSON line)")
     args = ap.parse_args()
@@ -354,6 +357,8 @@ def main():
 
     if args.attn_ds_bytes is not None:
         TR.set_attn_ds_bytes(args.attn_ds_bytes)
+    if args.alloc_history:
+        TR.alloc_history_start()   # from the first allocation: setup, warmup and timed steps
     t0 = time.time()
     tr = TR.Trainer(cfg, seed=0, init_std=0.02, norm_value=1.0)
     tr.set_checkpointing(ckpt)
@@ -383,6 +388,8 @@ def main():
             f"loss {st.loss:.4f}")
     tr.synchronize()
     wall = time.perf_counter() - t_wall
+    if args.alloc_history:
+        TR.alloc_history_stop(args.alloc_history)
     TR.gemm_profile(False)
     prof = TR.gemm_profile()
     mem = TR.memory()
@@ -390,6 +397,7 @@ def main():
     # staged on the device (AdamW::prefetch): they cross host->device before
     # the step's transfer window, so that window's rate is the device->host one.
     prefetched = tr.offload_stats()[2] if offload else 0.0
+    step_dirs = tr.offload_detail() if offload else None
 
     ms_step = wall / args.steps * 1e3
     tokens = B * T
@@ -438,9 +446,17 @@ def main():
                    "batch": B, "seq_len": T, "parallelism": "none (1 GPU)",
                    "gradient_checkpointing": ckpt, "offload_optimizer": offload,
                    "params": n_params},
-        "peak_hbm_gb": round(mem.peak_allocated / 1e9, 3),
+        # The device memory the process holds (hipMemGetInfo total - free, peak
+        # of the samples taken at every segment the allocator obtains and at
+        # each step's phase boundaries), then the allocator's own figures: the
+        # live-tensor high-water mark and the bytes it held from the driver.
+        "peak_hbm_gb": round(mem.peak_device_used / 1e9, 3),
+        "peak_hbm_live_gb": round(mem.peak_allocated / 1e9, 3),
         "peak_hbm_reserved_gb": round(mem.peak_reserved / 1e9, 3),
         "hbm_device_used_gb": round(mem.device_used / 1e9, 3),
+        "allocator": {"reserved_over_live": round(mem.peak_reserved / max(mem.peak_allocated, 1), 4),
+                      "segments_obtained": int(mem.device_mallocs),
+                      "cache_flushes": int(mem.cache_flushes)},
         "pinned_host_gb": round(mem.pinned_host / 1e9, 3),
         "active_tokens_per_s": round(mask_sum / (ms_step / 1e3), 2),
         # The fused LM head + loss computes only rows whose mask value is
@@ -456,6 +472,10 @@ def main():
                     "overlapped_with_next_forward": bool(offload),
                     "prefetched_bytes_per_direction": prefetched,
                     "pcie_gen5_x16_gbps": PCIE_GEN5_X16_GBPS},
+        # Each direction over its own active window in the last timed step's
+        # offloaded update (running beside the next forward): copies in from
+        # the first to the last, copies out (with the updates between them)
+        # from the first to the last.
         "gemm_all": {"launches": sum(v.launches for v in prof.values()),
                      "tflops": round(all_fl / (all_ms / 1e3) / 1e12, 2) if all_ms else None,
                      "frac_of_fp32_mfma_peak":
@@ -478,6 +498,18 @@ def main():
                      "launches": p.launches, "avg_launch_ms": round(avg_ms, 4),
                      "flops_per_launch": per_launch_flops, "traffic": None},
     }
+    if step_dirs is not None:
+        gb = lambda b, ms: round(b / (ms / 1e3) / 1e9, 2) if ms > 0 else None  # noqa: E731
+        result["offload"]["in_step"] = {
+            "h2d_bytes": step_dirs.h2d_bytes, "h2d_ms": round(step_dirs.h2d_ms, 2),
+            "h2d_gbps": gb(step_dirs.h2d_bytes, step_dirs.h2d_ms),
+            "d2h_bytes": step_dirs.d2h_bytes, "d2h_ms": round(step_dirs.d2h_ms, 2),
+            "d2h_gbps": gb(step_dirs.d2h_bytes, step_dirs.d2h_ms),
+            "h2d_frac_of_pcie": round(gb(step_dirs.h2d_bytes, step_dirs.h2d_ms) /
+                                      PCIE_GEN5_X16_GBPS, 4) if step_dirs.h2d_ms > 0 else None,
+            "d2h_frac_of_pcie": round(gb(step_dirs.d2h_bytes, step_dirs.d2h_ms) /
+                                      PCIE_GEN5_X16_GBPS, 4) if step_dirs.d2h_ms > 0 else None,
+            "skipped_bytes_no_grad": step_dirs.skipped_bytes}
     traffic, src = profiled_traffic(args.workload, dom)
     if traffic is not None:
         result["roofline"]["traffic"] = traffic
@@ -492,7 +524,12 @@ def main():
         tr.opt_step()
         tr.zero_grad()
         iso_ms, iso_bytes, _ = tr.offload_stats()
+        iso = tr.offload_detail()
         gbps = iso_bytes / (iso_ms / 1e3) / 1e9 if iso_ms > 0 else 0.0
+        result["offload"]["isolated_h2d_gbps"] = round(
+            iso.h2d_bytes / (iso.h2d_ms / 1e3) / 1e9, 2) if iso.h2d_ms > 0 else None
+        result["offload"]["isolated_d2h_gbps"] = round(
+            iso.d2h_bytes / (iso.d2h_ms / 1e3) / 1e9, 2) if iso.d2h_ms > 0 else None
         result["offload"]["isolated_step_ms"] = round(iso_ms, 2)
         result["offload"]["isolated_gbps_per_direction"] = round(gbps, 2)
         result["offload"]["isolated_frac_of_pcie"] = round(gbps / PCIE_GEN5_X16_GBPS, 4)
@@ -516,7 +553,9 @@ def main():
         fb_ck = avg("forward_ms") + avg("backward_ms")
         result["no_checkpointing"] = {
             "ms_per_step": round(base, 2),
-            "peak_hbm_gb": round(mem2.peak_allocated / 1e9, 3),
+            "peak_hbm_gb": round(mem2.peak_device_used / 1e9, 3),
+            "peak_hbm_live_gb": round(mem2.peak_allocated / 1e9, 3),
+            "peak_hbm_reserved_gb": round(mem2.peak_reserved / 1e9, 3),
             "recompute_overhead_step": round(avg("total_ms") / base - 1.0, 4),
             "recompute_overhead_fwd_bwd": round(fb_ck / fb - 1.0, 4),
         }

@@ -100,6 +100,8 @@ SIGNATURES = {
     "ember_adamw_bounded": (i32, [vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, f32, f32, i32, vp]),
     "ember_sumsq_workspace_bytes": (sz, [i32]),
     "ember_sumsq_multi": (i32, [C.POINTER(vp), C.POINTER(i64), i32, vp, vp, sz, vp]),
+    "ember_scale_multi_workspace_bytes": (sz, [i32]),
+    "ember_scale_multi": (i32, [C.POINTER(vp), C.POINTER(i64), i32, f32, vp, sz, vp]),
     "ember_kv_write": (i32, [vp, vp, i64, i64, i64, i64, i64, i64, vp]),
     "ember_kv_read_expanded": (i32, [vp, vp, i64, i64, i64, i64, i64, i64, vp]),
     "ember_attn_decode_workspace_bytes": (sz, [i64, i64, i64, i64, i64, i64]),

@@ -106,10 +106,15 @@ namespace {
 std::atomic<int64_t> g_head_chunk_rows{0};
 std::atomic<bool> g_head_active_rows{true};
 
-// Rows per chunk: at most ~2.5 GB of logits, a multiple of 256, at least 256.
+// Rows per chunk: at most ~0.64 GB of logits (1024 rows at V = 151936), a
+// multiple of 256, at least 256.  The chunk is the LM head's largest buffer;
+// at this size it fits the holes the layers' activations leave in the
+// device allocator's cache, where 4096-row chunks (2.5 GB) made the allocator
+// hold ~1.4x the live bytes at Qwen3-0.6B.  The head's GEMMs run at the same
+// rate on 1024 rows; dE is read and written once more per chunk.
 int64_t head_chunk_rows(int64_t N, int64_t V) {
   if (const int64_t fixed = g_head_chunk_rows.load()) return std::min(N, fixed);
-  const int64_t budget = static_cast<int64_t>(2.5e9) / (V * static_cast<int64_t>(sizeof(float)));
+  const int64_t budget = static_cast<int64_t>(0.64e9) / (V * static_cast<int64_t>(sizeof(float)));
   int64_t r = std::max<int64_t>(256, budget / 256 * 256);
   return std::min(N, r);
 }
@@ -330,8 +335,25 @@ struct EmbeddingBackward : autograd::Node {
   int64_t vocab = 0;
   const char* name() const override { return "EmbeddingBackward"; }
   std::vector<Tensor> backward(const std::vector<Tensor>& go) override {
+    return backward_with_partials(go, {});
+  }
+  // A tied embedding's weight already holds the LM head's dE when this runs:
+  // the rows' sums are added into it (each touched row gets dE + its total,
+  // the same rounding as a separate dW and add), so no [V, H] dW is
+  // allocated, zeroed and added.
+  bool accepts_partials() const override { return true; }
+  std::vector<Tensor> backward_with_partials(const std::vector<Tensor>& go,
+                                             const std::vector<Tensor>& partials) override {
     autograd::NoGradGuard ng;
-    Tensor dw = embedding_backward_impl(ids, go.at(0), vocab);
+    const Tensor* into = partials.size() > 1 && partials[1].defined() ? &partials[1] : nullptr;
+    Tensor dw;
+    if (into && into->dtype() == DType::kFloat32 && into->is_contiguous() &&
+        into->device().is_hip() && into->dim() == 2 && into->shape()[0] == vocab) {
+      dw = *into;
+      embedding_backward_into(ids, go.at(0), dw);
+    } else {
+      dw = embedding_backward_impl(ids, go.at(0), vocab);
+    }
     release_saved(ids);
     return {Tensor{}, dw};
   }
@@ -350,18 +372,35 @@ Tensor embedding_impl(const Tensor& ids, const Tensor& weight) {
   return out;
 }
 
-Tensor embedding_backward_impl(const Tensor& ids, const Tensor& dy, int64_t vocab) {
+namespace {
+// dw (= 0 first unless accumulate) += the rows of dy summed per id.
+void embedding_backward_launch(const Tensor& ids, const Tensor& dy, Tensor& dw, bool accumulate) {
   require(ids.dtype() == DType::kInt64 && ids.device().is_hip(), "embedding_backward: bad ids");
   check_f32(dy, "embedding_backward", "dy");
-  const int64_t n = ids.numel();
+  const int64_t n = ids.numel(), vocab = dw.shape()[0];
   require(n > 0 ? dy.numel() % n == 0 : true, "embedding_backward: dy shape mismatch");
   const int64_t H = n ? dy.numel() / n : dy.shape().back();
-  Tensor dw = Tensor::empty({vocab, H}, DType::kFloat32, dy.device());
+  require(dw.dim() == 2 && dw.shape()[1] == H, "embedding_backward: dw shape mismatch");
   const size_t wsb = ember_embedding_bwd_workspace_bytes(n, H, vocab);
   Tensor ws = wsb ? workspace(wsb) : Tensor{};
   CTD_CHECK(ember_embedding_bwd(static_cast<const int64_t*>(ids.data_ptr()), cfp(dy), fp(dw), n, H,
-                                vocab, /*accumulate=*/0, wsb ? ws.data_ptr() : nullptr, wsb, S()));
+                                vocab, accumulate ? 1 : 0, wsb ? ws.data_ptr() : nullptr, wsb,
+                                S()));
+}
+}  // namespace
+
+Tensor embedding_backward_impl(const Tensor& ids, const Tensor& dy, int64_t vocab) {
+  check_f32(dy, "embedding_backward", "dy");
+  const int64_t n = ids.numel();
+  const int64_t H = n && dy.numel() % n == 0 ? dy.numel() / n : dy.shape().back();
+  Tensor dw = Tensor::empty({vocab, H}, DType::kFloat32, dy.device());
+  embedding_backward_launch(ids, dy, dw, false);
   return dw;
+}
+
+void embedding_backward_into(const Tensor& ids, const Tensor& dy, Tensor& dw) {
+  check_f32(dw, "embedding_backward", "dw");
+  embedding_backward_launch(ids, dy, dw, true);
 }
 
 Tensor embedding(const Tensor& ids, const Tensor& weight) {

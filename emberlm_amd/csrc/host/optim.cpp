@@ -128,6 +128,8 @@ AdamW::~AdamW() {
   ember_event_destroy(ev_pf_ready_);
   ember_event_destroy(ev_pf_loaded_);
   ember_event_destroy(ev_pf_drained_);
+  ember_event_destroy(ev_h2d_end_);
+  ember_event_destroy(ev_d2h_begin_);
 }
 
 Tensor& AdamW::m_tensor(size_t gi, size_t pi) {
@@ -165,6 +167,10 @@ void AdamW::wait_idle() {
     float ms = 0.f;
     CTD_CHECK(ember_event_elapsed_ms(&ms, ev_begin_, ev_done_));
     stats_.last_stream_ms = ms;
+    CTD_CHECK(ember_event_elapsed_ms(&ms, ev_begin_, ev_h2d_end_));
+    stats_.last_h2d_ms = ms;
+    CTD_CHECK(ember_event_elapsed_ms(&ms, ev_d2h_begin_, ev_done_));
+    stats_.last_d2h_ms = ms;
     in_flight_ = false;
   }
   runtime::collect_released();
@@ -243,6 +249,8 @@ void AdamW::init_offload_state() {
     CTD_CHECK(ember_event_create(&ev_pf_ready_));
     CTD_CHECK(ember_event_create(&ev_pf_loaded_));
     CTD_CHECK(ember_event_create(&ev_pf_drained_));
+    CTD_CHECK(ember_event_create(&ev_h2d_end_));
+    CTD_CHECK(ember_event_create(&ev_d2h_begin_));
   }
   ev_param_.resize(groups_.size());
   for (size_t gi = 0; gi < groups_.size(); ++gi)
@@ -287,13 +295,28 @@ void AdamW::prefetch() {
   const Segment& first = layout_.front();
   const int64_t nch = std::min((first.off + first.n + chunk_elems_ - 1) / chunk_elems_,
                                max_prefetch_chunks_);
-  const int64_t elems = std::min(nch * chunk_elems_, flat_n_);
+  int64_t elems = std::min(nch * chunk_elems_, flat_n_);
+  // Fewer chunks when the allocator's largest free block holds fewer (at
+  // least one): the staging then fills a hole instead of growing the memory
+  // held, and the step streams the rest through the ring as usual.
+  const auto fit = [&](int64_t want) {
+    const size_t got = elastic_workspace_bytes(static_cast<size_t>(want) * sizeof(float),
+                                               static_cast<size_t>(chunk_elems_) * sizeof(float));
+    const int64_t n = static_cast<int64_t>(got / sizeof(float));
+    return n >= want ? want : std::max<int64_t>(chunk_elems_, n / chunk_elems_ * chunk_elems_);
+  };
+  elems = std::min(elems, fit(elems));
   ember_stream_t cs = S(), hs = runtime::h2d_stream();
   // The buffer comes from the caching allocator, which orders reuse on the
   // compute stream: the copies wait until that stream has reached this call.
   // They also wait for the previous step's copies out, which write the host
   // state read here.
   pf_m_ = Tensor::empty({elems}, DType::kFloat32, kHIP0);
+  if (const int64_t v_elems = fit(elems); v_elems < elems) {
+    elems = v_elems;
+    pf_m_ = Tensor{};
+    pf_m_ = Tensor::empty({elems}, DType::kFloat32, kHIP0);
+  }
   pf_v_ = Tensor::empty({elems}, DType::kFloat32, kHIP0);
   CTD_CHECK(ember_event_record(ev_pf_ready_, cs));
   CTD_CHECK(ember_stream_wait_event(hs, ev_pf_ready_));
@@ -355,16 +378,17 @@ void AdamW::step_offloaded() {
   float* hm = static_cast<float*>(flat_m_.data_ptr());
   float* hv = static_cast<float*>(flat_v_.data_ptr());
   size_t k = 0;  // first segment not yet finished
-  // Updates every parameter piece inside [c0, c0 + len), whose m/v sit at
-  // cm/cv on the device, and marks each parameter that ends there as done.
-  auto update_range = [&](int64_t c0, int64_t len, float* cm, float* cv) {
+  // Updates every parameter piece with a gradient inside [c0, c0 + len),
+  // whose m/v sit on the device at cm/cv from state element `base` on, and
+  // marks each parameter that ends there as done.
+  auto update_range = [&](int64_t c0, int64_t len, int64_t base, float* cm, float* cv) {
     while (k < layout_.size() && layout_[k].off < c0 + len) {
       const Segment& sg = layout_[k];
       const int64_t lo = std::max(sg.off, c0), hi = std::min(sg.off + sg.n, c0 + len);
       if (work[k].p && hi > lo) {
         const ParamGroup& group = groups_[sg.gi];
         CTD_CHECK(ember_adamw_bounded(work[k].p + (lo - sg.off), work[k].g + (lo - sg.off),
-                                      cm + (lo - c0), cv + (lo - c0), hi - lo, group.lr,
+                                      cm + (lo - base), cv + (lo - base), hi - lo, group.lr,
                                       beta1_, beta2_, eps_, group.weight_decay, bc1, bc2,
                                       kUpdateBlocks, ds));
       }
@@ -381,32 +405,60 @@ void AdamW::step_offloaded() {
     }
   };
 
-  double bytes_in = 0.0, bytes_out = 0.0;
+  // [lo, hi) of the state in [c0, c0 + len) that belongs to parameters with
+  // a gradient (empty when none has one): only that part crosses the link.
+  auto graded_span = [&](int64_t c0, int64_t len) {
+    int64_t lo = c0 + len, hi = c0;
+    for (size_t j = k; j < layout_.size() && layout_[j].off < c0 + len; ++j) {
+      const Segment& sg = layout_[j];
+      if (!work[j].p || sg.off + sg.n <= c0) continue;
+      lo = std::min(lo, std::max(sg.off, c0));
+      hi = std::max(hi, std::min(sg.off + sg.n, c0 + len));
+    }
+    return std::pair<int64_t, int64_t>{lo, hi};
+  };
+
+  double bytes_in = 0.0, bytes_out = 0.0, skipped = 0.0;
+  bool first_out = true;
+  auto mark_first_out = [&] {
+    if (first_out) CTD_CHECK(ember_event_record(ev_d2h_begin_, ds));
+    first_out = false;
+  };
   // The prefetched state (a whole number of chunks, or the whole state) is
   // updated before anything else and copied out after everything else: the
   // d2h stream runs the updates in streaming order, which is the order the
   // next forward waits for them, and no copy of it holds back a later one.
-  if (pf_elems > 0) update_range(0, pf_elems, pf_m, pf_v);
+  if (pf_elems > 0) update_range(0, pf_elems, 0, pf_m, pf_v);
   int64_t ring = 0;  // chunks streamed through the ring so far
-  for (int64_t c0 = pf_elems; c0 < flat_n_; c0 += chunk_elems_, ++ring) {
+  for (int64_t c0 = pf_elems; c0 < flat_n_; c0 += chunk_elems_) {
     const int64_t len = std::min(chunk_elems_, flat_n_ - c0);
-    const size_t nb = static_cast<size_t>(len) * sizeof(float);
+    const auto [lo, hi] = graded_span(c0, len);
+    skipped += 2.0 * static_cast<double>(len - std::max<int64_t>(hi - lo, 0)) * sizeof(float);
+    if (hi <= lo) {  // no gradient in this chunk: its state stays on the host
+      update_range(c0, len, c0, nullptr, nullptr);
+      continue;
+    }
+    const size_t nb = static_cast<size_t>(hi - lo) * sizeof(float);
     const int s = static_cast<int>(ring % kSlots);
     if (ring >= kSlots) CTD_CHECK(ember_stream_wait_event(hs, ev_drained_[s]));
-    CTD_CHECK(ember_memcpy_async(d_m_[s], hm + c0, nb, 0, hs));
-    CTD_CHECK(ember_memcpy_async(d_v_[s], hv + c0, nb, 0, hs));
+    CTD_CHECK(ember_memcpy_async(d_m_[s], hm + lo, nb, 0, hs));
+    CTD_CHECK(ember_memcpy_async(d_v_[s], hv + lo, nb, 0, hs));
     CTD_CHECK(ember_event_record(ev_loaded_[s], hs));
     CTD_CHECK(ember_stream_wait_event(ds, ev_loaded_[s]));
-    update_range(c0, len, d_m_[s], d_v_[s]);
-    CTD_CHECK(ember_memcpy_async(hm + c0, d_m_[s], nb, 1, ds));
-    CTD_CHECK(ember_memcpy_async(hv + c0, d_v_[s], nb, 1, ds));
+    update_range(c0, len, lo, d_m_[s], d_v_[s]);  // the slot holds [lo, hi)
+    mark_first_out();
+    CTD_CHECK(ember_memcpy_async(hm + lo, d_m_[s], nb, 1, ds));
+    CTD_CHECK(ember_memcpy_async(hv + lo, d_v_[s], nb, 1, ds));
     CTD_CHECK(ember_event_record(ev_drained_[s], ds));
     bytes_in += 2.0 * static_cast<double>(nb);
     bytes_out += 2.0 * static_cast<double>(nb);
+    ++ring;
   }
+  CTD_CHECK(ember_event_record(ev_h2d_end_, hs));
   if (pf_elems > 0) {
     // One copy out per buffer, after which it goes back to the allocator.
     const size_t nb = static_cast<size_t>(pf_elems) * sizeof(float);
+    mark_first_out();
     CTD_CHECK(ember_memcpy_async(hm, pf_m, nb, 1, ds));
     CTD_CHECK(ember_memcpy_async(hv, pf_v, nb, 1, ds));
     CTD_CHECK(ember_event_record(ev_pf_drained_, ds));
@@ -416,6 +468,7 @@ void AdamW::step_offloaded() {
     pf_elems_ = 0;
     bytes_out += 2.0 * static_cast<double>(nb);
   }
+  if (first_out) CTD_CHECK(ember_event_record(ev_d2h_begin_, ds));  // nothing was moved
   CTD_CHECK(ember_event_record(ev_done_, ds));
   // Only now, after the last data_ptr() above: later users of a parameter or
   // its gradient on the compute stream wait for that parameter's update.
@@ -429,6 +482,7 @@ void AdamW::step_offloaded() {
   stats_.last_h2d_bytes = bytes_in;
   stats_.last_d2h_bytes = bytes_out;
   stats_.last_prefetch_bytes = bytes_out - bytes_in;
+  stats_.last_skipped_bytes = skipped;
   stats_.last_step_ms =
       std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
 }
@@ -462,7 +516,13 @@ float clip_grad_norm_(const std::vector<Tensor>& params, float max_norm, float e
   const float total = std::sqrt(sum);
   if (total > max_norm) {
     const float scale = max_norm / (total + eps);
-    for (auto& g : grads) CTD_CHECK(ember_scale(cfp(g), scale, fp(g), g.numel(), S()));
+    std::vector<float*> wptrs;
+    wptrs.reserve(grads.size());
+    for (auto& g : grads) wptrs.push_back(fp(g));
+    const size_t swb = ember_scale_multi_workspace_bytes(count);
+    Tensor sws = swb ? workspace(swb) : Tensor{};
+    CTD_CHECK(ember_scale_multi(wptrs.data(), sizes.data(), count, scale,
+                                swb ? sws.data_ptr() : nullptr, swb, S()));
   }
   return total;
 }

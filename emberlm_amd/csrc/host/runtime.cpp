@@ -2,14 +2,18 @@
 //
 // Reference: src/core/allocator.cpp:14-57 (raw cudaMalloc/cudaFree per tensor,
 // malloc CPU allocator, cudaMallocHost pinned allocator) and
-// src/core/storage.cpp.  The device allocator here caches freed blocks per
-// rounded size so the training loop never reaches the driver after its first
-// step (hipFree would also synchronise the device), and it keeps the
-// high-water mark of live bytes that the peak-HBM figure is read from.
+// src/core/storage.cpp.  The device allocator here keeps freed memory for
+// reuse (BlockArena: best fit, split, coalesce) so the training loop never
+// reaches the driver after its first step (hipFree would also synchronise the
+// device), and it records the high-water marks of live bytes, of bytes held
+// from the driver, and of the device's used memory (hipMemGetInfo, sampled
+// whenever a segment is obtained and at the callers' phase boundaries).
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <fstream>
 #include <mutex>
+#include <sstream>
 #include <stdexcept>
 #include <string>
 #include <unordered_map>
@@ -18,6 +22,7 @@
 #include "ctd/allocator.h"
 #include "ctd/runtime.h"
 #include "ctd/storage.h"
+#include "block_arena.h"
 
 namespace ctd {
 
@@ -232,102 +237,161 @@ void gemm_profile_collect(int64_t* launches, double* flops, double* total_ms) {
 
 namespace {
 
+// Device memory through BlockArena (best fit, split, coalesce) over hipMalloc.
+class HipBackend final : public detail::ArenaBackend {
+ public:
+  bool obtain(size_t bytes, uintptr_t* base) override {
+    void* p = nullptr;
+    if (ember_device_malloc(&p, bytes) != EMBER_OK) return false;
+    *base = reinterpret_cast<uintptr_t>(p);
+    return true;
+  }
+  void give_back(uintptr_t base, size_t) override {
+    ember_device_free(reinterpret_cast<void*>(base));
+  }
+  // Blocks are freed on the host while kernels queued earlier may still read
+  // them; a segment goes back to the driver only once the device is idle.
+  void quiesce() override { ember_device_synchronize(); }
+};
+
 class HipCachingAllocator final : public Allocator {
  public:
+  HipCachingAllocator() : arena_(backend_) {}
+
   void* allocate(size_t nbytes) override {
     if (nbytes == 0) return nullptr;
-    const size_t r = round_up(nbytes);
     // Blocks a side stream has finished with go back first.  If some are
-    // still in use and this request would set a new lifetime high-water
-    // mark, wait for them instead: the host runs ahead of the GPU, and the side stream's
-    // buffers (gradients the offloaded update still reads) would otherwise
-    // count on top of the next forward's own peak.
+    // still in use and this request would set a new lifetime high-water mark
+    // of live bytes, wait for them instead: the host runs ahead of the GPU,
+    // and the side stream's buffers (gradients the offloaded update still
+    // reads) would otherwise count on top of the next forward's own peak.
     if (runtime::collect_released() > 0) {
       bool over;
       {
         std::lock_guard<std::mutex> lk(mu_);
-        over = stats_.allocated_bytes + r > high_water_;
+        over = arena_.stats().live_bytes + nbytes > high_water_;
       }
       if (over) runtime::drain_released();
     }
     std::lock_guard<std::mutex> lk(mu_);
-    void* p = nullptr;
-    auto it = free_.find(r);
-    if (it != free_.end() && !it->second.empty()) {
-      p = it->second.back();
-      it->second.pop_back();
-    } else {
-      int rc = ember_device_malloc(&p, r);
-      if (rc != EMBER_OK) {  // give cached blocks back and retry once
-        release_cached_locked();
-        rc = ember_device_malloc(&p, r);
-      }
-      if (rc != EMBER_OK)
-        throw std::runtime_error("hip_allocator: out of device memory allocating " +
-                                 std::to_string(r) + " bytes (" + ember_status_string(rc) + ")");
-      stats_.reserved_bytes += r;
-      stats_.num_device_mallocs += 1;
-      if (stats_.reserved_bytes > stats_.peak_reserved_bytes)
-        stats_.peak_reserved_bytes = stats_.reserved_bytes;
+    const int64_t segments_before = arena_.stats().segments_obtained;
+    const uintptr_t a = arena_.allocate(nbytes);
+    const detail::ArenaStats& st = arena_.stats();
+    high_water_ = std::max(high_water_, st.live_bytes);
+    if (st.segments_obtained != segments_before) sample_locked();
+    if (tracing_) {
+      const uint64_t id = next_id_++;
+      trace_ids_[a] = id;
+      trace_ << "a " << id << ' ' << nbytes << '\n';
     }
-    live_[p] = r;
-    stats_.allocated_bytes += r;
-    if (stats_.allocated_bytes > stats_.peak_allocated_bytes)
-      stats_.peak_allocated_bytes = stats_.allocated_bytes;
-    if (stats_.allocated_bytes > high_water_) high_water_ = stats_.allocated_bytes;
-    return p;
+    return reinterpret_cast<void*>(a);
   }
 
   void deallocate(void* ptr) noexcept override {
     if (!ptr) return;
     std::lock_guard<std::mutex> lk(mu_);
-    auto it = live_.find(ptr);
-    if (it == live_.end()) return;
-    const size_t r = it->second;
-    live_.erase(it);
-    stats_.allocated_bytes -= r;
-    free_[r].push_back(ptr);
+    const uintptr_t a = reinterpret_cast<uintptr_t>(ptr);
+    if (arena_.release(a) == 0) return;
+    if (tracing_) {
+      auto it = trace_ids_.find(a);
+      if (it != trace_ids_.end()) {
+        trace_ << "f " << it->second << '\n';
+        trace_ids_.erase(it);
+      }
+    }
   }
 
   Device device() const override { return kHIP0; }
 
   DeviceMemoryStats stats() {
     std::lock_guard<std::mutex> lk(mu_);
-    return stats_;
+    const detail::ArenaStats& a = arena_.stats();
+    DeviceMemoryStats s;
+    s.allocated_bytes = a.live_bytes;
+    s.peak_allocated_bytes = a.peak_live_bytes;
+    s.reserved_bytes = a.held_bytes;
+    s.peak_reserved_bytes = a.peak_held_bytes;
+    s.num_device_mallocs = a.segments_obtained;
+    s.num_cache_flushes = a.trims;
+    s.device_used_bytes = device_used_;
+    s.peak_device_used_bytes = peak_device_used_;
+    s.limit_bytes = arena_.limit();
+    s.largest_free_block = arena_.largest_free();
+    return s;
   }
   void reset_peak() {
     std::lock_guard<std::mutex> lk(mu_);
-    stats_.peak_allocated_bytes = stats_.allocated_bytes;
-    stats_.peak_reserved_bytes = stats_.reserved_bytes;
+    arena_.reset_peaks();
+    peak_device_used_ = 0;
+    sample_locked();
   }
   void empty_cache() {
     std::lock_guard<std::mutex> lk(mu_);
-    release_cached_locked();
+    arena_.trim();
+  }
+  void set_limit(size_t bytes) {
+    std::lock_guard<std::mutex> lk(mu_);
+    arena_.set_limit(bytes);
+  }
+  void sample() {
+    std::lock_guard<std::mutex> lk(mu_);
+    sample_locked();
+  }
+  size_t elastic(size_t want, size_t least) {
+    if (least > want) least = want;
+    std::lock_guard<std::mutex> lk(mu_);
+    // Recorded so that a replay can make the same choice against its own
+    // arena: the request that follows is the buffer sized by this answer.
+    if (tracing_) trace_ << "e " << want << ' ' << least << '\n';
+    return arena_.elastic_fit(want, least);
+  }
+
+  // Allocation history: every live block first (as allocated), then each
+  // request and release in order.
+  void history_start() {
+    std::lock_guard<std::mutex> lk(mu_);
+    trace_.str(std::string());
+    trace_.clear();
+    trace_ids_.clear();
+    next_id_ = 0;
+    tracing_ = true;
+    for (const auto& [addr, size] : arena_live_snapshot()) {
+      trace_ids_[addr] = next_id_;
+      trace_ << "a " << next_id_++ << ' ' << size << '\n';
+    }
+  }
+  void history_mark(const std::string& label) {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (tracing_) trace_ << "m " << label << '\n';
+  }
+  void history_stop(const std::string& path) {
+    std::lock_guard<std::mutex> lk(mu_);
+    tracing_ = false;
+    trace_ids_.clear();
+    std::ofstream out(path);
+    if (!out) throw std::runtime_error("allocation history: cannot write " + path);
+    out << trace_.str();
+    trace_.str(std::string());
   }
 
  private:
-  // 512-byte granules below 1 MiB, 2 MiB granules above.
-  static size_t round_up(size_t n) {
-    if (n <= (size_t{1} << 20)) return (n + 511) & ~size_t{511};
-    const size_t g = size_t{2} << 20;
-    return (n + g - 1) / g * g;
-  }
-  void release_cached_locked() {
-    ember_device_synchronize();
-    for (auto& [r, v] : free_) {
-      for (void* p : v) {
-        ember_device_free(p);
-        stats_.reserved_bytes -= r;
-      }
-      v.clear();
-    }
+  std::vector<std::pair<uintptr_t, size_t>> arena_live_snapshot() { return arena_.live_blocks(); }
+  void sample_locked() {
+    size_t fr = 0, tot = 0;
+    if (ember_mem_get_info(&fr, &tot) != EMBER_OK) return;
+    device_used_ = tot - fr;
+    peak_device_used_ = std::max(peak_device_used_, device_used_);
   }
 
   std::mutex mu_;
-  std::unordered_map<size_t, std::vector<void*>> free_;
-  std::unordered_map<void*, size_t> live_;
-  DeviceMemoryStats stats_;
-  size_t high_water_ = 0;  // like peak_allocated_bytes, but never reset
+  HipBackend backend_;
+  detail::BlockArena arena_;
+  size_t high_water_ = 0;  // like the peak of live bytes, but never reset
+  size_t device_used_ = 0, peak_device_used_ = 0;
+  bool tracing_ = false;
+  std::ostringstream trace_;
+  std::unordered_map<uintptr_t, uint64_t> trace_ids_;
+  uint64_t next_id_ = 0;
 };
 
 class CpuAllocator final : public Allocator {
@@ -401,6 +465,14 @@ Allocator& allocator_for(const Device& device) {
 DeviceMemoryStats device_memory_stats() { return hip_cache().stats(); }
 void reset_peak_device_memory() { hip_cache().reset_peak(); }
 void empty_device_cache() { hip_cache().empty_cache(); }
+void set_device_memory_limit(size_t bytes) { hip_cache().set_limit(bytes); }
+void sample_device_memory() { hip_cache().sample(); }
+size_t elastic_workspace_bytes(size_t want, size_t least) {
+  return hip_cache().elastic(want, least);
+}
+void start_allocation_history() { hip_cache().history_start(); }
+void mark_allocation_history(const std::string& label) { hip_cache().history_mark(label); }
+void stop_allocation_history(const std::string& path) { hip_cache().history_stop(path); }
 size_t pinned_host_bytes() { return pinned().bytes(); }
 
 // ------------------------------------------------------------------ Storage

@@ -27,6 +27,7 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <cstdint>
 #include <cerrno>
 #include <cstring>
 #include <map>
@@ -179,20 +180,29 @@ SafetensorsReader::SafetensorsReader(const std::filesystem::path& path) : path_(
       e.name = name;
       if (!readable_dtype(dt->str, &e.dtype))
         fault(Fault::kDtype, path, name + " is " + dt->str + " (readable: F32, I64, I32)");
+      // Element and byte counts are formed without wrapping: a shape whose
+      // product passes 2^63 cannot describe bytes of this file.
       uint64_t count = 1;
+      bool too_big = false;
       for (const json::JVal& d : sh->arr) {
         const uint64_t extent = json_uint(d, path, "a shape extent");
+        too_big = too_big || extent > static_cast<uint64_t>(INT64_MAX) ||
+                  __builtin_mul_overflow(count, extent, &count);
         e.shape.push_back(static_cast<int64_t>(extent));
-        count *= extent;
       }
+      uint64_t need = 0;
+      too_big = too_big || __builtin_mul_overflow(count, static_cast<uint64_t>(dtype_size(e.dtype)),
+                                                  &need) ||
+                need > static_cast<uint64_t>(INT64_MAX);
+      if (too_big) fault(Fault::kLayout, path, name + " has a shape too large to address");
       e.begin = json_uint(of->arr[0], path, "a data offset");
       e.end = json_uint(of->arr[1], path, "a data offset");
       if (e.end < e.begin || e.end > data_bytes)
         fault(Fault::kLayout, path, name + " lies outside the data region");
-      if (e.end - e.begin != count * dtype_size(e.dtype))
+      if (e.end - e.begin != need)
         fault(Fault::kLayout, path, name + " holds " + std::to_string(e.end - e.begin) +
                                         " bytes, its dtype and shape need " +
-                                        std::to_string(count * dtype_size(e.dtype)));
+                                        std::to_string(need));
       index_.emplace(name, entries_.size());
       entries_.push_back(std::move(e));
     }

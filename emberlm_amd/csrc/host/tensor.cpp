@@ -30,6 +30,12 @@ class ReshapeBackward : public autograd::Node {
   const char* name() const override { return "ReshapeBackward"; }
 };
 
+[[noreturn]] void placeholder_access() {
+  throw std::runtime_error(
+      "tensor values are not computed: this tensor only carries autograd history "
+      "(a recompute placeholder); use it for backward() only");
+}
+
 int64_t shape_numel(const std::vector<int64_t>& shape) {
   int64_t n = 1;
   for (auto d : shape) {
@@ -98,6 +104,7 @@ Tensor Tensor::from_host(const void* host_data, std::vector<int64_t> shape, DTyp
 }
 
 void Tensor::copy_to_host(void* dst) const {
+  if (placeholder_) placeholder_access();
   if (!is_contiguous()) throw std::runtime_error("copy_to_host: tensor must be contiguous");
   const size_t nb = nbytes();
   if (nb == 0) return;
@@ -133,6 +140,7 @@ Tensor Tensor::reshape(std::vector<int64_t> new_shape) const {
   t.shape_ = std::move(new_shape);
   t.dtype_ = dtype_;
   t.device_ = device_;
+  t.placeholder_ = placeholder_;
   // ReshapeBackward as in src/core/tensor.cpp:17-25, 124-129 of the reference.
   if (autograd::any_requires_grad({*this})) {
     auto node = std::make_shared<ReshapeBackward>();
@@ -154,6 +162,7 @@ Tensor Tensor::view_at(int64_t offset, std::vector<int64_t> shape) const {
   t.shape_ = std::move(shape);
   t.dtype_ = dtype_;
   t.device_ = device_;
+  t.placeholder_ = placeholder_;
   return t;
 }
 
@@ -162,12 +171,14 @@ int64_t Tensor::numel() const { return shape_numel(shape_); }
 bool Tensor::is_contiguous() const { return strides_ == contiguous_strides(shape_); }
 
 void* Tensor::data_ptr() {
+  if (placeholder_) placeholder_access();
   if (!storage_) return nullptr;
   if (storage_->ready_event()) runtime::wait_ready(*storage_);
   return static_cast<char*>(storage_->data()) + storage_offset_ * dtype_size(dtype_);
 }
 
 const void* Tensor::data_ptr() const {
+  if (placeholder_) placeholder_access();
   if (!storage_) return nullptr;
   if (storage_->ready_event()) runtime::wait_ready(*storage_);
   return static_cast<const char*>(storage_->data()) + storage_offset_ * dtype_size(dtype_);

@@ -231,40 +231,46 @@ float lr_at_step(int step, const Config& c) {
 }
 
 float run_val(const nn::Model& model, const DataSplit& val, int seq_len, Device device) {
-  // The whole split goes to the device in one batch of copies; each document
-  // is then one forward over row views of it, its loss left on the device
-  // until every forward is queued, so the pass has no per-document round
-  // trip.  Weighting and skipping follow main.cpp:195-207: each document's
-  // masked-mean loss weighs by its own mask sum (summed in float, in token
-  // order, like make_host_batch), documents without targets are skipped, and
-  // the weighted sum is formed in double in document order.
+  // Documents go to the device in groups of about kValGroupTokens tokens (one
+  // batch of copies each); each document is then one forward over row views
+  // of its group, its loss left on the device until the group's forwards are
+  // queued, so a group has one round trip and the device holds one group's
+  // inputs at a time however large the split.  Weighting and skipping follow
+  // main.cpp:195-207: each document's masked-mean loss weighs by its own mask
+  // sum (summed in float, in token order, like make_host_batch), documents
+  // without targets are skipped, and the weighted sum is formed in double in
+  // document order.
+  constexpr int64_t kValGroupTokens = int64_t{1} << 20;
   if (val.num_docs == 0) return 0.0f;
-  std::vector<int64_t> all(static_cast<size_t>(val.num_docs));
-  for (int64_t i = 0; i < val.num_docs; ++i) all[static_cast<size_t>(i)] = i;
-  const HostBatch h = make_host_batch(val, all, seq_len);
-  const int64_t T = h.T;
-  const Tensor ids = Tensor::from_host(h.input_ids.data(), {h.B, T}, DType::kInt64, device);
-  const Tensor tgt = Tensor::from_host(h.targets.data(), {h.B, T}, DType::kInt64, device);
-  const Tensor msk = Tensor::from_host(h.loss_mask.data(), {h.B, T}, DType::kFloat32, device);
-
+  const int64_t per_group = std::max<int64_t>(1, kValGroupTokens / std::max(seq_len, 1));
   autograd::NoGradGuard no_grad;
-  std::vector<float> weight;
-  std::vector<Tensor> losses;
-  for (int64_t d = 0; d < h.B; ++d) {
-    float w = 0.0f;
-    for (int64_t t = 0; t < T; ++t) w += h.loss_mask[static_cast<size_t>(d * T + t)];
-    if (w <= 0.0f) continue;
-    losses.push_back(model.forward_train_masked(ids.view_at(d * T, {1, T}),
-                                                tgt.view_at(d * T, {1, T}),
-                                                msk.view_at(d * T, {1, T})));
-    weight.push_back(w);
-  }
   double num = 0.0, den = 0.0;
-  for (size_t i = 0; i < losses.size(); ++i) {
-    float l = 0.0f;
-    losses[i].copy_to_host(&l);
-    num += static_cast<double>(l) * static_cast<double>(weight[i]);
-    den += static_cast<double>(weight[i]);
+  for (int64_t d0 = 0; d0 < val.num_docs; d0 += per_group) {
+    const int64_t d1 = std::min(val.num_docs, d0 + per_group);
+    std::vector<int64_t> docs(static_cast<size_t>(d1 - d0));
+    for (int64_t i = d0; i < d1; ++i) docs[static_cast<size_t>(i - d0)] = i;
+    const HostBatch h = make_host_batch(val, docs, seq_len);
+    const int64_t T = h.T;
+    const Tensor ids = Tensor::from_host(h.input_ids.data(), {h.B, T}, DType::kInt64, device);
+    const Tensor tgt = Tensor::from_host(h.targets.data(), {h.B, T}, DType::kInt64, device);
+    const Tensor msk = Tensor::from_host(h.loss_mask.data(), {h.B, T}, DType::kFloat32, device);
+    std::vector<float> weight;
+    std::vector<Tensor> losses;
+    for (int64_t d = 0; d < h.B; ++d) {
+      float w = 0.0f;
+      for (int64_t t = 0; t < T; ++t) w += h.loss_mask[static_cast<size_t>(d * T + t)];
+      if (w <= 0.0f) continue;
+      losses.push_back(model.forward_train_masked(ids.view_at(d * T, {1, T}),
+                                                  tgt.view_at(d * T, {1, T}),
+                                                  msk.view_at(d * T, {1, T})));
+      weight.push_back(w);
+    }
+    for (size_t i = 0; i < losses.size(); ++i) {
+      float l = 0.0f;
+      losses[i].copy_to_host(&l);
+      num += static_cast<double>(l) * static_cast<double>(weight[i]);
+      den += static_cast<double>(weight[i]);
+    }
   }
   return den > 0.0 ? static_cast<float>(num / den) : 0.0f;
 }

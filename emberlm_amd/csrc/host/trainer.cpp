@@ -26,6 +26,7 @@
 #include "ctd/sampling.h"
 #include "ctd/train.h"
 #include "ctd_capi.h"
+#include "block_arena.h"
 
 using namespace ctd;
 
@@ -460,6 +461,24 @@ int ctd_trainer_offload_stats(ctd_trainer_t t, double* stream_ms, double* bytes_
   });
 }
 
+int ctd_trainer_offload_detail(ctd_trainer_t t, ctd_offload_detail* out) {
+  return guarded([&] {
+    if (!out) throw std::runtime_error("null argument");
+    Trainer* tr = as_trainer(t);
+    *out = ctd_offload_detail{};
+    if (!tr->opt || !tr->opt->is_offloaded()) return;
+    tr->opt->wait_idle();
+    const optim::OffloadStats& st = tr->opt->offload_stats();
+    out->stream_ms = st.last_stream_ms;
+    out->h2d_ms = st.last_h2d_ms;
+    out->d2h_ms = st.last_d2h_ms;
+    out->h2d_bytes = st.last_h2d_bytes;
+    out->d2h_bytes = st.last_d2h_bytes;
+    out->prefetch_bytes = st.last_prefetch_bytes;
+    out->skipped_bytes = st.last_skipped_bytes;
+  });
+}
+
 int ctd_trainer_set_prefetch_chunks(ctd_trainer_t t, int64_t chunks) {
   return guarded([&] {
     Trainer* tr = as_trainer(t);
@@ -492,8 +511,11 @@ int ctd_trainer_train_step(ctd_trainer_t t, float max_norm, ctd_step_times* time
     ember_event_t ev[5];
     for (auto& e : ev) CTD_CHECK(ember_event_create(&e));
     CTD_CHECK(ember_event_record(ev[0], cs));
+    mark_allocation_history("forward");
     Tensor loss = tr->model.forward_train_masked(tr->ids, tr->targets, tr->mask);
     CTD_CHECK(ember_event_record(ev[1], cs));
+    sample_device_memory();
+    mark_allocation_history("backward");
     {
       struct Arm {
         bool& flag;
@@ -503,6 +525,8 @@ int ctd_trainer_train_step(ctd_trainer_t t, float max_norm, ctd_step_times* time
       loss.backward();
     }
     CTD_CHECK(ember_event_record(ev[2], cs));
+    sample_device_memory();
+    mark_allocation_history("clip+step");
     float gn = 0.f;
     if (max_norm > 0.f) {
       gn = optim::clip_grad_norm_(clip_order(*tr), max_norm);
@@ -510,6 +534,7 @@ int ctd_trainer_train_step(ctd_trainer_t t, float max_norm, ctd_step_times* time
     CTD_CHECK(ember_event_record(ev[3], cs));
     tr->opt->step();
     CTD_CHECK(ember_event_record(ev[4], cs));
+    sample_device_memory();
     for (auto& [n, p] : tr->named.all) p.zero_grad_();
     float lv = 0.f;
     loss.copy_to_host(&lv);
@@ -551,11 +576,50 @@ int ctd_memory_stats(ctd_memory* out) {
     CTD_CHECK(ember_mem_get_info(&fr, &tot));
     out->device_used = tot - fr;
     out->device_total = tot;
+    out->peak_device_used = std::max<uint64_t>(s.peak_device_used_bytes, out->device_used);
+    out->device_mallocs = static_cast<uint64_t>(s.num_device_mallocs);
+    out->cache_flushes = static_cast<uint64_t>(s.num_cache_flushes);
+    out->limit = s.limit_bytes;
   });
 }
 
 int ctd_reset_peak_memory(void) {
   return guarded([] { reset_peak_device_memory(); });
+}
+
+int ctd_set_device_memory_limit(uint64_t bytes) {
+  return guarded([&] { set_device_memory_limit(static_cast<size_t>(bytes)); });
+}
+
+int ctd_empty_device_cache(void) {
+  return guarded([] { empty_device_cache(); });
+}
+
+int ctd_alloc_history_start(void) {
+  return guarded([] { start_allocation_history(); });
+}
+
+int ctd_alloc_history_mark(const char* label) {
+  return guarded([&] { mark_allocation_history(label ? label : ""); });
+}
+
+int ctd_alloc_history_stop(const char* path) {
+  return guarded([&] {
+    if (!path) throw std::runtime_error("null path");
+    stop_allocation_history(path);
+  });
+}
+
+int ctd_alloc_replay(const char* path, uint64_t limit, ctd_alloc_replay_stats* out) {
+  return guarded([&] {
+    if (!path || !out) throw std::runtime_error("null argument");
+    const detail::ArenaStats a = detail::replay_history(path, static_cast<size_t>(limit));
+    out->peak_allocated = a.peak_live_bytes;
+    out->peak_reserved = a.peak_held_bytes;
+    out->reserved_end = a.held_bytes;
+    out->segments_obtained = static_cast<uint64_t>(a.segments_obtained);
+    out->cache_flushes = static_cast<uint64_t>(a.trims);
+  });
 }
 
 int ctd_gemm_profile_enable(int32_t on) {

@@ -638,7 +638,11 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce(const float* __restric
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (i >= M * cols) return;
   const int64_t m = i / cols, n = (i % cols) * per;
-  if (dyn && m >= min(max(*dyn - dyn_base, int64_t{0}), M)) return;  // rows not needed
+  // Rows past the device-side count are not needed, except up to its 16-row
+  // group: a later dyn_dim 1 product reads K rounded up to 16, and those rows
+  // (products of zero-filled operand rows) must hold their zeros, as the
+  // unsplit tiles store them.
+  if (dyn && m >= min((max(*dyn - dyn_base, int64_t{0}) + 15) / 16 * 16, M)) return;
   const int64_t plane = M * N;
   if (VEC) {
     f32x4 s = *reinterpret_cast<const f32x4*>(P + m * N + n);

@@ -1,10 +1,14 @@
-// AdamW update and the grad-norm sum of squares.
+// AdamW update, SGD, and the gradient-clipping sum of squares and scale.
 //
 // Reference: adamw_step_kernel_f32 (src/core/optim.cu:54-73) and
 // sum_sq_kernel_f32 + atomicAdd (optim.cu:221-239).  The AdamW kernel is the
 // same element formula streamed as float4 (28 bytes per parameter of HBM
 // traffic); the sum of squares is a two-stage fixed-order reduction so the
-// clip norm is reproducible.
+// clip norm is reproducible, all of a model's gradients in one launch (the
+// reference launches one kernel per parameter, optim.cu:262-270, and scales
+// them one by one, optim.cu:277-289).
+#include <mutex>
+
 #include "common.h"
 
 // No FMA contraction in this file: the float4 and scalar paths (taken for
@@ -71,16 +75,39 @@ __global__ __launch_bounds__(kThreads) void adamw_kernel(float* __restrict__ p,
   }
 }
 
-// part[block] = the block's sum of x[i]^2 over a fixed set of i, in a fixed
-// order (four running sums per lane, then a fixed tree), so the total does
-// not depend on timing.
+// One tensor of a batched launch: its elements, the first block of the
+// launch that is its (also its first partial), its number of blocks, and
+// whether its float4 loads are aligned.
+struct ListItem {
+  const float* x;
+  int64_t n;
+  int64_t first;
+  int32_t blocks;
+  int32_t vec;
+};
+
+// The tensor that block `blk` of a batched launch works on (items sorted by
+// `first`, which starts at 0).
+__device__ __forceinline__ ListItem find_item(const ListItem* __restrict__ items, int count,
+                                              int64_t blk) {
+  int lo = 0, hi = count - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) / 2;
+    if (items[mid].first <= blk) lo = mid;
+    else hi = mid - 1;
+  }
+  return items[lo];
+}
+
+// Block b of nb: its sum of x[i]^2 over a fixed set of i, in a fixed order
+// (four running sums per lane, then a fixed tree), so the total does not
+// depend on timing or on how the tensors are grouped into launches.
 template <bool VEC>
-__global__ __launch_bounds__(kThreads) void sumsq_partial(const float* __restrict__ x, int64_t n,
-                                                          float* __restrict__ part) {
-  __shared__ float red[kThreads / kWave];
+__device__ __forceinline__ float sumsq_block(const float* __restrict__ x, int64_t n, int64_t b,
+                                             int64_t nb, float* red) {
   float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
-  const int64_t tid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t stride = nb * kThreads;
+  const int64_t tid = b * kThreads + threadIdx.x;
   int64_t tail = 0;
   if (VEC) {
     const int64_t n4 = n / 4;
@@ -100,9 +127,35 @@ __global__ __launch_bounds__(kThreads) void sumsq_partial(const float* __restric
     tail = n4 * 4;
   }
   for (int64_t j = tail + tid; j < n; j += stride) a0 += x[j] * x[j];
-  float a = (a0 + a1) + (a2 + a3);
-  a = block_sum(a, red);
+  return block_sum((a0 + a1) + (a2 + a3), red);
+}
+
+// All tensors of a list in one launch: part[block] = that block's partial.
+__global__ __launch_bounds__(kThreads) void sumsq_list(const ListItem* __restrict__ items,
+                                                       int count, float* __restrict__ part) {
+  __shared__ float red[kThreads / kWave];
+  const ListItem it = find_item(items, count, blockIdx.x);
+  const int64_t b = static_cast<int64_t>(blockIdx.x) - it.first;
+  const float a = it.vec ? sumsq_block<true>(it.x, it.n, b, it.blocks, red)
+                         : sumsq_block<false>(it.x, it.n, b, it.blocks, red);
   if (threadIdx.x == 0) part[blockIdx.x] = a;
+}
+
+// x *= alpha for every tensor of a list in one launch.
+__global__ __launch_bounds__(kThreads) void scale_list(const ListItem* __restrict__ items,
+                                                       int count, float alpha) {
+  const ListItem it = find_item(items, count, blockIdx.x);
+  float* x = const_cast<float*>(it.x);
+  const int64_t stride = static_cast<int64_t>(it.blocks) * kThreads;
+  const int64_t tid = (static_cast<int64_t>(blockIdx.x) - it.first) * kThreads + threadIdx.x;
+  int64_t tail = 0;
+  if (it.vec) {
+    f32x4* x4 = reinterpret_cast<f32x4*>(x);
+    const int64_t n4 = it.n / 4;
+    for (int64_t i = tid; i < n4; i += stride) x4[i] = x4[i] * alpha;
+    tail = n4 * 4;
+  }
+  for (int64_t j = tail + tid; j < it.n; j += stride) x[j] = x[j] * alpha;
 }
 
 // out[0] = sum of the np partials in double, in a fixed order: four running
@@ -134,7 +187,9 @@ __global__ __launch_bounds__(kPartsThreads) void sum_parts(const float* __restri
 
 namespace {
 
-// p -= lr * g, two roundings (contraction is off in this file).
+// p -= lr * g as one fused multiply-add, fma(-lr, g, p): the single rounding
+// nvcc gives the reference's sgd_step_kernel_f32 (src/core/optim.cu:14-20),
+// whose p[i] -= lr * g[i] it contracts by default (-fmad=true).
 template <bool VEC>
 __global__ __launch_bounds__(kThreads) void sgd_kernel(float* __restrict__ p,
                                                        const float* __restrict__ g, int64_t n,
@@ -146,12 +201,12 @@ __global__ __launch_bounds__(kThreads) void sgd_kernel(float* __restrict__ p,
       f32x4 pp = reinterpret_cast<f32x4*>(p)[i];
       const f32x4 gg = reinterpret_cast<const f32x4*>(g)[i];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) pp[e] = pp[e] - lr * gg[e];
+      for (int e = 0; e < 4; ++e) pp[e] = __builtin_fmaf(-lr, gg[e], pp[e]);
       reinterpret_cast<f32x4*>(p)[i] = pp;
     }
-    for (int64_t i = n / 4 * 4 + tid; i < n; i += stride) p[i] = p[i] - lr * g[i];
+    for (int64_t i = n / 4 * 4 + tid; i < n; i += stride) p[i] = __builtin_fmaf(-lr, g[i], p[i]);
   } else {
-    for (int64_t i = tid; i < n; i += stride) p[i] = p[i] - lr * g[i];
+    for (int64_t i = tid; i < n; i += stride) p[i] = __builtin_fmaf(-lr, g[i], p[i]);
   }
 }
 
@@ -196,8 +251,83 @@ extern "C" int ember_adamw_bounded(float* p, const float* g, float* m, float* v,
   return launch_status();
 }
 
+namespace {
+
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+// Page-locked staging for the item tables of batched launches: written on the
+// host, copied to the caller's workspace on the launch's stream.  The copy of
+// one call must have left before the next call rewrites the table.
+struct ListStaging {
+  std::mutex mu;
+  ListItem* host = nullptr;
+  size_t cap = 0;
+  hipEvent_t copied = nullptr;
+};
+ListStaging& staging() {
+  static ListStaging* s = new ListStaging();  // lives as long as the process
+  return *s;
+}
+
+// Builds the item table of `count` tensors (blocks per tensor from
+// blocks_of(n), 0 for empty tensors) and copies it to `dev_items` on stream
+// st; returns the total number of blocks, or a negative status.
+template <typename BlocksOf>
+int64_t upload_items(const float* const* ptrs, const int64_t* sizes, int count, ListItem* dev_items,
+                     hipStream_t st, BlocksOf blocks_of, int* kept) {
+  ListStaging& sg = staging();
+  std::lock_guard<std::mutex> lk(sg.mu);
+  if (sg.copied) {
+    const hipError_t e = hipEventSynchronize(sg.copied);
+    if (e != hipSuccess) return -status_of(e);
+  } else if (hipEventCreateWithFlags(&sg.copied, hipEventDisableTiming) != hipSuccess) {
+    return -EMBER_EINVAL;
+  }
+  if (sg.cap < static_cast<size_t>(count)) {
+    if (sg.host) (void)hipHostFree(sg.host);
+    sg.host = nullptr;
+    sg.cap = 0;
+    void* h = nullptr;
+    const hipError_t e = hipHostMalloc(&h, static_cast<size_t>(count) * sizeof(ListItem));
+    if (e != hipSuccess) return -status_of(e);
+    sg.host = static_cast<ListItem*>(h);
+    sg.cap = static_cast<size_t>(count);
+  }
+  int64_t total = 0;
+  int m = 0;
+  for (int i = 0; i < count; ++i) {
+    const int64_t n = sizes[i];
+    if (n < 0 || (n > 0 && !ptrs[i])) return -EMBER_EINVAL;
+    if (n == 0) continue;
+    const int64_t nb = blocks_of(n);
+    sg.host[m++] = ListItem{ptrs[i], n, total, static_cast<int32_t>(nb),
+                            aligned16(ptrs[i]) ? 1 : 0};
+    total += nb;
+  }
+  *kept = m;
+  if (m == 0) return 0;
+  hipError_t e = hipMemcpyAsync(dev_items, sg.host, static_cast<size_t>(m) * sizeof(ListItem),
+                                hipMemcpyHostToDevice, st);
+  if (e == hipSuccess) e = hipEventRecord(sg.copied, st);
+  return e == hipSuccess ? total : -status_of(e);
+}
+
+int64_t sumsq_blocks_of(int64_t n) {
+  const int64_t nb = (n + kThreads * kSumsqPerThread - 1) / (kThreads * kSumsqPerThread);
+  return nb < kSumsqBlocksPerTensor ? nb : kSumsqBlocksPerTensor;
+}
+
+int64_t scale_blocks_of(int64_t n) {
+  const int64_t nb = (n + kThreads * 16 - 1) / (kThreads * 16);
+  return nb < 1024 ? nb : 1024;
+}
+
+}  // namespace
+
 extern "C" size_t ember_sumsq_workspace_bytes(int count) {
-  return count > 0 ? static_cast<size_t>(count) * kSumsqBlocksPerTensor * sizeof(float) : 0;
+  if (count <= 0) return 0;
+  return align256(static_cast<size_t>(count) * kSumsqBlocksPerTensor * sizeof(float)) +
+         static_cast<size_t>(count) * sizeof(ListItem);
 }
 
 extern "C" int ember_sumsq_multi(const float* const* ptrs_host, const int64_t* sizes_host, int count,
@@ -208,21 +338,38 @@ extern "C" int ember_sumsq_multi(const float* const* ptrs_host, const int64_t* s
   if (count == 0) return ember_fill(out, 1, 0.f, s);
   if (!workspace || workspace_bytes < ember_sumsq_workspace_bytes(count)) return EMBER_EWORKSPACE;
   float* part = static_cast<float*>(workspace);
-  int64_t np = 0;
-  for (int i = 0; i < count; ++i) {
-    const int64_t n = sizes_host[i];
-    if (n < 0 || (n > 0 && !ptrs_host[i])) return EMBER_EINVAL;
-    if (n == 0) continue;
-    int64_t nb = (n + kThreads * kSumsqPerThread - 1) / (kThreads * kSumsqPerThread);
-    if (nb > kSumsqBlocksPerTensor) nb = kSumsqBlocksPerTensor;
-    if (aligned16(ptrs_host[i]))
-      sumsq_partial<true><<<static_cast<unsigned>(nb), kThreads, 0, st>>>(ptrs_host[i], n, part + np);
-    else
-      sumsq_partial<false><<<static_cast<unsigned>(nb), kThreads, 0, st>>>(ptrs_host[i], n, part + np);
-    const int rc = launch_status();
-    if (rc) return rc;
-    np += nb;
-  }
+  ListItem* items = reinterpret_cast<ListItem*>(
+      static_cast<char*>(workspace) +
+      align256(static_cast<size_t>(count) * kSumsqBlocksPerTensor * sizeof(float)));
+  int kept = 0;
+  const int64_t np = upload_items(ptrs_host, sizes_host, count, items, st, sumsq_blocks_of, &kept);
+  if (np < 0) return static_cast<int>(-np);
+  if (np == 0) return ember_fill(out, 1, 0.f, s);
+  sumsq_list<<<static_cast<unsigned>(np), kThreads, 0, st>>>(items, kept, part);
+  int rc = launch_status();
+  if (rc) return rc;
   sum_parts<<<1, kPartsThreads, 0, st>>>(part, np, out);
+  return launch_status();
+}
+
+extern "C" size_t ember_scale_multi_workspace_bytes(int count) {
+  return count > 0 ? static_cast<size_t>(count) * sizeof(ListItem) : 0;
+}
+
+extern "C" int ember_scale_multi(float* const* ptrs_host, const int64_t* sizes_host, int count,
+                                 float alpha, void* workspace, size_t workspace_bytes,
+                                 ember_stream_t s) {
+  if (count < 0 || (count > 0 && (!ptrs_host || !sizes_host))) return EMBER_EINVAL;
+  if (count == 0) return EMBER_OK;
+  if (!workspace || workspace_bytes < ember_scale_multi_workspace_bytes(count))
+    return EMBER_EWORKSPACE;
+  hipStream_t st = as_stream(s);
+  ListItem* items = static_cast<ListItem*>(workspace);
+  int kept = 0;
+  const int64_t nb = upload_items(const_cast<const float* const*>(ptrs_host), sizes_host, count,
+                                  items, st, scale_blocks_of, &kept);
+  if (nb < 0) return static_cast<int>(-nb);
+  if (nb == 0) return EMBER_OK;
+  scale_list<<<static_cast<unsigned>(nb), kThreads, 0, st>>>(items, kept, alpha);
   return launch_status();
 }

@@ -36,7 +36,18 @@ class StepTimes(C.Structure):
 class Memory(C.Structure):
     _fields_ = [(n, C.c_uint64) for n in ("allocated", "peak_allocated", "reserved",
                                           "peak_reserved", "pinned_host", "device_used",
-                                          "device_total")]
+                                          "device_total", "peak_device_used", "device_mallocs",
+                                          "cache_flushes", "limit")]
+
+
+class OffloadDetail(C.Structure):
+    _fields_ = [(n, C.c_double) for n in ("stream_ms", "h2d_ms", "d2h_ms", "h2d_bytes",
+                                          "d2h_bytes", "prefetch_bytes", "skipped_bytes")]
+
+
+class AllocReplay(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("peak_allocated", "peak_reserved", "reserved_end",
+                                          "segments_obtained", "cache_flushes")]
 
 
 class GemmProfile(C.Structure):
@@ -73,11 +84,18 @@ _SIGS = {
     "ctd_trainer_offload_stats": (i32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_double),
                                         C.POINTER(C.c_double)]),
     "ctd_trainer_set_prefetch_chunks": (i32, [vp, i64]),
+    "ctd_trainer_offload_detail": (i32, [vp, C.POINTER(OffloadDetail)]),
     "ctd_trainer_set_prefetch_layer": (i32, [vp, i32]),
     "ctd_trainer_train_step": (i32, [vp, f32, C.POINTER(StepTimes)]),
     "ctd_trainer_synchronize": (i32, [vp]),
     "ctd_memory_stats": (i32, [C.POINTER(Memory)]),
     "ctd_reset_peak_memory": (i32, []),
+    "ctd_set_device_memory_limit": (i32, [u64]),
+    "ctd_empty_device_cache": (i32, []),
+    "ctd_alloc_history_start": (i32, []),
+    "ctd_alloc_history_mark": (i32, [C.c_char_p]),
+    "ctd_alloc_history_stop": (i32, [C.c_char_p]),
+    "ctd_alloc_replay": (i32, [C.c_char_p, u64, C.POINTER(AllocReplay)]),
     "ctd_gemm_profile_enable": (i32, [i32]),
     "ctd_gemm_profile_collect": (i32, [C.POINTER(GemmProfile)]),
     "ctd_trainer_save": (i32, [vp, C.c_char_p]),
@@ -156,6 +174,31 @@ def memory() -> Memory:
 
 def reset_peak_memory():
     _ck(lib().ctd_reset_peak_memory(), "reset_peak_memory")
+
+
+def set_memory_limit(nbytes: int):
+    """Caps the bytes the device allocator holds (0: no cap)."""
+    _ck(lib().ctd_set_device_memory_limit(int(nbytes)), "set_memory_limit")
+
+
+def empty_cache():
+    _ck(lib().ctd_empty_device_cache(), "empty_cache")
+
+
+def alloc_history_start():
+    _ck(lib().ctd_alloc_history_start(), "alloc_history_start")
+
+
+def alloc_history_stop(path: str):
+    _ck(lib().ctd_alloc_history_stop(str(path).encode()), "alloc_history_stop")
+
+
+def alloc_replay(path: str, limit: int = 0) -> AllocReplay:
+    """Replays a recorded allocation history on the allocator's placement
+    policy (host only, no GPU)."""
+    r = AllocReplay()
+    _ck(lib().ctd_alloc_replay(str(path).encode(), int(limit), C.byref(r)), "alloc_replay")
+    return r
 
 
 def gemm_profile(enable=None):
@@ -295,6 +338,12 @@ class Trainer:
         _ck(lib().ctd_trainer_offload_stats(self.h, C.byref(ms), C.byref(b), C.byref(pf)),
             "offload_stats")
         return ms.value, b.value, pf.value
+
+    def offload_detail(self) -> OffloadDetail:
+        """Per-direction device times and bytes of the last finished offloaded step."""
+        d = OffloadDetail()
+        _ck(lib().ctd_trainer_offload_detail(self.h, C.byref(d)), "offload_detail")
+        return d
 
     def set_prefetch_chunks(self, chunks):
         """Cap (in optimizer-state chunks) of the m/v that train_step's backward
@@ -441,5 +490,6 @@ def param_count(cfg: ModelConfig) -> int:
 
 
 __all__ = ["ModelConfig", "Trainer", "preset", "make_config", "memory", "reset_peak_memory",
-           "gemm_profile", "param_count", "StepTimes", "train_run", "lr_at_step", "host_batch",
+           "set_memory_limit", "empty_cache", "alloc_history_start", "alloc_history_stop",
+           "alloc_replay", "gemm_profile", "param_count", "StepTimes", "train_run", "lr_at_step", "host_batch",
            "event_json", "KVCache", "sample", "math"]

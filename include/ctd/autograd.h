@@ -19,6 +19,7 @@ struct Edge {
 
 class Node {
  public:
+  Node();
   virtual ~Node() = default;
   virtual std::vector<Tensor> backward(const std::vector<Tensor>& grads_out) = 0;
   // A node that accepts partials is run through backward_with_partials: for
@@ -38,6 +39,11 @@ class Node {
   // Set once a backward pass that does not retain the graph has run this
   // node and released its edges.
   bool consumed = false;
+  // Creation order (process-wide counter).  Among the nodes whose inputs are
+  // complete, the engine runs the most recently created one first (leaf
+  // gradient sinks before any), i.e. the forward in reverse.  Added in this
+  // build.
+  const uint64_t sequence_nr;
 };
 
 struct AutogradMeta {

@@ -61,15 +61,16 @@ struct TransformerBlock {
   // forward_train(x) for a checkpoint's recompute, whose backward reads only
   // the graph of the block's output: down_proj and the last residual add are
   // recorded but not run, so the returned tensor has forward_train(x)'s
-  // grad_fn and h's values (not the block's output).  Its gradients are
-  // forward_train's, kernel for kernel.  The checkpointed forward already
-  // computed the real output: it is the next block's saved input.
+  // grad_fn but no values of its own (a placeholder: data_ptr() and
+  // copy_to_host() throw).  Its gradients are forward_train's, kernel for
+  // kernel.  The checkpointed forward already computed the real output: it is
+  // the next block's saved input.
   Tensor forward_train_for_backward(const Tensor& x) const {
     Tensor h1 = input_layernorm.forward(x);
     Tensor h = self_attn.o_proj.forward_add(self_attn.forward_train_context(h1), x);
     Tensor h2 = post_attention_layernorm.forward(h);
     Tensor m = mlp.down_proj.forward_graph_only(mlp.activation(h2), h);
-    return ops::add_graph_only(h, m.reshape(h.shape()), h);
+    return ops::add_graph_only(h, m.reshape(h.shape()), h).mark_placeholder();
   }
 };
 

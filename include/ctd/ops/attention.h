@@ -14,11 +14,14 @@ Tensor causal_attention(const Tensor& q, const Tensor& k, const Tensor& v, float
 // passes (ember_attn_bwd): less than a layer's full dS splits the pass into
 // chunks of KV heads, 0 recomputes dS in the dQ pass instead; -1 restores the
 // default (kAttentionBackwardDsBytes).  Results do not depend on it.  The
-// default holds Qwen3-1.7B's dS at B=8, T=4096 (4.4 GB per layer) in two
-// chunks, which leaves the step's peak HBM where it is (the workspace is live
-// only while a layer's backward runs) at 1.7% more attention-backward time
-// than one chunk; smaller models fit in one.
-constexpr int64_t kAttentionBackwardDsBytes = 2500000000;
+// default holds Qwen3-1.7B's dS at B=8, T=4096 (4.4 GB per layer) in four
+// chunks, and the backward takes less than that when the device allocator
+// holds no free block that large but one of at least half of it.  A budget of
+// 2.5 GB (two chunks) ran 0.67 ms per layer faster there, but no block that
+// size stays free among the checkpoints and gradients of a step, so the
+// allocator grew by 2.4 GB at a time and held 1.32x the live bytes (1.10x at
+// this default); smaller models fit in one or two chunks.
+constexpr int64_t kAttentionBackwardDsBytes = 1250000000;
 void set_attention_backward_ds_bytes(int64_t bytes);
 // Forward only; lse (if non-null) receives the [B,H,T] log-sum-exp.
 Tensor causal_attention_impl(const Tensor& q, const Tensor& k, const Tensor& v, float scale,

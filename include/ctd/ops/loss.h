@@ -27,7 +27,7 @@ Tensor cross_entropy_masked_impl(const Tensor& logits, const Tensor& targets,
 Tensor linear_cross_entropy_masked(const Tensor& h, const Tensor& w, const Tensor& targets,
                                    const Tensor& loss_mask);
 // Rows per chunk of linear_cross_entropy_masked (process-wide); 0 restores the
-// automatic choice (about 2.5 GB of logits per chunk).
+// automatic choice (about 0.64 GB of logits per chunk).
 void set_linear_cross_entropy_chunk_rows(int64_t rows);
 // Whether linear_cross_entropy_masked computes only the active rows where it
 // can (default true; false runs every row, for comparisons).

@@ -55,6 +55,16 @@ struct OffloadStats {
   // Bytes per direction (m and v) of the last step's state that prefetch()
   // had copied in before step(); last_h2d_bytes excludes them.
   double last_prefetch_bytes = 0.0;
+  // Device time of each direction in the most recent finished step: the
+  // copies in from the first to the last (on the h2d stream), the copies out
+  // from the first to the last (on the d2h stream, with the updates between
+  // them).  Rates per direction are last_h2d_bytes / last_h2d_ms and
+  // last_d2h_bytes / last_d2h_ms.
+  double last_h2d_ms = 0.0;
+  double last_d2h_ms = 0.0;
+  // Bytes per direction the last step did not move because no parameter in
+  // them had a gradient (frozen or unused parameters keep their m/v on the host).
+  double last_skipped_bytes = 0.0;
 };
 
 class AdamW {
@@ -164,6 +174,8 @@ class AdamW {
   void* ev_pf_ready_ = nullptr;    // compute stream: the buffer's memory is free
   void* ev_pf_loaded_ = nullptr;   // h2d stream: the prefetch copies are done
   void* ev_pf_drained_ = nullptr;  // d2h stream: its chunks are copied out
+  void* ev_h2d_end_ = nullptr;     // h2d stream: after the step's last copy in
+  void* ev_d2h_begin_ = nullptr;   // d2h stream: before the step's first copy out
 };
 
 // Global L2 norm clipping; returns the pre-clip total norm.

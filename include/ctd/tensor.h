@@ -52,6 +52,17 @@ class Tensor {
   const StoragePtr& storage() const { return storage_; }
   int64_t storage_offset() const { return storage_offset_; }
 
+  // A tensor that carries autograd history but whose elements are not its
+  // values (the recompute form of a checkpointed block's output, the product
+  // node of a GEMM fused with an add): backward() works through it, while
+  // data_ptr() and copy_to_host() throw.  Views of it are placeholders too.
+  // Added in this build.
+  bool is_placeholder() const { return placeholder_; }
+  Tensor& mark_placeholder() {
+    placeholder_ = true;
+    return *this;
+  }
+
   // Autograd interface.
   Tensor& requires_grad_(bool v = true);
   bool requires_grad() const;
@@ -78,6 +89,7 @@ class Tensor {
   DType dtype_ = DType::kFloat32;
   Device device_{};
   std::shared_ptr<autograd::AutogradMeta> autograd_meta_;
+  bool placeholder_ = false;
 };
 
 std::vector<int64_t> contiguous_strides(const std::vector<int64_t>& shape);

@@ -39,8 +39,18 @@ typedef struct ctd_step_times {
 
 typedef struct ctd_memory {
   uint64_t allocated, peak_allocated, reserved, peak_reserved, pinned_host;
-  uint64_t device_used, device_total; /* hipMemGetInfo: total - free, total */
+  uint64_t device_used, device_total; /* hipMemGetInfo now: total - free, total */
+  /* Highest hipMemGetInfo total - free since ctd_reset_peak_memory, sampled
+   * whenever the allocator obtains a segment and at each train step's phase
+   * boundaries; the allocator's segments obtained and cache flushes (segments
+   * given back to serve a request); its cap (0: none). */
+  uint64_t peak_device_used, device_mallocs, cache_flushes, limit;
 } ctd_memory;
+
+/* Statistics of an allocation history replayed on the host (ctd_alloc_replay). */
+typedef struct ctd_alloc_replay_stats {
+  uint64_t peak_allocated, peak_reserved, reserved_end, segments_obtained, cache_flushes;
+} ctd_alloc_replay_stats;
 
 typedef struct ctd_gemm_profile {
   int64_t launches;
@@ -114,6 +124,16 @@ int ctd_trainer_offload_stats(ctd_trainer_t t, double* stream_ms, double* bytes_
  * prefetches for the offloaded step (default 32; 0 turns the prefetch off).
  * The staged m/v of the first parameter are device memory held from late in
  * the backward until their copy out. */
+/* Per-direction figures of the most recent finished offloaded step
+ * (optim::OffloadStats): device ms of the copies in (first to last) and of the
+ * copies out with the updates between them, the bytes each moved (m and v
+ * together), the prefetched bytes per direction and the bytes per direction
+ * left on the host because no parameter in them had a gradient. */
+typedef struct ctd_offload_detail {
+  double stream_ms, h2d_ms, d2h_ms, h2d_bytes, d2h_bytes, prefetch_bytes, skipped_bytes;
+} ctd_offload_detail;
+int ctd_trainer_offload_detail(ctd_trainer_t t, ctd_offload_detail* out);
+
 int ctd_trainer_set_prefetch_chunks(ctd_trainer_t t, int64_t chunks);
 /* Layer whose re-run in train_step's backward starts that prefetch: a layer
  * index, -1 for none, or -2 (the default) for ctd::train's estimate from the
@@ -127,6 +147,19 @@ int ctd_trainer_train_step(ctd_trainer_t t, float max_norm, ctd_step_times* time
 int ctd_trainer_synchronize(ctd_trainer_t t);
 int ctd_memory_stats(ctd_memory* out);
 int ctd_reset_peak_memory(void);
+/* Caps the bytes the device allocator holds (0: no cap); see
+ * ctd::set_device_memory_limit. */
+int ctd_set_device_memory_limit(uint64_t bytes);
+/* Gives cached free segments back to the driver (synchronises). */
+int ctd_empty_device_cache(void);
+/* Allocation history (ctd::start_allocation_history): start, label, stop and
+ * write to path. */
+int ctd_alloc_history_start(void);
+int ctd_alloc_history_mark(const char* label);
+int ctd_alloc_history_stop(const char* path);
+/* Replays a recorded history on the allocator's placement policy with a
+ * host-only backend (no GPU needed); limit as for the device allocator. */
+int ctd_alloc_replay(const char* path, uint64_t limit, ctd_alloc_replay_stats* out);
 
 /* Kernel timing: while enabled, every ember_gemm_f32 and fused-attention call
  * launched by the ops layer is bracketed by HIP events on the compute stream;

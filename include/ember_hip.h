@@ -447,8 +447,9 @@ int ember_embedding_bwd(const int64_t* ids, const float* dy, float* dw, int64_t 
                         ember_stream_t s);
 
 /* -------------------------------------------------------------------- SGD
- * p -= lr * g, as p - (lr * g) with two roundings (sgd_step_kernel_f32,
- * src/core/optim.cu:14-20, launched per parameter by SGD::step, optim.cu:29-44). */
+ * p -= lr * g as one fused multiply-add, fma(-lr, g, p) (sgd_step_kernel_f32,
+ * src/core/optim.cu:14-20, launched per parameter by SGD::step, optim.cu:29-44,
+ * whose p[i] -= lr * g[i] nvcc contracts to one FMA by default). */
 int ember_sgd(float* p, const float* g, int64_t n, float lr, ember_stream_t s);
 
 /* ------------------------------------------------------------------ AdamW
@@ -467,12 +468,22 @@ int ember_adamw_bounded(float* p, const float* g, float* m, float* v, int64_t n,
                         int max_blocks, ember_stream_t s);
 
 /* ------------------------------------------------------- grad-norm clip
- * out[0] = sum over tensors of sum(g^2), fixed-order two-stage reduction.
- * ptrs/sizes are host arrays of `count` device pointers and lengths.
- * Replaces sum_sq_kernel_f32 + atomicAdd (src/core/optim.cu:221-239). */
+ * out[0] = sum over tensors of sum(g^2), fixed-order two-stage reduction,
+ * all tensors in one launch (plus the final sum).  ptrs/sizes are host
+ * arrays of `count` device pointers and lengths; the call copies a table of
+ * them into the workspace on stream s.  Replaces the per-parameter
+ * sum_sq_kernel_f32 launches + atomicAdd of clip_grad_norm_
+ * (src/core/optim.cu:221-239, 262-270). */
 size_t ember_sumsq_workspace_bytes(int count);
 int ember_sumsq_multi(const float* const* ptrs_host, const int64_t* sizes_host, int count,
                       float* out, void* workspace, size_t workspace_bytes, ember_stream_t s);
+/* x *= alpha in place for every tensor of a host list (device pointers and
+ * lengths), in one launch; the workspace holds the list's table.  Replaces
+ * clip_grad_norm_'s per-parameter scale_kernel_f32 launches
+ * (src/core/optim.cu:241-245, 277-289). */
+size_t ember_scale_multi_workspace_bytes(int count);
+int ember_scale_multi(float* const* ptrs_host, const int64_t* sizes_host, int count, float alpha,
+                      void* workspace, size_t workspace_bytes, ember_stream_t s);
 
 #ifdef __cplusplus
 }

@@ -21,9 +21,11 @@
 #include "ctd/nn/kv_cache.h"
 #include "ctd/nn/model.h"
 #include "ctd/ops/elementwise.h"
+#include "ctd/ops/loss.h"
 #include "ctd/ops/matmul.h"
 #include "ctd/ops/repeat_kv.h"
 #include "ctd/optim.h"
+#include "ctd/runtime.h"
 #include "ctd/safetensors.h"
 #include "ctd/tensor.h"
 #include "ember_oracle.h"
@@ -294,6 +296,77 @@ void prefetch_then_host_state_change() {
   check(finals[0] == finals[1], "prefetch leaves the weights bits unchanged");
 }
 
+// The offloaded step moves m/v only for parameters that have a gradient (the
+// reference skips the others, src/core/optim.cu:183): with some parameters'
+// gradients dropped before each step, the offloaded run equals the on-device
+// run bit for bit (weights and m/v), the dropped parameters' state stays zero
+// on the host, and exactly their chunks are not transferred.
+void offload_skips_state_without_grad() {
+  const int B = 2, T = 4;
+  std::vector<int64_t> hx = {1, 4, 0, 6, 7, 2, 3, 5};
+  std::vector<int64_t> hy = {4, 0, 6, 3, 2, 3, 5, 1};
+  TinyCfg c;
+  c.L = 2;
+  std::vector<std::vector<float>> weights[2], ms[2], vs[2];
+  double moved = -1.0, skipped = -1.0;
+  int64_t frozen_elems = 0, graded_elems = 0;
+  for (int variant = 0; variant < 2; ++variant) {  // 0: on the device, 1: offloaded
+    std::mt19937 rng(7);
+    nn::Model m = build_tiny(c, rng, /*grad=*/true);
+    Tensor x = Tensor::from_host(hx.data(), {B, T}, DType::kInt64, kHIP0);
+    Tensor y = Tensor::from_host(hy.data(), {B, T}, DType::kInt64, kHIP0);
+    std::vector<Tensor> ps = params_of(m);
+    optim::AdamW opt(ps, /*lr=*/1e-2f, /*wd=*/0.1f, 0.9f, 0.95f, 1e-8f, variant == 1);
+    opt.set_offload_chunk(64);  // parameters start on 64-float boundaries: one owner per chunk
+    opt.set_prefetch_chunks(0);
+    // Dropped: every parameter of layer 1 and layer 0's q_proj.
+    std::vector<std::string> names;
+    for (const auto& [name, t] : m.collect_parameters().all) names.push_back(name);
+    auto dropped = [&](size_t i) {
+      return names[i].find("layers.1.") != std::string::npos ||
+             names[i].find("layers.0.self_attn.q_proj") != std::string::npos;
+    };
+    for (int step = 0; step < 2; ++step) {
+      opt.zero_grad();
+      Tensor loss = m.forward_train(x, y);
+      loss.backward();
+      for (size_t i = 0; i < ps.size(); ++i)
+        if (dropped(i)) ps[i].zero_grad_();
+      opt.step();
+      opt.wait_idle();
+    }
+    frozen_elems = graded_elems = 0;
+    for (size_t i = 0; i < ps.size(); ++i) {
+      if (!dropped(i)) graded_elems += ps[i].numel();
+      weights[variant].push_back(host(ps[i]));
+      ms[variant].push_back(host(opt.m_tensor(0, i)));
+      vs[variant].push_back(host(opt.v_tensor(0, i)));
+      if (dropped(i)) {
+        frozen_elems += (ps[i].numel() + 63) / 64 * 64;
+        const auto& mm = ms[variant].back();
+        const auto& vv = vs[variant].back();
+        check(std::all_of(mm.begin(), mm.end(), [](float f) { return f == 0.0f; }) &&
+                  std::all_of(vv.begin(), vv.end(), [](float f) { return f == 0.0f; }),
+              "state of a parameter without gradient stays zero");
+      }
+    }
+    if (variant == 1) {
+      moved = opt.offload_stats().last_h2d_bytes;
+      skipped = opt.offload_stats().last_skipped_bytes;
+    }
+  }
+  check(weights[0] == weights[1], "offloaded weights equal on-device bitwise");
+  check(ms[0] == ms[1] && vs[0] == vs[1], "offloaded m/v equal on-device bitwise");
+  // Each 64-float chunk holds one parameter (and its padding to 256 bytes):
+  // only the elements of parameters with a gradient cross the link, m and v.
+  check(moved == 8.0 * static_cast<double>(graded_elems),
+        "only parameters with a gradient are moved (" + std::to_string(moved) + " B, expected " +
+            std::to_string(8 * graded_elems) + ")");
+  check(frozen_elems > 0 && skipped >= 8.0 * static_cast<double>(frozen_elems),
+        "the dropped parameters' chunks stay on the host (skipped " + std::to_string(skipped) +
+            " B)");
+}
+
 // reference test_integration_kvcache.cpp:57-123 on a tiny random model
 void kv_cache_equivalences(TinyCfg c) {
   std::mt19937 rng(7);
@@ -405,8 +478,8 @@ void sgd_step() {
   opt.step();
   const std::vector<float> a1 = host(a), b1 = host(b);
   bool ok = true;
-  for (size_t i = 0; i < 300; ++i) ok = ok && a1[i] == a0[i] - 0.1f * ga[i];
-  check(ok, "SGD: p - lr g");
+  for (size_t i = 0; i < 300; ++i) ok = ok && a1[i] == std::fma(-0.1f, ga[i], a0[i]);
+  check(ok, "SGD: fma(-lr, g, p), one rounding");
   check(b1 == b0, "SGD: parameters without a gradient are untouched");
   opt.zero_grad();
   check(!a.grad().storage(), "SGD: zero_grad drops the gradient");
@@ -505,6 +578,16 @@ void safetensors_format_and_faults(Device dev) {
        "unsupported dtype"},
       {"negative extent", "{\"x\":{\"dtype\":\"F32\",\"shape\":[-2],\"data_offsets\":[0,8]}}", 8,
        "malformed header"},
+      // Products that wrap 64 bits to 0 must not pass as an empty tensor.
+      {"element count wraps",
+       "{\"x\":{\"dtype\":\"F32\",\"shape\":[8589934592,2147483648],\"data_offsets\":[0,0]}}", 8,
+       "too large to address"},
+      {"byte count wraps",
+       "{\"x\":{\"dtype\":\"F32\",\"shape\":[4611686018427387904],\"data_offsets\":[0,0]}}", 8,
+       "too large to address"},
+      {"extent past int64",
+       "{\"x\":{\"dtype\":\"F32\",\"shape\":[9223372036854775808,0],\"data_offsets\":[0,0]}}", 8,
+       "too large to address"},
   };
   for (const Bad& b : bad) {
     const fs::path p = dir / "bad.safetensors";
@@ -556,24 +639,32 @@ void block_graph_only_recompute_matches_forward_train() {
     Tensor x = x0.detach();
     x.requires_grad_(true);
     Tensor y = graph_only ? blk.forward_train_for_backward(x) : blk.forward_train(x);
-    if (y_host) *y_host = host(y);
+    if (y_host && !graph_only) *y_host = host(y);
+    if (graph_only) {
+      // Its elements are not the block output: reading them throws, the
+      // graph is still there for backward.
+      check(y.is_placeholder(), "the recompute form is a placeholder");
+      check(throws_with([&] { (void)y.data_ptr(); }, "autograd history"),
+            "data_ptr() of the recompute form throws");
+      check(throws_with([&] { std::vector<float> t(y.numel()); y.copy_to_host(t.data()); },
+                        "autograd history"),
+            "copy_to_host() of the recompute form throws");
+      check(throws_with([&] { (void)y.reshape({-1}).data_ptr(); }, "autograd history"),
+            "a view of the recompute form throws too");
+      check(y.autograd_meta() && y.autograd_meta()->grad_fn, "the recompute form keeps its grad_fn");
+    }
     y.backward(dy);
     std::vector<std::vector<float>> g{host(x.grad())};
     for (auto& p : params()) g.push_back(host(p.grad()));
     return g;
   };
-  std::vector<float> y_full, y_graph;
+  std::vector<float> y_full;
   const auto g_full = run_once(false, &y_full);
-  const auto g_graph = run_once(true, &y_graph);
+  const auto g_graph = run_once(true, nullptr);
   check(g_full.size() == g_graph.size(), "same gradient count");
   for (size_t i = 0; i < g_full.size() && i < g_graph.size(); ++i)
     check(g_full[i] == g_graph[i], "gradient " + std::to_string(i) + " bitwise equal");
-
-  // The graph-only result holds h = x + attn(norm(x)), not the block output.
-  autograd::NoGradGuard ng;
-  Tensor h = ops::add(x0, blk.self_attn.forward_train(blk.input_layernorm.forward(x0)));
-  check(host(h) == y_graph, "graph-only result holds h's values");
-  check(y_full != y_graph, "the block output differs from h");
+  check(!y_full.empty(), "forward_train's output is readable");
 
   // ops-level: the result is a view of `values`, which are left as they were.
   Tensor a2 = rand_tensor({5, 8}, rng, 1.0f, true), w = rand_tensor({3, 8}, rng, 1.0f, true);
@@ -582,6 +673,9 @@ void block_graph_only_recompute_matches_forward_train() {
   Tensor y2 = ops::matmul_graph_only(a2, w, false, true, vals);
   check(y2.shape() == std::vector<int64_t>{5, 3}, "matmul_graph_only shape");
   check(y2.storage() == vals.storage() && host(vals) == before, "matmul_graph_only is a view");
+  check(y2.is_placeholder() && throws_with([&] { (void)y2.data_ptr(); }, "autograd history"),
+        "matmul_graph_only's result cannot be read");
+  check(!vals.is_placeholder(), "the values tensor itself stays readable");
   check(throws_with([&] { ops::matmul_graph_only(a2, w, false, true, a2); }, "M*N"),
         "matmul_graph_only rejects values of another size");
 }
@@ -634,10 +728,101 @@ void fan_in_fold_matches_separate_adds() {
 
 }  // namespace
 
+
+// The reference's masked CE offsets the logits by an int32 row * V
+// (src/ops/loss.cu:263-264, 322-323), which wraps once row * V passes 2^31:
+// row 14134 straddles it at V = 151936 (its first element sits at
+// 2,147,463,424, its last past 2^31) and every later row starts beyond it.
+// Through ops::cross_entropy_masked and its backward, N = 14200 rows
+// (2.16e9 logits, 8.6 GB): the loss over all rows, and dlogits of rows on
+// both sides of the wrap, against the oracle.  Row r holds pattern row r % 16,
+// so the oracle needs only the 16 pattern rows for the loss.
+void ce_masked_past_int32() {
+  const int64_t N = 14200, V = 151936, P = 16;
+  std::mt19937 rng(5);
+  std::normal_distribution<float> nd(0.0f, 2.0f);
+  std::vector<float> pat(static_cast<size_t>(P * V));
+  for (auto& x : pat) x = nd(rng);
+  std::vector<int64_t> tg(N);
+  std::vector<float> mask(N);
+  for (int64_t r = 0; r < N; ++r) {
+    tg[r] = (r * 7919 + 13) % V;
+    mask[r] = r % 7 == 3 ? 0.0f : 1.0f;
+  }
+  Tensor logits = Tensor::empty({N, V}, DType::kFloat32, kHIP0);
+  {
+    Tensor rows = Tensor::from_host(pat.data(), {P, V}, DType::kFloat32, kHIP0);
+    auto copy_rows = [&](const void* src, int64_t row0, int64_t n) {
+      CTD_CHECK(ember_memcpy_async(static_cast<float*>(logits.data_ptr()) + row0 * V, src,
+                                   static_cast<size_t>(n * V) * sizeof(float), 2,
+                                   runtime::compute_stream()));
+    };
+    copy_rows(rows.data_ptr(), 0, P);
+    for (int64_t filled = P; filled < N;) {  // doubling copies of the rows so far
+      const int64_t n = std::min(filled, N - filled);
+      copy_rows(logits.data_ptr(), filled, n);
+      filled += n;
+    }
+    runtime::synchronize();
+  }
+  logits.requires_grad_(true);
+  Tensor t = Tensor::from_host(tg.data(), {N}, DType::kInt64, kHIP0);
+  Tensor m = Tensor::from_host(mask.data(), {N}, DType::kFloat32, kHIP0);
+  Tensor loss = ops::cross_entropy_masked(logits, t, m);
+  float got = 0.0f;
+  loss.copy_to_host(&got);
+
+  // Oracle: lse of each pattern row, then sum over rows of mask*(lse - logit[t]).
+  std::vector<double> patd(pat.begin(), pat.end()), lse(P);
+  std::vector<int64_t> zero_t(P, 0);
+  std::vector<double> ones(P, 1.0);
+  orc_ce_masked_fwd(patd.data(), zero_t.data(), ones.data(), P, V, lse.data(), nullptr);
+  double num = 0.0, den = 0.0;
+  for (int64_t r = 0; r < N; ++r) {
+    if (mask[r] == 0.0f) continue;
+    num += lse[r % P] - patd[static_cast<size_t>((r % P) * V + tg[r])];
+    den += 1.0;
+  }
+  const double ref = num / den;
+  check(std::abs(got - ref) <= 1e-4 * std::abs(ref), "loss over 2.16e9 logits vs oracle (" +
+                                                          std::to_string(got) + " vs " +
+                                                          std::to_string(ref) + ")");
+
+  loss.backward();
+  Tensor g = logits.grad();
+  check(g.defined() && g.shape() == logits.shape(), "dlogits shape");
+  for (int64_t r : {int64_t{0}, int64_t{3}, int64_t{14133}, int64_t{14134}, int64_t{14135},
+                    int64_t{14136}, int64_t{N - 1}}) {
+    std::vector<float> row(V);
+    g.view_at(r * V, {V}).copy_to_host(row.data());
+    std::vector<double> ref_row(V);
+    const double one = 1.0;
+    const int64_t tr = tg[r];
+    orc_ce_masked_bwd(patd.data() + (r % P) * V, &tr, &one, 1, V, mask[r] / den, ref_row.data());
+    double worst = 0.0, scale = 0.0;
+    for (int64_t j = 0; j < V; ++j) {
+      worst = std::max(worst, std::abs(row[j] - ref_row[j]));
+      scale = std::max(scale, std::abs(ref_row[j]));
+    }
+    if (mask[r] == 0.0f)
+      check(worst == 0.0, "masked row " + std::to_string(r) + " has zero dlogits");
+    else
+      check(worst <= 1e-4 * scale, "dlogits row " + std::to_string(r) + " vs oracle (max err " +
+                                       std::to_string(worst) + ", scale " +
+                                       std::to_string(scale) + ")");
+  }
+}
+
 int main(int argc, char** argv) {
   // --cpu: only the tests that need no GPU (host tensors only).
   if (argc > 1 && std::strcmp(argv[1], "--cpu") == 0) {
     run("Safetensors.FormatAndFaults_Host", [] { safetensors_format_and_faults(kCPU); });
+    std::printf("%d failure(s)\n", g_failed);
+    return g_failed;
+  }
+  // --large: the test that needs ~18 GB of device memory, on its own.
+  if (argc > 1 && std::strcmp(argv[1], "--large") == 0) {
+    run("Loss.CrossEntropyMaskedPastInt32Offsets", [] { ce_masked_past_int32(); });
     std::printf("%d failure(s)\n", g_failed);
     return g_failed;
   }
@@ -658,6 +843,7 @@ int main(int argc, char** argv) {
       [] { train_logits_match_inference_logits(TinyCfg{32, 128, 2, 1, 64, 64, 2, 1e-5f, 1e4f}); });
   run("ModelTrain.OverfitsTinyBatch", [] { overfits_tiny_batch(); });
   run("Optim.PrefetchThenHostStateChange", [] { prefetch_then_host_state_change(); });
+  run("Optim.OffloadSkipsStateWithoutGrad", [] { offload_skips_state_without_grad(); });
   run("Integration.KVCacheEquivalences", [] { kv_cache_equivalences(TinyCfg{}); });
   run("Integration.KVCacheEquivalences_D64",
       [] { kv_cache_equivalences(TinyCfg{32, 128, 2, 1, 64, 64, 2, 1e-5f, 1e4f}); });

@@ -21,12 +21,17 @@ versions), so the files hold only expected outputs:
   scaling: factor 32, low 1, high 4, original context 8192) cut to 2 layers,
   at T=2048 (positions up to 2047 cross all three llama3 bands) and B=2, with
   the all-ones mask the config implies.
+- c5_model.npz: BASELINE config 4's Qwen3-1.7B shape (hidden 2048, 16/8 heads
+  of 128 with per-head QK-RMSNorm, MLP 6144, vocab 151936, eps 1e-6, theta
+  1e6) cut to 2 layers, at the config's T=4096 with B=1 and the prefix loss
+  mask.
 
 Full tensors would be megabytes, so each output is stored as its float64 sum,
 sum of squares, maximum magnitude, and values at fixed sampled positions (and,
 for y and dx, the sum and sum of squares of every row).  Run from the
-repository root: python tests/golden/make_golden.py [c1 c2 c3 c4] (c1 and c2 about
-a minute each on 8 cores, c3 and c4 a few minutes and up to 30 GB of memory).
+repository root: python tests/golden/make_golden.py [c1 c2 c3 c4 c5] (c1 and c2
+about a minute each on 8 cores, c3, c4 and c5 a few minutes and up to 30 GB of
+memory).
 """
 import math
 import os
@@ -46,6 +51,8 @@ C3 = dict(vocab=151936, hidden=1024, inter=3072, layers=2, heads=16, kv_heads=8,
           eps=1e-6, theta=1e6, qk_norm=True, B=4, T=1024, seed=2, masked=True)
 C4 = dict(vocab=128256, hidden=2048, inter=8192, layers=2, heads=32, kv_heads=8, head_dim=64,
           eps=1e-5, theta=5e5, rope=(32.0, 1.0, 4.0, 8192), B=2, T=2048, seed=3, masked=False)
+C5 = dict(vocab=151936, hidden=2048, inter=6144, layers=2, heads=16, kv_heads=8, head_dim=128,
+          eps=1e-6, theta=1e6, qk_norm=True, B=1, T=4096, seed=4, masked=True)
 BLOCK_KEYS = ["input_layernorm", "q_proj", "k_proj", "v_proj", "o_proj",
               "post_attention_layernorm", "gate_proj", "up_proj", "down_proj"]
 # collect_parameters' order inside a layer when the model has QK-Norm
@@ -235,9 +242,9 @@ def make_model(c, filename):
 if __name__ == "__main__":
     torch.set_default_dtype(torch.float64)
     torch.set_num_threads(min(8, os.cpu_count() or 1))
-    which = sys.argv[1:] or ["c1", "c2", "c3", "c4"]
+    which = sys.argv[1:] or ["c1", "c2", "c3", "c4", "c5"]
     if "c1" in which:
         make_c1()
-    for name, c in (("c2", C2), ("c3", C3), ("c4", C4)):
+    for name, c in (("c2", C2), ("c3", C3), ("c4", C4), ("c5", C5)):
         if name in which:
             make_model(c, f"{name}_model.npz")

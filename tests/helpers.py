@@ -91,3 +91,23 @@ def assert_matches_golden(golden, prefix, got, rtol=1e-4, rows=False):
         rn = np.sqrt(rq)
         assert (np.abs(r2.sum(1) - rs) <= rtol * rn * math.sqrt(r2.shape[1])).all(), (prefix, "row sums")
         assert (np.abs(np.sqrt((r2 * r2).sum(1)) - rn) <= rtol * rn).all(), (prefix, "row norms")
+
+
+def fma_f32(a, b, c):
+    """float32(a * b + c) rounded once, for float32 arrays.  a * b is exact in
+    float64; TwoSum recovers the float64 sum's rounding error, whose sign
+    decides the float32 rounding where the float64 sum lies exactly on a
+    float32 midpoint (the only case where rounding twice can differ)."""
+    x = np.asarray(a, np.float64) * np.asarray(b, np.float64)
+    y = np.asarray(c, np.float64)
+    s = x + y
+    bb = s - x
+    err = (x - (s - bb)) + (y - bb)
+    f = s.astype(np.float32)
+    lo = np.nextafter(f, np.float32(-np.inf))
+    hi = np.nextafter(f, np.float32(np.inf))
+    up_mid = (f.astype(np.float64) + hi.astype(np.float64)) / 2 == s
+    dn_mid = (f.astype(np.float64) + lo.astype(np.float64)) / 2 == s
+    f = np.where(up_mid & (err > 0), hi, f)
+    f = np.where(dn_mid & (err < 0), lo, f)
+    return f

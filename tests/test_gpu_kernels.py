@@ -15,7 +15,7 @@ import pytest
 
 import oracle as O
 from emberlm_amd import capi
-from tests.helpers import assert_close, call, dev, empty, host, p
+from tests.helpers import assert_close, call, dev, empty, fma_f32, host, p
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -591,6 +591,31 @@ def test_gemm_dyn_rows_vs_oracle(ta, tb, M, N, K, count, base):
     assert (got[past:] == 7.0).all()   # whole row tiles past v are skipped
 
 
+@pytest.mark.parametrize("H,V,count", [(1024, 2048, 300), (1024, 2048, 17), (512, 4096, 33)])
+def test_gemm_dyn_rows_split_k_writes_the_last_16_row_group(H, V, count):
+    # The LM head's logits GEMM (NT, rows sized on the device) on a grid of few
+    # tiles, which splits K: rows [count, round16(count)) come from zero-filled
+    # rows of h and must be stored as zeros (the dW product that follows reads
+    # K rounded up to 16), whatever the output buffer held before.
+    M = -(-count // 16) * 16 + 16
+    assert capi.lib().ember_gemm_f32_workspace_bytes(M, V, H, 1) > 0   # K is split
+    r = rng(H + V + count)
+    hc = r.standard_normal((M, H)).astype(np.float32)
+    hc[count:] = 0.0                                  # the gather's zero rows
+    w = r.standard_normal((V, H)).astype(np.float32)
+    a, b = dev(hc), dev(w)
+    out = torch.full((M, V), float("nan"), device="cuda")
+    wsb = int(capi.lib().ember_gemm_f32_workspace_bytes(M, V, H, 1))
+    ws = empty((wsb // 4,))
+    cnt = dev(np.array([count], np.int64))
+    call("ember_gemm_f32_dyn", 0, 1, M, V, H, 1.0, p(a), H, p(b), H, 0.0, p(out), V, p(cnt), 0,
+         0, p(ws), wsb, None)
+    got = host(out)
+    r16 = -(-count // 16) * 16
+    assert_close(got[:count], O.matmul(hc[:count], w, False, True), name="logits rows")
+    assert (got[count:r16] == 0.0).all(), "rows of the last 16-row group must be zeros"
+
+
 @pytest.mark.parametrize("M,N,K,count,beta", [
     (1024, 512, 4096, 4096, 0.0), (1024, 512, 4096, 1000, 0.0), (1024, 512, 4096, 17, 0.0),
     (1024, 512, 4096, 1000, 1.0), (1024, 512, 4096, 0, 1.0), (1024, 512, 4096, 0, 0.0),
@@ -808,6 +833,43 @@ def test_adamw_bounded_equals_adamw_bitwise(max_blocks, offset):
         assert np.array_equal(hb[offset + n:], (pp, g, m, v)[("p", "g", "m", "v").index(name)][offset + n:])
 
 
+def test_scale_multi_equals_per_tensor_scale():
+    # The batched in-place scale of the gradient clip: every tensor (float4
+    # and scalar paths, one a float off a 16-byte boundary, one empty) equals
+    # ember_scale on it alone, bit for bit.
+    r = rng(17)
+    arrs = [r.standard_normal(n).astype(np.float32) for n in (4, 9, 1000003, 1, 50_001, 0, 1025)]
+    alpha = 0.37
+    ts = [dev(a) if a.size else empty((1,)) for a in arrs]
+    want = []
+    for a in arrs:
+        if not a.size:
+            want.append(a)
+            continue
+        t = dev(a)
+        call("ember_scale", p(t), alpha, p(t), a.size, None)
+        want.append(host(t))
+    off = [0, 0, 0, 0, 4, 0, 0]   # the 50001-element one starts a float in
+    ptrs = (C.c_void_p * len(ts))(*[t.data_ptr() + o for t, o in zip(ts, off)])
+    sizes = (C.c_int64 * len(ts))(*[a.size - (1 if o else 0) for a, o in zip(arrs, off)])
+    lib = capi.lib()
+    wsb = lib.ember_scale_multi_workspace_bytes(len(ts))
+    ws = empty((wsb // 4,))
+    call("ember_scale_multi", ptrs, sizes, len(ts), alpha, p(ws), wsb, None)
+    for i, (a, t) in enumerate(zip(arrs, ts)):
+        if not a.size:
+            continue
+        got = host(t)
+        if off[i]:
+            ref = a.copy()
+            sub = dev(a[1:])
+            call("ember_scale", p(sub), alpha, p(sub), a.size - 1, None)
+            ref[1:] = host(sub)
+            assert np.array_equal(got, ref), i
+        else:
+            assert np.array_equal(got, want[i]), i
+
+
 def test_sumsq_multi():
     r = rng(8)
     arrs = [r.standard_normal(s).astype(np.float32) for s in (4, 9, 16, 1000003, 1)]
@@ -845,7 +907,7 @@ def test_sumsq_multi():
 
 
 def test_sgd_exact():
-    # p - lr * g with two float32 roundings (float4 path and a ragged tail on
+    # fma(-lr, g, p): one float32 rounding (float4 path and a ragged tail on
     # the scalar one); gradients of 0 leave p unchanged.
     r = rng(12)
     for n, off in ((1_000_003, 0), (1001, 1)):
@@ -857,7 +919,7 @@ def test_sgd_exact():
              0.01, None)
         lr = np.float32(0.01)
         want = p0.copy()
-        want[off:] = (p0[off:] - (lr * g[off:]).astype(np.float32)).astype(np.float32)
+        want[off:] = fma_f32(np.full(n, -lr, np.float32), g[off:], p0[off:])
         assert np.array_equal(host(P), want)
 
 

@@ -220,6 +220,17 @@ def test_c4_llama32_1b_two_layers_vs_golden():
     _model_step_vs_golden(MG.C4, c, "c4_model.npz")
 
 
+def test_c5_qwen3_17b_two_layers_vs_golden():
+    # BASELINE config 4's Qwen3-1.7B at its real width (hidden 2048, MLP 6144),
+    # heads (16/8 of 128, QK-Norm) and vocabulary (151936), at T=4096 with the
+    # prefix loss mask, cut to 2 layers at B=1.
+    c = _reduced("qwen3-1.7b", MG.C5["layers"])
+    assert (c.hidden_size, c.intermediate_size, c.num_heads, c.num_kv_heads, c.head_dim,
+            c.vocab_size, c.qk_norm) == (MG.C5["hidden"], MG.C5["inter"], MG.C5["heads"],
+                                         MG.C5["kv_heads"], MG.C5["head_dim"], MG.C5["vocab"], 1)
+    _model_step_vs_golden(MG.C5, c, "c5_model.npz")
+
+
 def tiny_cfg(qk_norm=False, llama3=False, D=64, vocab=1000):
     # vocab 1000 takes the LM head's all-rows form, a multiple of 16 (1024) the
     # form that computes only rows with a nonzero mask value.
@@ -509,15 +520,18 @@ def test_full_step_checkpoint_bitwise(preset, B, T, masked):
     tr.close()
 
 
-def test_c5_offloaded_steps_equal_on_device_full_size():
-    # Two recompute + offload train steps of Qwen3-1.7B at B=8, T=4096 against
-    # the same steps with m/v on the device: every parameter, m and v equal bit
-    # for bit.  The offloaded state is one 6.9 GB pinned buffer each for m and v
-    # (byte offsets past 2^32), cut into 16M-float chunks that cross parameter
-    # boundaries, and the embedding's 20 chunks are prefetched during the
-    # backward at the default layer (a), or not at all (p); the second step
-    # reads back what the first wrote.
-    c = TR.preset("qwen3-1.7b")
+@pytest.mark.parametrize("preset,B,T,masked", [("llama3.2-1b", 4, 2048, False),
+                                                ("qwen3-1.7b", 8, 4096, True)])
+def test_full_size_offloaded_steps_equal_on_device(preset, B, T, masked):
+    # Two recompute + offload train steps of BASELINE config 3 (LLaMA-3.2-1B,
+    # B=4, T=2048, llama3 RoPE, all-ones mask) and config 4 (Qwen3-1.7B, B=8,
+    # T=4096) against the same steps with m/v on the device: every parameter,
+    # m and v equal bit for bit.  The offloaded state is one pinned buffer
+    # each for m and v (4.9 / 6.9 GB: byte offsets past 2^32), cut into
+    # 16M-float chunks that cross parameter boundaries, and the embedding's
+    # chunks are prefetched during the backward at the default layer (a), or
+    # not at all (p); the second step reads back what the first wrote.
+    c = TR.preset(preset)
     a = TR.Trainer(c, seed=0, init_std=0.02)
     p = TR.Trainer(c, seed=0, init_std=0.02)
     b = TR.Trainer(c, seed=0, init_std=0.02)
@@ -530,7 +544,7 @@ def test_c5_offloaded_steps_equal_on_device_full_size():
     for step in range(2):
         losses = []
         for t in (a, p, b):
-            t.synthetic_batch(8, 4096, seed=step, masked=True)
+            t.synthetic_batch(B, T, seed=step, masked=masked)
             losses.append(t.train_step(1.0).loss)
         assert losses[0] == losses[1] == losses[2], (step, losses)
     ms, nbytes, prefetched = a.offload_stats()
