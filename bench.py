@@ -310,12 +310,19 @@ def main():
     ap.add_argument("--alloc-history", default=None,
                     help="write the device allocator's history of the timed steps to this file "
                          "(replayable on the host: emberlm_amd.trainer.alloc_replay)")
+    ap.add_argument("--kernels", action="store_true",
+                    help="only the per-kernel table at this workload's shapes "
+                         "(emberlm_amd/kernel_bench.py): one JSON line per kernel")
     ap.add_argument("--link-probe", action="store_true",
                     help="only the pinned host<->device copy rates of this box (one JSON line)")
     args = ap.parse_args()
 
     if args.link_probe:
         print(json.dumps(pinned_copy_rates()))
+        return
+    if args.kernels:
+        from emberlm_amd import kernel_bench
+        kernel_bench.run()
         return
 
     if args.gpus != 1:

@@ -153,6 +153,42 @@ size_t BlockArena::largest_free() const {
   return m;
 }
 
+std::vector<size_t> BlockArena::scatter_fit(size_t unit, size_t want, size_t least,
+                                            size_t multiple, size_t max_pieces) const {
+  std::vector<size_t> pieces;
+  if (unit == 0 || want == 0 || max_pieces == 0) return pieces;
+  least = std::min(least, want);
+  size_t placed = 0;
+  // Descending piece sizes, each no larger than the block it was sized for:
+  // served in this order, best fit puts every piece in some free block.
+  for (auto it = free_large_.rbegin();
+       it != free_large_.rend() && placed < want && pieces.size() + 1 < max_pieces; ++it) {
+    size_t n = std::min((*it)->size / unit, want - placed);
+    while (n > 0 && round_request(n * unit) > (*it)->size) --n;
+    if (n == 0) break;  // the rest are smaller still
+    pieces.push_back(n * unit);
+    placed += n;
+  }
+  if (placed < least) {
+    pieces.push_back((want - placed) * unit);
+    return pieces;
+  }
+  if (multiple > 1 && placed < want && placed >= multiple) {
+    size_t cut = placed % multiple;  // taken off the smallest pieces
+    while (cut > 0) {
+      const size_t last = pieces.back() / unit;
+      if (last <= cut) {
+        pieces.pop_back();
+        cut -= last;
+      } else {
+        pieces.back() -= cut * unit;
+        cut = 0;
+      }
+    }
+  }
+  return pieces;
+}
+
 std::vector<std::pair<uintptr_t, size_t>> BlockArena::live_blocks() const {
   std::vector<std::pair<uintptr_t, size_t>> out;
   out.reserve(live_.size());
@@ -188,6 +224,9 @@ ArenaStats replay_history(const std::string& path, size_t limit) {
   std::string line;
   int64_t lineno = 0;
   uint64_t elastic_bytes = 0;  // nonzero: the next request's size (from an "e" record)
+  uint64_t split_pending = 0;  // recorded pieces of a split workspace still to come
+  std::vector<uintptr_t> split_blocks;
+  std::unordered_map<uint64_t, std::vector<uintptr_t>> groups;
   while (std::getline(in, line)) {
     ++lineno;
     if (line.empty()) continue;
@@ -195,6 +234,21 @@ ArenaStats replay_history(const std::string& path, size_t limit) {
     char op = 0;
     ls >> op;
     if (op == 'm') continue;
+    if (op == 's') {
+      // a split workspace: the replay plans its own pieces and allocates
+      // them now; the recorded pieces (the next `count` requests) map to
+      // them, all released with the first
+      uint64_t unit = 0, want = 0, least = 0, multiple = 0, maxp = 0, count = 0;
+      ls >> unit >> want >> least >> multiple >> maxp >> count;
+      if (!ls || unit == 0 || want == 0)
+        throw std::runtime_error("replay_history: bad split record at line " +
+                                 std::to_string(lineno));
+      std::vector<uintptr_t> got;
+      for (size_t b : arena.scatter_fit(unit, want, least, multiple, maxp)) got.push_back(arena.allocate(b));
+      split_pending = count;
+      split_blocks = std::move(got);
+      continue;
+    }
     if (op == 'e') {
       uint64_t want = 0, least = 0;
       ls >> want >> least;
@@ -215,6 +269,13 @@ ArenaStats replay_history(const std::string& path, size_t limit) {
       if (ids.count(id))
         throw std::runtime_error("replay_history: id allocated twice at line " +
                                  std::to_string(lineno));
+      if (split_pending) {
+        --split_pending;
+        groups[id] = std::move(split_blocks);
+        split_blocks.clear();
+        ids[id] = 0;
+        continue;
+      }
       if (elastic_bytes) bytes = elastic_bytes;
       elastic_bytes = 0;
       ids[id] = arena.allocate(bytes);
@@ -223,7 +284,13 @@ ArenaStats replay_history(const std::string& path, size_t limit) {
       if (it == ids.end())
         throw std::runtime_error("replay_history: free of unknown id at line " +
                                  std::to_string(lineno));
-      arena.release(it->second);
+      auto g = groups.find(id);
+      if (g != groups.end()) {
+        for (uintptr_t a : g->second) arena.release(a);
+        groups.erase(g);
+      } else {
+        arena.release(it->second);
+      }
       ids.erase(it);
     } else {
       throw std::runtime_error("replay_history: unknown record at line " + std::to_string(lineno));

@@ -87,6 +87,15 @@ class BlockArena {
     const size_t largest = largest_free() / kGranule * kGranule;
     return largest >= want || largest < least ? want : largest;
   }
+  // Pieces (byte sizes, each a whole number of `unit`s) for a workspace
+  // that may be split: the largest free blocks are taken first, each for as
+  // many units as it holds, until `want` units are placed or `max_pieces`
+  // blocks are used, then cut to a multiple of `multiple` units when that
+  // leaves at least one multiple.  Fewer than `least` units placed that way:
+  // one more piece for the rest of `want`, which grows the arena.  See
+  // device_scatter_plan.
+  std::vector<size_t> scatter_fit(size_t unit, size_t want, size_t least, size_t multiple,
+                                  size_t max_pieces) const;
   // (address, size) of every block handed out, in address order.
   std::vector<std::pair<uintptr_t, size_t>> live_blocks() const;
 
@@ -133,7 +142,10 @@ class BlockArena {
 // Replays an allocation history recorded by the device allocator (lines
 // "a <id> <bytes>", "f <id>", "m <label>", and "e <want> <least>" before a
 // workspace whose size followed elastic_fit: the replay asks its own arena
-// and allocates that answer instead of the recorded size) on a BlockArena
+// and allocates that answer instead of the recorded size; "s <unit> <want>
+// <least> <multiple> <max_pieces> <count>" before the `count` pieces of a split
+// workspace planned by scatter_fit: the replay plans and allocates its own
+// pieces and frees them with the first recorded one) on a BlockArena
 // whose backend only counts addresses, so a placement policy can be judged
 // on a real training step's requests without a GPU.  Returns the arena's
 // statistics at the end.

@@ -630,20 +630,31 @@ double attn_fwd_flops(const AttnDims& d) {
 
 std::atomic<int64_t> g_attn_ds_bytes{kAttentionBackwardDsBytes};
 
-// Workspace for ember_attn_bwd: rowsum(dO*O) plus as much of dS as the budget
-// allows, cut further to a free block the allocator already holds when one
-// takes at least half of it (the kernel then keeps dS for fewer KV rows at a
-// time; dQ, dK and dV are bitwise the same for every cut).  With a quarter as
-// the floor, a Qwen3-1.7B step whose holes were small took 176 ms longer in
-// the attention backward (about 6 ms per layer).
-size_t attn_bwd_workspace(const AttnDims& d) {
-  const size_t lo = ember_attn_bwd_workspace_bytes_min(d.B, d.T, d.H);
-  const size_t hi = ember_attn_bwd_workspace_bytes(d.B, d.T, d.H);
+constexpr size_t kAttnDsMaxPieces = 16;
+
+// Buffers for the dS that ember_attn_bwd_scattered keeps, whole KV rows
+// (one (batch, KV head) pair's strips) each: as many rows as the budget
+// holds, in multiples of 8, the rows per chunk of the pass.  They are placed
+// in free blocks the allocator already holds, several if need be, so that
+// the 2+ GB of dS a Qwen3-1.7B layer keeps at B=8, T=4096 does not need a
+// contiguous block (and grows the memory held only when the free blocks
+// hold fewer than 16 rows).  dQ, dK and dV are bitwise the same for any
+// rows per chunk; fewer rows leave the dK/dV launch too few workgroups to
+// balance the causal triangle's heavy key blocks: with 8-row chunks it took
+// 13.2 ms per Qwen3-1.7B layer against 8.8 ms with 32-row chunks.
+std::vector<Tensor> attn_bwd_ds_buffers(const AttnDims& d) {
   const int64_t budget = g_attn_ds_bytes.load();
-  if (budget <= 0) return lo;
-  const size_t want = std::min(hi, lo + static_cast<size_t>(budget));
-  const size_t got = elastic_workspace_bytes(want, lo + (want - lo) / 2);
-  return std::max(lo, std::min(want, got));
+  const size_t row = ember_attn_bwd_ds_row_bytes(d.T, d.H, d.Hk);
+  const size_t kv_rows = static_cast<size_t>(d.B * d.Hk);
+  std::vector<Tensor> bufs;
+  if (budget <= 0 || row == 0) return bufs;
+  size_t want = std::min(kv_rows, static_cast<size_t>(budget) / row);
+  if (want < kv_rows && want >= 8) want -= want % 8;
+  if (want == 0) return bufs;
+  for (size_t bytes : device_scatter_plan(row, want, std::min<size_t>(want, 16), 8,
+                                          kAttnDsMaxPieces))
+    bufs.push_back(workspace(bytes));
+  return bufs;
 }
 
 struct CausalAttentionBackward : autograd::Node {
@@ -656,11 +667,20 @@ struct CausalAttentionBackward : autograd::Node {
     check_f32(dout, "causal_attention backward", "grad");
     const AttnDims d = attn_dims(q, k, v);
     Tensor dq = empty_like(q), dk = empty_like(k), dv = empty_like(v);
-    const size_t wsb = attn_bwd_workspace(d);
+    const size_t wsb = ember_attn_bwd_workspace_bytes_min(d.B, d.T, d.H);
     Tensor ws = workspace(wsb);
+    std::vector<Tensor> ds = attn_bwd_ds_buffers(d);
+    std::vector<float*> ds_ptr;
+    std::vector<size_t> ds_bytes;
+    for (Tensor& t : ds) {
+      ds_ptr.push_back(fp(t));
+      ds_bytes.push_back(static_cast<size_t>(t.numel()) * sizeof(float));
+    }
     void* ev = runtime::gemm_profile_begin();
-    CTD_CHECK(ember_attn_bwd(cfp(q), cfp(k), cfp(v), cfp(o), cfp(lse), cfp(dout), fp(dq), fp(dk),
-                             fp(dv), d.B, d.T, d.H, d.Hk, d.D, scale, ws.data_ptr(), wsb, S()));
+    CTD_CHECK(ember_attn_bwd_scattered(cfp(q), cfp(k), cfp(v), cfp(o), cfp(lse), cfp(dout),
+                                       fp(dq), fp(dk), fp(dv), d.B, d.T, d.H, d.Hk, d.D, scale,
+                                       ws.data_ptr(), wsb, ds_ptr.data(), ds_bytes.data(),
+                                       static_cast<int>(ds_ptr.size()), S()));
     runtime::gemm_profile_end(ev, 2.0 * attn_fwd_flops(d), runtime::kProfileAttnBwd);
     release_saved(q, k, v, o, lse);
     return {dq, dk, dv};

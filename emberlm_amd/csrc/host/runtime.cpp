@@ -337,6 +337,15 @@ class HipCachingAllocator final : public Allocator {
     std::lock_guard<std::mutex> lk(mu_);
     sample_locked();
   }
+  std::vector<size_t> scatter_plan(size_t unit, size_t want, size_t least, size_t multiple,
+                                   size_t max_pieces) {
+    std::lock_guard<std::mutex> lk(mu_);
+    std::vector<size_t> pieces = arena_.scatter_fit(unit, want, least, multiple, max_pieces);
+    if (tracing_)
+      trace_ << "s " << unit << ' ' << want << ' ' << least << ' ' << multiple << ' '
+             << max_pieces << ' ' << pieces.size() << '\n';
+    return pieces;
+  }
   size_t elastic(size_t want, size_t least) {
     if (least > want) least = want;
     std::lock_guard<std::mutex> lk(mu_);
@@ -467,6 +476,10 @@ void reset_peak_device_memory() { hip_cache().reset_peak(); }
 void empty_device_cache() { hip_cache().empty_cache(); }
 void set_device_memory_limit(size_t bytes) { hip_cache().set_limit(bytes); }
 void sample_device_memory() { hip_cache().sample(); }
+std::vector<size_t> device_scatter_plan(size_t unit, size_t want, size_t least, size_t multiple,
+                                        size_t max_pieces) {
+  return hip_cache().scatter_plan(unit, want, least, multiple, max_pieces);
+}
 size_t elastic_workspace_bytes(size_t want, size_t least) {
   return hip_cache().elastic(want, least);
 }

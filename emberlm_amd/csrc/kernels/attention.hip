@@ -50,6 +50,8 @@
 // registers per lane there), the dQ-from-dS kernel 128 queries (32 per wave,
 // three waves per SIMD at D = 128); all double-buffer their streamed tiles the
 // same way.
+#include <vector>
+
 #include "common.h"
 
 using namespace ember;
@@ -468,8 +470,8 @@ template <int D>
 __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta,
-    float* __restrict__ dk, float* __restrict__ dv, float* __restrict__ ds, int row0, int T,
-    int H, int Hk, float scale_log2, float scale) {
+    float* __restrict__ dk, float* __restrict__ dv, float* const* __restrict__ ds_rows, int row0,
+    int T, int H, int Hk, float scale_log2, float scale) {
   using C = DkvCfg<D>;
   constexpr int NT = D / 16;  // d tiles; float4 groups of a lane's K/V row
   __shared__ __attribute__((aligned(16))) float smem[C::kSmem];
@@ -502,12 +504,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
   for (int t = 0; t < NT; ++t) adk[t] = adv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // This lane's row of the key block's dS strip for the group's first query
-  // head (the chunk-local (b, h) rows of a KV row are consecutive); columns
-  // count queries from key0.
+  // head (a KV row's region holds its group's heads one after another; the
+  // table gives each KV row's region); columns count queries from key0.
   const int64_t T32 = ds_t32(T), ds_row = ds_row_floats(T), lr = T32 - key0;
-  float* ds_lane = ds ? ds + static_cast<int64_t>(wi.row) * group * ds_row +
-                            ds_strip_offset(kb, T32) + static_cast<int64_t>(16 * w + i) * lr + 4 * g
-                      : nullptr;
+  float* ds_lane = ds_rows ? ds_rows[kvrow] + ds_strip_offset(kb, T32) +
+                                 static_cast<int64_t>(16 * w + i) * lr + 4 * g
+                           : nullptr;
 
   // The streamed sequence: for each query head of the group, the query tiles
   // key0, key0 + 32, ... below T.
@@ -629,8 +631,8 @@ struct DqDsCfg {
 
 template <int D>
 __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_ds_kernel(
-    const float* __restrict__ k, const float* __restrict__ ds, float* __restrict__ dq, int row0,
-    int T, int H, int Hk, float scale) {
+    const float* __restrict__ k, const float* const* __restrict__ ds_rows, float* __restrict__ dq,
+    int row0, int T, int H, int Hk, float scale) {
   using C = DqDsCfg<D>;
   constexpr int NT = D / 16;
   __shared__ __attribute__((aligned(16))) float smem[C::kSmem];
@@ -646,7 +648,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_ds_kernel(
   const int64_t qs = static_cast<int64_t>(H) * D, ks = static_cast<int64_t>(Hk) * D;
   const float* kbase = k + static_cast<int64_t>(b) * T * ks + static_cast<int64_t>(hk) * D;
   const int64_t T32 = ds_t32(T);
-  const float* dsrow = ds + static_cast<int64_t>(wi.row) * ds_row_floats(T);
+  // Head h's part of its KV row's dS region (heads of a group in order).
+  const float* dsrow = ds_rows[b * Hk + hk] + static_cast<int64_t>(h - hk * (H / Hk)) * ds_row_floats(T);
 
   // dS^T[key][query] for keys k0 + 16kt + 4g + e of 32-key tile kbi and the
   // lane's queries qw0 + 16n + i.
@@ -768,12 +771,25 @@ namespace {
 size_t delta_bytes(int64_t B, int64_t T, int64_t H) {
   return static_cast<size_t>((B * T * H * 4 + 255) / 256 * 256);
 }
+// The KV-row table: room for B*H pointers (B*Hk are used; H >= Hk keeps the
+// workspace query independent of Hk).
+size_t table_bytes(int64_t B, int64_t H) {
+  return static_cast<size_t>((B * H * 8 + 255) / 256 * 256);
+}
+// dS bytes of one KV row: its group's (b, h) rows of causal strips.
+size_t kv_row_ds_bytes(int64_t T, int64_t group) {
+  return static_cast<size_t>(group * ds_row_floats(T)) * sizeof(float);
+}
 
+// The backward over buffers for dS (host array of device pointers and sizes;
+// none: dQ recomputes dS).  `ws` holds rowsum(dO*O) and the KV-row table.
 template <int D>
 int launch_bwd(const float* q, const float* k, const float* v, const float* o, const float* lse,
                const float* dout, float* dq, float* dk, float* dv, int64_t B, int64_t T,
-               int64_t H, int64_t Hk, float scale, char* ws, size_t ws_bytes, hipStream_t st) {
+               int64_t H, int64_t Hk, float scale, char* ws, float* const* bufs,
+               const size_t* buf_bytes, int nbufs, hipStream_t st) {
   float* delta = reinterpret_cast<float*>(ws);
+  float** table = reinterpret_cast<float**>(ws + delta_bytes(B, T, H));
   const int64_t rows = B * T * H;
   const int Ti = static_cast<int>(T), Hi = static_cast<int>(H), Hki = static_cast<int>(Hk);
   const float sl = scale * kLog2e;
@@ -787,9 +803,10 @@ int launch_bwd(const float* q, const float* k, const float* v, const float* o, c
   const unsigned nqb = static_cast<unsigned>((T + 63) / 64);
   const unsigned nqb_ds = static_cast<unsigned>((T + DqDsCfg<D>::kBQ - 1) / DqDsCfg<D>::kBQ);
   const int64_t group = H / Hk, kv_rows = B * Hk;
-  const size_t dlt = delta_bytes(B, T, H);
-  const size_t kv_row_bytes = static_cast<size_t>(group * ds_row_floats(T)) * sizeof(float);
-  int64_t chunk = static_cast<int64_t>((ws_bytes - dlt) / kv_row_bytes);
+  const size_t row_bytes = kv_row_ds_bytes(T, group);
+  // KV-row slots in the buffers, in buffer order.
+  int64_t chunk = 0;
+  for (int i = 0; i < nbufs; ++i) chunk += static_cast<int64_t>(buf_bytes[i] / row_bytes);
   if (chunk < 1) {  // no room for dS: dQ recomputes S and dP
     attn_bwd_dq_kernel<D><<<dim3(nqb * static_cast<unsigned>(B * H)), kThreads, 0, st>>>(
         q, k, v, dout, lse, delta, dq, Ti, Hi, Hki, sl, scale);
@@ -802,36 +819,37 @@ int launch_bwd(const float* q, const float* k, const float* v, const float* o, c
   // regrouping of the work items.
   if (chunk < kv_rows && chunk >= 8) chunk -= chunk % 8;
   if (chunk > kv_rows) chunk = kv_rows;
-  float* ds = reinterpret_cast<float*>(ws + dlt);
+  // KV row r of a chunk takes slot r - r0: the same slots for every chunk.
+  std::vector<float*> host_table(static_cast<size_t>(kv_rows));
+  std::vector<float*> slot(static_cast<size_t>(chunk));
+  {
+    int64_t j = 0;
+    for (int i = 0; i < nbufs && j < chunk; ++i)
+      for (size_t off = 0; off + row_bytes <= buf_bytes[i] && j < chunk; off += row_bytes)
+        slot[static_cast<size_t>(j++)] = bufs[i] + off / sizeof(float);
+  }
+  for (int64_t r = 0; r < kv_rows; ++r)
+    host_table[static_cast<size_t>(r)] = slot[static_cast<size_t>(r % chunk)];
+  if ((rc = upload_async(table, host_table.data(), host_table.size() * sizeof(float*), st)))
+    return rc;
   for (int64_t r0 = 0; r0 < kv_rows; r0 += chunk) {
     const int64_t n = kv_rows - r0 < chunk ? kv_rows - r0 : chunk;
     attn_bwd_dkdv_kernel<D><<<dim3(nqb * static_cast<unsigned>(n)), kThreads, 0, st>>>(
-        q, k, v, dout, lse, delta, dk, dv, ds, static_cast<int>(r0), Ti, Hi, Hki, sl, scale);
+        q, k, v, dout, lse, delta, dk, dv, table, static_cast<int>(r0), Ti, Hi, Hki, sl, scale);
     if ((rc = launch_status())) return rc;
     attn_bwd_dq_ds_kernel<D><<<dim3(nqb_ds * static_cast<unsigned>(n * group)), kThreads, 0,
                                st>>>(
-        k, ds, dq, static_cast<int>(r0 * group), Ti, Hi, Hki, scale);
+        k, table, dq, static_cast<int>(r0 * group), Ti, Hi, Hki, scale);
     if ((rc = launch_status())) return rc;
   }
   return EMBER_OK;
 }
 
-}  // namespace
-
-extern "C" size_t ember_attn_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H) {
-  if (B <= 0 || T <= 0 || H <= 0) return 0;
-  return delta_bytes(B, T, H) + static_cast<size_t>(B * H * ds_row_floats(T)) * sizeof(float);
-}
-
-extern "C" size_t ember_attn_bwd_workspace_bytes_min(int64_t B, int64_t T, int64_t H) {
-  if (B <= 0 || T <= 0 || H <= 0) return 0;
-  return delta_bytes(B, T, H);
-}
-
-extern "C" int ember_attn_bwd(const float* q, const float* k, const float* v, const float* o,
-                              const float* lse, const float* dout, float* dq, float* dk, float* dv,
-                              int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D, float scale,
-                              void* workspace, size_t workspace_bytes, ember_stream_t s) {
+int attn_bwd_run(const float* q, const float* k, const float* v, const float* o, const float* lse,
+                 const float* dout, float* dq, float* dk, float* dv, int64_t B, int64_t T,
+                 int64_t H, int64_t Hk, int64_t D, float scale, void* workspace,
+                 size_t workspace_bytes, float* const* bufs, const size_t* buf_bytes, int nbufs,
+                 ember_stream_t s) {
   int rc = check_shapes(B, T, H, Hk, D);
   if (rc) return rc;
   if (B == 0 || T == 0) return EMBER_OK;
@@ -839,11 +857,60 @@ extern "C" int ember_attn_bwd(const float* q, const float* k, const float* v, co
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(dout) ||
       !aligned16(dq) || !aligned16(dk) || !aligned16(dv) || !aligned16(workspace))
     return EMBER_EALIGN;
-  if (!workspace || workspace_bytes < delta_bytes(B, T, H)) return EMBER_EWORKSPACE;
+  if (!workspace || workspace_bytes < ember_attn_bwd_workspace_bytes_min(B, T, H))
+    return EMBER_EWORKSPACE;
+  if (nbufs < 0 || (nbufs > 0 && (!bufs || !buf_bytes))) return EMBER_EINVAL;
+  for (int i = 0; i < nbufs; ++i) {
+    if (buf_bytes[i] > 0 && !bufs[i]) return EMBER_EINVAL;
+    if (!aligned16(bufs[i])) return EMBER_EALIGN;
+  }
   char* ws = static_cast<char*>(workspace);
   if (D == 64)
-    return launch_bwd<64>(q, k, v, o, lse, dout, dq, dk, dv, B, T, H, Hk, scale, ws,
-                          workspace_bytes, as_stream(s));
-  return launch_bwd<128>(q, k, v, o, lse, dout, dq, dk, dv, B, T, H, Hk, scale, ws,
-                         workspace_bytes, as_stream(s));
+    return launch_bwd<64>(q, k, v, o, lse, dout, dq, dk, dv, B, T, H, Hk, scale, ws, bufs,
+                          buf_bytes, nbufs, as_stream(s));
+  return launch_bwd<128>(q, k, v, o, lse, dout, dq, dk, dv, B, T, H, Hk, scale, ws, bufs,
+                         buf_bytes, nbufs, as_stream(s));
+}
+
+}  // namespace
+
+extern "C" size_t ember_attn_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H) {
+  if (B <= 0 || T <= 0 || H <= 0) return 0;
+  return ember_attn_bwd_workspace_bytes_min(B, T, H) +
+         static_cast<size_t>(B * H * ds_row_floats(T)) * sizeof(float);
+}
+
+extern "C" size_t ember_attn_bwd_workspace_bytes_min(int64_t B, int64_t T, int64_t H) {
+  if (B <= 0 || T <= 0 || H <= 0) return 0;
+  return delta_bytes(B, T, H) + table_bytes(B, H);
+}
+
+extern "C" size_t ember_attn_bwd_ds_row_bytes(int64_t T, int64_t H, int64_t Hk) {
+  if (T <= 0 || H <= 0 || Hk <= 0 || H % Hk) return 0;
+  return kv_row_ds_bytes(T, H / Hk);
+}
+
+extern "C" int ember_attn_bwd(const float* q, const float* k, const float* v, const float* o,
+                              const float* lse, const float* dout, float* dq, float* dk, float* dv,
+                              int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D, float scale,
+                              void* workspace, size_t workspace_bytes, ember_stream_t s) {
+  // dS goes in the workspace after rowsum(dO*O) and the KV-row table.
+  const size_t lo = ember_attn_bwd_workspace_bytes_min(B, T, H);
+  float* buf = workspace && workspace_bytes > lo
+                   ? reinterpret_cast<float*>(static_cast<char*>(workspace) + lo)
+                   : nullptr;
+  const size_t bytes = buf ? workspace_bytes - lo : 0;
+  return attn_bwd_run(q, k, v, o, lse, dout, dq, dk, dv, B, T, H, Hk, D, scale, workspace,
+                      workspace_bytes, &buf, &bytes, buf ? 1 : 0, s);
+}
+
+extern "C" int ember_attn_bwd_scattered(const float* q, const float* k, const float* v,
+                                        const float* o, const float* lse, const float* dout,
+                                        float* dq, float* dk, float* dv, int64_t B, int64_t T,
+                                        int64_t H, int64_t Hk, int64_t D, float scale,
+                                        void* workspace, size_t workspace_bytes,
+                                        float* const* ds_bufs_host, const size_t* ds_bytes_host,
+                                        int nbufs, ember_stream_t s) {
+  return attn_bwd_run(q, k, v, o, lse, dout, dq, dk, dv, B, T, H, Hk, D, scale, workspace,
+                      workspace_bytes, ds_bufs_host, ds_bytes_host, nbufs, s);
 }

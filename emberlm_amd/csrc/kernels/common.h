@@ -21,6 +21,13 @@ inline int launch_status() { return status_of(hipGetLastError()); }
 
 inline hipStream_t as_stream(ember_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Copies `bytes` of host memory to device memory on stream st through a
+// page-locked staging buffer owned by the library, so the caller's host
+// memory may be reused as soon as this returns.  The staging buffer is
+// reused by the next call once this copy has left (an event, waited on by
+// the next call).  Small tables only (launch descriptors).
+int upload_async(void* dev_dst, const void* host_src, size_t bytes, hipStream_t st);
+
 inline unsigned grid_1d(int64_t n, int threads, int64_t cap = 1 << 20) {
   int64_t g = (n + threads - 1) / threads;
   if (g > cap) g = cap;

@@ -148,15 +148,19 @@ __device__ __forceinline__ float bwd_dw_term(float acc, float g, float x, float 
   return fmaf(g * x, s, acc);
 }
 
-// Backward, float4 path.  Block b handles rows b*RPB + slot + k*grid*RPB.
-// MAXC = float4 chunks per lane (H/4/LPR rounded up) kept as dw partials.
-// ACC: dx += the gradient (dx holds a running sum, read with the row).
+// Backward, float4 path.  Block b handles rows b*RPB + slot + k*grid*RPB,
+// NR of them (k, k+1, ...) per pass of the loop so that a lane has NR rows'
+// loads in flight; the dw partials still take the rows in increasing k, the
+// same order (and sums) for any NR.  MAXC = float4 chunks per lane (H/4/LPR
+// rounded up) kept as dw partials.  ACC: dx += the gradient (dx holds a
+// running sum, read with the row; one row per pass keeps its registers).
 template <int LPR, int MAXC, bool ACC>
 __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
     const float* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ w,
     const float* __restrict__ rstd, float* __restrict__ dx, float* __restrict__ dw_part,
     int64_t rows, int64_t H, float eps) {
   constexpr int RPB = kThreads / LPR;
+  constexpr int NR = ACC ? 1 : 2;
   extern __shared__ __attribute__((aligned(16))) float red[];  // [RPB][H]
   const int slot = threadIdx.x / LPR;
   const int sub = threadIdx.x % LPR;
@@ -168,64 +172,80 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
   for (int j = 0; j < MAXC; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int64_t step = static_cast<int64_t>(gridDim.x) * RPB;
-  for (int64_t row0 = static_cast<int64_t>(blockIdx.x) * RPB; row0 < rows; row0 += step) {
-    const int64_t row = row0 + slot;
-    const bool live = row < rows;
-    const f32x4* xr = reinterpret_cast<const f32x4*>(x + (live ? row : 0) * H);
-    const f32x4* gr = reinterpret_cast<const f32x4*>(dy + (live ? row : 0) * H);
-    // The row's x and dy chunks stay in registers for the dx pass below.
-    f32x4 xv[MAXC], gv[MAXC], ov[ACC ? MAXC : 1];  // ov: dx's running sum (ACC)
-    float ss = 0.f, c = 0.f;
-    if (live) {
+  for (int64_t row0 = static_cast<int64_t>(blockIdx.x) * RPB; row0 < rows; row0 += NR * step) {
+    int64_t rr[NR];
+    bool live[NR];
+    // The rows' x and dy chunks stay in registers for the dx pass below.
+    f32x4 xv[NR][MAXC], gv[NR][MAXC], ov[ACC ? MAXC : 1];  // ov: dx's running sum (ACC)
+    float ss[NR], c[NR];
+#pragma unroll
+    for (int u = 0; u < NR; ++u) {
+      rr[u] = row0 + u * step + slot;
+      live[u] = rr[u] < rows;
+      ss[u] = 0.f;
+      c[u] = 0.f;
+      const f32x4* xr = reinterpret_cast<const f32x4*>(x + (live[u] ? rr[u] : 0) * H);
+      const f32x4* gr = reinterpret_cast<const f32x4*>(dy + (live[u] ? rr[u] : 0) * H);
 #pragma unroll
       for (int j = 0; j < MAXC; ++j) {
         const int64_t ci = sub + static_cast<int64_t>(j) * LPR;
-        xv[j] = ci < nc ? xr[ci] : f32x4{0.f, 0.f, 0.f, 0.f};
-        gv[j] = ci < nc ? gr[ci] : f32x4{0.f, 0.f, 0.f, 0.f};
+        xv[u][j] = live[u] && ci < nc ? xr[ci] : f32x4{0.f, 0.f, 0.f, 0.f};
+        gv[u][j] = live[u] && ci < nc ? gr[ci] : f32x4{0.f, 0.f, 0.f, 0.f};
       }
-      if constexpr (ACC) {  // loaded with the row, not behind the sums below
+    }
+    if constexpr (ACC) {  // loaded with the row, not behind the sums below
 #pragma unroll
-        for (int j = 0; j < MAXC; ++j) {
-          const int64_t ci = sub + static_cast<int64_t>(j) * LPR;
-          ov[j] = ci < nc ? reinterpret_cast<const f32x4*>(dx + row * H)[ci]
-                          : f32x4{0.f, 0.f, 0.f, 0.f};
-        }
+      for (int j = 0; j < MAXC; ++j) {
+        const int64_t ci = sub + static_cast<int64_t>(j) * LPR;
+        ov[j] = live[0] && ci < nc ? reinterpret_cast<const f32x4*>(dx + rr[0] * H)[ci]
+                                   : f32x4{0.f, 0.f, 0.f, 0.f};
       }
+    }
+#pragma unroll
+    for (int u = 0; u < NR; ++u) {
+      if (!live[u]) continue;
 #pragma unroll
       for (int j = 0; j < MAXC; ++j) {
         const int64_t ci = sub + static_cast<int64_t>(j) * LPR;
         if (ci < nc) {
-          const f32x4 v = xv[j], g = gv[j], ww = wv[ci];
+          const f32x4 v = xv[u][j], g = gv[u][j], ww = wv[ci];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            ss = fmaf(v[e], v[e], ss);
-            c = bwd_c_term(c, g[e], ww[e], v[e]);
+            ss[u] = fmaf(v[e], v[e], ss[u]);
+            c[u] = bwd_c_term(c[u], g[e], ww[e], v[e]);
           }
         }
       }
     }
-    ss = group_sum(ss, LPR);
-    c = group_sum(c, LPR);
-    if (!live) continue;
-    const float s = rstd ? rstd[row] : 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
-    const float k = s * s * c * invH;
 #pragma unroll
-    for (int j = 0; j < MAXC; ++j) {
-      const int64_t ci = sub + static_cast<int64_t>(j) * LPR;
-      if (ci < nc) {
-        const f32x4 v = xv[j], g = gv[j], ww = wv[ci];
-        f32x4 o;
+    for (int u = 0; u < NR; ++u) {  // every lane takes part in the group sums
+      ss[u] = group_sum(ss[u], LPR);
+      c[u] = group_sum(c[u], LPR);
+    }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          o[e] = bwd_dx(s, g[e], ww[e], v[e], k);
-          acc[j][e] = bwd_dw_term(acc[j][e], g[e], v[e], s);
-        }
-        if (dx) {
-          if constexpr (ACC) {  // dx += this gradient (one add, as ember_accumulate)
+    for (int u = 0; u < NR; ++u) {
+      if (!live[u]) continue;
+      const int64_t row = rr[u];
+      const float s = rstd ? rstd[row] : 1.0f / sqrtf(ss[u] / static_cast<float>(H) + eps);
+      const float k = s * s * c[u] * invH;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = ov[j][e] + o[e];
+      for (int j = 0; j < MAXC; ++j) {
+        const int64_t ci = sub + static_cast<int64_t>(j) * LPR;
+        if (ci < nc) {
+          const f32x4 v = xv[u][j], g = gv[u][j], ww = wv[ci];
+          f32x4 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            o[e] = bwd_dx(s, g[e], ww[e], v[e], k);
+            acc[j][e] = bwd_dw_term(acc[j][e], g[e], v[e], s);
           }
-          reinterpret_cast<f32x4*>(dx + row * H)[ci] = o;
+          if (dx) {
+            if constexpr (ACC) {  // dx += this gradient (one add, as ember_accumulate)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) o[e] = ov[j][e] + o[e];
+            }
+            reinterpret_cast<f32x4*>(dx + row * H)[ci] = o;
+          }
         }
       }
     }

@@ -7,7 +7,7 @@
 // clip norm is reproducible, all of a model's gradients in one launch (the
 // reference launches one kernel per parameter, optim.cu:262-270, and scales
 // them one by one, optim.cu:277-289).
-#include <mutex>
+#include <vector>
 
 #include "common.h"
 
@@ -255,61 +255,28 @@ namespace {
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
-// Page-locked staging for the item tables of batched launches: written on the
-// host, copied to the caller's workspace on the launch's stream.  The copy of
-// one call must have left before the next call rewrites the table.
-struct ListStaging {
-  std::mutex mu;
-  ListItem* host = nullptr;
-  size_t cap = 0;
-  hipEvent_t copied = nullptr;
-};
-ListStaging& staging() {
-  static ListStaging* s = new ListStaging();  // lives as long as the process
-  return *s;
-}
-
 // Builds the item table of `count` tensors (blocks per tensor from
-// blocks_of(n), 0 for empty tensors) and copies it to `dev_items` on stream
-// st; returns the total number of blocks, or a negative status.
+// blocks_of(n); empty tensors are left out) and copies it to `dev_items` on
+// stream st; returns the total number of blocks, or a negative status.
 template <typename BlocksOf>
 int64_t upload_items(const float* const* ptrs, const int64_t* sizes, int count, ListItem* dev_items,
                      hipStream_t st, BlocksOf blocks_of, int* kept) {
-  ListStaging& sg = staging();
-  std::lock_guard<std::mutex> lk(sg.mu);
-  if (sg.copied) {
-    const hipError_t e = hipEventSynchronize(sg.copied);
-    if (e != hipSuccess) return -status_of(e);
-  } else if (hipEventCreateWithFlags(&sg.copied, hipEventDisableTiming) != hipSuccess) {
-    return -EMBER_EINVAL;
-  }
-  if (sg.cap < static_cast<size_t>(count)) {
-    if (sg.host) (void)hipHostFree(sg.host);
-    sg.host = nullptr;
-    sg.cap = 0;
-    void* h = nullptr;
-    const hipError_t e = hipHostMalloc(&h, static_cast<size_t>(count) * sizeof(ListItem));
-    if (e != hipSuccess) return -status_of(e);
-    sg.host = static_cast<ListItem*>(h);
-    sg.cap = static_cast<size_t>(count);
-  }
+  std::vector<ListItem> items;
+  items.reserve(static_cast<size_t>(count));
   int64_t total = 0;
-  int m = 0;
   for (int i = 0; i < count; ++i) {
     const int64_t n = sizes[i];
     if (n < 0 || (n > 0 && !ptrs[i])) return -EMBER_EINVAL;
     if (n == 0) continue;
     const int64_t nb = blocks_of(n);
-    sg.host[m++] = ListItem{ptrs[i], n, total, static_cast<int32_t>(nb),
-                            aligned16(ptrs[i]) ? 1 : 0};
+    items.push_back(ListItem{ptrs[i], n, total, static_cast<int32_t>(nb),
+                             aligned16(ptrs[i]) ? 1 : 0});
     total += nb;
   }
-  *kept = m;
-  if (m == 0) return 0;
-  hipError_t e = hipMemcpyAsync(dev_items, sg.host, static_cast<size_t>(m) * sizeof(ListItem),
-                                hipMemcpyHostToDevice, st);
-  if (e == hipSuccess) e = hipEventRecord(sg.copied, st);
-  return e == hipSuccess ? total : -status_of(e);
+  *kept = static_cast<int>(items.size());
+  if (items.empty()) return 0;
+  const int rc = upload_async(dev_items, items.data(), items.size() * sizeof(ListItem), st);
+  return rc ? -rc : total;
 }
 
 int64_t sumsq_blocks_of(int64_t n) {

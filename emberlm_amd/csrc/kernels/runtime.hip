@@ -1,9 +1,52 @@
 // Runtime half of the C ABI: memory, copies, streams, events, seeded fills.
 #include <cstring>
+#include <mutex>
 
 #include "common.h"
 
 using namespace ember;
+
+namespace ember {
+
+namespace {
+struct Staging {
+  std::mutex mu;
+  void* host = nullptr;
+  size_t cap = 0;
+  hipEvent_t copied = nullptr;
+};
+Staging& staging() {
+  static Staging* s = new Staging();  // lives as long as the process
+  return *s;
+}
+}  // namespace
+
+int upload_async(void* dev_dst, const void* host_src, size_t bytes, hipStream_t st) {
+  if (bytes == 0) return EMBER_OK;
+  if (!dev_dst || !host_src) return EMBER_EINVAL;
+  Staging& sg = staging();
+  std::lock_guard<std::mutex> lk(sg.mu);
+  hipError_t e = hipSuccess;
+  if (sg.copied) {
+    e = hipEventSynchronize(sg.copied);  // the previous table has left the buffer
+  } else {
+    e = hipEventCreateWithFlags(&sg.copied, hipEventDisableTiming);
+  }
+  if (e != hipSuccess) return status_of(e);
+  if (sg.cap < bytes) {
+    if (sg.host) (void)hipHostFree(sg.host);
+    sg.host = nullptr;
+    sg.cap = 0;
+    if ((e = hipHostMalloc(&sg.host, bytes)) != hipSuccess) return status_of(e);
+    sg.cap = bytes;
+  }
+  std::memcpy(sg.host, host_src, bytes);
+  e = hipMemcpyAsync(dev_dst, sg.host, bytes, hipMemcpyHostToDevice, st);
+  if (e == hipSuccess) e = hipEventRecord(sg.copied, st);
+  return status_of(e);
+}
+
+}  // namespace ember
 
 extern "C" const char* ember_status_string(int status) {
   switch (status) {

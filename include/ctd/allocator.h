@@ -12,6 +12,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <string>
+#include <vector>
 
 #include "ctd/device.h"
 
@@ -65,6 +66,15 @@ void sample_device_memory();
 // large workspaces fill the holes that other tensors' lifetimes leave instead
 // of growing the device memory held.
 size_t elastic_workspace_bytes(size_t want, size_t least);
+// Byte sizes of the pieces for a workspace that may be split into separate
+// allocations of whole `unit`s (the rows of a chunked computation): up to
+// `want` units from the largest cached free blocks, at most `max_pieces`
+// pieces, cut to a multiple of `multiple` units when short of `want`; when
+// those hold fewer than `least` units, one more piece for the rest of
+// `want`, which grows the memory held.  Allocate the pieces in the order
+// given, before any other allocation, for them to land where planned.
+std::vector<size_t> device_scatter_plan(size_t unit, size_t want, size_t least, size_t multiple,
+                                        size_t max_pieces);
 // Allocation history for offline study of the allocator's placement: start
 // records the blocks live now and then every request and release; stop
 // writes the record to `path` (lines "a <id> <bytes>", "f <id>", "m <label>").

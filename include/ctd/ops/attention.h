@@ -11,17 +11,16 @@ namespace ctd::ops {
 // Autograd-aware: saves q, k, v, o and the per-row log-sum-exp.
 Tensor causal_attention(const Tensor& q, const Tensor& k, const Tensor& v, float scale);
 // Device memory the backward may use to keep dS between its dK/dV and dQ
-// passes (ember_attn_bwd): less than a layer's full dS splits the pass into
-// chunks of KV heads, 0 recomputes dS in the dQ pass instead; -1 restores the
-// default (kAttentionBackwardDsBytes).  Results do not depend on it.  The
-// default holds Qwen3-1.7B's dS at B=8, T=4096 (4.4 GB per layer) in four
-// chunks, and the backward takes less than that when the device allocator
-// holds no free block that large but one of at least half of it.  A budget of
-// 2.5 GB (two chunks) ran 0.67 ms per layer faster there, but no block that
-// size stays free among the checkpoints and gradients of a step, so the
-// allocator grew by 2.4 GB at a time and held 1.32x the live bytes (1.10x at
-// this default); smaller models fit in one or two chunks.
-constexpr int64_t kAttentionBackwardDsBytes = 1250000000;
+// passes (ember_attn_bwd_scattered): less than a layer's full dS splits the
+// pass into chunks of KV rows (one (batch, KV head) pair each, in multiples
+// of 8), 0 recomputes dS in the dQ pass instead; -1 restores the default
+// (kAttentionBackwardDsBytes).  Results do not depend on it.  The default
+// holds Qwen3-1.7B's dS at B=8, T=4096 (4.4 GB per layer, 68 MB per KV row)
+// in two chunks of 32 rows.  The rows are spread over up to 16 free blocks
+// the device allocator already holds, and the backward keeps fewer rows
+// (down to 16) rather than grow the memory held, so the budget costs held
+// memory only when the free blocks together hold fewer than 16 rows.
+constexpr int64_t kAttentionBackwardDsBytes = 2500000000;
 void set_attention_backward_ds_bytes(int64_t bytes);
 // Forward only; lse (if non-null) receives the [B,H,T] log-sum-exp.
 Tensor causal_attention_impl(const Tensor& q, const Tensor& k, const Tensor& v, float scale,

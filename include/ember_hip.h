@@ -263,19 +263,33 @@ int ember_attn_fwd(const float* q, const float* k, const float* v, float* o, flo
  * BmmBackward, SoftmaxBackward, CausalMaskBackward, MulScalarBackward,
  * RepeatKvBackward and PermuteBackward of the chain (matmul.cpp:137-152,
  * softmax.cu:54-80, mask.cu:41-52, repeat_kv.cu:29-43, permute.cu).
- * The workspace holds rowsum(dO*O) ([B,H,T]) and, when it is large enough, dS
- * for the causal part of as many KV heads' query groups as fit (4*T^2/2 bytes
- * per (batch, query head) roughly); the dQ product then reads dS instead of
- * recomputing it, and the work runs in chunks of KV heads.
+ * The workspace holds rowsum(dO*O) ([B,H,T]), a table of KV-row pointers and,
+ * when it is large enough, dS for the causal part of as many KV heads' query
+ * groups as fit (ember_attn_bwd_ds_row_bytes per (batch, KV head), about
+ * group*4*T^2/2 bytes); the dQ product then reads dS instead of recomputing
+ * it, and the work runs in chunks of KV heads.
  * ember_attn_bwd_workspace_bytes: the size that keeps all of dS (fastest);
  * ember_attn_bwd_workspace_bytes_min: the smallest accepted (no dS kept).
  * Any size in between works; dq, dk and dv do not depend on the chunking. */
 size_t ember_attn_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H);
 size_t ember_attn_bwd_workspace_bytes_min(int64_t B, int64_t T, int64_t H);
+size_t ember_attn_bwd_ds_row_bytes(int64_t T, int64_t H, int64_t Hk);
 int ember_attn_bwd(const float* q, const float* k, const float* v, const float* o,
                    const float* lse, const float* dout, float* dq, float* dk, float* dv,
                    int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D, float scale,
                    void* workspace, size_t workspace_bytes, ember_stream_t s);
+/* ember_attn_bwd with dS in separate buffers (a host array of nbufs device
+ * pointers and sizes; the workspace needs only ember_attn_bwd_workspace_bytes_min):
+ * each buffer holds whole KV rows of dS (ember_attn_bwd_ds_row_bytes each), and
+ * a chunk is as many KV rows as the buffers hold together, so dS can sit in
+ * free blocks of the caller's allocator that no single block would hold.
+ * Same results, bit for bit, as ember_attn_bwd with the same number of rows
+ * per chunk.  Same replaced chain as ember_attn_bwd. */
+int ember_attn_bwd_scattered(const float* q, const float* k, const float* v, const float* o,
+                             const float* lse, const float* dout, float* dq, float* dk, float* dv,
+                             int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D, float scale,
+                             void* workspace, size_t workspace_bytes, float* const* ds_bufs_host,
+                             const size_t* ds_bytes_host, int nbufs, ember_stream_t s);
 
 /* ------------------------------------------------------ KV cache (inference)
  * Cache layout [B, Hk, S, D] (S = max_seq_len), fp32, as nn::KVCache holds it.

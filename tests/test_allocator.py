@@ -6,7 +6,8 @@ the cap and a recorded training step can be checked without a GPU.
 The recorded history (tests/golden/alloc_history_qwen3-1.7b_B8_T4096.txt.gz)
 is the device allocator's own record (bench.py --alloc-history) of setup, one
 warmup and three timed recompute + offload steps of Qwen3-1.7B at B=8,
-T=4096 on an MI355X."""
+T=4096 on an MI355X, including the split dS workspaces of the attention
+backward ("s" records), which the replay plans again against its own arena."""
 import gzip
 import os
 import shutil
@@ -63,6 +64,43 @@ def test_cap_empties_the_cache_then_refuses(tmp_path):
     # Live blocks alone above the cap: the request is refused.
     with pytest.raises(TR.CtdError, match="out of memory"):
         replay(tmp_path, ["a 0 629145600", "a 1 629145600"], limit=1024 * MiB)
+
+
+# Three free segments of 300, 200 and 100 MiB, kept apart (each its own
+# segment, so they never coalesce).
+HOLES = ["a 0 314572800", "a 1 209715200", "a 2 104857600", "f 0", "f 1", "f 2"]
+UNIT = 64 * MiB
+
+
+def test_split_workspace_fills_the_free_blocks_without_growing(tmp_path):
+    # 8 units of 64 MiB: 4 in the 300 MiB block, 3 in the 200, 1 in the 100.
+    r = replay(tmp_path, HOLES + [f"s {UNIT} 8 4 1 16 1", "a 9 536870912", "f 9",
+                                  "a 10 314572800"])
+    assert r.segments_obtained == 3
+    assert r.peak_reserved == 600 * MiB
+    assert r.peak_allocated == 600 * MiB
+
+
+def test_split_workspace_grows_for_the_rest_below_least(tmp_path):
+    # Only the 100 MiB block is free (1 unit < least 4): the rest of the 8
+    # units (448 MiB) is one new piece.
+    r = replay(tmp_path, ["a 0 104857600", "f 0", f"s {UNIT} 8 4 1 16 1", "a 9 536870912"])
+    assert r.segments_obtained == 2
+    assert r.peak_reserved == 100 * MiB + 448 * MiB
+    assert r.peak_allocated == 64 * MiB + 448 * MiB
+
+
+def test_split_workspace_is_cut_to_a_multiple(tmp_path):
+    # The 300 and 200 MiB blocks hold 7 units; cut to a multiple of 4, the
+    # 200 MiB block stays free and serves the next 200 MiB request.
+    lines = ["a 0 314572800", "a 1 209715200", "f 0", "f 1", f"s {UNIT} 16 4 4 16 1",
+             "a 9 1073741824", "a 10 209715200"]
+    r = replay(tmp_path, lines)
+    assert r.segments_obtained == 2 and r.peak_reserved == 500 * MiB
+    # At most one piece: only the largest block is used.
+    r = replay(tmp_path, ["a 0 314572800", "a 1 209715200", "f 0", "f 1",
+                          f"s {UNIT} 7 2 1 2 1", "a 9 1073741824", "a 10 209715200"])
+    assert r.segments_obtained == 2 and r.peak_reserved == 500 * MiB
 
 
 def test_replay_rejects_malformed_histories(tmp_path):

@@ -57,12 +57,17 @@ def test_argument_validation_without_gpu():
     # zero-size work is a no-op
     assert lib.ember_add(None, None, None, 0, None) == 0
     assert lib.ember_rmsnorm_bwd_workspace_bytes(32768, 2048) > 0
-    assert lib.ember_attn_bwd_workspace_bytes_min(8, 4096, 16) == 8 * 4096 * 16 * 4
+    # rowsum(dO*O) per (batch, head, query) + a table of B*H row pointers,
+    # each part padded to 256 bytes
+    assert lib.ember_attn_bwd_workspace_bytes_min(8, 4096, 16) == 8 * 4096 * 16 * 4 + 1024
     # + dS strips: 64 keys x (4096 - 64 kb) queries for kb < 64 = 8519680 floats
     # per (batch, head)
-    assert lib.ember_attn_bwd_workspace_bytes(8, 4096, 16) == 8 * 16 * (4096 + 8519680) * 4
+    assert lib.ember_attn_bwd_workspace_bytes(8, 4096, 16) == 8 * 16 * (4096 + 8519680) * 4 + 1024
+    # a KV row holds its group's heads: 2 x 8519680 floats for 16 / 8 heads
+    assert lib.ember_attn_bwd_ds_row_bytes(4096, 16, 8) == 2 * 8519680 * 4
+    assert lib.ember_attn_bwd_ds_row_bytes(4096, 16, 3) == 0
     # T = 100: T32 = 128, strips of 64 x 128 and 64 x 64 floats
-    assert lib.ember_attn_bwd_workspace_bytes(1, 100, 1) == 512 + (64 * 128 + 64 * 64) * 4
+    assert lib.ember_attn_bwd_workspace_bytes(1, 100, 1) == 512 + 256 + (64 * 128 + 64 * 64) * 4
     assert lib.ember_ce_masked_fwd_workspace_bytes(32768) == 32768 * 4
 
 

@@ -1007,7 +1007,9 @@ def test_attention_bwd_workspace_paths(B, T, H, Hk, D):
     lo = lib.ember_attn_bwd_workspace_bytes_min(B, T, H)
     hi = lib.ember_attn_bwd_workspace_bytes(B, T, H)
     kv_row = (H // Hk) * _ds_row_floats(T) * 4
-    assert lo == (B * T * H * 4 + 255) // 256 * 256 and hi == lo + B * Hk * kv_row
+    table = (B * H * 8 + 255) // 256 * 256
+    assert lo == (B * T * H * 4 + 255) // 256 * 256 + table and hi == lo + B * Hk * kv_row
+    assert lib.ember_attn_bwd_ds_row_bytes(T, H, Hk) == kv_row
     Q, K, Vv, DO = dev(q), dev(k), dev(v), dev(do)
     runs = {}
     for name, wsb in [("full", hi), ("one", lo + kv_row), ("three", lo + 3 * kv_row + 100),
@@ -1024,6 +1026,57 @@ def test_attention_bwd_workspace_paths(B, T, H, Hk, D):
         assert_close(dq, dq_ref, name=f"{name} dq")
         assert_close(dk, dk_ref, name=f"{name} dk")
         assert_close(dv, dv_ref, name=f"{name} dv")
+
+
+@pytest.mark.parametrize("B,T,H,Hk,D,split", [
+    (2, 96, 32, 8, 64, [3, 5.5, 0, 8]),   # 16 KV rows over four buffers (one empty)
+    (2, 96, 32, 8, 64, [5, 6]),           # 11 rows: chunks cut to 8
+    (2, 96, 32, 8, 64, [1, 1, 1]),        # 3 rows: chunks of 3
+    (1, 200, 32, 8, 64, [2, 2, 2, 2]),    # all 8 rows, group 4
+    (4, 130, 8, 1, 128, [0.5, 2.9]),      # D 128: a buffer too small for a row
+])
+def test_attention_bwd_scattered_equals_contiguous(B, T, H, Hk, D, split):
+    # dS in separate buffers (ember_attn_bwd_scattered) gives dQ, dK and dV
+    # bitwise equal to one contiguous workspace with the same rows per chunk,
+    # and writes nothing outside the whole rows of each buffer.
+    r = rng(B * 77 + T + len(split))
+    q, k, v, do = (r.standard_normal(s).astype(np.float32)
+                   for s in ((B, T, H, D), (B, T, Hk, D), (B, T, Hk, D), (B, T, H, D)))
+    scale = 1.0 / math.sqrt(D)
+    lib = capi.lib()
+    lo = lib.ember_attn_bwd_workspace_bytes_min(B, T, H)
+    row = lib.ember_attn_bwd_ds_row_bytes(T, H, Hk)
+    kv_rows = B * Hk
+    sizes = [int(f * row) // 256 * 256 if f != int(f) else int(f) * row for f in split]
+    rows = sum(s // row for s in sizes)
+    chunk = min(rows, kv_rows)
+    if 8 <= chunk < kv_rows:
+        chunk -= chunk % 8
+    Q, K, Vv, DO = dev(q), dev(k), dev(v), dev(do)
+    Ot, L, DQc, DKc, DVc = _attn_hip(Q, K, Vv, DO, B, T, H, Hk, D, scale, lo + chunk * row)
+    # the buffers: one device allocation, each buffer followed by a guard band
+    guard = 4096
+    offs, o = [], 0
+    for s in sizes:
+        offs.append(o)
+        o += (s + guard + 255) // 256 * 256
+    POOL = torch.full(((o + 3) // 4,), 7.25, device="cuda")
+    base = POOL.data_ptr()
+    ptrs = (C.c_void_p * len(sizes))(*[base + off if s else None for off, s in zip(offs, sizes)])
+    szs = (C.c_size_t * len(sizes))(*sizes)
+    WS = empty(((lo + 3) // 4,))
+    DQ, DK, DV = empty((B, T, H, D)), empty((B, T, Hk, D)), empty((B, T, Hk, D))
+    call("ember_attn_bwd_scattered", p(Q), p(K), p(Vv), p(Ot), p(L), p(DO), p(DQ), p(DK), p(DV),
+         B, T, H, Hk, D, scale, p(WS), lo, ptrs, szs, len(sizes), None)
+    assert torch.equal(DQ, DQc) and torch.equal(DK, DKc) and torch.equal(DV, DVc)
+    pool = host(POOL).view(np.uint8)
+    fill = np.frombuffer(np.float32(7.25).tobytes(), np.uint8)
+    left = chunk  # row slots are taken in buffer order
+    for off, s in zip(offs, sizes):
+        used = min(s // row, left)
+        left -= used
+        tail = pool[off + used * row: off + s + guard]
+        assert np.array_equal(tail.reshape(-1, 4), np.broadcast_to(fill, (tail.size // 4, 4)))
 
 
 # The launch layouts of the BASELINE configs: c3 Qwen3-0.6B (64 (batch, head)
