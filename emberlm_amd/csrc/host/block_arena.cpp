@@ -169,8 +169,8 @@ std::vector<size_t> BlockArena::scatter_fit(size_t unit, size_t want, size_t lea
     pieces.push_back(n * unit);
     placed += n;
   }
-  if (placed < least) {
-    pieces.push_back((want - placed) * unit);
+  if (placed < least) {  // grow by no more than `least` needs
+    pieces.push_back((least - placed) * unit);
     return pieces;
   }
   if (multiple > 1 && placed < want && placed >= multiple) {

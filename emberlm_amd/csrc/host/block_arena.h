@@ -92,7 +92,7 @@ class BlockArena {
   // many units as it holds, until `want` units are placed or `max_pieces`
   // blocks are used, then cut to a multiple of `multiple` units when that
   // leaves at least one multiple.  Fewer than `least` units placed that way:
-  // one more piece for the rest of `want`, which grows the arena.  See
+  // one more piece for the rest of `least`, which grows the arena.  See
   // device_scatter_plan.
   std::vector<size_t> scatter_fit(size_t unit, size_t want, size_t least, size_t multiple,
                                   size_t max_pieces) const;

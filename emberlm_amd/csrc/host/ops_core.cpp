@@ -634,14 +634,14 @@ constexpr size_t kAttnDsMaxPieces = 16;
 
 // Buffers for the dS that ember_attn_bwd_scattered keeps, whole KV rows
 // (one (batch, KV head) pair's strips) each: as many rows as the budget
-// holds, in multiples of 8, the rows per chunk of the pass.  They are placed
-// in free blocks the allocator already holds, several if need be, so that
-// the 2+ GB of dS a Qwen3-1.7B layer keeps at B=8, T=4096 does not need a
-// contiguous block (and grows the memory held only when the free blocks
-// hold fewer than 16 rows).  dQ, dK and dV are bitwise the same for any
-// rows per chunk; fewer rows leave the dK/dV launch too few workgroups to
-// balance the causal triangle's heavy key blocks: with 8-row chunks it took
-// 13.2 ms per Qwen3-1.7B layer against 8.8 ms with 32-row chunks.
+// holds, in multiples of 8.  They are placed in free blocks the allocator
+// already holds, several if need be, so that the 4.4 GB of dS a Qwen3-1.7B
+// layer has at B=8, T=4096 needs no contiguous block; the memory held grows
+// only when the free blocks hold fewer than 16 rows, and then to 16.  dQ, dK
+// and dV are bitwise the same for any rows per chunk; fewer rows leave the
+// dK/dV launch too few workgroups to balance the causal triangle's heavy key
+// blocks: with 8-row chunks it took 13.2 ms per Qwen3-1.7B layer against
+// 8.8 ms with 32-row chunks.
 std::vector<Tensor> attn_bwd_ds_buffers(const AttnDims& d) {
   const int64_t budget = g_attn_ds_bytes.load();
   const size_t row = ember_attn_bwd_ds_row_bytes(d.T, d.H, d.Hk);

@@ -9,7 +9,8 @@
 //
 // Layout: q, o, dq [B,T,H,D]; k, v, dk, dv [B,T,Hk,D]; lse, delta [B,H,T].
 //
-// Every kernel runs on v_mfma_f32_16x16x4_f32 tiles (wave64): lane
+// The forward, dK/dV and recompute-dQ kernels run on v_mfma_f32_16x16x4_f32
+// tiles (wave64; the dQ-from-dS kernel is a GEMM, described there): lane
 // (g = lane/16, i = lane%16) holds A[m=i][k=g] and B[k=g][n=i]; accumulator
 // register e holds C[m = 4*g + e][n = i].  A wave owns 16 rows (queries or
 // keys), so its register-resident rows and accumulators take half of what 32
@@ -31,8 +32,8 @@
 //                registers across every query tile and every query head of
 //                the KV head's group, in a fixed order.  With a dS buffer it
 //                also stores dS (fp32, the causal part only, see below);
-//   attn_bwd_dq_ds: dQ^T += K^T dS^T per 32 queries from the stored dS, a
-//                plain product in key order;
+//   attn_bwd_dq_gemm: dQ = dS K from the stored dS, a plain product in key
+//                order on the GEMM kernel's 256 x D tiles;
 //   attn_bwd_dq (no dS buffer): per 16 queries, S^T = K Q^T and dP^T =
 //                V dO^T recomputed, then dQ^T += K^T dS^T.
 // Counted in units of one T x T x D product per head, the algorithm needs 4
@@ -43,16 +44,19 @@
 // starting at query 64 kb, so only the causal part is kept; strips follow
 // each other in kb order (ds_strip_offset).  The dK/dV kernel writes one
 // float4 of four consecutive queries per lane; entries it skips (query tiles
-// no key of a wave sees) are never read, because the dQ kernel masks keys
-// after the query.
+// no key of a wave sees) are read, but zeroed with every other query < key
+// entry, by the dQ kernel.  The table at the end of the workspace gives each
+// (batch, KV head) row's dS region; the regions of one chunk of rows may lie
+// in separate buffers (ember_attn_bwd_scattered).
 // The dK/dV and recompute-dQ kernels take 64 rows per workgroup (two waves
 // per SIMD at D = 128; 32 rows per wave on 32x32x2 tiles needed more than 256
-// registers per lane there), the dQ-from-dS kernel 128 queries (32 per wave,
-// three waves per SIMD at D = 128); all double-buffer their streamed tiles the
-// same way.
+// registers per lane there) and double-buffer their streamed tiles the same
+// way.
+#include <type_traits>
 #include <vector>
 
 #include "common.h"
+#include "mfma_sched.h"
 
 using namespace ember;
 
@@ -507,7 +511,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
   // head (a KV row's region holds its group's heads one after another; the
   // table gives each KV row's region); columns count queries from key0.
   const int64_t T32 = ds_t32(T), ds_row = ds_row_floats(T), lr = T32 - key0;
-  float* ds_lane = ds_rows ? ds_rows[kvrow] + ds_strip_offset(kb, T32) +
+  gfloat* ds_lane = ds_rows ? as_global(ds_rows[kvrow]) + ds_strip_offset(kb, T32) +
                                  static_cast<int64_t>(16 * w + i) * lr + 4 * g
                            : nullptr;
 
@@ -581,9 +585,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
           dp[mt][e] = p * (dp[mt][e] - Es[ql]);
         }
       if (ds_lane) {  // queries qt0 + 16mt + 4g + (0..3) of this lane's key
-        float* dst = ds_lane + (step / ntile) * ds_row + (qt0 - key0);
+        gfloat* dst = ds_lane + (step / ntile) * ds_row + (qt0 - key0);
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) *reinterpret_cast<f32x4*>(dst + 16 * mt) = dp[mt];
+        for (int mt = 0; mt < 2; ++mt) *reinterpret_cast<gf32x4*>(dst + 16 * mt) = dp[mt];
       }
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
@@ -612,126 +616,202 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
   }
 }
 
-// dQ from the stored dS: dQ^T += K^T dS^T (m = d, n = query, contraction
-// over keys), 32 queries per wave as two 16-query MFMA tiles, so that every
-// b32 LDS read of K feeds two MFMAs; 128 queries per workgroup, over 32-key
-// tiles in key order.  K tiles are double-buffered in LDS; the next tile's dS
-// values (sixteen per lane: keys 16kt + 4g + e for queries i and 16 + i of
-// the wave) are loaded into registers before the current tile's MFMAs.  Keys
-// after a lane's query, and queries at or past T, read nothing and count as
-// 0, which adds exact zeros: every dQ element sums the same products in the
-// same key order as a 16-query tiling would.
+// dQ = scale * dS K from the stored dS on the GEMM kernel's machinery
+// (gemm.hip's gemm_f32_dma): m = query, n = d, contraction over keys; 256
+// queries x D per workgroup, four waves in 2 x 2 on v_mfma_f32_32x32x2f32
+// tiles; 16-key stages copied global -> LDS by global_load_lds_dwordx4 into a
+// 3-stage ring two stages ahead of the MFMAs, up to the tile's last query.
+//   A = dS^T: a key's row of its strip holds queries 64 sb ... contiguously,
+//     so one 1 KB DMA block is one key's 256 queries (chunk q of key row k at
+//     chunk position q ^ (8 ((k >> 2) & 1)), as the GEMM lays out an
+//     M-contiguous tile), read back as b128 rows of four consecutive queries.
+//   B = K rows (d contiguous), laid out the same way.
+// Entries with query < key are zeroed in registers after the LDS read: the
+// dK/dV kernel does not write all of them, and a tile's queries before a
+// strip's first query read the end of the strip before it (inside the same
+// (b, h) region); query columns past a strip row's end are clamped into it
+// (they only reach rows past T, which are not stored), keys past T into the
+// last key.  Every dQ element sums the same products in the same key order
+// whatever the chunking or placement of dS.
 template <int D>
-struct DqDsCfg {
-  static constexpr int kWQ = 32;  // queries per wave
-  static constexpr int kBQ = 4 * kWQ, kBK = 32, kKS = D + 4;
-  static constexpr int kBuf = kBK * kKS;
-  static constexpr int kSmem = 2 * kBuf;
+struct DqGemmCfg {
+  static constexpr int kBM = 256, kBN = D, FI = 4, FJ = D / 64;
+  static constexpr int kAFloats = kBM * 16, kBFloats = kBN * 16;
+  static constexpr int kStage = kAFloats + kBFloats;
+  static constexpr int kInstA = kBM / 64, kInstB = kBN / 64;  // DMA per wave per stage
 };
 
 template <int D>
-__global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_ds_kernel(
+__global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_gemm_kernel(
     const float* __restrict__ k, const float* const* __restrict__ ds_rows, float* __restrict__ dq,
     int row0, int T, int H, int Hk, float scale) {
-  using C = DqDsCfg<D>;
-  constexpr int NT = D / 16;
-  __shared__ __attribute__((aligned(16))) float smem[C::kSmem];
+  using C = DqGemmCfg<D>;
+  constexpr int FI = C::FI, FJ = C::FJ, BM = C::kBM, BN = C::kBN;
+  constexpr int NR = 4 + 4 * FJ;           // LDS reads per slab: A b128 x 4, B b32 x 4 FJ
+  constexpr int NM = 4 * FI * FJ;          // MFMAs per slab
+  constexpr int NI = C::kInstA + C::kInstB;
+  __shared__ __attribute__((aligned(1024))) float lds[3 * C::kStage];
 
-  const int nqb = (T + C::kBQ - 1) / C::kBQ;
-  const WorkItem wi = work_item(nqb);
-  const int qb = nqb - 1 - wi.tile;  // longest rows first
+  const int nmt = (T + BM - 1) / BM;
+  const WorkItem wi = work_item(nmt);
+  const int mt = nmt - 1 - wi.tile;  // longest rows first
   const int row = row0 + wi.row;     // (b, h)
   const int h = row % H, b = row / H;
   const int hk = h / (H / Hk);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, i = lane & 15;
-  const int q0 = qb * C::kBQ, qw0 = q0 + C::kWQ * w;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1, g = lane >> 5, r = lane & 31;
+  const int m0 = mt * BM;
   const int64_t qs = static_cast<int64_t>(H) * D, ks = static_cast<int64_t>(Hk) * D;
   const float* kbase = k + static_cast<int64_t>(b) * T * ks + static_cast<int64_t>(hk) * D;
   const int64_t T32 = ds_t32(T);
-  // Head h's part of its KV row's dS region (heads of a group in order).
-  const float* dsrow = ds_rows[b * Hk + hk] + static_cast<int64_t>(h - hk * (H / Hk)) * ds_row_floats(T);
+  const float* dsrow =
+      ds_rows[b * Hk + hk] + static_cast<int64_t>(h - hk * (H / Hk)) * ds_row_floats(T);
 
-  // dS^T[key][query] for keys k0 + 16kt + 4g + e of 32-key tile kbi and the
-  // lane's queries qw0 + 16n + i.
-  auto load_ds = [&](int kbi, float (&dst)[2][2][4]) {
-    const int k0 = kbi * C::kBK, sb = k0 >> 6;
+  // DMA of stage kt (keys 16 kt ... 16 kt + 15, all in strip sb) into `dst`.
+  auto issue = [&](float* dst, int kt) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass would drop the kernel's launch stub
+    const int k0 = 16 * kt, sb = k0 >> 6;
     const int64_t lr = T32 - 64 * sb;
+    const float* strip = dsrow + ds_strip_offset(sb, T32);
 #pragma unroll
-    for (int n = 0; n < 2; ++n) {
-      const int myq = qw0 + 16 * n + i;
-      const float* strip = dsrow + ds_strip_offset(sb, T32) + (myq - 64 * sb);
+    for (int q = 0; q < C::kInstA; ++q) {
+      const int t = wave + 4 * q;  // key row of the stage = 1 KB block of the tile
+      const int q4 = lane ^ (8 * ((t >> 2) & 1));
+      const int64_t col = min(static_cast<int64_t>(m0 - 64 * sb + 4 * q4), lr - 4);
+      __builtin_amdgcn_global_load_lds(strip + (k0 + t - 64 * sb) * lr + col, dst + 256 * t, 16,
+                                       0, 0);
+    }
+    constexpr int kRowsPer = 256 / BN, kLanesPer = 64 / kRowsPer;
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+    for (int q = 0; q < C::kInstB; ++q) {
+      const int t = wave + 4 * q;
+      const int kr = t * kRowsPer + lane / kLanesPer;
+      const int q4 = (lane % kLanesPer) ^ (8 * ((kr >> 2) & 1));
+      const int key = min(k0 + kr, T - 1);
+      __builtin_amdgcn_global_load_lds(kbase + key * ks + 4 * q4, dst + C::kAFloats + 256 * t,
+                                       16, 0, 0);
+    }
+#endif
+  };
+  // A fragments of slab s: query m0 + 128 wm + 4 r + i at k-step j (key
+  // 16 kt + 8 s + 4 g + j) in fa[i][j]; query < key zeroed where the slab
+  // reaches past the wave's first query.
+  const int qw = m0 + (BM / 2) * wm;
+  auto load_a = [&](const float* st, int kt, int s, f32x4 (&fa)[FI]) {
+    const int off = 4 * (((BM / 8) * wm + r) ^ (8 * g));  // chunk (qw - m0) / 4 + r
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int key = k0 + 16 * kt + 4 * g + e;
-          dst[n][kt][e] = (myq < T && key <= myq)
-                              ? strip[static_cast<int64_t>(key - 64 * sb) * lr]
-                              : 0.f;
-        }
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(st + (8 * s + 4 * g + j) * BM + off);
+#pragma unroll
+      for (int i = 0; i < FI; ++i) fa[i][j] = v[i];
+    }
+    if (16 * kt + 8 * s + 7 > qw) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < FI; ++i)
+          fa[i][j] = qw + 4 * r + i < 16 * kt + 8 * s + 4 * g + j ? 0.f : fa[i][j];
+    }
+  };
+  const int mbB = (wn * (BN / 2)) >> 2;
+  auto load_b = [&](const float* st, int s, f32x4 (&fb)[FJ]) {
+#pragma unroll
+    for (int jj = 0; jj < FJ; ++jj) {
+      const int qc = (mbB + 8 * jj) ^ (8 * g);
+      const float* p = st + C::kAFloats + (8 * s + 4 * g) * BN + (qc << 2) + r;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) fb[jj][j] = p[j * BN];
     }
   };
 
-  f32x4 acc[2][NT];
+  f32x16 acc[FI][FJ];
 #pragma unroll
-  for (int n = 0; n < 2; ++n)
+  for (int i = 0; i < FI; ++i)
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[n][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int jj = 0; jj < FJ; ++jj)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][jj][e] = 0.f;
 
-  const int kend = min(T, q0 + C::kBQ);
-  const int nkb = (kend + C::kBK - 1) / C::kBK;
-  RowTile<D, C::kBK> tk;
-  float cur[2][2][4], nxt[2][2][4];
-  tk.load(kbase, ks, T);
-  load_ds(0, cur);
-  tk.store(smem, C::kKS);
-  __syncthreads();
-
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int k0 = kb * C::kBK;
-    const bool more = kb + 1 < nkb;
-    if (more) {
-      tk.load(kbase + static_cast<int64_t>(k0 + C::kBK) * ks, ks, T - k0 - C::kBK);
-      load_ds(kb + 1, nxt);
-    }
-    const float* Ks = smem + (kb & 1) * C::kBuf;
-    if (k0 <= qw0 + C::kWQ - 1) {  // some key of the tile is seen by some query of this wave
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = (16 * kt + 4 * g + e) * C::kKS;
-#pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            const float kv = Ks[r + 16 * t + i];
-#pragma unroll
-            for (int n = 0; n < 2; ++n) acc[n][t] = mfma16(kv, cur[n][kt][e], acc[n][t]);
-          }
-        }
-    }
-    if (more) {
-      tk.store(smem + ((kb + 1) & 1) * C::kBuf, C::kKS);
-#pragma unroll
-      for (int n = 0; n < 2; ++n)
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) cur[n][kt][e] = nxt[n][kt][e];
-    }
-    __syncthreads();
+  const int kend = min(T, m0 + BM);
+  const int nk = (kend + 15) / 16;
+  issue(lds, 0);
+  if (nk > 1) {
+    issue(lds + C::kStage, 1);
+    wait_vm_lgkm0<NI>();
+  } else {
+    wait_vm_lgkm0<0>();
   }
+  block_barrier();
+  f32x4 fa0[FI], fb0[FJ], fa1[FI], fb1[FJ];
+  load_a(lds, 0, 0, fa0);
+  load_b(lds, 0, fb0);
 
+  // The GEMM kernel's stage: slab 1's reads, slab 0's MFMAs with them spread
+  // among, the DMA two stages ahead, slab 1's first MFMAs, the barrier after
+  // stage kt+1's copy has landed, the next stage's slab-0 reads under slab
+  // 1's last MFMAs.
+  int ic = 0;  // kt % 3
+  auto stage = [&](int kt, auto with_dma) {
+    constexpr bool kDma = decltype(with_dma)::value;
+    float* cur = lds + ic * C::kStage;
+    float* nxt = lds + (ic == 2 ? 0 : ic + 1) * C::kStage;
+    float* nx2 = lds + (ic == 0 ? 2 : ic - 1) * C::kStage;
+    load_a(cur, kt, 1, fa1);
+    load_b(cur, 1, fb1);
 #pragma unroll
-  for (int n = 0; n < 2; ++n) {
-    const int myq = qw0 + 16 * n + i;
-    if (myq < T) {
-      f32x4* dqr = reinterpret_cast<f32x4*>(dq + static_cast<int64_t>(b) * T * qs +
-                                            static_cast<int64_t>(h) * D + myq * qs);
-      // Accumulator tile t, lane (g, i), register e holds d = 16t + 4g + e.
+    for (int s = 0; s < 4; ++s)
 #pragma unroll
-      for (int t = 0; t < NT; ++t) dqr[4 * t + g] = acc[n][t] * scale;
+      for (int i = 0; i < FI; ++i)
+#pragma unroll
+        for (int jj = 0; jj < FJ; ++jj)
+          acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa0[i][s], fb0[jj][s], acc[i][jj], 0,
+                                                            0, 0);
+    interleave_mfma_first<NR, NM, 0x100>();
+    if constexpr (kDma) issue(nx2, kt + 2);
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int i = 0; i < FI; ++i)
+#pragma unroll
+        for (int jj = 0; jj < FJ; ++jj)
+          acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[i][s], fb1[jj][s], acc[i][jj], 0,
+                                                            0, 0);
+    if constexpr (kDma) interleave<NI, NM / 2, 0x020>();
+    if constexpr (kDma)
+      wait_vm_lgkm0<NI>();
+    else
+      wait_vm_lgkm0<0>();
+    block_barrier();
+    load_a(nxt, kt + 1, 0, fa0);  // past the last stage: unused reads inside the ring
+    load_b(nxt, 0, fb0);
+#pragma unroll
+    for (int s = 2; s < 4; ++s)
+#pragma unroll
+      for (int i = 0; i < FI; ++i)
+#pragma unroll
+        for (int jj = 0; jj < FJ; ++jj)
+          acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1[i][s], fb1[jj][s], acc[i][jj], 0,
+                                                            0, 0);
+    interleave<NR, NM / 2, 0x100>();
+    ic = ic == 2 ? 0 : ic + 1;
+  };
+  int kt = 0;
+  for (; kt + 2 < nk; ++kt) stage(kt, std::true_type{});
+  for (; kt < nk; ++kt) stage(kt, std::false_type{});
+
+  float* dqb = dq + static_cast<int64_t>(b) * T * qs + static_cast<int64_t>(h) * D;
+#pragma unroll
+  for (int i = 0; i < FI; ++i)
+#pragma unroll
+    for (int jj = 0; jj < FJ; ++jj) {
+      const int col = wn * (BN / 2) + jj * 32 + r;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int x = 8 * (e >> 2) + 4 * g + (e & 3);  // the MFMA tile's row slot
+        const int q = qw + 4 * x + i;
+        if (q < T) dqb[static_cast<int64_t>(q) * qs + col] = scale * acc[i][jj][e];
+      }
     }
-  }
 }
 
 int check_shapes(int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D) {
@@ -801,7 +881,7 @@ int launch_bwd(const float* q, const float* k, const float* v, const float* o, c
   static_assert(DqCfg<D>::kBQ == 64, "recompute dQ grid assumes 64 queries");
   static_assert(DkvCfg<D>::kBKeys == 64, "dK/dV grid assumes 64 keys");
   const unsigned nqb = static_cast<unsigned>((T + 63) / 64);
-  const unsigned nqb_ds = static_cast<unsigned>((T + DqDsCfg<D>::kBQ - 1) / DqDsCfg<D>::kBQ);
+  const unsigned nmt = static_cast<unsigned>((T + DqGemmCfg<D>::kBM - 1) / DqGemmCfg<D>::kBM);
   const int64_t group = H / Hk, kv_rows = B * Hk;
   const size_t row_bytes = kv_row_ds_bytes(T, group);
   // KV-row slots in the buffers, in buffer order.
@@ -815,10 +895,19 @@ int launch_bwd(const float* q, const float* k, const float* v, const float* o, c
         q, k, v, dout, lse, delta, dk, dv, nullptr, 0, Ti, Hi, Hki, sl, scale);
     return launch_status();
   }
-  // Chunks of KV rows whose dS fits; a multiple of 8 rows keeps the XCD
-  // regrouping of the work items.
-  if (chunk < kv_rows && chunk >= 8) chunk -= chunk % 8;
-  if (chunk > kv_rows) chunk = kv_rows;
+  // Chunks of KV rows whose dS fits, as equal as the room allows (a short
+  // last chunk leaves its dK/dV launch too few workgroups for the causal
+  // triangle's uneven blocks), in multiples of 8 rows where the room has 8,
+  // which keeps the XCD regrouping of the work items.
+  if (chunk >= kv_rows) {
+    chunk = kv_rows;
+  } else {
+    if (chunk >= 8) chunk -= chunk % 8;
+    const int64_t nch = (kv_rows + chunk - 1) / chunk;
+    int64_t even = (kv_rows + nch - 1) / nch;
+    if (chunk >= 8) even = (even + 7) / 8 * 8;
+    chunk = even < chunk ? even : chunk;
+  }
   // KV row r of a chunk takes slot r - r0: the same slots for every chunk.
   std::vector<float*> host_table(static_cast<size_t>(kv_rows));
   std::vector<float*> slot(static_cast<size_t>(chunk));
@@ -837,8 +926,7 @@ int launch_bwd(const float* q, const float* k, const float* v, const float* o, c
     attn_bwd_dkdv_kernel<D><<<dim3(nqb * static_cast<unsigned>(n)), kThreads, 0, st>>>(
         q, k, v, dout, lse, delta, dk, dv, table, static_cast<int>(r0), Ti, Hi, Hki, sl, scale);
     if ((rc = launch_status())) return rc;
-    attn_bwd_dq_ds_kernel<D><<<dim3(nqb_ds * static_cast<unsigned>(n * group)), kThreads, 0,
-                               st>>>(
+    attn_bwd_dq_gemm_kernel<D><<<dim3(nmt * static_cast<unsigned>(n * group)), kThreads, 0, st>>>(
         k, table, dq, static_cast<int>(r0 * group), Ti, Hi, Hki, scale);
     if ((rc = launch_status())) return rc;
   }

@@ -14,6 +14,15 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kWave = 64;
 
+// Global-memory views of a pointer the compiler cannot place (one loaded from
+// a table in device memory is a generic pointer): accesses through them are
+// global_* instructions, not flat_* ones, which also count on the LDS wait
+// counter and so hold up the kernel's LDS waits until the stores complete.
+typedef __attribute__((address_space(1))) float gfloat;
+typedef __attribute__((address_space(1))) f32x4 gf32x4;
+__device__ __forceinline__ gfloat* as_global(float* p) { return (gfloat*)p; }
+__device__ __forceinline__ const gfloat* as_global(const float* p) { return (const gfloat*)p; }
+
 inline int status_of(hipError_t e) { return e == hipSuccess ? EMBER_OK : static_cast<int>(e); }
 
 // Status of the most recent launch on this thread.

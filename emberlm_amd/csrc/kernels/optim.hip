@@ -103,7 +103,7 @@ __device__ __forceinline__ ListItem find_item(const ListItem* __restrict__ items
 // (four running sums per lane, then a fixed tree), so the total does not
 // depend on timing or on how the tensors are grouped into launches.
 template <bool VEC>
-__device__ __forceinline__ float sumsq_block(const float* __restrict__ x, int64_t n, int64_t b,
+__device__ __forceinline__ float sumsq_block(const gfloat* __restrict__ x, int64_t n, int64_t b,
                                              int64_t nb, float* red) {
   float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
   const int64_t stride = nb * kThreads;
@@ -111,7 +111,7 @@ __device__ __forceinline__ float sumsq_block(const float* __restrict__ x, int64_
   int64_t tail = 0;
   if (VEC) {
     const int64_t n4 = n / 4;
-    const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
+    const gf32x4* x4 = reinterpret_cast<const gf32x4*>(x);
     int64_t i = tid;
     for (; i + 3 * stride < n4; i += 4 * stride) {
       const f32x4 v0 = x4[i], v1 = x4[i + stride], v2 = x4[i + 2 * stride], v3 = x4[i + 3 * stride];
@@ -136,8 +136,8 @@ __global__ __launch_bounds__(kThreads) void sumsq_list(const ListItem* __restric
   __shared__ float red[kThreads / kWave];
   const ListItem it = find_item(items, count, blockIdx.x);
   const int64_t b = static_cast<int64_t>(blockIdx.x) - it.first;
-  const float a = it.vec ? sumsq_block<true>(it.x, it.n, b, it.blocks, red)
-                         : sumsq_block<false>(it.x, it.n, b, it.blocks, red);
+  const float a = it.vec ? sumsq_block<true>(as_global(it.x), it.n, b, it.blocks, red)
+                         : sumsq_block<false>(as_global(it.x), it.n, b, it.blocks, red);
   if (threadIdx.x == 0) part[blockIdx.x] = a;
 }
 
@@ -145,12 +145,12 @@ __global__ __launch_bounds__(kThreads) void sumsq_list(const ListItem* __restric
 __global__ __launch_bounds__(kThreads) void scale_list(const ListItem* __restrict__ items,
                                                        int count, float alpha) {
   const ListItem it = find_item(items, count, blockIdx.x);
-  float* x = const_cast<float*>(it.x);
+  gfloat* x = as_global(const_cast<float*>(it.x));  // a pointer from the table
   const int64_t stride = static_cast<int64_t>(it.blocks) * kThreads;
   const int64_t tid = (static_cast<int64_t>(blockIdx.x) - it.first) * kThreads + threadIdx.x;
   int64_t tail = 0;
   if (it.vec) {
-    f32x4* x4 = reinterpret_cast<f32x4*>(x);
+    gf32x4* x4 = reinterpret_cast<gf32x4*>(x);
     const int64_t n4 = it.n / 4;
     for (int64_t i = tid; i < n4; i += stride) x4[i] = x4[i] * alpha;
     tail = n4 * 4;

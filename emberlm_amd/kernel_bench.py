@@ -152,7 +152,7 @@ def entries():
                     8.0 * total, 0.0, f"{cnt} tensors")
         return setup
 
-    def attention(bwd, ds_bytes=1250000000):
+    def attention(bwd, ds_rows=None):
         def setup():
             q, k, v = rand(B, T, H, D) * 0.5, rand(B, T, HK, D) * 0.5, rand(B, T, HK, D)
             o, lse = torch.empty(B, T, H, D, device="cuda"), torch.empty(B, H, T, device="cuda")
@@ -166,12 +166,14 @@ def entries():
             do = rand(B, T, H, D)
             dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
             lo = lib.ember_attn_bwd_workspace_bytes_min(B, T, H)
-            wsb = lo + ds_bytes
+            rows = B * HK if ds_rows is None else ds_rows  # KV rows of dS kept per chunk
+            wsb = lo + rows * lib.ember_attn_bwd_ds_row_bytes(T, H, HK)
             ws = torch.empty(wsb // 4 + 1, device="cuda")
             return (lambda: ck(lib.ember_attn_bwd(P(q), P(k), P(v), P(o), P(lse), P(do), P(dq), P(dk),
                                                   P(dv), B, T, H, HK, D, scale, P(ws), wsb, None),
                                "attn bwd"),
-                    0.0, 2.0 * fwd_flops, f"B{B} T{T} H{H}/{HK} D{D}, dS {ds_bytes / 1e9:.2f} GB")
+                    0.0, 2.0 * fwd_flops,
+                    f"B{B} T{T} H{H}/{HK} D{D}, dS of {rows} KV rows per chunk ({(wsb - lo) / 1e9:.2f} GB)")
         return setup
 
     return {
@@ -180,7 +182,7 @@ def entries():
         "qknorm_rope_bwd": qknorm_rope(True), "swiglu_fwd": swiglu(False), "swiglu_bwd": swiglu(True),
         "embedding_fwd": embedding(False), "embedding_bwd": embedding(True), "adamw": adamw,
         "clip_sumsq": clip(False), "clip_scale": clip(True), "attn_fwd": attention(False),
-        "attn_bwd": attention(True), "attn_bwd_ds2.5GB": attention(True, 2500000000),
+        "attn_bwd": attention(True), "attn_bwd_32_rows": attention(True, 32),
     }
 
 

@@ -71,7 +71,7 @@ size_t elastic_workspace_bytes(size_t want, size_t least);
 // `want` units from the largest cached free blocks, at most `max_pieces`
 // pieces, cut to a multiple of `multiple` units when short of `want`; when
 // those hold fewer than `least` units, one more piece for the rest of
-// `want`, which grows the memory held.  Allocate the pieces in the order
+// `least`, which grows the memory held.  Allocate the pieces in the order
 // given, before any other allocation, for them to land where planned.
 std::vector<size_t> device_scatter_plan(size_t unit, size_t want, size_t least, size_t multiple,
                                         size_t max_pieces);

@@ -12,15 +12,15 @@ namespace ctd::ops {
 Tensor causal_attention(const Tensor& q, const Tensor& k, const Tensor& v, float scale);
 // Device memory the backward may use to keep dS between its dK/dV and dQ
 // passes (ember_attn_bwd_scattered): less than a layer's full dS splits the
-// pass into chunks of KV rows (one (batch, KV head) pair each, in multiples
-// of 8), 0 recomputes dS in the dQ pass instead; -1 restores the default
+// pass into chunks of KV rows (one (batch, KV head) pair each), 0 recomputes
+// dS in the dQ pass instead; -1 restores the default
 // (kAttentionBackwardDsBytes).  Results do not depend on it.  The default
-// holds Qwen3-1.7B's dS at B=8, T=4096 (4.4 GB per layer, 68 MB per KV row)
-// in two chunks of 32 rows.  The rows are spread over up to 16 free blocks
-// the device allocator already holds, and the backward keeps fewer rows
-// (down to 16) rather than grow the memory held, so the budget costs held
-// memory only when the free blocks together hold fewer than 16 rows.
-constexpr int64_t kAttentionBackwardDsBytes = 2500000000;
+// holds the whole dS of a Qwen3-1.7B layer at B=8, T=4096 (4.36 GB, 68 MB
+// per KV row).  The rows are spread over up to 16 free blocks the device
+// allocator already holds, and the backward keeps fewer rows (in equal
+// chunks) rather than grow the memory held: it grows it only when the free
+// blocks hold fewer than 16 rows, and then only to 16.
+constexpr int64_t kAttentionBackwardDsBytes = 4500000000;
 void set_attention_backward_ds_bytes(int64_t bytes);
 // Forward only; lse (if non-null) receives the [B,H,T] log-sum-exp.
 Tensor causal_attention_impl(const Tensor& q, const Tensor& k, const Tensor& v, float scale,

@@ -81,13 +81,13 @@ def test_split_workspace_fills_the_free_blocks_without_growing(tmp_path):
     assert r.peak_allocated == 600 * MiB
 
 
-def test_split_workspace_grows_for_the_rest_below_least(tmp_path):
-    # Only the 100 MiB block is free (1 unit < least 4): the rest of the 8
-    # units (448 MiB) is one new piece.
+def test_split_workspace_grows_only_to_least(tmp_path):
+    # Only the 100 MiB block is free (1 unit < least 4): the rest of the 4
+    # units (192 MiB) is one new piece; the other 4 units wanted are not.
     r = replay(tmp_path, ["a 0 104857600", "f 0", f"s {UNIT} 8 4 1 16 1", "a 9 536870912"])
     assert r.segments_obtained == 2
-    assert r.peak_reserved == 100 * MiB + 448 * MiB
-    assert r.peak_allocated == 64 * MiB + 448 * MiB
+    assert r.peak_reserved == 100 * MiB + 192 * MiB
+    assert r.peak_allocated == 64 * MiB + 192 * MiB
 
 
 def test_split_workspace_is_cut_to_a_multiple(tmp_path):

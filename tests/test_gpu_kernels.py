@@ -1028,10 +1028,26 @@ def test_attention_bwd_workspace_paths(B, T, H, Hk, D):
         assert_close(dv, dv_ref, name=f"{name} dv")
 
 
+def _bwd_chunk(rows, kv_rows):
+    """KV rows per chunk of the attention backward with room for `rows`: the
+    chunks as equal as the room allows, multiples of 8 where it holds 8."""
+    if rows >= kv_rows:
+        return kv_rows
+    if rows >= 8:
+        rows -= rows % 8
+    nch = -(-kv_rows // rows)
+    even = -(-kv_rows // nch)
+    if rows >= 8:
+        even = -(-even // 8) * 8
+    return min(even, rows)
+
+
 @pytest.mark.parametrize("B,T,H,Hk,D,split", [
     (2, 96, 32, 8, 64, [3, 5.5, 0, 8]),   # 16 KV rows over four buffers (one empty)
     (2, 96, 32, 8, 64, [5, 6]),           # 11 rows: chunks cut to 8
-    (2, 96, 32, 8, 64, [1, 1, 1]),        # 3 rows: chunks of 3
+    (2, 96, 32, 8, 64, [1, 1, 1]),        # 3 rows: chunks of 3 (the last of 1)
+    (2, 96, 32, 8, 64, [3, 2]),           # 5 rows: four equal chunks of 4
+    (3, 64, 32, 8, 64, [9, 9]),           # 24 KV rows, 18 fit: chunks of 16 and 8
     (1, 200, 32, 8, 64, [2, 2, 2, 2]),    # all 8 rows, group 4
     (4, 130, 8, 1, 128, [0.5, 2.9]),      # D 128: a buffer too small for a row
 ])
@@ -1049,9 +1065,7 @@ def test_attention_bwd_scattered_equals_contiguous(B, T, H, Hk, D, split):
     kv_rows = B * Hk
     sizes = [int(f * row) // 256 * 256 if f != int(f) else int(f) * row for f in split]
     rows = sum(s // row for s in sizes)
-    chunk = min(rows, kv_rows)
-    if 8 <= chunk < kv_rows:
-        chunk -= chunk % 8
+    chunk = _bwd_chunk(rows, kv_rows)
     Q, K, Vv, DO = dev(q), dev(k), dev(v), dev(do)
     Ot, L, DQc, DKc, DVc = _attn_hip(Q, K, Vv, DO, B, T, H, Hk, D, scale, lo + chunk * row)
     # the buffers: one device allocation, each buffer followed by a guard band
