@@ -364,6 +364,9 @@ def main():
 
     if args.attn_ds_bytes is not None:
         TR.set_attn_ds_bytes(args.attn_ds_bytes)
+    # Device memory in use before the first tensor: the HIP runtime's context
+    # and code objects (part of peak_hbm_gb, not of the allocator's figures).
+    base_used = TR.memory().device_used
     if args.alloc_history:
         TR.alloc_history_start()   # from the first allocation: setup, warmup and timed steps
     t0 = time.time()
@@ -461,6 +464,7 @@ def main():
         "peak_hbm_live_gb": round(mem.peak_allocated / 1e9, 3),
         "peak_hbm_reserved_gb": round(mem.peak_reserved / 1e9, 3),
         "hbm_device_used_gb": round(mem.device_used / 1e9, 3),
+        "hbm_runtime_gb": round(base_used / 1e9, 3),
         "allocator": {"reserved_over_live": round(mem.peak_reserved / max(mem.peak_allocated, 1), 4),
                       "segments_obtained": int(mem.device_mallocs),
                       "cache_flushes": int(mem.cache_flushes)},

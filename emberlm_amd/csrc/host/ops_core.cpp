@@ -635,8 +635,8 @@ constexpr size_t kAttnDsMaxPieces = 16;
 // Buffers for the dS that ember_attn_bwd_scattered keeps, whole KV rows
 // (one (batch, KV head) pair's strips) each: as many rows as the budget
 // holds, in multiples of 8.  They are placed in free blocks the allocator
-// already holds, several if need be, so that the 4.4 GB of dS a Qwen3-1.7B
-// layer has at B=8, T=4096 needs no contiguous block; the memory held grows
+// already holds, several if need be, so that the 2.2 GB of dS a Qwen3-1.7B
+// layer keeps per chunk at B=8, T=4096 needs no contiguous block; the memory held grows
 // only when the free blocks hold fewer than 16 rows, and then to 16.  dQ, dK
 // and dV are bitwise the same for any rows per chunk; fewer rows leave the
 // dK/dV launch too few workgroups to balance the causal triangle's heavy key

@@ -18,6 +18,10 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kMaxBwdBlocks = 1024;
+// The float4 path on rows of 1024 floats or more: fewer blocks running more
+// rows each (and half the dw partials for the column sum): 0.1545 against
+// 0.1725 ms at 32768 x 2048 with the non-temporal loads below.
+constexpr int kMaxBwdBlocksWide = 512;
 
 __device__ __forceinline__ float group_sum(float v, int lpr) {
   for (int o = lpr >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
@@ -87,7 +91,8 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_reg(const float* __restr
 #pragma unroll
     for (int j = 0; j < MAXC; ++j) {
       const int64_t ci = sub + static_cast<int64_t>(j) * LPR;
-      v[j] = ci < nc ? xr[ci] : f32x4{0.f, 0.f, 0.f, 0.f};
+      // non-temporal: read once (0.084 against 0.103 ms at 32768 x 2048)
+      v[j] = ci < nc ? __builtin_nontemporal_load(xr + ci) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
     for (int j = 0; j < MAXC; ++j)
@@ -189,8 +194,12 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
 #pragma unroll
       for (int j = 0; j < MAXC; ++j) {
         const int64_t ci = sub + static_cast<int64_t>(j) * LPR;
-        xv[u][j] = live[u] && ci < nc ? xr[ci] : f32x4{0.f, 0.f, 0.f, 0.f};
-        gv[u][j] = live[u] && ci < nc ? gr[ci] : f32x4{0.f, 0.f, 0.f, 0.f};
+        // read once: non-temporal loads (x and dy do not displace the dx
+        // running sum the accumulating form reads back)
+        xv[u][j] = live[u] && ci < nc ? __builtin_nontemporal_load(xr + ci)
+                                      : f32x4{0.f, 0.f, 0.f, 0.f};
+        gv[u][j] = live[u] && ci < nc ? __builtin_nontemporal_load(gr + ci)
+                                      : f32x4{0.f, 0.f, 0.f, 0.f};
       }
     }
     if constexpr (ACC) {  // loaded with the row, not behind the sums below
@@ -394,13 +403,14 @@ __global__ __launch_bounds__(kThreads) void qknorm_rope_fwd(const float* __restr
   constexpr int64_t H = 4 * LPR;
   __shared__ RopeTable<LPR> tb;
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * RPB;
-  int64_t tok0;
-  fill_rope_table<LPR>(tb, row0, rows, rr, tok0);
   const int64_t row = row0 + threadIdx.x / LPR;
   const int sub = threadIdx.x % LPR;
   const bool live = row < rows;  // the same for every lane of a row's group
   const int64_t r = live ? row : rows - 1;
+  // the row's load is in flight while the block computes its sine table
   const f32x4 v = reinterpret_cast<const f32x4*>(x + r * H)[sub];
+  int64_t tok0;
+  fill_rope_table<LPR>(tb, row0, rows, rr, tok0);
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 4; ++e) ss = fmaf(v[e], v[e], ss);
@@ -432,32 +442,46 @@ __global__ __launch_bounds__(kThreads) void qknorm_rope_bwd(
   const float invH = 1.0f / static_cast<float>(H);
   const f32x4 ww = reinterpret_cast<const f32x4*>(w)[sub];
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  // NR rows per pass (rows k, k+1, ... of the slot, so the dw partials take
+  // them in the same order as one at a time), loaded (non-temporal: read
+  // once) before any is reduced.  q of Qwen3-1.7B at B=8, T=4096: 0.148 ms
+  // with two rows, 0.195 with four, 0.198 with one.
+  constexpr int NR = 2;
   const int64_t step = static_cast<int64_t>(gridDim.x) * RPB;
-  for (int64_t row0 = static_cast<int64_t>(blockIdx.x) * RPB; row0 < rows; row0 += step) {
-    const int64_t row = row0 + slot;
-    const bool live = row < rows;
-    const int64_t r = live ? row : rows - 1;
-    const f32x4 v = reinterpret_cast<const f32x4*>(x + r * H)[sub];
-    const f32x4 g =
-        rotate_row_chunk_regs<LPR>(reinterpret_cast<const f32x4*>(dy + r * H)[sub], sub, r, rr);
-    float ss = 0.f, c = 0.f;
+  for (int64_t row0 = static_cast<int64_t>(blockIdx.x) * RPB; row0 < rows; row0 += NR * step) {
+    f32x4 v[NR], graw[NR];
+    int64_t rr_[NR];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      ss = fmaf(v[e], v[e], ss);
-      c = bwd_c_term(c, g[e], ww[e], v[e]);
+    for (int u = 0; u < NR; ++u) {
+      const int64_t row = row0 + u * step + slot;
+      rr_[u] = row < rows ? row : rows - 1;
+      v[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(x + rr_[u] * H) + sub);
+      graw[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(dy + rr_[u] * H) + sub);
     }
-    ss = group_sum(ss, LPR);
-    c = group_sum(c, LPR);
-    if (!live) continue;
-    const float s = rstd ? rstd[row] : 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
-    const float k = s * s * c * invH;
-    f32x4 o;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      o[e] = bwd_dx(s, g[e], ww[e], v[e], k);
-      acc[e] = bwd_dw_term(acc[e], g[e], v[e], s);
+    for (int u = 0; u < NR; ++u) {
+      const int64_t row = row0 + u * step + slot;
+      const bool live = row < rows;
+      const f32x4 g = rotate_row_chunk_regs<LPR>(graw[u], sub, rr_[u], rr);
+      float ss = 0.f, c = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        ss = fmaf(v[u][e], v[u][e], ss);
+        c = bwd_c_term(c, g[e], ww[e], v[u][e]);
+      }
+      ss = group_sum(ss, LPR);
+      c = group_sum(c, LPR);
+      if (!live) continue;
+      const float s = rstd ? rstd[row] : 1.0f / sqrtf(ss / static_cast<float>(H) + eps);
+      const float k = s * s * c * invH;
+      f32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o[e] = bwd_dx(s, g[e], ww[e], v[u][e], k);
+        acc[e] = bwd_dw_term(acc[e], g[e], v[u][e], s);
+      }
+      if (dx) reinterpret_cast<f32x4*>(dx + row * H)[sub] = o;
     }
-    if (dx) reinterpret_cast<f32x4*>(dx + row * H)[sub] = o;
   }
   if (!dw_part) return;
   reinterpret_cast<f32x4*>(red + slot * H)[sub] = acc;
@@ -514,7 +538,8 @@ bool vec_ok(int64_t H, const void* a, const void* b) {
 int64_t bwd_blocks(int64_t rows, int64_t H, bool vec) {
   const int64_t rpb = vec ? kThreads / lanes_per_row(H) : 1;
   int64_t nb = (rows + rpb - 1) / rpb;
-  if (nb > kMaxBwdBlocks) nb = kMaxBwdBlocks;
+  const int64_t cap = vec && H >= 1024 ? kMaxBwdBlocksWide : kMaxBwdBlocks;
+  if (nb > cap) nb = cap;
   if (nb < 1) nb = 1;
   return nb;
 }

@@ -15,12 +15,15 @@ Tensor causal_attention(const Tensor& q, const Tensor& k, const Tensor& v, float
 // pass into chunks of KV rows (one (batch, KV head) pair each), 0 recomputes
 // dS in the dQ pass instead; -1 restores the default
 // (kAttentionBackwardDsBytes).  Results do not depend on it.  The default
-// holds the whole dS of a Qwen3-1.7B layer at B=8, T=4096 (4.36 GB, 68 MB
-// per KV row).  The rows are spread over up to 16 free blocks the device
-// allocator already holds, and the backward keeps fewer rows (in equal
-// chunks) rather than grow the memory held: it grows it only when the free
-// blocks hold fewer than 16 rows, and then only to 16.
-constexpr int64_t kAttentionBackwardDsBytes = 4500000000;
+// holds half the dS of a Qwen3-1.7B layer at B=8, T=4096 (32 of 64 KV rows
+// of 68 MB: two chunks).  The rows are spread over up to 16 free blocks the
+// device allocator already holds, and the backward keeps fewer rows (in
+// equal chunks) rather than grow the memory held: it grows it only when the
+// free blocks hold fewer than 16 rows, and then only to 16.  All 64 rows
+// (one chunk) ran the layer's backward 0.2 ms faster (11.05 against 11.25
+// ms) but raised the step's live peak from 22.0 to 23.9 GB, since the 4.4 GB
+// of dS then outgrow what the MLP's backward holds before it.
+constexpr int64_t kAttentionBackwardDsBytes = 2500000000;
 void set_attention_backward_ds_bytes(int64_t bytes);
 // Forward only; lse (if non-null) receives the [B,H,T] log-sum-exp.
 Tensor causal_attention_impl(const Tensor& q, const Tensor& k, const Tensor& v, float scale,

@@ -3,8 +3,8 @@ through the C ABI, against the workspace entry point ember_rmsnorm_bwd on the
 same inputs: dx and dw bitwise equal, over two calls in a row of which the
 second is smaller, so the second reads a scratch array that still holds the
 first call's partials.  Sizes: the Qwen3-1.7B block norm (32768 rows x 2048,
-8 MiB of partials), then its QK-Norm rows (x 128), then a ragged H that takes
-the scalar kernel."""
+4 MiB of partials), then QK-Norm-width rows (x 128), then a ragged H that
+takes the scalar kernel."""
 import numpy as np
 import pytest
 
@@ -49,8 +49,8 @@ def _both(rows, H, seed, with_rstd=True, with_dx=True):
 
 
 def test_noalloc_equals_workspace_entry_over_calls():
-    _both(32768, 2048, seed=1)                  # 1024 partial rows x 2048
-    _both(4096, 128, seed=2)                    # smaller: 64 partial rows x 128
+    _both(32768, 2048, seed=1)                  # 512 partial rows x 2048
+    _both(4096, 128, seed=2)                    # smaller: 512 partial rows x 128
     _both(300, 70, seed=3, with_rstd=False)     # scalar kernel, rstd recomputed
     _both(257, 2048, seed=4, with_dx=False)     # dw only
 
