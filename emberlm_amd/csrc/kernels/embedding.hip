@@ -7,11 +7,12 @@
 //   - with a workspace (ember_embedding_bwd_workspace_bytes): the token
 //     positions are sorted by id with a stable radix sort (hipCUB), cut into
 //     windows of 64 sorted entries; one workgroup per window sums each run of
-//     equal ids in position order into a partial row, and one workgroup per
-//     window then adds up, for every id whose run starts in it, the partials
-//     of the windows the run spans, in window order, into dW.  The work per
-//     token is bounded however the ids repeat: a batch of one repeated id
-//     (padding) spreads over n/64 workgroups instead of one serial chain.
+//     equal ids in position order and adds it into dW when the run lies in
+//     the window, or keeps it as a partial row when the run crosses a window
+//     edge; a second pass adds, for every crossing run, the partials of the
+//     windows it spans, in window order, into dW.  The work per token is
+//     bounded however the ids repeat: a batch of one repeated id (padding)
+//     spreads over n/64 workgroups instead of one serial chain.
 //   - without one: each block owns kIdsPerBlock vocabulary rows, scans the id
 //     list in order, compacts the positions that hit its range with a wave
 //     ballot (keeping ascending order), and adds those dy rows into its dW
@@ -27,16 +28,24 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kIdsPerBlock = 128;
 
+template <int VEC>
 __global__ __launch_bounds__(kThreads) void embedding_fwd_kernel(const int64_t* __restrict__ ids,
                                                                  const float* __restrict__ w,
                                                                  float* __restrict__ out,
                                                                  int64_t n, int64_t H, int64_t V) {
-  // One block per token row (grid-stride); ids outside [0,V) give zero rows.
+  // One block per token row (grid-stride), VEC columns per thread; ids
+  // outside [0,V) give zero rows.
   for (int64_t r = blockIdx.x; r < n; r += gridDim.x) {
     const int64_t id = ids[r];
     const bool ok = id >= 0 && id < V;
-    for (int64_t c = threadIdx.x; c < H; c += kThreads)
-      out[r * H + c] = ok ? w[id * H + c] : 0.f;
+    for (int64_t c = static_cast<int64_t>(threadIdx.x) * VEC; c < H; c += kThreads * VEC) {
+      if constexpr (VEC == 4) {
+        *reinterpret_cast<f32x4*>(out + r * H + c) =
+            ok ? *reinterpret_cast<const f32x4*>(w + id * H + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+      } else {
+        out[r * H + c] = ok ? w[id * H + c] : 0.f;
+      }
+    }
   }
 }
 
@@ -93,14 +102,46 @@ __global__ __launch_bounds__(kThreads) void emb_sort_prep(const int64_t* __restr
   vals[i] = static_cast<uint32_t>(i);
 }
 
+// Columns a thread handles at once: four (float4) when rows allow it.
+template <int VEC>
+struct Cols;
+template <>
+struct Cols<4> {
+  using T = f32x4;
+  static __device__ __forceinline__ T zero() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+  static __device__ __forceinline__ T load(const float* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+  }
+  static __device__ __forceinline__ T get(const float* p) {
+    return *reinterpret_cast<const f32x4*>(p);
+  }
+  static __device__ __forceinline__ void put(float* p, T v) { *reinterpret_cast<f32x4*>(p) = v; }
+};
+template <>
+struct Cols<1> {
+  using T = float;
+  static __device__ __forceinline__ T zero() { return 0.f; }
+  static __device__ __forceinline__ T load(const float* p) { return *p; }
+  static __device__ __forceinline__ T get(const float* p) { return *p; }
+  static __device__ __forceinline__ void put(float* p, T v) { *p = v; }
+};
+
+constexpr int kAhead = 8;  // dy rows a thread loads before adding them up
+
 // Window w: the sum, in position order, of the dy rows of each run of equal
-// keys among sorted entries [64w, 64w + 64), written to part[64w + k] for the
-// window's k-th run.
+// keys among sorted entries [64w, 64w + 64).  A run that lies wholly in the
+// window is added into dW[key] here (its only owner); the window's first run
+// when it continues one from the window before, and its last run when it
+// continues into the next window, go to part[64w + k] (the window's k-th run)
+// for emb_window_combine.
+template <int VEC>
 __global__ __launch_bounds__(kThreads) void emb_window_sums(const uint32_t* __restrict__ keys,
                                                             const uint32_t* __restrict__ vals,
                                                             const float* __restrict__ dy,
-                                                            float* __restrict__ part, int64_t n,
+                                                            float* __restrict__ part,
+                                                            float* __restrict__ dw, int64_t n,
                                                             int64_t H, int64_t V) {
+  using C = Cols<VEC>;
   __shared__ uint32_t k_s[kWin], v_s[kWin];
   const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kWin;
   const int cnt = static_cast<int>(n - e0 < kWin ? n - e0 : kWin);
@@ -108,61 +149,77 @@ __global__ __launch_bounds__(kThreads) void emb_window_sums(const uint32_t* __re
     k_s[threadIdx.x] = keys[e0 + threadIdx.x];
     v_s[threadIdx.x] = vals[e0 + threadIdx.x];
   }
+  const uint32_t prev_key = e0 > 0 ? keys[e0 - 1] : 0xffffffffu;
+  const uint32_t next_key = e0 + cnt < n ? keys[e0 + cnt] : 0xffffffffu;
   __syncthreads();
-  for (int64_t c = threadIdx.x; c < H; c += kThreads) {
-    float acc = 0.f;
+  for (int64_t c = static_cast<int64_t>(threadIdx.x) * VEC; c < H; c += kThreads * VEC) {
+    typename C::T acc = C::zero();
     int k = 0;
-    for (int e = 0; e < cnt; ++e) {
-      const uint32_t key = k_s[e];
-      if (key >= V) break;  // invalid ids sort last
-      acc += dy[static_cast<int64_t>(v_s[e]) * H + c];
-      if (e + 1 == cnt || k_s[e + 1] != key) {
-        part[(e0 + k) * H + c] = acc;
-        acc = 0.f;
-        ++k;
+    for (int b = 0; b < cnt; b += kAhead) {
+      typename C::T row[kAhead];
+#pragma unroll
+      for (int i = 0; i < kAhead; ++i)
+        row[i] = b + i < cnt && k_s[b + i] < V
+                     ? C::load(dy + static_cast<int64_t>(v_s[b + i]) * H + c)
+                     : C::zero();
+#pragma unroll
+      for (int i = 0; i < kAhead; ++i) {
+        const int e = b + i;
+        if (e >= cnt) break;
+        const uint32_t key = k_s[e];
+        if (key >= V) break;  // invalid ids sort last
+        acc += row[i];
+        if (e + 1 == cnt || k_s[e + 1] != key) {
+          const bool spans = (k == 0 && prev_key == key) || (e + 1 == cnt && next_key == key);
+          if (spans) {
+            C::put(part + (e0 + k) * H + c, acc);
+          } else {
+            float* d = dw + static_cast<int64_t>(key) * H + c;
+            C::put(d, C::get(d) + acc);
+          }
+          acc = C::zero();
+          ++k;
+        }
       }
     }
   }
 }
 
-// Window w: for each run that starts in it (not a continuation of the
-// previous window's last run), dW[key] += its partial + the partials of the
-// following windows the run continues into, in window order.
+// Window w: if its last run starts in it (not a continuation of the previous
+// window's last run) and continues into the next window, dW[key] += its
+// partial + the partials of the following windows the run continues into, in
+// window order.  Every other run was added by emb_window_sums.
+template <int VEC>
 __global__ __launch_bounds__(kThreads) void emb_window_combine(const uint32_t* __restrict__ keys,
                                                                const float* __restrict__ part,
                                                                float* __restrict__ dw, int64_t n,
                                                                int64_t H, int64_t V) {
-  __shared__ uint32_t k_s[kWin];
+  using C = Cols<VEC>;
   const int64_t nwin = (n + kWin - 1) / kWin;
   const int64_t w = blockIdx.x;
   const int64_t e0 = w * kWin;
   const int cnt = static_cast<int>(n - e0 < kWin ? n - e0 : kWin);
-  if (threadIdx.x < cnt) k_s[threadIdx.x] = keys[e0 + threadIdx.x];
-  __syncthreads();
-  const bool continued = w > 0 && keys[e0 - 1] == k_s[0];
+  if (e0 + cnt >= n) return;  // the last window: nothing continues past it
+  const uint32_t key = keys[e0 + cnt - 1];
+  if (key >= V || keys[e0 + cnt] != key) return;
+  // the run's first entry in this window, and the window's number of runs
+  // before it (its part slot)
+  int first = cnt - 1;
+  while (first > 0 && keys[e0 + first - 1] == key) --first;
+  if (first == 0 && w > 0 && keys[e0 - 1] == key) return;  // owned by an earlier window
   int k = 0;
-  for (int e = 0; e < cnt; ++e) {
-    const uint32_t key = k_s[e];
-    if (key >= V) break;
-    const bool run_end = e + 1 == cnt || k_s[e + 1] != key;
-    if (!run_end) continue;
-    const bool owned = !(k == 0 && continued);
-    const bool last_in_window = e + 1 == cnt;
-    if (owned) {
-      for (int64_t c = threadIdx.x; c < H; c += kThreads) {
-        float t = part[(e0 + k) * H + c];
-        // a run ending at the window's end may continue into the next ones
-        for (int64_t w2 = w + 1; last_in_window && w2 < nwin; ++w2) {
-          const int64_t f = w2 * kWin;
-          if (keys[f] != key) break;
-          t += part[f * H + c];  // the continuation is window w2's first run
-          const int64_t fend = f + kWin < n ? f + kWin : n;
-          if (keys[fend - 1] != key) break;  // the run ends inside window w2
-        }
-        dw[static_cast<int64_t>(key) * H + c] += t;
-      }
+  for (int e = 1; e <= first; ++e) k += keys[e0 + e] != keys[e0 + e - 1];
+  for (int64_t c = static_cast<int64_t>(threadIdx.x) * VEC; c < H; c += kThreads * VEC) {
+    typename C::T t = C::get(part + (e0 + k) * H + c);
+    for (int64_t w2 = w + 1; w2 < nwin; ++w2) {
+      const int64_t f = w2 * kWin;
+      if (keys[f] != key) break;
+      t += C::get(part + f * H + c);  // the continuation is window w2's first run
+      const int64_t fend = f + kWin < n ? f + kWin : n;
+      if (keys[fend - 1] != key) break;  // the run ends inside window w2
     }
-    ++k;
+    float* d = dw + static_cast<int64_t>(key) * H + c;
+    C::put(d, C::get(d) + t);
   }
 }
 
@@ -191,7 +248,10 @@ extern "C" int ember_embedding_fwd(const int64_t* ids, const float* w, float* ou
   if (n == 0) return EMBER_OK;
   if (!ids || !w || !out) return EMBER_EINVAL;
   const unsigned g = static_cast<unsigned>(n < 65536 * 4 ? n : 65536 * 4);
-  embedding_fwd_kernel<<<g, kThreads, 0, as_stream(s)>>>(ids, w, out, n, H, V);
+  if (H % 4 == 0 && aligned16(w) && aligned16(out))
+    embedding_fwd_kernel<4><<<g, kThreads, 0, as_stream(s)>>>(ids, w, out, n, H, V);
+  else
+    embedding_fwd_kernel<1><<<g, kThreads, 0, as_stream(s)>>>(ids, w, out, n, H, V);
   return launch_status();
 }
 
@@ -234,9 +294,15 @@ extern "C" int ember_embedding_bwd(const int64_t* ids, const float* dy, float* d
                                                       emb_key_bits(V), st));
     if (rc) return rc;
     const unsigned nwin = static_cast<unsigned>((n + kWin - 1) / kWin);
-    emb_window_sums<<<nwin, kThreads, 0, st>>>(keys, vals, dy, part, n, H, V);
-    if ((rc = launch_status())) return rc;
-    emb_window_combine<<<nwin, kThreads, 0, st>>>(keys, part, dw, n, H, V);
+    if (H % 4 == 0 && aligned16(dy) && aligned16(dw)) {
+      emb_window_sums<4><<<nwin, kThreads, 0, st>>>(keys, vals, dy, part, dw, n, H, V);
+      if ((rc = launch_status())) return rc;
+      emb_window_combine<4><<<nwin, kThreads, 0, st>>>(keys, part, dw, n, H, V);
+    } else {
+      emb_window_sums<1><<<nwin, kThreads, 0, st>>>(keys, vals, dy, part, dw, n, H, V);
+      if ((rc = launch_status())) return rc;
+      emb_window_combine<1><<<nwin, kThreads, 0, st>>>(keys, part, dw, n, H, V);
+    }
     return launch_status();
   }
   const int64_t nb = (V + kIdsPerBlock - 1) / kIdsPerBlock;

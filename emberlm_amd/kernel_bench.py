@@ -115,9 +115,11 @@ def entries():
             ws = torch.empty(wsb // 4 + 1, device="cuda")
             # accumulate into an existing dW (the tied head's): dy read once, the
             # touched rows of dW read and written once
+            distinct = int(torch.unique(ids).numel())
             return (lambda: ck(lib.ember_embedding_bwd(P(ids), P(out), P(w), N, HID, V, 1, P(ws), wsb,
                                                        None), "emb bwd"),
-                    4.0 * N * HID + 8.0 * N * HID, 0.0, f"{N} ids x {HID}, V {V}")
+                    4.0 * N * HID + 8.0 * distinct * HID, 0.0,
+                    f"{N} ids ({distinct} distinct) x {HID}, V {V}")
         return setup
 
     def adamw():
@@ -183,6 +185,7 @@ def entries():
         "embedding_fwd": embedding(False), "embedding_bwd": embedding(True), "adamw": adamw,
         "clip_sumsq": clip(False), "clip_scale": clip(True), "attn_fwd": attention(False),
         "attn_bwd": attention(True), "attn_bwd_32_rows": attention(True, 32),
+        "attn_bwd_no_ds": attention(True, 0),
     }
 
 

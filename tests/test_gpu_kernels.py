@@ -738,6 +738,20 @@ def test_embedding_kat_and_bwd():
     assert_close(host(DW2)[:300], 2 * O.embedding_bwd(ids, dy, V)[:300], name="emb accumulate")
 
 
+def test_embedding_fwd_rows_of_four_columns():
+    # The float4 gather (H % 4 == 0), ids outside [0, V) giving zero rows.
+    r = rng(23)
+    V, H, n = 1000, 2048, 777
+    w = r.standard_normal((V, H)).astype(np.float32)
+    ids = r.integers(-2, V + 2, n).astype(np.int64)
+    out = empty((n, H))
+    I, W = dev(ids), dev(w)
+    call("ember_embedding_fwd", p(I), p(W), p(out), n, H, V, None)
+    valid = (ids >= 0) & (ids < V)
+    want = np.where(valid[:, None], w[np.clip(ids, 0, V - 1)], 0.0).astype(np.float32)
+    assert np.array_equal(host(out), want)
+
+
 def _emb_bwd(ids, dy, V, accumulate=0, dw=None, sorted_path=True):
     n, H = dy.shape
     lib = capi.lib()
@@ -745,21 +759,25 @@ def _emb_bwd(ids, dy, V, accumulate=0, dw=None, sorted_path=True):
     assert (wsb > 0) == sorted_path
     WS = empty((max(wsb // 4, 1),))
     DW = dev(dw) if dw is not None else empty((V, H))
-    call("ember_embedding_bwd", p(dev(ids)), p(dev(dy)), p(DW), n, H, V, accumulate,
+    I, DY = dev(ids), dev(dy)  # held until the call has run (p() keeps only the address)
+    call("ember_embedding_bwd", p(I), p(DY), p(DW), n, H, V, accumulate,
          p(WS) if wsb else None, wsb, None)
+    torch.cuda.synchronize()
     return DW
 
 
-@pytest.mark.parametrize("case", ["repeats", "one_id", "mostly_one", "long_runs", "invalid"])
+@pytest.mark.parametrize("case", ["repeats", "one_id", "mostly_one", "long_runs", "invalid",
+                                  "odd_width"])
 def test_embedding_bwd_sorted_vs_oracle(case):
     # The sorted-window form: random ids with repeats, a batch of one repeated id
     # (every window continues the same run), 90% one id, runs longer than a
-    # window, and ids outside [0, V) (skipped).  Deterministic over repeat calls
-    # and equal to the oracle's sums; accumulate adds onto dw.
+    # window, ids outside [0, V) (skipped), and a row width not a multiple of 4
+    # (one column per thread).  Deterministic over repeat calls and equal to
+    # the oracle's sums; accumulate adds onto dw.
     r = rng(21)
-    V, H = 5000, 2048 if case in ("one_id", "mostly_one") else 96
+    V, H = 5000, {"one_id": 2048, "mostly_one": 2048, "odd_width": 30}.get(case, 96)
     n = 32768 if case in ("one_id", "mostly_one") else 3000
-    if case == "repeats":
+    if case in ("repeats", "odd_width"):
         ids = r.integers(0, 300, n)
     elif case == "one_id":
         ids = np.full(n, 17)
