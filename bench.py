@@ -307,6 +307,8 @@ def main():
     ap.add_argument("--attn-ds-bytes", type=int, default=None,
                     help="device bytes the attention backward may keep dS in (0: recompute it; "
                          "default: the library's)")
+    ap.add_argument("--head-chunk-rows", type=int, default=None,
+                    help="rows per chunk of the fused LM head + loss (default: the library's)")
     ap.add_argument("--alloc-history", default=None,
                     help="write the device allocator's history of the timed steps to this file "
                          "(replayable on the host: emberlm_amd.trainer.alloc_replay)")
@@ -364,6 +366,8 @@ def main():
 
     if args.attn_ds_bytes is not None:
         TR.set_attn_ds_bytes(args.attn_ds_bytes)
+    if args.head_chunk_rows is not None:
+        TR.set_head_chunk_rows(args.head_chunk_rows)
     # Device memory in use before the first tensor: the HIP runtime's context
     # and code objects (part of peak_hbm_gb, not of the allocator's figures).
     base_used = TR.memory().device_used
