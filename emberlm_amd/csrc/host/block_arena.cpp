@@ -153,6 +153,12 @@ size_t BlockArena::largest_free() const {
   return m;
 }
 
+bool BlockArena::fits(size_t bytes) const {
+  const size_t size = round_request(bytes);
+  const FreeSet& set = size <= kSmallRequest ? free_small_ : free_large_;
+  return !set.empty() && (*set.rbegin())->size >= size;
+}
+
 std::vector<size_t> BlockArena::scatter_fit(size_t unit, size_t want, size_t least,
                                             size_t multiple, size_t max_pieces) const {
   std::vector<size_t> pieces;

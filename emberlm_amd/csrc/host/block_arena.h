@@ -81,6 +81,8 @@ class BlockArena {
   }
   // Size of the largest free block (0 if none).
   size_t largest_free() const;
+  // Whether a cached free block serves a request of `bytes` (no new segment).
+  bool fits(size_t bytes) const;
   // `want` when a free block holds it or none holds `least`; else the
   // largest free block (a multiple of kGranule).  See elastic_workspace_bytes.
   size_t elastic_fit(size_t want, size_t least) const {

@@ -41,25 +41,37 @@ MM mm_dims(const Tensor& a, const Tensor& b, bool ta, bool tb, const char* op) {
   return d;
 }
 
-// Forward y = op(a) op(b); backward table of src/ops/matmul.cpp:99-118.
+// Forward y = op(a) op(b); backward table of src/ops/matmul.cpp:99-118, one
+// operand at a time: each gradient is op(x) op(y) of dy and the other operand,
+// dy first or second.
+struct GradForm {
+  bool dy_first, tx, ty;
+};
+GradForm grad_a_form(bool ta, bool tb) {
+  if (!ta && !tb) return {true, false, true};   // dy b^T
+  if (ta && !tb) return {false, false, true};   // b dy^T
+  if (!ta && tb) return {true, false, false};   // dy b
+  return {false, true, true};                   // b^T dy^T
+}
+GradForm grad_b_form(bool ta, bool tb) {
+  if (!ta && !tb) return {false, true, false};  // a^T dy
+  if (ta && !tb) return {false, false, false};  // a dy
+  if (!ta && tb) return {true, true, false};    // dy^T a
+  return {true, true, true};                    // dy^T a^T
+}
+
+template <typename F>
+Tensor grad_product(const GradForm& f, const Tensor& dy, const Tensor& other, F mm) {
+  return f.dy_first ? mm(dy, other, f.tx, f.ty) : mm(other, dy, f.tx, f.ty);
+}
+
 template <typename F>
 std::pair<Tensor, Tensor> matmul_like_backward(const Tensor& dy, const Tensor& a,
                                                const Tensor& b, bool ta, bool tb, bool need_a,
                                                bool need_b, F mm) {
   Tensor dA, dB;
-  if (!ta && !tb) {
-    if (need_a) dA = mm(dy, b, false, true);
-    if (need_b) dB = mm(a, dy, true, false);
-  } else if (ta && !tb) {
-    if (need_a) dA = mm(b, dy, false, true);
-    if (need_b) dB = mm(a, dy, false, false);
-  } else if (!ta && tb) {
-    if (need_a) dA = mm(dy, b, false, false);
-    if (need_b) dB = mm(dy, a, true, false);
-  } else {
-    if (need_a) dA = mm(b, dy, true, true);
-    if (need_b) dB = mm(dy, a, true, true);
-  }
+  if (need_a) dA = grad_product(grad_a_form(ta, tb), dy, b, mm);
+  if (need_b) dB = grad_product(grad_b_form(ta, tb), dy, a, mm);
   return {dA, dB};
 }
 
@@ -90,21 +102,31 @@ struct MatmulBackward : autograd::Node {
                                              const std::vector<Tensor>& partials) override {
     autograd::NoGradGuard ng;
     const bool na = next_edges.at(0).node != nullptr, nb = next_edges.at(1).node != nullptr;
+    const Tensor& dy = go.at(0);
     const Tensor* into = partials.empty() ? nullptr : &partials[0];
     const bool fold = na && into && into->storage() && into->dtype() == DType::kFloat32 &&
                       into->device() == a.device() && into->is_contiguous() &&
                       into->shape() == a.shape();
-    auto [dA, dB] = matmul_like_backward(go.at(0), a, b, ta, tb, na && !fold, nb, matmul_impl);
-    if (fold) {
-      // dA's operands per the same table: op(x) op(y) with (x, y, tx, ty).
-      Tensor acc = *into;
-      if (!ta && !tb) matmul_accumulate(go[0], b, false, true, acc);
-      else if (ta && !tb) matmul_accumulate(b, go[0], false, true, acc);
-      else if (!ta && tb) matmul_accumulate(go[0], b, false, false, acc);
-      else matmul_accumulate(b, go[0], true, true, acc);
-      dA = acc;
+    // dB first: it is a's last reader, so a's memory goes back to the
+    // allocator before dA is allocated (when this node held a alone, as the
+    // MLP's down projection holds the [tokens, intermediate] activation, the
+    // same block can hold the gradient of that activation).
+    Tensor dB;
+    if (nb) dB = grad_product(grad_b_form(ta, tb), dy, a, matmul_impl);
+    release_saved(a);
+    Tensor dA;
+    if (na) {
+      const GradForm f = grad_a_form(ta, tb);
+      if (fold) {
+        Tensor acc = *into;
+        if (f.dy_first) matmul_accumulate(dy, b, f.tx, f.ty, acc);
+        else matmul_accumulate(b, dy, f.tx, f.ty, acc);
+        dA = acc;
+      } else {
+        dA = grad_product(f, dy, b, matmul_impl);
+      }
     }
-    release_saved(a, b);
+    release_saved(b);
     return {dA, dB};
   }
 };
@@ -484,7 +506,15 @@ struct SwigluBackward : autograd::Node {
   std::vector<Tensor> backward(const std::vector<Tensor>& go) override {
     autograd::NoGradGuard ng;
     check_f32(go.at(0), "swiglu backward", "grad");
-    Tensor dg = empty_like(g), du = empty_like(u);
+    // The gradients overwrite gate and up when this node is their only
+    // holder and will not run again (the kernel reads each element before it
+    // writes it): two [tokens, intermediate] buffers fewer in the MLP's
+    // backward.
+    const bool reuse = !autograd::graph_retained();
+    Tensor dg = reuse && g.storage().use_count() == 1 ? g : empty_like(g);
+    Tensor du = reuse && u.storage().use_count() == 1 && u.storage() != g.storage()
+                    ? u
+                    : empty_like(u);
     CTD_CHECK(ember_swiglu_bwd(cfp(g), cfp(u), cfp(go[0]), fp(dg), fp(du), g.numel(), S()));
     release_saved(g, u);
     return {dg, du};
@@ -585,6 +615,15 @@ Tensor swiglu_impl(const Tensor& g, const Tensor& u) {
   Tensor h = empty_like(g);
   CTD_CHECK(ember_swiglu_fwd(cfp(g), cfp(u), fp(h), g.numel(), S()));
   return h;
+}
+
+Tensor swiglu_(Tensor& g, const Tensor& u) {
+  check_binary(g, u, "swiglu_");
+  require(!autograd::any_requires_grad({g, u}),
+          "swiglu_: in place on tensors that require grad would lose the saved gate");
+  require(g.storage() != u.storage(), "swiglu_: g and u share storage");
+  CTD_CHECK(ember_swiglu_fwd(cfp(g), cfp(u), fp(g), g.numel(), S()));
+  return g;
 }
 
 Tensor swiglu(const Tensor& g, const Tensor& u) {

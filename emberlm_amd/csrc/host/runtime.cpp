@@ -111,6 +111,20 @@ void drain_released() {
   }
 }
 
+bool wait_oldest_released() {
+  Deferred& d = deferred();
+  std::pair<ember_event_t, std::vector<StoragePtr>> item;
+  {
+    std::lock_guard<std::mutex> lk(d.mu);
+    if (d.items.empty()) return false;
+    item = std::move(d.items.front());
+    d.items.erase(d.items.begin());
+  }
+  check(ember_event_synchronize(item.first), "wait_oldest_released");
+  item.second.clear();
+  return true;
+}
+
 bool device_available() {
   int n = 0;
   return ember_get_device_count(&n) == EMBER_OK && n > 0;
@@ -262,16 +276,19 @@ class HipCachingAllocator final : public Allocator {
     if (nbytes == 0) return nullptr;
     // Blocks a side stream has finished with go back first.  If some are
     // still in use and this request would set a new lifetime high-water mark
-    // of live bytes, wait for them instead: the host runs ahead of the GPU,
+    // of live bytes, or needs a new large segment (no cached block holds it), wait
+    // for them, oldest first, until it fits: the host runs ahead of the GPU,
     // and the side stream's buffers (gradients the offloaded update still
-    // reads) would otherwise count on top of the next forward's own peak.
-    if (runtime::collect_released() > 0) {
-      bool over;
+    // reads, released in the order the update reaches them) would otherwise
+    // count on top of the next forward's own peak or make the arena grow.
+    while (runtime::collect_released() > 0) {
+      bool wait;
       {
         std::lock_guard<std::mutex> lk(mu_);
-        over = arena_.stats().live_bytes + nbytes > high_water_;
+        wait = arena_.stats().live_bytes + nbytes > high_water_ ||
+               (nbytes > detail::BlockArena::kSmallRequest && !arena_.fits(nbytes));
       }
-      if (over) runtime::drain_released();
+      if (!wait || !runtime::wait_oldest_released()) break;
     }
     std::lock_guard<std::mutex> lk(mu_);
     const int64_t segments_before = arena_.stats().segments_obtained;

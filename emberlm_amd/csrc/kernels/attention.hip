@@ -556,6 +556,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
     const float* Ls = Qs + 2 * C::kBQ * C::kQS;
     const float* Es = Ls + C::kBQ;
     if (qt0 + C::kBQ - 1 >= kw0) {  // some query of the tile sees some key of this wave
+      // The scaled lse and delta of this lane's queries 16mt + 4g + e, read
+      // as float4s ahead of the products (a read per entry, inside the mask
+      // test, serialised the softmax section on LDS round trips).
+      f32x4 lq[2], eq[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        lq[mt] = *reinterpret_cast<const f32x4*>(Ls + 16 * mt + 4 * g);
+        eq[mt] = *reinterpret_cast<const f32x4*>(Es + 16 * mt + 4 * g);
+      }
       f32x4 s[2], dp[2];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) s[mt] = dp[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -578,11 +587,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int ql = 16 * mt + 4 * g + e;
-          const int qq = qt0 + ql;
-          const float p = (qq < mykey || qq >= T) ? 0.f : fast_exp2(s[mt][e] - Ls[ql]);
+          const int qq = qt0 + 16 * mt + 4 * g + e;
+          // exp2 on every entry, then a select: no branch around the LDS data
+          const float pe = fast_exp2(s[mt][e] - lq[mt][e]);
+          const float p = (qq < mykey || qq >= T) ? 0.f : pe;
           s[mt][e] = p;
-          dp[mt][e] = p * (dp[mt][e] - Es[ql]);
+          dp[mt][e] = p * (dp[mt][e] - eq[mt][e]);
         }
       if (ds_lane) {  // queries qt0 + 16mt + 4g + (0..3) of this lane's key
         gfloat* dst = ds_lane + (step / ntile) * ds_row + (qt0 - key0);

@@ -84,10 +84,11 @@ int run(const float* a, const float* b, float* y, int64_t n, float alpha, ember_
 }
 
 template <bool VEC>
-__global__ __launch_bounds__(kThreads) void swiglu_bwd_kernel(const float* __restrict__ g,
-                                                              const float* __restrict__ u,
+__global__ __launch_bounds__(kThreads) void swiglu_bwd_kernel(const float* g, const float* u,
                                                               const float* dh, float* dg,
                                                               float* du, int64_t n) {
+  // dg may alias g and du may alias u: every element is read before the same
+  // thread writes it, so no pointer is __restrict__.
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
   const int64_t tid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   auto one = [](float gv, float uv, float d, float& og, float& ou) {

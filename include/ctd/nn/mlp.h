@@ -1,6 +1,7 @@
 #pragma once
 // SwiGLU feed-forward: y = down(silu(gate(x)) * up(x)) (mirrors nn/mlp.h of the
 // reference); silu and the product run as one fused op.
+#include "ctd/autograd.h"
 #include "ctd/nn/linear.h"
 #include "ctd/ops/elementwise.h"
 #include "ctd/tensor.h"
@@ -24,10 +25,15 @@ struct MLP {
     return down_proj.forward_add(activation(x), residual);
   }
 
-  // silu(gate(x)) * up(x) as [tokens, intermediate].
+  // silu(gate(x)) * up(x) as [tokens, intermediate].  With no graph to
+  // record (no-grad forward, e.g. the checkpointed forward), the activation
+  // overwrites the gate's buffer: one [tokens, intermediate] buffer fewer.
   Tensor activation(const Tensor& x) const {
     Tensor x2 = gate_proj.rows(x);
-    return ops::swiglu(gate_proj.forward(x2), up_proj.forward(x2));
+    Tensor g = gate_proj.forward(x2);
+    Tensor u = up_proj.forward(x2);
+    if (!autograd::any_requires_grad({g, u})) return ops::swiglu_(g, u);
+    return ops::swiglu(g, u);
   }
 };
 

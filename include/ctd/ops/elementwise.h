@@ -24,5 +24,10 @@ Tensor silu_backward_impl(const Tensor& x, const Tensor& g);
 // h = silu(g) * u in one pass; saves g and u, recomputes silu(g) in backward.
 Tensor swiglu(const Tensor& g, const Tensor& u);
 Tensor swiglu_impl(const Tensor& g, const Tensor& u);
+// g = silu(g) * u in place, returning g; records no graph and throws when g or
+// u requires grad.  For callers that own g and read it no more (nn::MLP under
+// no-grad, where the gate's buffer then holds the activation).  Added in this
+// build.
+Tensor swiglu_(Tensor& g, const Tensor& u);
 
 }  // namespace ctd::ops

@@ -37,6 +37,9 @@ void release_after(ember_event_t done, std::vector<StoragePtr> keep);
 size_t collect_released();
 // Waits for every pending entry's event and drops them all.
 void drain_released();
+// Waits for the oldest pending entry's event and drops it; false when none
+// is pending.
+bool wait_oldest_released();
 
 // Whether a HIP device is present (without creating a context on failure).
 bool device_available();

@@ -221,10 +221,12 @@ int ember_scale(const float* x, float alpha, float* y, int64_t n, ember_stream_t
 int ember_accumulate(float* y, const float* x, int64_t n, ember_stream_t s);
 int ember_silu(const float* x, float* y, int64_t n, ember_stream_t s);
 int ember_silu_bwd(const float* x, const float* g, float* dx, int64_t n, ember_stream_t s);
-/* Fused SwiGLU: h = silu(g) * u (MLP::forward, include/ctd/nn/mlp.h:16-21). */
+/* Fused SwiGLU: h = silu(g) * u (MLP::forward, include/ctd/nn/mlp.h:16-21).  h may
+ * be g or u. */
 int ember_swiglu_fwd(const float* g, const float* u, float* h, int64_t n, ember_stream_t s);
 /* dg = dh * u * silu'(g), du = dh * silu(g) (MulBackward + SiluBackward,
- * elementwise.cu:57-69, 186-238). */
+ * elementwise.cu:57-69, 186-238).  dg may be g and du may be u (each element
+ * is read before it is written); no other overlap is allowed. */
 int ember_swiglu_bwd(const float* g, const float* u, const float* dh, float* dg, float* du,
                      int64_t n, ember_stream_t s);
 

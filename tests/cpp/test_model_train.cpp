@@ -813,6 +813,57 @@ void ce_masked_past_int32() {
   }
 }
 
+// The MLP's memory-saving forms give the bits of the plain ones: the SwiGLU
+// backward writing its gradients over gate and up (when the node holds them
+// alone), the down projection's dW before its dA (its input's memory then
+// holds dA), and the no-grad activation written over the gate's buffer.
+void mlp_in_place_forms_match() {
+  std::mt19937 rng(21);
+  const int64_t N = 300, H = 96, I = 256;
+  Tensor x0 = rand_tensor({N, H}, rng, 1.0f, false);
+  Tensor wg = rand_tensor({I, H}, rng, 0.1f, true), wu = rand_tensor({I, H}, rng, 0.1f, true),
+         wd = rand_tensor({H, I}, rng, 0.1f, true);
+  Tensor dy = rand_tensor({N, H}, rng, 1.0f, false);
+  auto run_once = [&](bool hold) {
+    wg.zero_grad_();
+    wu.zero_grad_();
+    wd.zero_grad_();
+    Tensor x = x0.detach();
+    x.requires_grad_(true);
+    Tensor g = ops::matmul(x, wg, false, true), u = ops::matmul(x, wu, false, true);
+    std::vector<float> g_before = host(g), u_before = host(u);
+    Tensor y = ops::matmul(ops::swiglu(g, u), wd, false, true);
+    Tensor keep_g = hold ? g : Tensor{}, keep_u = hold ? u : Tensor{};
+    g = Tensor{};
+    u = Tensor{};
+    y.backward(dy);
+    if (hold)
+      check(host(keep_g) == g_before && host(keep_u) == u_before,
+            "gate and up held by the caller are not overwritten by the backward");
+    return std::vector<std::vector<float>>{host(x.grad()), host(wg.grad()), host(wu.grad()),
+                                           host(wd.grad())};
+  };
+  const auto in_place = run_once(false), held = run_once(true);
+  check(in_place == held, "gradients with gate/up overwritten equal the out-of-place ones");
+
+  nn::MLP mlp{nn::Linear{wg.detach()}, nn::Linear{wu.detach()}, nn::Linear{wd.detach()}};
+  std::vector<float> fused, plain;
+  {
+    autograd::NoGradGuard ng;
+    fused = host(mlp.activation(x0));
+    plain = host(ops::swiglu(ops::matmul(x0, wg, false, true), ops::matmul(x0, wu, false, true)));
+  }
+  check(fused == plain, "no-grad activation over the gate's buffer equals swiglu()");
+  bool threw = false;
+  try {
+    Tensor g = ops::matmul(x0, wg, false, true);  // requires grad through wg
+    ops::swiglu_(g, ops::matmul(x0, wu, false, true));
+  } catch (const std::runtime_error&) {
+    threw = true;
+  }
+  check(threw, "swiglu_ refuses tensors that require grad");
+}
+
 int main(int argc, char** argv) {
   // --cpu: only the tests that need no GPU (host tensors only).
   if (argc > 1 && std::strcmp(argv[1], "--cpu") == 0) {
@@ -832,6 +883,7 @@ int main(int argc, char** argv) {
   run("Autograd.BlockGraphOnlyRecompute",
       [] { block_graph_only_recompute_matches_forward_train(); });
   run("Autograd.FanInFoldMatchesSeparateAdds", [] { fan_in_fold_matches_separate_adds(); });
+  run("Ops.MLPInPlaceFormsMatch", [] { mlp_in_place_forms_match(); });
   run("Autograd.RetainedGraphRepeatBackward", [] { retained_graph_repeat_backward(false, 1.0f); });
   run("Autograd.RetainedGraphRepeatBackward_Checkpointed",
       [] { retained_graph_repeat_backward(true, 1.0f); });

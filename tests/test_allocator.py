@@ -5,9 +5,10 @@ the cap and a recorded training step can be checked without a GPU.
 
 The recorded history (tests/golden/alloc_history_qwen3-1.7b_B8_T4096.txt.gz)
 is the device allocator's own record (bench.py --alloc-history) of setup, one
-warmup and three timed recompute + offload steps of Qwen3-1.7B at B=8,
+warmup and fifteen timed recompute + offload steps of Qwen3-1.7B at B=8,
 T=4096 on an MI355X, including the split dS workspaces of the attention
-backward ("s" records), which the replay plans again against its own arena."""
+backward ("s" records), which the replay plans again against its own arena,
+and the elastic optimizer-state prefetch buffers ("e" records)."""
 import gzip
 import os
 import shutil

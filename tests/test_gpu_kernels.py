@@ -421,6 +421,24 @@ def test_elementwise_vs_oracle():
     call("ember_swiglu_bwd", p(A), p(Bt), p(G), p(DG), p(DU), n, None)
     assert_close(host(DG), O.silu_bwd(a, g * b), name="swiglu dg")
     assert_close(host(DU), g * O.silu(a), name="swiglu du")
+    # in place (dg over g, du over u, as the MLP's backward runs it): the same
+    # bits as into separate buffers, on the vector path and the scalar one
+    for off in (0, 1):
+        m = n - off
+        A2, B2 = dev(a), dev(b)
+        pa = C.c_void_p(A2.data_ptr() + 4 * off)
+        pb = C.c_void_p(B2.data_ptr() + 4 * off)
+        pg = C.c_void_p(G.data_ptr() + 4 * off)
+        DG2, DU2 = empty((m,)), empty((m,))
+        call("ember_swiglu_bwd", pa, pb, pg, p(DG2), p(DU2), m, None)
+        call("ember_swiglu_bwd", pa, pb, pg, pa, pb, m, None)
+        assert torch.equal(A2[off:], DG2) and torch.equal(B2[off:], DU2), off
+        # forward over the gate (nn::MLP's no-grad activation)
+        A3, H3 = dev(a), empty((m,))
+        pa3 = C.c_void_p(A3.data_ptr() + 4 * off)
+        call("ember_swiglu_fwd", pa3, pb, p(H3), m, None)
+        call("ember_swiglu_fwd", pa3, pb, pa3, m, None)
+        assert torch.equal(A3[off:], H3), off
     Z = dev(b)
     call("ember_accumulate", p(Z), p(A), n, None)
     assert np.array_equal(host(Z), b + a)
