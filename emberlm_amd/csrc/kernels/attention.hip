@@ -470,7 +470,7 @@ struct DkvCfg {
   static constexpr int kSmem = 2 * kBuf;
 };
 
-template <int D>
+template <int D, bool DS>
 __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta,
@@ -511,9 +511,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
   // head (a KV row's region holds its group's heads one after another; the
   // table gives each KV row's region); columns count queries from key0.
   const int64_t T32 = ds_t32(T), ds_row = ds_row_floats(T), lr = T32 - key0;
-  gfloat* ds_lane = ds_rows ? as_global(ds_rows[kvrow]) + ds_strip_offset(kb, T32) +
-                                 static_cast<int64_t>(16 * w + i) * lr + 4 * g
-                           : nullptr;
+  // (DS is a template argument so that the stores are unconditional: the
+  // compiler then counts them and waits only for the loads of the next tile
+  // before writing it to LDS, not for the dS stores too.)
+  gfloat* ds_lane = DS ? as_global(ds_rows[kvrow]) + ds_strip_offset(kb, T32) +
+                             static_cast<int64_t>(16 * w + i) * lr + 4 * g
+                       : nullptr;
 
   // The streamed sequence: for each query head of the group, the query tiles
   // key0, key0 + 32, ... below T.
@@ -556,22 +559,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
     const float* Ls = Qs + 2 * C::kBQ * C::kQS;
     const float* Es = Ls + C::kBQ;
     if (qt0 + C::kBQ - 1 >= kw0) {  // some query of the tile sees some key of this wave
-      // The scaled lse and delta of this lane's queries 16mt + 4g + e, read
-      // as float4s ahead of the products (a read per entry, inside the mask
-      // test, serialised the softmax section on LDS round trips).
-      f32x4 lq[2], eq[2];
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        lq[mt] = *reinterpret_cast<const f32x4*>(Ls + 16 * mt + 4 * g);
-        eq[mt] = *reinterpret_cast<const f32x4*>(Es + 16 * mt + 4 * g);
-      }
+      // The two 16-query halves in sequence: S and dP of half 1 are issued
+      // before the softmax of half 0 and the dV/dK products of half 0 before
+      // the softmax of half 1, so each softmax runs under MFMAs of this wave.
+      // Every accumulator sums in the same order as with the halves together.
       f32x4 s[2], dp[2];
+      auto scores = [&](int mt) {
+        s[mt] = dp[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) s[mt] = dp[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
+        for (int t = 0; t < NT; ++t) {
           const f32x4 qf =
               *reinterpret_cast<const f32x4*>(Qs + (16 * mt + i) * C::kQS + 16 * t + 4 * g);
           const f32x4 of =
@@ -582,25 +578,33 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
             dp[mt] = mfma16(of[j], vreg[t][j], dp[mt]);
           }
         }
-      }
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      };
+      auto softmax = [&](int mt) {
+        // The scaled lse and delta of this lane's queries 16mt + 4g + e, read
+        // as float4s (a read per entry, inside the mask test, serialised the
+        // softmax section on LDS round trips).
+        const f32x4 lq = *reinterpret_cast<const f32x4*>(Ls + 16 * mt + 4 * g);
+        const f32x4 eq = *reinterpret_cast<const f32x4*>(Es + 16 * mt + 4 * g);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int qq = qt0 + 16 * mt + 4 * g + e;
           // exp2 on every entry, then a select: no branch around the LDS data
-          const float pe = fast_exp2(s[mt][e] - lq[mt][e]);
+          const float pe = fast_exp2(s[mt][e] - lq[e]);
           const float p = (qq < mykey || qq >= T) ? 0.f : pe;
           s[mt][e] = p;
-          dp[mt][e] = p * (dp[mt][e] - eq[mt][e]);
+          dp[mt][e] = p * (dp[mt][e] - eq[e]);
         }
-      if (ds_lane) {  // queries qt0 + 16mt + 4g + (0..3) of this lane's key
-        gfloat* dst = ds_lane + (step / ntile) * ds_row + (qt0 - key0);
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) *reinterpret_cast<gf32x4*>(dst + 16 * mt) = dp[mt];
-      }
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+        if constexpr (DS) {  // queries qt0 + 16mt + 4g + (0..3) of this lane's key
+          *reinterpret_cast<gf32x4*>(ds_lane + (step / ntile) * ds_row + (qt0 - key0) +
+                                     16 * mt) = dp[mt];
+          // Keep the store ahead of this half's dV/dK products: the write of
+          // the next tile to LDS waits for every outstanding vector memory
+          // operation (loads and stores share the counter), so a store sunk
+          // to the end of the step would be waited for in full.
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+      auto grads = [&](int mt) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int row = (16 * mt + 4 * g + e) * C::kQS;
@@ -615,6 +619,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
             }
           }
         }
+      };
+      scores(0);
+      scores(1);
+      softmax(0);
+      grads(0);
+      softmax(1);
+      grads(1);
     }
     if (more) commit(smem + ((step + 1) & 1) * C::kBuf);
     __syncthreads();
@@ -901,7 +912,7 @@ int launch_bwd(const float* q, const float* k, const float* v, const float* o, c
     attn_bwd_dq_kernel<D><<<dim3(nqb * static_cast<unsigned>(B * H)), kThreads, 0, st>>>(
         q, k, v, dout, lse, delta, dq, Ti, Hi, Hki, sl, scale);
     if ((rc = launch_status())) return rc;
-    attn_bwd_dkdv_kernel<D><<<dim3(nqb * static_cast<unsigned>(kv_rows)), kThreads, 0, st>>>(
+    attn_bwd_dkdv_kernel<D, false><<<dim3(nqb * static_cast<unsigned>(kv_rows)), kThreads, 0, st>>>(
         q, k, v, dout, lse, delta, dk, dv, nullptr, 0, Ti, Hi, Hki, sl, scale);
     return launch_status();
   }
@@ -933,7 +944,7 @@ int launch_bwd(const float* q, const float* k, const float* v, const float* o, c
     return rc;
   for (int64_t r0 = 0; r0 < kv_rows; r0 += chunk) {
     const int64_t n = kv_rows - r0 < chunk ? kv_rows - r0 : chunk;
-    attn_bwd_dkdv_kernel<D><<<dim3(nqb * static_cast<unsigned>(n)), kThreads, 0, st>>>(
+    attn_bwd_dkdv_kernel<D, true><<<dim3(nqb * static_cast<unsigned>(n)), kThreads, 0, st>>>(
         q, k, v, dout, lse, delta, dk, dv, table, static_cast<int>(r0), Ti, Hi, Hki, sl, scale);
     if ((rc = launch_status())) return rc;
     attn_bwd_dq_gemm_kernel<D><<<dim3(nmt * static_cast<unsigned>(n * group)), kThreads, 0, st>>>(
