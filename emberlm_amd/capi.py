@@ -85,6 +85,11 @@ SIGNATURES = {
     "ember_attn_bwd_ds_row_bytes": (sz, [i64, i64, i64]),
     "ember_attn_bwd_scattered": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64,
                                        f32, vp, sz, C.POINTER(vp), C.POINTER(sz), i32, vp]),
+    "ember_attn_scores_workspace_bytes": (sz, [i64, i64]),
+    "ember_attn_fwd_scores": (i32, [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, f32,
+                                    C.POINTER(vp), C.POINTER(sz), i32, vp, sz, vp]),
+    "ember_attn_bwd_from_scores": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64,
+                                         i64, f32, vp, sz, C.POINTER(vp), C.POINTER(sz), i32, vp]),
     "ember_ce_masked_fwd_workspace_bytes": (sz, [i64]),
     "ember_ce_masked_fwd": (i32, [vp, vp, vp, i64, i64, vp, vp, vp, vp, sz, vp]),
     "ember_ce_masked_bwd": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, vp, vp]),

@@ -696,8 +696,29 @@ std::vector<Tensor> attn_bwd_ds_buffers(const AttnDims& d) {
   return bufs;
 }
 
+std::atomic<bool> g_attn_keep_scores{false};
+
+// Buffers for every KV row's scores (ember_attn_fwd_scores), from the free
+// blocks first.
+std::vector<Tensor> attn_scores_buffers(const AttnDims& d) {
+  const size_t row = ember_attn_bwd_ds_row_bytes(d.T, d.H, d.Hk);
+  const size_t kv_rows = static_cast<size_t>(d.B * d.Hk);
+  std::vector<Tensor> bufs;
+  for (size_t bytes : device_scatter_plan(row, kv_rows, kv_rows, 1, kAttnDsMaxPieces))
+    bufs.push_back(workspace(bytes));
+  return bufs;
+}
+
+void buffer_list(std::vector<Tensor>& bufs, std::vector<float*>& ptr, std::vector<size_t>& bytes) {
+  for (Tensor& t : bufs) {
+    ptr.push_back(fp(t));
+    bytes.push_back(static_cast<size_t>(t.numel()) * sizeof(float));
+  }
+}
+
 struct CausalAttentionBackward : autograd::Node {
   Tensor q, k, v, o, lse;
+  std::vector<Tensor> scores;  // the forward's S (set_attention_keep_scores)
   float scale = 1.0f;
   const char* name() const override { return "CausalAttentionBackward"; }
   std::vector<Tensor> backward(const std::vector<Tensor>& go) override {
@@ -708,6 +729,21 @@ struct CausalAttentionBackward : autograd::Node {
     Tensor dq = empty_like(q), dk = empty_like(k), dv = empty_like(v);
     const size_t wsb = ember_attn_bwd_workspace_bytes_min(d.B, d.T, d.H);
     Tensor ws = workspace(wsb);
+    if (!scores.empty() && !autograd::graph_retained()) {
+      // dS is written over the scores, so a retained graph takes the path below
+      std::vector<float*> s_ptr;
+      std::vector<size_t> s_bytes;
+      buffer_list(scores, s_ptr, s_bytes);
+      void* ev = runtime::gemm_profile_begin();
+      CTD_CHECK(ember_attn_bwd_from_scores(cfp(q), cfp(k), cfp(v), cfp(o), cfp(lse), cfp(dout),
+                                           fp(dq), fp(dk), fp(dv), d.B, d.T, d.H, d.Hk, d.D,
+                                           scale, ws.data_ptr(), wsb, s_ptr.data(),
+                                           s_bytes.data(), static_cast<int>(s_ptr.size()), S()));
+      runtime::gemm_profile_end(ev, 2.0 * attn_fwd_flops(d), runtime::kProfileAttnBwd);
+      scores.clear();
+      release_saved(q, k, v, o, lse);
+      return {dq, dk, dv};
+    }
     std::vector<Tensor> ds = attn_bwd_ds_buffers(d);
     std::vector<float*> ds_ptr;
     std::vector<size_t> ds_bytes;
@@ -722,6 +758,7 @@ struct CausalAttentionBackward : autograd::Node {
                                        static_cast<int>(ds_ptr.size()), S()));
     runtime::gemm_profile_end(ev, 2.0 * attn_fwd_flops(d), runtime::kProfileAttnBwd);
     release_saved(q, k, v, o, lse);
+    if (!autograd::graph_retained()) scores.clear();
     return {dq, dk, dv};
   }
 };
@@ -731,6 +768,8 @@ struct CausalAttentionBackward : autograd::Node {
 void set_attention_backward_ds_bytes(int64_t bytes) {
   g_attn_ds_bytes.store(bytes < 0 ? kAttentionBackwardDsBytes : bytes);
 }
+
+void set_attention_keep_scores(bool on) { g_attn_keep_scores.store(on); }
 
 Tensor causal_attention_impl(const Tensor& q, const Tensor& k, const Tensor& v, float scale,
                              Tensor* lse_out) {
@@ -746,10 +785,30 @@ Tensor causal_attention_impl(const Tensor& q, const Tensor& k, const Tensor& v, 
 }
 
 Tensor causal_attention(const Tensor& q, const Tensor& k, const Tensor& v, float scale) {
-  Tensor lse;
-  Tensor o = causal_attention_impl(q, k, v, scale, &lse);
-  if (autograd::any_requires_grad({q, k, v})) {
+  const bool grad = autograd::any_requires_grad({q, k, v});
+  Tensor lse, o;
+  std::vector<Tensor> scores;
+  if (grad && g_attn_keep_scores.load()) {
+    const AttnDims d = attn_dims(q, k, v);
+    o = empty_like(q);
+    lse = Tensor::empty({d.B, d.H, d.T}, DType::kFloat32, q.device());
+    scores = attn_scores_buffers(d);
+    std::vector<float*> s_ptr;
+    std::vector<size_t> s_bytes;
+    buffer_list(scores, s_ptr, s_bytes);
+    const size_t tb = ember_attn_scores_workspace_bytes(d.B, d.H);
+    Tensor table = workspace(tb);
+    void* ev = runtime::gemm_profile_begin();
+    CTD_CHECK(ember_attn_fwd_scores(cfp(q), cfp(k), cfp(v), fp(o), fp(lse), d.B, d.T, d.H, d.Hk,
+                                    d.D, scale, s_ptr.data(), s_bytes.data(),
+                                    static_cast<int>(s_ptr.size()), table.data_ptr(), tb, S()));
+    runtime::gemm_profile_end(ev, attn_fwd_flops(d), runtime::kProfileAttnFwd);
+  } else {
+    o = causal_attention_impl(q, k, v, scale, &lse);
+  }
+  if (grad) {
     auto node = std::make_shared<CausalAttentionBackward>();
+    node->scores = std::move(scores);
     node->q = q.detach();
     node->k = k.detach();
     node->v = v.detach();

@@ -808,4 +808,8 @@ int ctd_set_attn_ds_bytes(int64_t bytes) {
   return guarded([&] { ops::set_attention_backward_ds_bytes(bytes); });
 }
 
+int ctd_set_attn_keep_scores(int32_t on) {
+  return guarded([&] { ops::set_attention_keep_scores(on != 0); });
+}
+
 }  // extern "C"

@@ -169,10 +169,14 @@ struct FwdCfg {
   static constexpr int kSmem = 2 * kBuf;
 };
 
-template <int D>
+// SS: also store every computed score (log2 units, before the mask) in the
+// dS layout of the KV row's region given by `s_rows` (attn_bwd_from_scores
+// reads them back instead of computing S again).
+template <int D, bool SS>
 __global__ __launch_bounds__(FwdCfg<D>::kThreads, 2) void attn_fwd_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-    float* __restrict__ o, float* __restrict__ lse, int T, int H, int Hk, float scale_log2) {
+    float* __restrict__ o, float* __restrict__ lse, float* const* __restrict__ s_rows, int T,
+    int H, int Hk, float scale_log2) {
   using C = FwdCfg<D>;
   constexpr int NT = D / 16;
   __shared__ __attribute__((aligned(16))) float smem[C::kSmem];
@@ -188,6 +192,11 @@ __global__ __launch_bounds__(FwdCfg<D>::kThreads, 2) void attn_fwd_kernel(
   const int64_t qoff = static_cast<int64_t>(b) * T * qs + static_cast<int64_t>(h) * D;
   const float* kbase = k + static_cast<int64_t>(b) * T * ks + static_cast<int64_t>(hk) * D;
   const float* vbase = v + static_cast<int64_t>(b) * T * ks + static_cast<int64_t>(hk) * D;
+  const int64_t T32 = ds_t32(T);
+  gfloat* sregion = nullptr;  // this (b, h) row's strips
+  if constexpr (SS)
+    sregion = as_global(s_rows[b * Hk + hk]) + static_cast<int64_t>(h - hk * (H / Hk)) *
+                                                   ds_row_floats(T);
 
   f32x4 qreg[NT];
   if (myq < T) {
@@ -234,6 +243,20 @@ __global__ __launch_bounds__(FwdCfg<D>::kThreads, 2) void attn_fwd_kernel(
 #pragma unroll
           for (int j = 0; j < 4; ++j) s[kt] = mfma16(kf[j], qreg[t][j], s[kt]);
         }
+      if constexpr (SS) {
+        // The tile's 32 keys lie in one 64-key strip; this lane's query is at
+        // or past the strip's first key whenever the tile is processed.
+        if (myq < T) {
+          const int sb = k0 >> 6;
+          const int64_t lr = T32 - 64 * sb;
+          gfloat* col = sregion + ds_strip_offset(sb, T32) + (myq - 64 * sb) +
+                        static_cast<int64_t>(k0 - 64 * sb + 4 * g) * lr;
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) col[(16 * kt + e) * lr] = s[kt][e];
+        }
+      }
       const bool need_mask = (k0 + C::kBK - 1 > qw0) || (k0 + C::kBK > T);
       float tmax = -INFINITY;
 #pragma unroll
@@ -470,7 +493,10 @@ struct DkvCfg {
   static constexpr int kSmem = 2 * kBuf;
 };
 
-template <int D, bool DS>
+// DS: store dS.  FS: the dS buffers hold the forward's scores (attn_fwd_kernel
+// with SS), which are read back instead of computing S = Q K^T, and dS is
+// written over them.
+template <int D, bool DS, bool FS>
 __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta,
@@ -478,6 +504,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
     int T, int H, int Hk, float scale_log2, float scale) {
   using C = DkvCfg<D>;
   constexpr int NT = D / 16;  // d tiles; float4 groups of a lane's K/V row
+  static_assert(DS || !FS, "the scores live in the dS buffers");
   __shared__ __attribute__((aligned(16))) float smem[C::kSmem];
 
   const WorkItem wi = work_item((T + C::kBKeys - 1) / C::kBKeys);
@@ -490,13 +517,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
   const int64_t qs = static_cast<int64_t>(H) * D, ks = static_cast<int64_t>(Hk) * D;
   const int64_t koff = static_cast<int64_t>(b) * T * ks + static_cast<int64_t>(hk) * D;
 
-  f32x4 kreg[NT], vreg[NT];
+  f32x4 kreg[NT], vreg[NT];  // kreg: unused with FS
   if (mykey < T) {
     const f32x4* kr = reinterpret_cast<const f32x4*>(k + koff + mykey * ks);
     const f32x4* vr = reinterpret_cast<const f32x4*>(v + koff + mykey * ks);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      kreg[t] = kr[4 * t + g] * scale_log2;
+      if constexpr (!FS) kreg[t] = kr[4 * t + g] * scale_log2;
       vreg[t] = vr[4 * t + g];
     }
   } else {
@@ -511,9 +538,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
   // head (a KV row's region holds its group's heads one after another; the
   // table gives each KV row's region); columns count queries from key0.
   const int64_t T32 = ds_t32(T), ds_row = ds_row_floats(T), lr = T32 - key0;
-  // (DS is a template argument so that the stores are unconditional: the
-  // compiler then counts them and waits only for the loads of the next tile
-  // before writing it to LDS, not for the dS stores too.)
+  // (DS is a template argument so that the stores are unconditional, without a
+  // branch around them, and can be kept ahead of each half's products.)
   gfloat* ds_lane = DS ? as_global(ds_rows[kvrow]) + ds_strip_offset(kb, T32) +
                              static_cast<int64_t>(16 * w + i) * lr + 4 * g
                        : nullptr;
@@ -546,14 +572,31 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
       buf[2 * C::kBQ * C::kQS + C::kBQ + threadIdx.x] = te;
     }
   };
+  // FS: this lane's scores of a step (queries qt0 + 16mt + 4g + (0..3), the
+  // addresses its dS goes to), loaded one step ahead.
+  f32x4 snext[2];
+  auto load_scores = [&](int st) {
+    const gfloat* src = ds_lane + (st / ntile) * ds_row + (st % ntile) * C::kBQ;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) snext[mt] = *reinterpret_cast<const gf32x4*>(src + 16 * mt);
+  };
   issue(0);
+  if constexpr (FS) load_scores(0);
   commit(smem);
   __syncthreads();
 
   for (int step = 0; step < nsteps; ++step) {
     const int qt0 = key0 + (step % ntile) * C::kBQ;
     const bool more = step + 1 < nsteps;
-    if (more) issue(step + 1);
+    f32x4 scur[2];
+    if constexpr (FS) {
+      scur[0] = snext[0];
+      scur[1] = snext[1];
+    }
+    if (more) {
+      issue(step + 1);
+      if constexpr (FS) load_scores(step + 1);
+    }
     const float* Qs = smem + (step & 1) * C::kBuf;
     const float* Ds = Qs + C::kBQ * C::kQS;
     const float* Ls = Qs + 2 * C::kBQ * C::kQS;
@@ -566,16 +609,22 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
       f32x4 s[2], dp[2];
       auto scores = [&](int mt) {
         s[mt] = dp[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (FS) s[mt] = scur[mt];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          const f32x4 qf =
-              *reinterpret_cast<const f32x4*>(Qs + (16 * mt + i) * C::kQS + 16 * t + 4 * g);
           const f32x4 of =
               *reinterpret_cast<const f32x4*>(Ds + (16 * mt + i) * C::kQS + 16 * t + 4 * g);
+          if constexpr (FS) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            s[mt] = mfma16(qf[j], kreg[t][j], s[mt]);
-            dp[mt] = mfma16(of[j], vreg[t][j], dp[mt]);
+            for (int j = 0; j < 4; ++j) dp[mt] = mfma16(of[j], vreg[t][j], dp[mt]);
+          } else {
+            const f32x4 qf =
+                *reinterpret_cast<const f32x4*>(Qs + (16 * mt + i) * C::kQS + 16 * t + 4 * g);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              s[mt] = mfma16(qf[j], kreg[t][j], s[mt]);
+              dp[mt] = mfma16(of[j], vreg[t][j], dp[mt]);
+            }
           }
         }
       };
@@ -859,11 +908,11 @@ extern "C" int ember_attn_fwd(const float* q, const float* k, const float* v, fl
   const float sl = scale * kLog2e;
   const int Ti = static_cast<int>(T), Hi = static_cast<int>(H), Hki = static_cast<int>(Hk);
   if (D == 64)
-    attn_fwd_kernel<64><<<grid, FwdCfg<64>::kThreads, 0, as_stream(s)>>>(q, k, v, o, lse, Ti, Hi,
-                                                                         Hki, sl);
+    attn_fwd_kernel<64, false><<<grid, FwdCfg<64>::kThreads, 0, as_stream(s)>>>(
+        q, k, v, o, lse, nullptr, Ti, Hi, Hki, sl);
   else
-    attn_fwd_kernel<128><<<grid, FwdCfg<128>::kThreads, 0, as_stream(s)>>>(q, k, v, o, lse, Ti,
-                                                                           Hi, Hki, sl);
+    attn_fwd_kernel<128, false><<<grid, FwdCfg<128>::kThreads, 0, as_stream(s)>>>(
+        q, k, v, o, lse, nullptr, Ti, Hi, Hki, sl);
   return launch_status();
 }
 
@@ -888,12 +937,18 @@ template <int D>
 int launch_bwd(const float* q, const float* k, const float* v, const float* o, const float* lse,
                const float* dout, float* dq, float* dk, float* dv, int64_t B, int64_t T,
                int64_t H, int64_t Hk, float scale, char* ws, float* const* bufs,
-               const size_t* buf_bytes, int nbufs, hipStream_t st) {
+               const size_t* buf_bytes, int nbufs, bool from_scores, hipStream_t st) {
   float* delta = reinterpret_cast<float*>(ws);
   float** table = reinterpret_cast<float**>(ws + delta_bytes(B, T, H));
   const int64_t rows = B * T * H;
   const int Ti = static_cast<int>(T), Hi = static_cast<int>(H), Hki = static_cast<int>(Hk);
   const float sl = scale * kLog2e;
+  if (from_scores) {  // the scores of every KV row must be there: checked before any launch
+    int64_t slots = 0;
+    const size_t rb = kv_row_ds_bytes(T, H / Hk);
+    for (int i = 0; i < nbufs; ++i) slots += static_cast<int64_t>(buf_bytes[i] / rb);
+    if (slots < B * Hk) return EMBER_EWORKSPACE;
+  }
   constexpr int RPB = kThreads / (D / 4);
   attn_delta_kernel<D><<<static_cast<unsigned>((rows + RPB - 1) / RPB), kThreads, 0, st>>>(
       o, dout, delta, rows, Ti, Hi);
@@ -912,7 +967,7 @@ int launch_bwd(const float* q, const float* k, const float* v, const float* o, c
     attn_bwd_dq_kernel<D><<<dim3(nqb * static_cast<unsigned>(B * H)), kThreads, 0, st>>>(
         q, k, v, dout, lse, delta, dq, Ti, Hi, Hki, sl, scale);
     if ((rc = launch_status())) return rc;
-    attn_bwd_dkdv_kernel<D, false><<<dim3(nqb * static_cast<unsigned>(kv_rows)), kThreads, 0, st>>>(
+    attn_bwd_dkdv_kernel<D, false, false><<<dim3(nqb * static_cast<unsigned>(kv_rows)), kThreads, 0, st>>>(
         q, k, v, dout, lse, delta, dk, dv, nullptr, 0, Ti, Hi, Hki, sl, scale);
     return launch_status();
   }
@@ -944,8 +999,14 @@ int launch_bwd(const float* q, const float* k, const float* v, const float* o, c
     return rc;
   for (int64_t r0 = 0; r0 < kv_rows; r0 += chunk) {
     const int64_t n = kv_rows - r0 < chunk ? kv_rows - r0 : chunk;
-    attn_bwd_dkdv_kernel<D, true><<<dim3(nqb * static_cast<unsigned>(n)), kThreads, 0, st>>>(
-        q, k, v, dout, lse, delta, dk, dv, table, static_cast<int>(r0), Ti, Hi, Hki, sl, scale);
+    if (from_scores)
+      attn_bwd_dkdv_kernel<D, true, true><<<dim3(nqb * static_cast<unsigned>(n)), kThreads, 0,
+                                             st>>>(q, k, v, dout, lse, delta, dk, dv, table,
+                                                   static_cast<int>(r0), Ti, Hi, Hki, sl, scale);
+    else
+      attn_bwd_dkdv_kernel<D, true, false><<<dim3(nqb * static_cast<unsigned>(n)), kThreads, 0,
+                                              st>>>(q, k, v, dout, lse, delta, dk, dv, table,
+                                                    static_cast<int>(r0), Ti, Hi, Hki, sl, scale);
     if ((rc = launch_status())) return rc;
     attn_bwd_dq_gemm_kernel<D><<<dim3(nmt * static_cast<unsigned>(n * group)), kThreads, 0, st>>>(
         k, table, dq, static_cast<int>(r0 * group), Ti, Hi, Hki, scale);
@@ -958,7 +1019,7 @@ int attn_bwd_run(const float* q, const float* k, const float* v, const float* o,
                  const float* dout, float* dq, float* dk, float* dv, int64_t B, int64_t T,
                  int64_t H, int64_t Hk, int64_t D, float scale, void* workspace,
                  size_t workspace_bytes, float* const* bufs, const size_t* buf_bytes, int nbufs,
-                 ember_stream_t s) {
+                 bool from_scores, ember_stream_t s) {
   int rc = check_shapes(B, T, H, Hk, D);
   if (rc) return rc;
   if (B == 0 || T == 0) return EMBER_OK;
@@ -976,9 +1037,9 @@ int attn_bwd_run(const float* q, const float* k, const float* v, const float* o,
   char* ws = static_cast<char*>(workspace);
   if (D == 64)
     return launch_bwd<64>(q, k, v, o, lse, dout, dq, dk, dv, B, T, H, Hk, scale, ws, bufs,
-                          buf_bytes, nbufs, as_stream(s));
+                          buf_bytes, nbufs, from_scores, as_stream(s));
   return launch_bwd<128>(q, k, v, o, lse, dout, dq, dk, dv, B, T, H, Hk, scale, ws, bufs,
-                         buf_bytes, nbufs, as_stream(s));
+                         buf_bytes, nbufs, from_scores, as_stream(s));
 }
 
 }  // namespace
@@ -1010,7 +1071,7 @@ extern "C" int ember_attn_bwd(const float* q, const float* k, const float* v, co
                    : nullptr;
   const size_t bytes = buf ? workspace_bytes - lo : 0;
   return attn_bwd_run(q, k, v, o, lse, dout, dq, dk, dv, B, T, H, Hk, D, scale, workspace,
-                      workspace_bytes, &buf, &bytes, buf ? 1 : 0, s);
+                      workspace_bytes, &buf, &bytes, buf ? 1 : 0, false, s);
 }
 
 extern "C" int ember_attn_bwd_scattered(const float* q, const float* k, const float* v,
@@ -1021,5 +1082,65 @@ extern "C" int ember_attn_bwd_scattered(const float* q, const float* k, const fl
                                         float* const* ds_bufs_host, const size_t* ds_bytes_host,
                                         int nbufs, ember_stream_t s) {
   return attn_bwd_run(q, k, v, o, lse, dout, dq, dk, dv, B, T, H, Hk, D, scale, workspace,
-                      workspace_bytes, ds_bufs_host, ds_bytes_host, nbufs, s);
+                      workspace_bytes, ds_bufs_host, ds_bytes_host, nbufs, false, s);
+}
+
+extern "C" size_t ember_attn_scores_workspace_bytes(int64_t B, int64_t H) {
+  if (B <= 0 || H <= 0) return 0;
+  return table_bytes(B, H);
+}
+
+extern "C" int ember_attn_fwd_scores(const float* q, const float* k, const float* v, float* o,
+                                     float* lse, int64_t B, int64_t T, int64_t H, int64_t Hk,
+                                     int64_t D, float scale, float* const* s_bufs_host,
+                                     const size_t* s_bytes_host, int nbufs, void* workspace,
+                                     size_t workspace_bytes, ember_stream_t s) {
+  int rc = check_shapes(B, T, H, Hk, D);
+  if (rc) return rc;
+  if (B == 0 || T == 0) return EMBER_OK;
+  if (!q || !k || !v || !o || !lse) return EMBER_EINVAL;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)) return EMBER_EALIGN;
+  if (!workspace || workspace_bytes < ember_attn_scores_workspace_bytes(B, H))
+    return EMBER_EWORKSPACE;
+  if (nbufs < 1 || !s_bufs_host || !s_bytes_host) return EMBER_EINVAL;
+  const int64_t kv_rows = B * Hk;
+  const size_t row_bytes = kv_row_ds_bytes(T, H / Hk);
+  // Whole KV rows from the buffers in order, as the backward lays them out
+  // when one chunk holds every row.
+  std::vector<float*> host_table;
+  for (int i = 0; i < nbufs && static_cast<int64_t>(host_table.size()) < kv_rows; ++i) {
+    if (s_bytes_host[i] > 0 && !s_bufs_host[i]) return EMBER_EINVAL;
+    if (!aligned16(s_bufs_host[i])) return EMBER_EALIGN;
+    for (size_t off = 0; off + row_bytes <= s_bytes_host[i] &&
+                         static_cast<int64_t>(host_table.size()) < kv_rows;
+         off += row_bytes)
+      host_table.push_back(s_bufs_host[i] + off / sizeof(float));
+  }
+  if (static_cast<int64_t>(host_table.size()) < kv_rows) return EMBER_EWORKSPACE;
+  hipStream_t st = as_stream(s);
+  float** table = static_cast<float**>(workspace);
+  if ((rc = upload_async(table, host_table.data(), host_table.size() * sizeof(float*), st)))
+    return rc;
+  const dim3 grid(static_cast<unsigned>((T + 127) / 128 * H * B));
+  const float sl = scale * kLog2e;
+  const int Ti = static_cast<int>(T), Hi = static_cast<int>(H), Hki = static_cast<int>(Hk);
+  if (D == 64)
+    attn_fwd_kernel<64, true><<<grid, FwdCfg<64>::kThreads, 0, st>>>(q, k, v, o, lse, table, Ti,
+                                                                      Hi, Hki, sl);
+  else
+    attn_fwd_kernel<128, true><<<grid, FwdCfg<128>::kThreads, 0, st>>>(q, k, v, o, lse, table, Ti,
+                                                                        Hi, Hki, sl);
+  return launch_status();
+}
+
+extern "C" int ember_attn_bwd_from_scores(const float* q, const float* k, const float* v,
+                                          const float* o, const float* lse, const float* dout,
+                                          float* dq, float* dk, float* dv, int64_t B, int64_t T,
+                                          int64_t H, int64_t Hk, int64_t D, float scale,
+                                          void* workspace, size_t workspace_bytes,
+                                          float* const* s_bufs_host, const size_t* s_bytes_host,
+                                          int nbufs, ember_stream_t s) {
+  if (nbufs < 1) return EMBER_EINVAL;
+  return attn_bwd_run(q, k, v, o, lse, dout, dq, dk, dv, B, T, H, Hk, D, scale, workspace,
+                      workspace_bytes, s_bufs_host, s_bytes_host, nbufs, true, s);
 }

@@ -116,6 +116,7 @@ _SIGS = {
     "ctd_set_head_chunk_rows": (i32, [i64]),
     "ctd_set_head_active_rows": (i32, [i32]),
     "ctd_set_attn_ds_bytes": (i32, [i64]),
+    "ctd_set_attn_keep_scores": (i32, [i32]),
     "ctd_trainer_generate": (i32, [vp, lptr, i64, i32, f32, i32, f32, u64, i64, lptr,
                                    C.POINTER(C.c_double), C.POINTER(C.c_double)]),
 }
@@ -436,6 +437,11 @@ def sample(logits, temperature=1.0, top_k=0, top_p=0.0, seed=0, draws=1, on_devi
 def set_attn_ds_bytes(nbytes):
     """Device bytes the attention backward may keep dS in (-1 default, 0 none)."""
     _ck(lib().ctd_set_attn_ds_bytes(int(nbytes)), "set_attn_ds_bytes")
+
+
+def set_attn_keep_scores(on):
+    """Whether a recorded attention forward keeps its scores for its backward."""
+    _ck(lib().ctd_set_attn_keep_scores(int(bool(on))), "set_attn_keep_scores")
 
 
 def set_head_chunk_rows(rows):

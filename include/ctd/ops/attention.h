@@ -20,11 +20,22 @@ Tensor causal_attention(const Tensor& q, const Tensor& k, const Tensor& v, float
 // device allocator already holds, and the backward keeps fewer rows (in
 // equal chunks) rather than grow the memory held: it grows it only when the
 // free blocks hold fewer than 16 rows, and then only to 16.  All 64 rows
-// (one chunk) ran the layer's backward 0.2 ms faster (11.05 against 11.25
-// ms) but raised the step's live peak from 22.0 to 23.9 GB, since the 4.4 GB
-// of dS then outgrow what the MLP's backward holds before it.
+// (one chunk) ran the layer's backward 0.25 ms faster (10.83 against 11.08
+// ms) but would raise the step's live peak from 21.8 to 23.3 GB: the
+// attention backward starts at 18.9 GB live.
 constexpr int64_t kAttentionBackwardDsBytes = 2500000000;
 void set_attention_backward_ds_bytes(int64_t bytes);
+// Added in this build (off by default): a causal_attention whose inputs
+// require grad keeps its scores S = Q K^T (fp32, the causal part, 4.36 GB per
+// Qwen3-1.7B layer at B=8, T=4096) from the forward to its backward, which then
+// reads them instead of computing S again (4 of the 5 products it runs
+// otherwise) and writes dS over them.  Meant for a checkpointed block's re-run,
+// whose backward follows at once; every other forward that records a graph
+// holds its scores until its backward too.  The buffers come from the device
+// allocator's free blocks (up to 16 pieces, grown if need be); with a retained
+// graph the backward computes S again and leaves the scores intact.  dQ, dK
+// and dV agree with the default path to fp32 rounding.
+void set_attention_keep_scores(bool on);
 // Forward only; lse (if non-null) receives the [B,H,T] log-sum-exp.
 Tensor causal_attention_impl(const Tensor& q, const Tensor& k, const Tensor& v, float scale,
                              Tensor* lse = nullptr);

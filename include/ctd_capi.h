@@ -237,6 +237,9 @@ int ctd_set_head_active_rows(int32_t on);
 /* Device bytes the attention backward may keep dS in
  * (ops::set_attention_backward_ds_bytes; -1 = default, 0 = recompute). */
 int ctd_set_attn_ds_bytes(int64_t bytes);
+/* Whether a recorded attention forward keeps its scores for its backward
+ * (ops::set_attention_keep_scores; default 0). */
+int ctd_set_attn_keep_scores(int32_t on);
 
 #ifdef __cplusplus
 }

@@ -292,6 +292,31 @@ int ember_attn_bwd_scattered(const float* q, const float* k, const float* v, con
                              int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D, float scale,
                              void* workspace, size_t workspace_bytes, float* const* ds_bufs_host,
                              const size_t* ds_bytes_host, int nbufs, ember_stream_t s);
+/* The forward that keeps its scores for the backward (an added option of the
+ * same chain as ember_attn_fwd, for a forward whose backward follows while
+ * memory allows, e.g. a checkpointed block's re-run): o and lse as
+ * ember_attn_fwd, bit for bit; every score it computes, S = Q K^T scale log2(e)
+ * before the causal mask, is also written in the dS layout into buffers that
+ * together hold all B*Hk KV rows (ember_attn_bwd_ds_row_bytes each, whole rows
+ * per buffer, taken in order).  `workspace` >= ember_attn_scores_workspace_bytes
+ * holds the row table (enqueued, so it may be reused once the launch has run).
+ * EMBER_EWORKSPACE when the buffers hold fewer rows. */
+size_t ember_attn_scores_workspace_bytes(int64_t B, int64_t H);
+int ember_attn_fwd_scores(const float* q, const float* k, const float* v, float* o, float* lse,
+                          int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D, float scale,
+                          float* const* s_bufs_host, const size_t* s_bytes_host, int nbufs,
+                          void* workspace, size_t workspace_bytes, ember_stream_t s);
+/* ember_attn_bwd_scattered over the buffers ember_attn_fwd_scores filled (the
+ * same buffers, in the same order): the dK/dV pass reads the kept scores
+ * instead of computing S again and writes dS over them; one chunk of all rows.
+ * dq, dk, dv agree with ember_attn_bwd to fp32 rounding (S is the forward's
+ * rounding of the same products). */
+int ember_attn_bwd_from_scores(const float* q, const float* k, const float* v, const float* o,
+                               const float* lse, const float* dout, float* dq, float* dk,
+                               float* dv, int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D,
+                               float scale, void* workspace, size_t workspace_bytes,
+                               float* const* s_bufs_host, const size_t* s_bytes_host, int nbufs,
+                               ember_stream_t s);
 
 /* ------------------------------------------------------ KV cache (inference)
  * Cache layout [B, Hk, S, D] (S = max_seq_len), fp32, as nn::KVCache holds it.

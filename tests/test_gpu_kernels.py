@@ -1129,6 +1129,100 @@ def test_attention_bwd_scattered_equals_contiguous(B, T, H, Hk, D, split):
         assert np.array_equal(tail.reshape(-1, 4), np.broadcast_to(fill, (tail.size // 4, 4)))
 
 
+def _keep_scores_run(Q, K, Vv, DO, B, T, H, Hk, D, scale, sizes, fill=7.25, guard=4096):
+    """ember_attn_fwd_scores then ember_attn_bwd_from_scores over buffers of
+    `sizes` bytes carved from one pool, each followed by a guard band."""
+    lib = capi.lib()
+    offs, o = [], 0
+    for s in sizes:
+        offs.append(o)
+        o += (s + guard + 255) // 256 * 256
+    POOL = torch.full(((o + 3) // 4,), fill, device="cuda")
+    base = POOL.data_ptr()
+    ptrs = (C.c_void_p * len(sizes))(*[base + off if s else None for off, s in zip(offs, sizes)])
+    szs = (C.c_size_t * len(sizes))(*sizes)
+    tws = lib.ember_attn_scores_workspace_bytes(B, H)
+    TW = empty(((tws + 3) // 4,))
+    Ot, L = empty((B, T, H, D)), empty((B, H, T))
+    call("ember_attn_fwd_scores", p(Q), p(K), p(Vv), p(Ot), p(L), B, T, H, Hk, D, scale, ptrs, szs,
+         len(sizes), p(TW), tws, None)
+    lo = lib.ember_attn_bwd_workspace_bytes_min(B, T, H)
+    WS = empty(((lo + 3) // 4,))
+    DQ, DK, DV = empty((B, T, H, D)), empty((B, T, Hk, D)), empty((B, T, Hk, D))
+    call("ember_attn_bwd_from_scores", p(Q), p(K), p(Vv), p(Ot), p(L), p(DO), p(DQ), p(DK), p(DV),
+         B, T, H, Hk, D, scale, p(WS), lo, ptrs, szs, len(sizes), None)
+    return Ot, L, DQ, DK, DV, POOL, offs
+
+
+@pytest.mark.parametrize("B,T,H,Hk,D,split", [
+    (1, 256, 9, 3, 64, [3]),              # c1's heads, one buffer holding every row
+    (2, 300, 8, 2, 64, [1, 2.5, 0, 1]),   # ragged T (T32 = 320), rows over several buffers
+    (4, 130, 8, 1, 128, [4]),             # group 8, D 128
+    (1, 200, 32, 8, 64, [8]),             # group 4 (the c4 head layout)
+    (2, 96, 32, 8, 64, [5, 6, 5]),        # 16 KV rows: the XCD regrouping
+    (8, 256, 16, 8, 128, [64]),           # the c5 launch layout at T = 256
+])
+def test_attention_keep_scores(B, T, H, Hk, D, split):
+    # The forward that keeps its scores gives o and lse bitwise equal to the
+    # plain forward; the backward from them agrees with the oracle to the same
+    # tolerance as the recompute path, and with that path to fp32 rounding
+    # (S is the forward's rounding of the same products); runs repeat bit for
+    # bit; nothing is written past each buffer's whole rows.
+    r = rng(B * 131 + T + H)
+    q, k, v, do = (r.standard_normal(s).astype(np.float32)
+                   for s in ((B, T, H, D), (B, T, Hk, D), (B, T, Hk, D), (B, T, H, D)))
+    scale = 1.0 / math.sqrt(D)
+    lib = capi.lib()
+    row = lib.ember_attn_bwd_ds_row_bytes(T, H, Hk)
+    sizes = [int(f * row) // 256 * 256 if f != int(f) else int(f) * row for f in split]
+    assert sum(s // row for s in sizes) >= B * Hk
+    Q, K, Vv, DO = dev(q), dev(k), dev(v), dev(do)
+    Oc, Lc, DQc, DKc, DVc = _attn_hip(Q, K, Vv, DO, B, T, H, Hk, D, scale)
+    Ot, L, DQ, DK, DV, POOL, offs = _keep_scores_run(Q, K, Vv, DO, B, T, H, Hk, D, scale, sizes)
+    assert torch.equal(Ot, Oc) and torch.equal(L, Lc)
+    dq_ref, dk_ref, dv_ref = O.attention_bwd(q, k, v, do, scale)
+    assert_close(host(DQ), dq_ref, name="dq (kept scores)")
+    assert_close(host(DK), dk_ref, name="dk (kept scores)")
+    assert_close(host(DV), dv_ref, name="dv (kept scores)")
+    for got, want in ((DQ, DQc), (DK, DKc), (DV, DVc)):
+        rel = ((got - want).norm() / want.norm()).item()
+        assert rel < 2e-6, rel
+    again = _keep_scores_run(Q, K, Vv, DO, B, T, H, Hk, D, scale, sizes)
+    for a, b in zip((Ot, L, DQ, DK, DV), again[:5]):
+        assert torch.equal(a, b)
+    pool = host(POOL).view(np.uint8)
+    fill = np.frombuffer(np.float32(7.25).tobytes(), np.uint8)
+    left = B * Hk  # row slots are taken in buffer order
+    for off, s in zip(offs, sizes):
+        used = min(s // row, left)
+        left -= used
+        tail = pool[off + used * row: off + s + 4096]
+        assert np.array_equal(tail.reshape(-1, 4), np.broadcast_to(fill, (tail.size // 4, 4)))
+
+
+def test_attention_keep_scores_needs_every_row():
+    # Buffers that hold fewer KV rows than B*Hk are refused before any launch.
+    B, T, H, Hk, D = 2, 128, 8, 2, 64
+    lib = capi.lib()
+    row = lib.ember_attn_bwd_ds_row_bytes(T, H, Hk)
+    Q, K, Vv = dev(np.zeros((B, T, H, D), np.float32)), dev(np.zeros((B, T, Hk, D), np.float32)), \
+        dev(np.zeros((B, T, Hk, D), np.float32))
+    S = empty(((3 * row) // 4,))
+    ptrs = (C.c_void_p * 1)(S.data_ptr())
+    szs = (C.c_size_t * 1)(3 * row)
+    tws = lib.ember_attn_scores_workspace_bytes(B, H)
+    TW = empty(((tws + 3) // 4,))
+    Ot, L = empty((B, T, H, D)), empty((B, H, T))
+    rc = lib.ember_attn_fwd_scores(p(Q), p(K), p(Vv), p(Ot), p(L), B, T, H, Hk, D, 0.125, ptrs, szs,
+                                   1, p(TW), tws, None)
+    assert rc == -2, rc  # EMBER_EWORKSPACE
+    lo = lib.ember_attn_bwd_workspace_bytes_min(B, T, H)
+    WS = empty(((lo + 3) // 4,))
+    rc = lib.ember_attn_bwd_from_scores(p(Q), p(K), p(Vv), p(Ot), p(L), p(Q), p(Q), p(K), p(Vv), B,
+                                        T, H, Hk, D, 0.125, p(WS), lo, ptrs, szs, 1, None)
+    assert rc == -2, rc
+
+
 # The launch layouts of the BASELINE configs: c3 Qwen3-0.6B (64 (batch, head)
 # rows, group 2, D 128), c4 LLaMA-3.2-1B (128 rows, group 4, D 64), c5
 # Qwen3-1.7B (128 rows, group 2, D 128).  Row counts that are multiples of 8

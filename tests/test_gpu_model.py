@@ -296,6 +296,49 @@ def test_tiny_model_loss_and_grads_vs_oracle(qk_norm, llama3, D, vocab):
     tr.close()
 
 
+@pytest.mark.parametrize("qk_norm,D", [(False, 64), (True, 128)])
+def test_kept_attention_scores_with_checkpointing(qk_norm, D):
+    # Attention that keeps its scores for the backward (the checkpointed
+    # re-run's forward keeps them, its backward reads them): the same loss
+    # bits (the forward is unchanged), gradients within fp32 rounding of the
+    # default path and against the oracle, and bit for bit on a repeat.
+    c = tiny_cfg(qk_norm, False, D, 1024)
+    tr = TR.Trainer(c, seed=3, init_std=0.1, norm_value=None)
+    ids, tg, mask = batch(c, 2, 130, seed=4)
+    tr.set_batch(ids, tg, mask)
+    tr.set_checkpointing(True)
+    try:
+        loss = tr.forward_backward(True)
+        ref = [tr.get_grad(i) for i in range(tr.num_params())]
+        TR.set_attn_keep_scores(True)
+        runs = []
+        for _ in range(2):
+            tr.zero_grad()
+            runs.append((tr.forward_backward(True),
+                         [tr.get_grad(i) for i in range(tr.num_params())]))
+    finally:
+        TR.set_attn_keep_scores(False)
+    assert runs[0][0] == loss and runs[1][0] == loss
+    for name, a, b, g in zip(tr.names, runs[0][1], runs[1][1], ref):
+        assert np.array_equal(a, b), name
+        assert_close(a, g, rtol=1e-5, name=name)
+    sh = shapes(c)
+    params = []
+    for name, i in zip(tr.names, range(tr.num_params())):
+        pv = tr.get_param(i)
+        if name == "model.embed_tokens.weight":
+            params.append(pv.reshape(c.vocab_size, c.hidden_size))
+        elif name == "model.norm.weight":
+            params.append(pv)
+        else:
+            params.append(pv.reshape(sh[name.split(".")[-2]]))
+    _, ref_grads = O.model_loss(oracle_cfg(c), params, ids, tg, mask)
+    for i, name in enumerate(tr.names):
+        assert_close(runs[0][1][i], ref_grads[i].reshape(-1), name=name)
+    tr.close()
+
+
+
 @pytest.mark.parametrize("vocab,dead_rows", [(1000, 0), (1024, 0), (1024, 100)])
 def test_chunked_lm_head_loss_equals_single_chunk(vocab, dead_rows):
     """The LM head + loss run a chunk of rows at a time; the loss does not
