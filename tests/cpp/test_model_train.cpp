@@ -20,6 +20,7 @@
 #include "ctd/autograd.h"
 #include "ctd/nn/kv_cache.h"
 #include "ctd/nn/model.h"
+#include "ctd/ops/attention.h"
 #include "ctd/ops/elementwise.h"
 #include "ctd/ops/loss.h"
 #include "ctd/ops/matmul.h"
@@ -401,6 +402,54 @@ void kv_cache_equivalences(TinyCfg c) {
 // too and through a loss scaled before backward (the fused LM head's node
 // then scales into fresh buffers); a last pass without retaining consumes the
 // graph, after which another backward throws, as the default always does.
+// Attention that keeps its scores, under a retained graph (no checkpointing):
+// a retained pass computes S again and leaves the scores intact, so the last,
+// consuming pass reads them: its gradients are bitwise those of a fresh
+// forward + backward from kept scores, added to the retained passes' sum.
+void kept_scores_retained_graph() {
+  const int B = 2, T = 70;
+  std::mt19937 rng(9);
+  TinyCfg c{32, 128, 2, 1, 64, 64, 2, 1e-5f, 1e4f};
+  nn::Model m = build_tiny(c, rng, /*grad=*/true);
+  std::vector<int64_t> hx(B * T), hy(B * T);
+  for (int i = 0; i < B * T; ++i) {
+    hx[i] = (i * 7 + 3) % c.V;
+    hy[i] = (i * 5 + 1) % c.V;
+  }
+  Tensor x = Tensor::from_host(hx.data(), {B, T}, DType::kInt64, kHIP0);
+  Tensor y = Tensor::from_host(hy.data(), {B, T}, DType::kInt64, kHIP0);
+  std::vector<Tensor> ps = params_of(m);
+  struct Keep {
+    Keep() { ops::set_attention_keep_scores(true); }
+    ~Keep() { ops::set_attention_keep_scores(false); }
+  } keep;
+  m.forward_train(x, y).backward();
+  std::vector<std::vector<float>> gk;
+  for (Tensor& p : ps) {
+    gk.push_back(host(p.grad()));
+    p.zero_grad_();
+  }
+  Tensor loss = m.forward_train(x, y);
+  loss.backward(/*retain_graph=*/true);
+  std::vector<std::vector<float>> g1;
+  for (Tensor& p : ps) g1.push_back(host(p.grad()));
+  loss.backward(/*retain_graph=*/true);
+  loss.backward();
+  bool exact = true;
+  double num = 0.0, den = 0.0;
+  for (size_t i = 0; i < ps.size(); ++i) {
+    const std::vector<float> g3 = host(ps[i].grad());
+    for (size_t j = 0; j < g3.size(); ++j) {
+      const float two = g1[i][j] + g1[i][j];
+      exact = exact && g3[j] == two + gk[i][j];
+      num += (gk[i][j] - g1[i][j]) * static_cast<double>(gk[i][j] - g1[i][j]);
+      den += static_cast<double>(g1[i][j]) * g1[i][j];
+    }
+  }
+  check(exact, "the consuming pass reads the scores the retained passes left intact");
+  check(std::sqrt(num / den) < 1e-5, "kept-score gradients agree with the recompute path");
+}
+
 void retained_graph_repeat_backward(bool checkpointing, float upstream) {
   const int B = 2, T = 6;
   std::vector<int64_t> hx = {1, 4, 0, 6, 7, 2, 3, 5, 2, 2, 1, 0};
@@ -889,6 +938,18 @@ int main(int argc, char** argv) {
       [] { retained_graph_repeat_backward(true, 1.0f); });
   run("Autograd.RetainedGraphRepeatBackward_ScaledLoss",
       [] { retained_graph_repeat_backward(true, 0.25f); });
+  // The same with attention keeping its scores: a retained pass computes S
+  // again and leaves the scores for the last, consuming pass.
+  run("Autograd.RetainedGraphKeptScores", [] { kept_scores_retained_graph(); });
+  run("Autograd.RetainedGraphRepeatBackward_Checkpointed_KeptScores", [] {
+    // each pass re-runs the blocks, whose attention keeps fresh scores that
+    // the re-run's own (consuming) backward reads: the same path every pass
+    struct Keep {
+      Keep() { ops::set_attention_keep_scores(true); }
+      ~Keep() { ops::set_attention_keep_scores(false); }
+    } keep;
+    retained_graph_repeat_backward(true, 1.0f);
+  });
   run("ModelTrain.TrainLogitsMatchInferenceLogits",
       [] { train_logits_match_inference_logits(TinyCfg{}); });
   run("ModelTrain.TrainLogitsMatchInferenceLogits_D64",
