@@ -145,12 +145,55 @@ struct RowTile {
   }
 };
 
+// ROWS rows of D floats copied global -> LDS by global_load_lds_dwordx4 (no
+// registers, no LDS store instructions) by WAVES waves.  One wave
+// instruction fills a 1 KB block with 1024 / (4 D) rows; row r sits in block
+// r % kBlocks at (r / kBlocks) * D, and blocks are padded to 260 floats, so the
+// b128 reads of 16 consecutive rows at one column (the K fragments) and of
+// one row at 16 consecutive columns (V) both hit 16 distinct bank groups.
+template <int D, int ROWS, int WAVES>
+struct DmaTile {
+  static constexpr int kChunks = D / 4;              // 16-byte chunks per row
+  static constexpr int kRpi = 64 / kChunks;          // rows per block
+  static constexpr int kBlocks = ROWS / kRpi;
+  static constexpr int kBlockStride = 256 + 4;       // floats
+  static constexpr int kFloats = kBlocks * kBlockStride;
+  static constexpr int kInsts = kBlocks / WAVES;     // per wave
+  static_assert(kRpi * kChunks == 64 && ROWS % kRpi == 0, "rows do not fill 1 KB blocks");
+  static_assert(kBlocks % WAVES == 0, "tile does not split evenly over the waves");
+  __device__ __forceinline__ static int at(int row, int col) {
+    return (row % kBlocks) * kBlockStride + (row / kBlocks) * D + col;
+  }
+  // Rows [0, ROWS) of src (row stride gstride floats) into lds; rows at or
+  // past valid (>= 1) read row valid - 1 again, whose products are masked.
+  __device__ __forceinline__ static void issue(float* lds, const float* src, int64_t gstride,
+                                               int valid, int w, int lane) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass would drop the kernel's launch stub
+#pragma unroll
+    for (int q = 0; q < kInsts; ++q) {
+      const int blk = w + WAVES * q;
+      const int row = blk + kBlocks * (lane / kChunks);
+      const int64_t srow = min(row, valid - 1);
+      __builtin_amdgcn_global_load_lds(src + srow * gstride + 4 * (lane % kChunks),
+                                       lds + kBlockStride * blk, 16, 0, 0);
+    }
+#endif
+  }
+};
+
+// s_waitcnt vmcnt(0) lgkmcnt(0).
+__device__ __forceinline__ void wait_all_mem() {
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (0 << 8));
+}
+
 // ------------------------------------------------------------------ forward
 // Forward.  A wave owns 16 queries and a workgroup of eight waves 128, so
-// every K/V tile in LDS serves 128 queries, and at 124 registers per lane
+// every K/V tile in LDS serves 128 queries, and at 106 registers per lane
 // (D = 128) four waves fit on a SIMD (32 queries per wave on 32x32x2 tiles
-// took 239 and two waves: 1.14x slower at B=8, T=4096, H=16, Hk=8).  Per
-// 32-key tile (halves kt of 16 keys):
+// took 239 and two waves: 1.14x slower at B=8, T=4096, H=16, Hk=8).  K and V
+// tiles are copied global -> LDS by DMA into two buffers, the next tile's
+// copy in flight during this one's MFMAs.  Per 32-key tile (halves kt of 16
+// keys):
 //   S^T = K Q^T (m = key, n = query): MFMA step 4t+j contracts over
 //   d = 16t + 4g + j, each K fragment one b128 LDS read, Q in registers;
 //   register e of s[kt] in lane (g, i) is the score of key 16kt + 4g + e for
@@ -164,8 +207,10 @@ struct RowTile {
 //   d = 16t + x; only its register moves.
 template <int D>
 struct FwdCfg {
-  static constexpr int kThreads = 512, kBQ = 128, kBK = 32, kKS = D + 4;
-  static constexpr int kBuf = 2 * kBK * kKS;  // one K+V stage
+  static constexpr int kThreads = 512, kBQ = 128, kBK = 32;
+  using Tile = DmaTile<D, kBK, kThreads / 64>;
+  static constexpr int kTile = Tile::kFloats;
+  static constexpr int kBuf = 2 * kTile;  // one K+V stage
   static constexpr int kSmem = 2 * kBuf;
 };
 
@@ -214,35 +259,58 @@ __global__ __launch_bounds__(FwdCfg<D>::kThreads, 2) void attn_fwd_kernel(
 
   const int kend = min(T, q0 + C::kBQ);
   const int nkb = (kend + C::kBK - 1) / C::kBK;
-  RowTile<D, C::kBK, C::kThreads> tk, tv;
-  tk.load(kbase, ks, T);
-  tv.load(vbase, ks, T);
-  tk.store(smem, C::kKS);
-  tv.store(smem + C::kBK * C::kKS, C::kKS);
+  using Tile = typename C::Tile;
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  Tile::issue(smem, kbase, ks, T, wu, lane);
+  Tile::issue(smem + C::kTile, vbase, ks, T, wu, lane);
+  wait_all_mem();
   __syncthreads();
 
   for (int kb = 0; kb < nkb; ++kb) {
     const int k0 = kb * C::kBK;
     const bool more = kb + 1 < nkb;
-    if (more) {
-      tk.load(kbase + static_cast<int64_t>(k0 + C::kBK) * ks, ks, T - k0 - C::kBK);
-      tv.load(vbase + static_cast<int64_t>(k0 + C::kBK) * ks, ks, T - k0 - C::kBK);
+    if (more) {  // the next K/V tile lands in the other buffer during this one
+      float* nb = smem + ((kb + 1) & 1) * C::kBuf;
+      const int64_t off = static_cast<int64_t>(k0 + C::kBK) * ks;
+      Tile::issue(nb, kbase + off, ks, T - k0 - C::kBK, wu, lane);
+      Tile::issue(nb + C::kTile, vbase + off, ks, T - k0 - C::kBK, wu, lane);
     }
     const float* Ks = smem + (kb & 1) * C::kBuf;
-    const float* Vs = Ks + C::kBK * C::kKS;
+    const float* Vs = Ks + C::kTile;
     if (k0 <= qw0 + 15) {  // some key of the tile is seen by some query of this wave
       f32x4 s[2];
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      // K fragments one d tile ahead: the reads of tile t + 1 are in flight
+      // while the MFMAs of tile t run.
+      f32x4 kf[2][2];
+      auto read_k = [&](int t, f32x4 (&dst)[2]) {
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
+        for (int kt = 0; kt < 2; ++kt)
+          dst[kt] = *reinterpret_cast<const f32x4*>(Ks + Tile::at(16 * kt + i, 16 * t + 4 * g));
+      };
+      read_k(0, kf[0]);
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          const f32x4 kf =
-              *reinterpret_cast<const f32x4*>(Ks + (16 * kt + i) * C::kKS + 16 * t + 4 * g);
+      for (int t = 0; t < NT; ++t) {
+        if (t + 1 < NT) read_k(t + 1, kf[(t + 1) & 1]);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) s[kt] = mfma16(kf[j], qreg[t][j], s[kt]);
-        }
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) s[kt] = mfma16(kf[t & 1][kt][j], qreg[t][j], s[kt]);
+      }
+      // Order: tile 0's reads, then per tile two MFMAs, a read of the next
+      // tile, two MFMAs, the other read, four MFMAs (the wait for a tile's
+      // reads comes before the next tile's are issued).
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+      for (int t = 0; t + 1 < NT; ++t) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
       if constexpr (SS) {
         // The tile's 32 keys lie in one 64-key strip; this lane's query is at
         // or past the strip's first key whenever the tile is processed.
@@ -290,21 +358,17 @@ __global__ __launch_bounds__(FwdCfg<D>::kThreads, 2) void attn_fwd_kernel(
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int row = (16 * kt + 4 * g + e) * C::kKS;
+          const int row = 16 * kt + 4 * g + e;
 #pragma unroll
           for (int hq = 0; hq < NT / 4; ++hq) {
-            const f32x4 vv = *reinterpret_cast<const f32x4*>(Vs + row + 64 * hq + 4 * i);
+            const f32x4 vv = *reinterpret_cast<const f32x4*>(Vs + Tile::at(row, 64 * hq + 4 * i));
 #pragma unroll
             for (int c = 0; c < 4; ++c)
               acc[4 * hq + c] = mfma16(vv[c], s[kt][e], acc[4 * hq + c]);
           }
         }
     }
-    if (more) {
-      float* nb = smem + ((kb + 1) & 1) * C::kBuf;
-      tk.store(nb, C::kKS);
-      tv.store(nb + C::kBK * C::kKS, C::kKS);
-    }
+    wait_all_mem();  // this wave's DMA of the next tile has landed
     __syncthreads();
   }
 
