@@ -186,9 +186,34 @@ __device__ __forceinline__ void wait_all_mem() {
   __builtin_amdgcn_s_waitcnt((7 << 4) | (0 << 8));
 }
 
+// Max and sum over lanes i, i + 16, i + 32, i + 48 of a wave, the four
+// 16-lane rows' values exchanged in registers: v_permlane16_swap trades rows
+// 1 and 3 of its first operand for rows 0 and 2 of its second, so with x in
+// both each lane holds x of rows {0, 1} or {2, 3}; v_permlane32_swap trades
+// the upper 32 lanes of the first for the lower 32 of the second.  max and +
+// of two operands are commutative, so every lane gets the same bits.
+__device__ __forceinline__ float pair_rows16(float x, bool sum) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+  return sum ? a + b : fmaxf(a, b);
+}
+__device__ __forceinline__ float pair_rows32(float x, bool sum) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+  return sum ? a + b : fmaxf(a, b);
+}
+__device__ __forceinline__ float max_over_rows(float x) {
+  return pair_rows32(pair_rows16(x, false), false);
+}
+__device__ __forceinline__ float sum_over_rows(float x) {
+  return pair_rows32(pair_rows16(x, true), true);
+}
+
 // ------------------------------------------------------------------ forward
 // Forward.  A wave owns 16 queries and a workgroup of eight waves 128, so
-// every K/V tile in LDS serves 128 queries, and at 106 registers per lane
+// every K/V tile in LDS serves 128 queries, and at 102 registers per lane
 // (D = 128) four waves fit on a SIMD (32 queries per wave on 32x32x2 tiles
 // took 239 and two waves: 1.14x slower at B=8, T=4096, H=16, Hk=8).  K and V
 // tiles are copied global -> LDS by DMA into two buffers, the next tile's
@@ -261,6 +286,7 @@ __global__ __launch_bounds__(FwdCfg<D>::kThreads, 2) void attn_fwd_kernel(
   const int nkb = (kend + C::kBK - 1) / C::kBK;
   using Tile = typename C::Tile;
   const int wu = __builtin_amdgcn_readfirstlane(w);
+  const int qw0u = q0 + 16 * wu;  // qw0, known wave-uniform
   Tile::issue(smem, kbase, ks, T, wu, lane);
   Tile::issue(smem + C::kTile, vbase, ks, T, wu, lane);
   wait_all_mem();
@@ -325,18 +351,21 @@ __global__ __launch_bounds__(FwdCfg<D>::kThreads, 2) void attn_fwd_kernel(
             for (int e = 0; e < 4; ++e) col[(16 * kt + e) * lr] = s[kt][e];
         }
       }
-      const bool need_mask = (k0 + C::kBK - 1 > qw0) || (k0 + C::kBK > T);
+      // Keys past min(myq, T - 1) are masked, on the tiles that reach them (a
+      // wave-uniform test, so the other tiles skip it on a scalar branch).
+      if (k0 + C::kBK - 1 > qw0u || k0 + C::kBK > T) {
+        const int klim = min(myq, T - 1) - k0 - 4 * g;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s[kt][e] = 16 * kt + e > klim ? -INFINITY : s[kt][e];
+      }
       float tmax = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int key = k0 + 16 * kt + 4 * g + e;
-          if (need_mask && (key > myq || key >= T)) s[kt][e] = -INFINITY;
-          tmax = fmaxf(tmax, s[kt][e]);
-        }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+        for (int e = 0; e < 4; ++e) tmax = fmaxf(tmax, s[kt][e]);
+      tmax = max_over_rows(tmax);
       const float m_new = fmaxf(m_run, tmax);
       const float alpha = fast_exp2(m_run - m_new);
       float psum = 0.f;
@@ -372,8 +401,7 @@ __global__ __launch_bounds__(FwdCfg<D>::kThreads, 2) void attn_fwd_kernel(
     __syncthreads();
   }
 
-  float l_tot = l_run + __shfl_xor(l_run, 16, kWave);
-  l_tot += __shfl_xor(l_tot, 32, kWave);
+  const float l_tot = sum_over_rows(l_run);
   if (myq < T) {
     if (g == 0) lse[(static_cast<int64_t>(b) * H + h) * T + myq] = (m_run + log2f(l_tot)) * kLn2;
     store_d_row(reinterpret_cast<f32x4*>(o + qoff + myq * qs), acc, g, 1.0f / l_tot);
