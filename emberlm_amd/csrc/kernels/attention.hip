@@ -181,6 +181,14 @@ struct DmaTile {
   }
 };
 
+// One dword per lane copied global -> LDS by DMA: lane l's word lands at
+// lds[l].
+__device__ __forceinline__ void dma_dword(float* lds, const float* src) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass would drop the kernel's launch stub
+  __builtin_amdgcn_global_load_lds(src, lds, 4, 0, 0);
+#endif
+}
+
 // s_waitcnt vmcnt(0) lgkmcnt(0).
 __device__ __forceinline__ void wait_all_mem() {
   __builtin_amdgcn_s_waitcnt((7 << 4) | (0 << 8));
@@ -567,7 +575,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
 // wave holds half the accumulators and half the K/V registers that 32 keys
 // on 32x32x2 tiles would need (those spill past 256 VGPRs into AGPRs at
 // D = 128, one wave per SIMD): two waves fit on a SIMD, and one wave's
-// softmax section and barrier waits run under the other's MFMAs.  Per
+// softmax section and barrier waits run under the other's MFMAs.  The Q and
+// dO tiles of a step (and its lse and delta) are copied global -> LDS by DMA
+// into two buffers, the next step's copy in flight during this one.  Per
 // 32-query tile:
 //   S = Q K^T and dP = dO V^T (m = query, n = key): MFMA step 4t+j contracts
 //   over d = 16t + 4g + j, so each Q / dO fragment is one b128 LDS read and
@@ -580,8 +590,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_kernel(
 //   store_d_row).
 template <int D>
 struct DkvCfg {
-  static constexpr int kBKeys = 64, kBQ = 32, kQS = D + 4;
-  static constexpr int kBuf = 2 * kBQ * kQS + 2 * kBQ;  // Q, dO, lse, delta
+  static constexpr int kBKeys = 64, kBQ = 32;
+  using Tile = DmaTile<D, kBQ, kThreads / 64>;
+  static constexpr int kTile = Tile::kFloats;
+  static constexpr int kBuf = 2 * kTile + 2 * kBQ;  // Q, dO, lse, delta
   static constexpr int kSmem = 2 * kBuf;
 };
 
@@ -640,28 +652,23 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
   // key0, key0 + 32, ... below T.
   const int ntile = (T - key0 + C::kBQ - 1) / C::kBQ;
   const int nsteps = group * ntile;
-  RowTile<D, C::kBQ> tq, tdo;
-  float tl = 0.f, te = 0.f;
-  auto issue = [&](int step) {
+  using Tile = typename C::Tile;
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  // Step `step`'s Q and dO tiles, lse and delta copied global -> LDS by DMA
+  // into `buf`.  Query rows at or past T read row T - 1 again (their P is
+  // selected to 0 below, and their dQ rows are not stored); wave 0 copies
+  // lse (lanes 0-31) and delta (lanes 32-63) in one dword instruction.
+  auto issue = [&](int step, float* buf) {
     const int hh = step / ntile, qt0 = key0 + (step % ntile) * C::kBQ;
     const int h = hk * group + hh;
     const int64_t qoff = static_cast<int64_t>(b) * T * qs + static_cast<int64_t>(h) * D +
                          static_cast<int64_t>(qt0) * qs;
-    tq.load(q + qoff, qs, T - qt0);
-    tdo.load(dout + qoff, qs, T - qt0);
-    if (threadIdx.x < C::kBQ) {
-      const int t = qt0 + static_cast<int>(threadIdx.x);
+    Tile::issue(buf, q + qoff, qs, T - qt0, wu, lane);
+    Tile::issue(buf + C::kTile, dout + qoff, qs, T - qt0, wu, lane);
+    if (wu == 0) {
       const int64_t srow = (static_cast<int64_t>(b) * H + h) * T;
-      tl = t < T ? lse[srow + t] : 0.f;  // scaled at the LDS store: no wait here
-      te = t < T ? delta[srow + t] : 0.f;
-    }
-  };
-  auto commit = [&](float* buf) {
-    tq.store(buf, C::kQS);
-    tdo.store(buf + C::kBQ * C::kQS, C::kQS);
-    if (threadIdx.x < C::kBQ) {
-      buf[2 * C::kBQ * C::kQS + threadIdx.x] = tl * kLog2e;
-      buf[2 * C::kBQ * C::kQS + C::kBQ + threadIdx.x] = te;
+      const int t = min(qt0 + (lane & (C::kBQ - 1)), T - 1);
+      dma_dword(buf + 2 * C::kTile, (lane < C::kBQ ? lse : delta) + srow + t);
     }
   };
   // FS: this lane's scores of a step (queries qt0 + 16mt + 4g + (0..3), the
@@ -672,9 +679,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) snext[mt] = *reinterpret_cast<const gf32x4*>(src + 16 * mt);
   };
-  issue(0);
+  issue(0, smem);
   if constexpr (FS) load_scores(0);
-  commit(smem);
+  wait_all_mem();
   __syncthreads();
 
   for (int step = 0; step < nsteps; ++step) {
@@ -685,13 +692,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
       scur[0] = snext[0];
       scur[1] = snext[1];
     }
-    if (more) {
-      issue(step + 1);
+    if (more) {  // the next step's tiles land in the other buffer during this one
+      issue(step + 1, smem + ((step + 1) & 1) * C::kBuf);
       if constexpr (FS) load_scores(step + 1);
     }
     const float* Qs = smem + (step & 1) * C::kBuf;
-    const float* Ds = Qs + C::kBQ * C::kQS;
-    const float* Ls = Qs + 2 * C::kBQ * C::kQS;
+    const float* Ds = Qs + C::kTile;
+    const float* Ls = Qs + 2 * C::kTile;
     const float* Es = Ls + C::kBQ;
     if (qt0 + C::kBQ - 1 >= kw0) {  // some query of the tile sees some key of this wave
       // The two 16-query halves in sequence: S and dP of half 1 are issued
@@ -705,13 +712,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           const f32x4 of =
-              *reinterpret_cast<const f32x4*>(Ds + (16 * mt + i) * C::kQS + 16 * t + 4 * g);
+              *reinterpret_cast<const f32x4*>(Ds + Tile::at(16 * mt + i, 16 * t + 4 * g));
           if constexpr (FS) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) dp[mt] = mfma16(of[j], vreg[t][j], dp[mt]);
           } else {
             const f32x4 qf =
-                *reinterpret_cast<const f32x4*>(Qs + (16 * mt + i) * C::kQS + 16 * t + 4 * g);
+                *reinterpret_cast<const f32x4*>(Qs + Tile::at(16 * mt + i, 16 * t + 4 * g));
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               s[mt] = mfma16(qf[j], kreg[t][j], s[mt]);
@@ -721,10 +728,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
         }
       };
       auto softmax = [&](int mt) {
-        // The scaled lse and delta of this lane's queries 16mt + 4g + e, read
-        // as float4s (a read per entry, inside the mask test, serialised the
-        // softmax section on LDS round trips).
-        const f32x4 lq = *reinterpret_cast<const f32x4*>(Ls + 16 * mt + 4 * g);
+        // lse (scaled to log2 units here; the product is rounded on its own,
+        // not fused into the subtraction) and delta of this lane's queries
+        // 16mt + 4g + e, read as float4s (a read per entry, inside the mask
+        // test, serialised the softmax section on LDS round trips).
+#pragma clang fp contract(off)
+        const f32x4 lq = *reinterpret_cast<const f32x4*>(Ls + 16 * mt + 4 * g) * kLog2e;
         const f32x4 eq = *reinterpret_cast<const f32x4*>(Es + 16 * mt + 4 * g);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -748,11 +757,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
       auto grads = [&](int mt) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int row = (16 * mt + 4 * g + e) * C::kQS;
+          const int row = 16 * mt + 4 * g + e;
 #pragma unroll
           for (int hq = 0; hq < NT / 4; ++hq) {
-            const f32x4 ov = *reinterpret_cast<const f32x4*>(Ds + row + 64 * hq + 4 * i);
-            const f32x4 qv = *reinterpret_cast<const f32x4*>(Qs + row + 64 * hq + 4 * i);
+            const f32x4 ov = *reinterpret_cast<const f32x4*>(Ds + Tile::at(row, 64 * hq + 4 * i));
+            const f32x4 qv = *reinterpret_cast<const f32x4*>(Qs + Tile::at(row, 64 * hq + 4 * i));
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
               adv[4 * hq + c] = mfma16(ov[c], s[mt][e], adv[4 * hq + c]);
@@ -768,7 +777,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dkdv_kernel(
       softmax(1);
       grads(1);
     }
-    if (more) commit(smem + ((step + 1) & 1) * C::kBuf);
+    wait_all_mem();  // this wave's DMA of the next step has landed
     __syncthreads();
   }
 
