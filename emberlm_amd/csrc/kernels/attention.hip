@@ -823,14 +823,17 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_gemm_kernel(
   constexpr int NI = C::kInstA + C::kInstB;
   __shared__ __attribute__((aligned(1024))) float lds[3 * C::kStage];
 
+  // A workgroup takes query tiles nmt - 1 - p and p of its row (the middle
+  // tile alone when nmt is odd): nmt + 1 key-tiles of work for every pair.
   const int nmt = (T + BM - 1) / BM;
-  const WorkItem wi = work_item(nmt);
-  const int mt = nmt - 1 - wi.tile;  // longest rows first
+  const WorkItem wi = work_item((nmt + 1) / 2);
+  const int p = wi.tile;
   const int row = row0 + wi.row;     // (b, h)
   const int h = row % H, b = row / H;
   const int hk = h / (H / Hk);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1, g = lane >> 5, r = lane & 31;
+  auto run_tile = [&](const int mt) {
   const int m0 = mt * BM;
   const int64_t qs = static_cast<int64_t>(H) * D, ks = static_cast<int64_t>(Hk) * D;
   const float* kbase = k + static_cast<int64_t>(b) * T * ks + static_cast<int64_t>(hk) * D;
@@ -983,6 +986,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_gemm_kernel(
         if (q < T) dqb[static_cast<int64_t>(q) * qs + col] = scale * acc[i][jj][e];
       }
     }
+  };
+  run_tile(nmt - 1 - p);
+  if (nmt - 1 - p != p) {
+    wait_vm_lgkm0<0>();  // every wave is done with the ring before it is refilled
+    block_barrier();
+    run_tile(p);
+  }
 }
 
 int check_shapes(int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D) {
@@ -1109,8 +1119,9 @@ int launch_bwd(const float* q, const float* k, const float* v, const float* o, c
                                               st>>>(q, k, v, dout, lse, delta, dk, dv, table,
                                                     static_cast<int>(r0), Ti, Hi, Hki, sl, scale);
     if ((rc = launch_status())) return rc;
-    attn_bwd_dq_gemm_kernel<D><<<dim3(nmt * static_cast<unsigned>(n * group)), kThreads, 0, st>>>(
-        k, table, dq, static_cast<int>(r0 * group), Ti, Hi, Hki, scale);
+    attn_bwd_dq_gemm_kernel<D><<<dim3((nmt + 1) / 2 * static_cast<unsigned>(n * group)), kThreads,
+                                 0, st>>>(k, table, dq, static_cast<int>(r0 * group), Ti, Hi, Hki,
+                                          scale);
     if ((rc = launch_status())) return rc;
   }
   return EMBER_OK;
