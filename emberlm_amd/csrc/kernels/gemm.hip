@@ -317,39 +317,66 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_mfma(GemmArgs a) {
 // Both keep the fragment reads free of bank conflicts without padding.
 __device__ __forceinline__ int swz(int x) { return ((x >> 1) ^ (x >> 3)) & 3; }
 
-template <bool KC, int ROWS>
+//   BUF: the copies are buffer_load_dwordx4 ... lds through a buffer resource
+//     based at the block's first row (K-contiguous) or column (MN-contiguous),
+//     with 32-bit per-lane byte offsets and the stage's offset in an SGPR;
+//     otherwise global_load_lds_dwordx4 with a 64-bit address per lane.  Same
+//     bytes to the same LDS places: 1.3-2.1% faster on the c5 NT shapes (fewer
+//     address registers and address operations per copy).  The launcher picks
+//     BUF when every offset of the product stays below 2^31 bytes.
+template <bool KC, int ROWS, bool BUF>
 struct DmaTile {
   static constexpr int kFloats = ROWS * 16;   // one stage
   static constexpr int kInsts = ROWS / 64;    // wave-instructions per wave per stage
-  const float* src[kInsts];                    // this lane's 16 bytes, stage 0
-  int64_t step;                                // element stride between stages
+  const float* src[kInsts];                    // !BUF: this lane's 16 bytes, stage 0
+  int64_t step;                                // !BUF: element stride between stages
+  __amdgpu_buffer_rsrc_t rsrc;                 // BUF: the block's first row / column
+  int voff[kInsts];                            // BUF: this lane's byte offset, stage 0
+  int bstep;                                   // BUF: bytes between stages
 
   __device__ __forceinline__ void init(const float* X, int64_t ld, int64_t R, int64_t row0,
                                        int w, int lane) {
+    const int64_t base = KC ? row0 * ld : row0;  // elements from X to the buffer's start
+    if constexpr (BUF)
+      rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(X + base), 0, 0x7fffffff,
+                                               0x00020000);
 #pragma unroll
     for (int q = 0; q < kInsts; ++q) {
       const int t = w + 4 * q;  // 1 KB block of the tile
+      int64_t e;                // this lane's first element
       if (KC) {
         const int x = lane >> 2;
         const int64_t row = min(row0 + 16 * t + x, R - 1);  // rows past R: never stored
-        src[q] = X + row * ld + 4 * ((lane & 3) ^ swz(x));
+        e = row * ld + 4 * ((lane & 3) ^ swz(x));
       } else {
         constexpr int kRowsPer = 256 / ROWS;   // k-rows per 1 KB block
         constexpr int kLanesPer = 64 / kRowsPer;
         const int k = t * kRowsPer + lane / kLanesPer;
         const int q4 = (lane % kLanesPer) ^ (8 * ((k >> 2) & 1));
         const int64_t col = min(row0 + 4 * q4, R - 4);      // R % 4 == 0 on this path
-        src[q] = X + k * ld + col;
+        e = k * ld + col;
       }
+      if constexpr (BUF)
+        voff[q] = static_cast<int>((e - base) * 4);
+      else
+        src[q] = X + e;
     }
     step = KC ? 16 : 16 * ld;
+    bstep = static_cast<int>(4 * step);
   }
   // Stage kt of this lane's loads into the stage buffer `dst` (LDS).
   __device__ __forceinline__ void issue(float* dst, int64_t kt, int w) const {
 #if defined(__HIP_DEVICE_COMPILE__)  // the host pass would drop the kernel's launch stub
 #pragma unroll
-    for (int q = 0; q < kInsts; ++q)
-      __builtin_amdgcn_global_load_lds(src[q] + kt * step, dst + 256 * (w + 4 * q), 16, 0, 0);
+    for (int q = 0; q < kInsts; ++q) {
+      float* d = dst + 256 * (w + 4 * q);
+      if constexpr (BUF)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rsrc, (__attribute__((address_space(3))) void*)d, 16, voff[q],
+            static_cast<int>(kt) * bstep, 0, 0);
+      else
+        __builtin_amdgcn_global_load_lds(src[q] + kt * step, d, 16, 0, 0);
+    }
 #endif
   }
 };
@@ -370,10 +397,10 @@ __device__ __forceinline__ f32x4 dma_frag(const float* st, int off, int i, int s
   return v;
 }
 
-template <bool A_KC, bool B_KC, int BM, int BN, int OCC>
+template <bool A_KC, bool B_KC, int BM, int BN, int OCC, bool BUF>
 __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_dma(GemmArgs a) {
-  using TA = DmaTile<A_KC, BM>;
-  using TB = DmaTile<B_KC, BN>;
+  using TA = DmaTile<A_KC, BM, BUF>;
+  using TB = DmaTile<B_KC, BN, BUF>;
   constexpr int FI = BM / 64, FJ = BN / 64;
   // An M-contiguous A on 256-row tiles is read as b128 rows of four
   // consecutive tile rows (see load_a), one read per MFMA k-step of a slab.
@@ -774,7 +801,14 @@ int launch_dma_t(GemmArgs a, int64_t ny, hipStream_t st) {
   a.tiles_m = static_cast<int>(cdiv(a.M, BM));
   a.tiles_n = static_cast<int>(cdiv(a.N, BN));
   dim3 grid(static_cast<unsigned>(a.tiles_m) * a.tiles_n, static_cast<unsigned>(ny));
-  gemm_f32_dma<A_KC, B_KC, BM, BN, OCC><<<grid, kThreads, 0, st>>>(a);
+  // Largest byte offset a block's buffer resource must reach: BM (BN) rows of
+  // K plus K, or K rows of lda (ldb) plus the tile's columns.
+  const int64_t span_a = A_KC ? BM * a.lda + a.K : a.K * a.lda + BM;
+  const int64_t span_b = B_KC ? BN * a.ldb + a.K : a.K * a.ldb + BN;
+  if (4 * std::max(span_a, span_b) < (int64_t{1} << 31) - 256)
+    gemm_f32_dma<A_KC, B_KC, BM, BN, OCC, true><<<grid, kThreads, 0, st>>>(a);
+  else
+    gemm_f32_dma<A_KC, B_KC, BM, BN, OCC, false><<<grid, kThreads, 0, st>>>(a);
   return launch_status();
 }
 
