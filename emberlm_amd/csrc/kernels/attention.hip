@@ -166,16 +166,21 @@ struct DmaTile {
   }
   // Rows [0, ROWS) of src (row stride gstride floats) into lds; rows at or
   // past valid (>= 1) read row valid - 1 again, whose products are masked.
+  // buffer_load_dwordx4 ... lds through a buffer resource based at src, with
+  // a 32-bit byte offset per lane (under ROWS * gstride * 4 bytes).
   __device__ __forceinline__ static void issue(float* lds, const float* src, int64_t gstride,
                                                int valid, int w, int lane) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the host pass would drop the kernel's launch stub
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(src), 0, 0x7fffffff, 0x00020000);
 #pragma unroll
     for (int q = 0; q < kInsts; ++q) {
       const int blk = w + WAVES * q;
       const int row = blk + kBlocks * (lane / kChunks);
-      const int64_t srow = min(row, valid - 1);
-      __builtin_amdgcn_global_load_lds(src + srow * gstride + 4 * (lane % kChunks),
-                                       lds + kBlockStride * blk, 16, 0, 0);
+      const int srow = min(row, valid - 1);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, (__attribute__((address_space(3))) void*)(lds + kBlockStride * blk), 16,
+          static_cast<int>((srow * gstride + 4 * (lane % kChunks)) * 4), 0, 0, 0);
     }
 #endif
   }
@@ -812,7 +817,11 @@ struct DqGemmCfg {
   static constexpr int kInstA = kBM / 64, kInstB = kBN / 64;  // DMA per wave per stage
 };
 
-template <int D>
+// BUF: the DMA goes through buffer resources based at the (b, h) region of dS
+// and at the KV head's first key, with 32-bit byte offsets (the launcher
+// checks that both regions are under 2^31 bytes); otherwise through 64-bit
+// global addresses.  The same bytes either way.
+template <int D, bool BUF>
 __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_gemm_kernel(
     const float* __restrict__ k, const float* const* __restrict__ ds_rows, float* __restrict__ dq,
     int row0, int T, int H, int Hk, float scale) {
@@ -842,18 +851,34 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_gemm_kernel(
       ds_rows[b * Hk + hk] + static_cast<int64_t>(h - hk * (H / Hk)) * ds_row_floats(T);
 
   // DMA of stage kt (keys 16 kt ... 16 kt + 15, all in strip sb) into `dst`.
+#if defined(__HIP_DEVICE_COMPILE__)
+  __amdgpu_buffer_rsrc_t rs_ds, rs_k;
+  if constexpr (BUF) {
+    rs_ds = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(dsrow), 0, 0x7fffffff,
+                                              0x00020000);
+    rs_k = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(kbase), 0, 0x7fffffff,
+                                             0x00020000);
+  }
+#endif
   auto issue = [&](float* dst, int kt) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the host pass would drop the kernel's launch stub
+    auto copy16 = [&](const __amdgpu_buffer_rsrc_t& rs, const float* base, int64_t e,
+                      float* to) {
+      if constexpr (BUF)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)to,
+                                                 16, static_cast<int>(e * 4), 0, 0, 0);
+      else
+        __builtin_amdgcn_global_load_lds(base + e, to, 16, 0, 0);
+    };
     const int k0 = 16 * kt, sb = k0 >> 6;
     const int64_t lr = T32 - 64 * sb;
-    const float* strip = dsrow + ds_strip_offset(sb, T32);
+    const int64_t strip = ds_strip_offset(sb, T32);
 #pragma unroll
     for (int q = 0; q < C::kInstA; ++q) {
       const int t = wave + 4 * q;  // key row of the stage = 1 KB block of the tile
       const int q4 = lane ^ (8 * ((t >> 2) & 1));
       const int64_t col = min(static_cast<int64_t>(m0 - 64 * sb + 4 * q4), lr - 4);
-      __builtin_amdgcn_global_load_lds(strip + (k0 + t - 64 * sb) * lr + col, dst + 256 * t, 16,
-                                       0, 0);
+      copy16(rs_ds, dsrow, strip + (k0 + t - 64 * sb) * lr + col, dst + 256 * t);
     }
     constexpr int kRowsPer = 256 / BN, kLanesPer = 64 / kRowsPer;
 #pragma unroll
@@ -862,8 +887,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_gemm_kernel(
       const int kr = t * kRowsPer + lane / kLanesPer;
       const int q4 = (lane % kLanesPer) ^ (8 * ((kr >> 2) & 1));
       const int key = min(k0 + kr, T - 1);
-      __builtin_amdgcn_global_load_lds(kbase + key * ks + 4 * q4, dst + C::kAFloats + 256 * t,
-                                       16, 0, 0);
+      copy16(rs_k, kbase, static_cast<int64_t>(key) * ks + 4 * q4, dst + C::kAFloats + 256 * t);
     }
 #endif
   };
@@ -1071,6 +1095,10 @@ int launch_bwd(const float* q, const float* k, const float* v, const float* o, c
   const unsigned nmt = static_cast<unsigned>((T + DqGemmCfg<D>::kBM - 1) / DqGemmCfg<D>::kBM);
   const int64_t group = H / Hk, kv_rows = B * Hk;
   const size_t row_bytes = kv_row_ds_bytes(T, group);
+  // The dQ GEMM's 32-bit DMA offsets span one (b, h) region of dS and one KV
+  // head's keys.
+  const bool dq_buf =
+      4 * std::max<int64_t>(ds_row_floats(T), T * Hk * D) < (int64_t{1} << 31) - 256;
   // KV-row slots in the buffers, in buffer order.
   int64_t chunk = 0;
   for (int i = 0; i < nbufs; ++i) chunk += static_cast<int64_t>(buf_bytes[i] / row_bytes);
@@ -1119,9 +1147,13 @@ int launch_bwd(const float* q, const float* k, const float* v, const float* o, c
                                               st>>>(q, k, v, dout, lse, delta, dk, dv, table,
                                                     static_cast<int>(r0), Ti, Hi, Hki, sl, scale);
     if ((rc = launch_status())) return rc;
-    attn_bwd_dq_gemm_kernel<D><<<dim3((nmt + 1) / 2 * static_cast<unsigned>(n * group)), kThreads,
-                                 0, st>>>(k, table, dq, static_cast<int>(r0 * group), Ti, Hi, Hki,
-                                          scale);
+    const dim3 grid((nmt + 1) / 2 * static_cast<unsigned>(n * group));
+    if (dq_buf)
+      attn_bwd_dq_gemm_kernel<D, true><<<grid, kThreads, 0, st>>>(
+          k, table, dq, static_cast<int>(r0 * group), Ti, Hi, Hki, scale);
+    else
+      attn_bwd_dq_gemm_kernel<D, false><<<grid, kThreads, 0, st>>>(
+          k, table, dq, static_cast<int>(r0 * group), Ti, Hi, Hki, scale);
     if ((rc = launch_status())) return rc;
   }
   return EMBER_OK;

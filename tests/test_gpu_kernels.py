@@ -714,6 +714,36 @@ def test_gemm_add_bitwise_equals_product_then_add(ta, tb, M, N, K):
         assert_close(host(Cm), O.matmul(a, b, ta, tb) + d, name="gemm add")
 
 
+@pytest.mark.parametrize("ta,tb,big", [(0, 1, "a"), (1, 0, "a"), (0, 0, "b"), (1, 1, "b")])
+def test_gemm_global_address_dma_bitwise_equals_buffer_dma(ta, tb, big):
+    """The DMA kernels copy operands into LDS through a buffer resource with
+    32-bit offsets unless some offset of the product reaches 2^31 bytes; then
+    with 64-bit global addresses.  A leading dimension large enough to force
+    the second form (a few strided rows of a 0.3-2.1 GB buffer) gives the same
+    bits as the compact operands, which take the first."""
+    M, N, K = 20, 20, 32
+    r = rng(11 + 2 * ta + tb)
+    a = r.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+    b = r.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+    want = gemm(a, b, ta, tb)
+    x = a if big == "a" else b
+    rows, cols = x.shape
+    kc = (big == "a" and not ta) or (big == "b" and tb)
+    ld = (1 << 22) if kc else (1 << 24)   # 128 * ld or K * ld floats: 2^31 bytes
+    X = torch.zeros((rows - 1) * ld + cols, device="cuda")
+    for i in range(rows):
+        X[i * ld: i * ld + cols].copy_(torch.from_numpy(x[i]))
+    Y = dev(b if big == "a" else a)
+    A, lda = (X, ld) if big == "a" else (Y, a.shape[1])
+    B, ldb = (X, ld) if big == "b" else (Y, b.shape[1])
+    Cm = empty((M, N))
+    call("ember_gemm_f32", int(ta), int(tb), M, N, K, 1.0, p(A), lda, 0, p(B), ldb, 0, 0.0,
+         p(Cm), N, 0, 1, None)
+    assert np.array_equal(host(Cm), want)
+    del X
+    torch.cuda.empty_cache()
+
+
 def test_gemm_add_rejects_overlap_and_short_rows():
     A = empty((64, 32))
     buf = empty((65, 64))
