@@ -860,6 +860,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_gemm_kernel(
                                              0x00020000);
   }
 #endif
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);  // M0 from the scalar unit
   auto issue = [&](float* dst, int kt) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the host pass would drop the kernel's launch stub
     auto copy16 = [&](const __amdgpu_buffer_rsrc_t& rs, const float* base, int64_t e,
@@ -875,7 +876,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_gemm_kernel(
     const int64_t strip = ds_strip_offset(sb, T32);
 #pragma unroll
     for (int q = 0; q < C::kInstA; ++q) {
-      const int t = wave + 4 * q;  // key row of the stage = 1 KB block of the tile
+      const int t = wave_s + 4 * q;  // key row of the stage = 1 KB block of the tile
       const int q4 = lane ^ (8 * ((t >> 2) & 1));
       const int64_t col = min(static_cast<int64_t>(m0 - 64 * sb + 4 * q4), lr - 4);
       copy16(rs_ds, dsrow, strip + (k0 + t - 64 * sb) * lr + col, dst + 256 * t);
@@ -883,7 +884,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_bwd_dq_gemm_kernel(
     constexpr int kRowsPer = 256 / BN, kLanesPer = 64 / kRowsPer;
 #pragma unroll
     for (int q = 0; q < C::kInstB; ++q) {
-      const int t = wave + 4 * q;
+      const int t = wave_s + 4 * q;
       const int kr = t * kRowsPer + lane / kLanesPer;
       const int q4 = (lane % kLanesPer) ^ (8 * ((kr >> 2) & 1));
       const int key = min(k0 + kr, T - 1);

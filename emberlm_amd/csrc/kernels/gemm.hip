@@ -431,13 +431,16 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_dma(GemmArgs a) {
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  // The wave index as a uniform (SGPR) value: the DMA's LDS address (M0) is then
+  // computed on the scalar unit, not read back from a vector register per copy.
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   const int wm = wave >> 1, wn = wave & 1;
   const int g = lane >> 5, r = lane & 31;
 
   TA ta;
   TB tb;
-  ta.init(A, a.lda, a.M, m0, wave, lane);
-  tb.init(B, a.ldb, a.N, n0, wave, lane);
+  ta.init(A, a.lda, a.M, m0, wave_s, lane);
+  tb.init(B, a.ldb, a.N, n0, wave_s, lane);
 
   // Per-lane fragment offsets (floats) inside a stage's A / B tile.
   // K-contiguous: slab s reads unit 4 (r % 16) + ((2 s + g) ^ swz(r % 16)) of
@@ -481,12 +484,12 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_dma(GemmArgs a) {
 
   const int64_t nk = K / 16;
   if (nk > 0) {
-    ta.issue(lds, 0, wave);
-    tb.issue(lds + TA::kFloats, 0, wave);
+    ta.issue(lds, 0, wave_s);
+    tb.issue(lds + TA::kFloats, 0, wave_s);
   }
   if (nk > 1) {
-    ta.issue(lds + kStage, 1, wave);
-    tb.issue(lds + kStage + TA::kFloats, 1, wave);
+    ta.issue(lds + kStage, 1, wave_s);
+    tb.issue(lds + kStage + TA::kFloats, 1, wave_s);
     wait_vm_lgkm0<NI>();
   } else {
     wait_vm_lgkm0<0>();
@@ -517,8 +520,8 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_dma(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < FJ; ++j) fb1[j] = dma_frag<B_KC, BN>(cur + TA::kFloats, offB[1], j, 1, g, r, mbB);
     if constexpr (kDma && !kLateDma) {
-      ta.issue(nx2, kt + 2, wave);
-      tb.issue(nx2 + TA::kFloats, kt + 2, wave);
+      ta.issue(nx2, kt + 2, wave_s);
+      tb.issue(nx2 + TA::kFloats, kt + 2, wave_s);
     }
 #pragma unroll
     for (int s = 0; s < 4; ++s)
@@ -532,8 +535,8 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_dma(GemmArgs a) {
     else
       interleave_mfma_first<NR, NM, 0x100>();
     if constexpr (kDma && kLateDma) {
-      ta.issue(nx2, kt + 2, wave);
-      tb.issue(nx2 + TA::kFloats, kt + 2, wave);
+      ta.issue(nx2, kt + 2, wave_s);
+      tb.issue(nx2 + TA::kFloats, kt + 2, wave_s);
     }
 #pragma unroll
     for (int s = 0; s < 2; ++s)
