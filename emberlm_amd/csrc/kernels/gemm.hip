@@ -570,23 +570,91 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_dma(GemmArgs a) {
   for (; kt + 2 < nk; ++kt) stage(kt, std::true_type{});
   for (; kt < nk; ++kt) stage(kt, std::false_type{});
 
+  if constexpr (BUF) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    // Stores (and the beta term's loads) through buffer resources based at
+    // this wave's first output row of C (and of D): a row's byte offset splits
+    // into a uniform part (the MFMA register's row slot, in an SGPR) and the
+    // lane's part (computed once), with no 64-bit address arithmetic per
+    // element.  Rows at or past M are skipped by an explicit test, made only on
+    // the wave tiles that reach M.  Same values as the form below.
+    const int wm_s = wave_s >> 1, wn_s = wave_s & 1;
+    const int64_t rw0 = m0 + wm_s * (BM / 2), cw0 = n0 + wn_s * (BN / 2);
+    if (rw0 < a.M) {
+      const float* Dm = a.D ? a.D : C;
+      const int64_t ldd = a.D ? a.ldd : a.ldc;
+      const __amdgpu_buffer_rsrc_t rc =
+          __builtin_amdgcn_make_buffer_rsrc(C + rw0 * a.ldc + cw0, 0, 0x7fffffff, 0x00020000);
+      const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<float*>(Dm + rw0 * ldd + cw0), 0, 0x7fffffff, 0x00020000);
+      const int lrow = kPermA ? 16 * g : 4 * g;  // the lane's part of the row
+      const int lc = static_cast<int>((lrow * a.ldc + r) * 4);
+      const int ld = static_cast<int>((lrow * ldd + r) * 4);
+      const int rows_left = static_cast<int>(min(a.M - rw0, int64_t{BM}));
+      // CHECKED: the wave tile reaches M.  BETA: the beta term is read, all 16
+      // values of an MFMA tile before the first is used (one wait per tile).
+      auto store_all = [&](auto checked, auto with_beta) {
+        constexpr bool kChecked = decltype(checked)::value, kBeta = decltype(with_beta)::value;
 #pragma unroll
-  for (int i = 0; i < FI; ++i)
+        for (int j = 0; j < FJ; ++j) {
+          if (cw0 + j * 32 + r >= a.N) continue;
 #pragma unroll
-    for (int j = 0; j < FJ; ++j) {
-      const int64_t col = n0 + wn * (BN / 2) + j * 32 + r;
-      if (col >= a.N) continue;
+          for (int i = 0; i < FI; ++i) {
+            float d[16];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int x = 8 * (e >> 2) + 4 * g + (e & 3);  // the MFMA tile's row slot
-        const int64_t row = m0 + wm * (BM / 2) + (kPermA ? 4 * x + i : i * 32 + x);
-        if (row < a.M) {
-          float* dst = C + row * a.ldc + col;
-          const float v = a.alpha * acc[i][j][e];
-          *dst = (a.beta != 0.f) ? v + a.beta * *addend(a, dst, row, col) : v;
+            for (int e = 0; e < 16; ++e) {
+              const int ru = kPermA ? 4 * (8 * (e >> 2) + (e & 3)) + i
+                                    : i * 32 + 8 * (e >> 2) + (e & 3);
+              d[e] = 0.f;
+              if (kBeta && !(kChecked && ru + lrow >= rows_left))
+                d[e] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(
+                               rd, ld + 128 * j, static_cast<int>(ru * ldd * 4), 0));
+            }
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              // the row slot's uniform part; the lane's part is in lc / ld
+              const int ru = kPermA ? 4 * (8 * (e >> 2) + (e & 3)) + i
+                                    : i * 32 + 8 * (e >> 2) + (e & 3);
+              if (kChecked && ru + lrow >= rows_left) continue;
+              const float v = a.alpha * acc[i][j][e];
+              const float out = kBeta ? v + a.beta * d[e] : v;
+              __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, out), rc,
+                                                    lc + 128 * j,
+                                                    static_cast<int>(ru * a.ldc * 4), 0);
+            }
+          }
         }
+      };
+      const bool full = rows_left >= BM / 2;
+      if (a.beta != 0.f) {
+        if (full) store_all(std::false_type{}, std::true_type{});
+        else store_all(std::true_type{}, std::true_type{});
+      } else {
+        if (full) store_all(std::false_type{}, std::false_type{});
+        else store_all(std::true_type{}, std::false_type{});
       }
     }
+#endif
+  } else {
+#pragma unroll
+    for (int i = 0; i < FI; ++i)
+#pragma unroll
+      for (int j = 0; j < FJ; ++j) {
+        const int64_t col = n0 + wn * (BN / 2) + j * 32 + r;
+        if (col >= a.N) continue;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int x = 8 * (e >> 2) + 4 * g + (e & 3);  // the MFMA tile's row slot
+          const int64_t row = m0 + wm * (BM / 2) + (kPermA ? 4 * x + i : i * 32 + x);
+          if (row < a.M) {
+            float* dst = C + row * a.ldc + col;
+            const float v = a.alpha * acc[i][j][e];
+            *dst = (a.beta != 0.f) ? v + a.beta * *addend(a, dst, row, col) : v;
+          }
+        }
+      }
+  }
 }
 
 // C = alpha * sum_{s<S} P[s] + beta * D (D = C when null), the split partials
@@ -808,7 +876,8 @@ int launch_dma_t(GemmArgs a, int64_t ny, hipStream_t st) {
   // K plus K, or K rows of lda (ldb) plus the tile's columns.
   const int64_t span_a = A_KC ? BM * a.lda + a.K : a.K * a.lda + BM;
   const int64_t span_b = B_KC ? BN * a.ldb + a.K : a.K * a.ldb + BN;
-  if (4 * std::max(span_a, span_b) < (int64_t{1} << 31) - 256)
+  const int64_t span_c = BM * std::max(a.ldc, a.D ? a.ldd : int64_t{0});  // the epilogue's rows
+  if (4 * std::max({span_a, span_b, span_c}) < (int64_t{1} << 31) - 256)
     gemm_f32_dma<A_KC, B_KC, BM, BN, OCC, true><<<grid, kThreads, 0, st>>>(a);
   else
     gemm_f32_dma<A_KC, B_KC, BM, BN, OCC, false><<<grid, kThreads, 0, st>>>(a);
