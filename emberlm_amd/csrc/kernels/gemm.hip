@@ -505,11 +505,11 @@ __global__ __launch_bounds__(kThreads, OCC) void gemm_f32_dma(GemmArgs a) {
   // ahead, the last two none, so the DMA instructions sit in straight-line
   // code the scheduler can spread among the MFMAs (one burst of them holds up
   // this wave's MFMA issue while the memory pipe takes them).  Where: among
-  // the slab-1 MFMAs before the barrier for 256-row tiles, among the slab-0
-  // MFMAs for 128-row tiles; each placement measured 1-3% faster on its own
-  // tile shape and up to 2% slower on the other.  The arithmetic is the same
-  // either way.
-  constexpr bool kLateDma = BM == 256;
+  // the slab-1 MFMAs before the barrier (the late form), or among the slab-0
+  // MFMAs.  With buffer-resource copies the late form is 0.2-1.7% faster on
+  // both tile shapes; with 64-bit-address copies the slab-0 form was 1-3%
+  // faster on 128-row tiles.  The arithmetic is the same either way.
+  constexpr bool kLateDma = BUF || BM == 256;
   int ic = 0;  // kt % 3
   auto stage = [&](int64_t kt, auto with_dma) {
     constexpr bool kDma = decltype(with_dma)::value;
