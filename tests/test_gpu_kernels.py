@@ -1056,6 +1056,7 @@ def _ds_row_floats(T):
     (4, 130, 8, 1, 128),    # 4 KV rows of group 8, D 128
     (1, 200, 32, 8, 64),    # 8 KV rows of group 4 (the c4 head layout)
     (2, 96, 32, 8, 64),     # 16 KV rows: chunks of 8 keep the XCD regrouping
+    (1, 700, 4, 2, 128),    # three 256-query dQ tiles: a workgroup takes 2 and 0, one 1 alone
 ])
 def test_attention_bwd_workspace_paths(B, T, H, Hk, D):
     # The backward keeps dS in the workspace when it fits, in chunks of KV rows
