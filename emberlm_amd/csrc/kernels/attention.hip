@@ -226,7 +226,7 @@ __device__ __forceinline__ float sum_over_rows(float x) {
 
 // ------------------------------------------------------------------ forward
 // Forward.  A wave owns 16 queries and a workgroup of eight waves 128, so
-// every K/V tile in LDS serves 128 queries, and at 102 registers per lane
+// every K/V tile in LDS serves 128 queries, and at 100 registers per lane
 // (D = 128) four waves fit on a SIMD (32 queries per wave on 32x32x2 tiles
 // took 239 and two waves: 1.14x slower at B=8, T=4096, H=16, Hk=8).  K and V
 // tiles are copied global -> LDS by DMA into two buffers, the next tile's
